@@ -1,0 +1,213 @@
+"""ctypes front-end of the CPU oracle (liborc_q4k.so).
+
+TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py import this module as the checker. The product
+(sera.c_amd/) never does.
+
+Every function returns numpy arrays in the oracle's layouts:
+    W  uint8  [N, K/256*144]   GGUF Q4_K rows
+    xq int8   [M, K]           Q8_1 quants
+    xd uint16 [M, K/32]        fp16 bits of the Q8_1 scale d
+    xs uint16 [M, K/32]        fp16 bits of the Q8_1 sum
+The C sources (q4k_oracle.c) cite the reference file:line each one restates.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liborc_q4k.so")
+REF_LIB_PATH = os.path.join(HERE, "_ref", "libq3quant_ref.so")
+
+_lib = None
+_ref = None
+
+
+def build():
+    """Compile the oracle (and the reference dequant when the tree is mounted)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        SZ = ctypes.c_size_t
+        for name, args, res in [
+            ("orc_h2f_n", [P, SZ, P], None),
+            ("orc_f2h_n", [P, SZ, P], None),
+            ("orc_np_f32_to_f16_n", [P, SZ, P], None),
+            ("orc_np_f16_to_f32_n", [P, SZ, P], None),
+            ("orc_dequant_q4k", [P, SZ, P], None),
+            ("orc_quantize_q4k", [P, I64, I64, P], ctypes.c_int),
+            ("orc_q8_1_row", [P, I64, P, P, P], None),
+            ("orc_q8_1_mmq", [P, I64, P, P, P], None),
+            ("orc_subblock_dots", [P, P, I64, I64, I64, P], None),
+            ("orc_q8_sums", [P, I64, I64, P], None),
+            ("orc_gemm_mmvq", [P, P, P, I64, I64, I64, P], None),
+            ("orc_gemm_mmq", [P, P, P, P, I64, I64, I64, P], None),
+            ("orc_gemm_dequant", [P, P, I64, I64, I64, P], None),
+        ]:
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def ref_lib():
+    """The reference's own src/q3_quant.c built into _ref/, or None."""
+    global _ref
+    if _ref is None and os.path.exists(REF_LIB_PATH):
+        R = ctypes.CDLL(REF_LIB_PATH)
+        R.q3_half_to_float.argtypes = [ctypes.c_uint16]
+        R.q3_half_to_float.restype = ctypes.c_float
+        R.q3_quant_dequantize_row.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_size_t,
+                                              ctypes.c_void_p, ctypes.c_size_t, ctypes.c_char_p,
+                                              ctypes.c_size_t]
+        R.q3_quant_dequantize_row.restype = ctypes.c_bool
+        _ref = R
+    return _ref
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def h2f(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_h2f_n(_p(h), h.size, _p(out))
+    return out
+
+
+def f2h(f):
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().orc_f2h_n(_p(f), f.size, _p(out))
+    return out
+
+
+def np_f32_to_f16(f):
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().orc_np_f32_to_f16_n(_p(f), f.size, _p(out))
+    return out
+
+
+def np_f16_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_np_f16_to_f32_n(_p(h), h.size, _p(out))
+    return out
+
+
+def dequant(W, N, K):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    assert W.size == N * (K // 256) * 144
+    out = np.empty((N, K), np.float32)
+    lib().orc_dequant_q4k(_p(W), N * (K // 256), _p(out))
+    return out
+
+
+def ref_dequant(W, N, K):
+    """Dequant through the reference's compiled q3_quant.c (None if absent)."""
+    R = ref_lib()
+    if R is None:
+        return None
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    out = np.empty((N, K), np.float32)
+    err = ctypes.create_string_buffer(256)
+    ok = R.q3_quant_dequantize_row(12, _p(W), N * (K // 256), _p(out), N * K, err, 256)
+    assert ok, err.value
+    return out
+
+
+def quantize_q4k(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, K = x.shape
+    out = np.empty((rows, K // 256 * 144), np.uint8)
+    rc = lib().orc_quantize_q4k(_p(x), rows, K, _p(out))
+    if rc != 0:
+        raise ValueError("K must be a multiple of 256")
+    return out
+
+
+def _q8(fn, X):
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    M, K = X.shape
+    xq = np.empty((M, K), np.int8)
+    xd = np.empty((M, K // 32), np.uint16)
+    xs = np.empty((M, K // 32), np.uint16)
+    for m in range(M):
+        fn(_p(X[m]), K, _p(xq[m]), _p(xd[m]), _p(xs[m]))
+    return xq, xd, xs
+
+
+def q8_1_row(X):
+    """MMVQ activation quantizer (cuda/mmq/quantize.cu:4-48)."""
+    return _q8(lib().orc_q8_1_row, X)
+
+
+def q8_1_mmq(X):
+    """MMQ DS4 activation quantizer (cuda/mmq/quantize.cu:271-367)."""
+    return _q8(lib().orc_q8_1_mmq, X)
+
+
+def subblock_dots(W, xq, N, K):
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    M = xq.shape[0]
+    out = np.empty((M, N, K // 32), np.int32)
+    lib().orc_subblock_dots(_p(np.ascontiguousarray(W)), _p(xq), M, N, K, _p(out))
+    return out
+
+
+def q8_sums(xq):
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    M, K = xq.shape
+    out = np.empty((M, K // 32), np.int32)
+    lib().orc_q8_sums(_p(xq), M, K, _p(out))
+    return out
+
+
+def gemm_mmvq(W, xq, xd, N, K):
+    M = xq.shape[0]
+    Y = np.empty((M, N), np.float64)
+    lib().orc_gemm_mmvq(_p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(xq)),
+                        _p(np.ascontiguousarray(xd)), M, N, K, _p(Y))
+    return Y
+
+
+def gemm_mmq(W, xq, xd, xs, N, K):
+    M = xq.shape[0]
+    Y = np.empty((M, N), np.float64)
+    lib().orc_gemm_mmq(_p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(xq)),
+                       _p(np.ascontiguousarray(xd)), _p(np.ascontiguousarray(xs)),
+                       M, N, K, _p(Y))
+    return Y
+
+
+def gemm_dequant(W, X, N, K):
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    M = X.shape[0]
+    Y = np.empty((M, N), np.float64)
+    lib().orc_gemm_dequant(_p(np.ascontiguousarray(W)), _p(X), M, N, K, _p(Y))
+    return Y
+
+
+def linear_reference(W, X, N, K):
+    """Output the reference path would produce for X [M,K]: MMVQ formula with
+    row-layout Q8_1 when M <= 8, MMQ formula with DS4 Q8_1 otherwise
+    (src/q3_q4_linear.cu:198-210)."""
+    M = X.shape[0]
+    if M <= 8:
+        xq, xd, _ = q8_1_row(X)
+        return gemm_mmvq(W, xq, xd, N, K)
+    xq, xd, xs = q8_1_mmq(X)
+    return gemm_mmq(W, xq, xd, xs, N, K)
