@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Bench driver for the MI355X Q4_K linear path (one GPU).
+
+Headline (the metric BASELINE.json quotes, config 2 at M=1): the whole
+q3_cuda_q4k_linear call (Q8_1 quantize + MMVQ) on the Qwen3-32B gate/up
+projection, 5120 -> 25600, M=1, as algorithmic HBM GB/s:
+    bytes/step = N*K*144/256 (Q4_K weights) + M*K*36/32 (Q8_1 read) + M*N*4 (Y write)
+Weights are seeded N(0,0.02) fp32 quantized to Q4_K on the device; eight
+copies (590 MB) are used round robin so that every step reads HBM, not the
+256 MB last-level cache. Activations are N(0,1) with 1% of channels x20.
+
+Also printed in the same JSON line:
+  roofline      the MMVQ kernel alone: algorithmic bytes per launch over its
+                average launch duration (HIP event pair around each launch on
+                the launch stream), against 8 TB/s
+  cpu_baseline  the reference's CPU path on this host: Q4_K dequant with the
+                reference's q3_quant.c (oracle/_ref, single thread) plus
+                numpy fp32 matmul, on the full gate/up matrix at M=1
+  results       MMVQ sweep M in {1,2,4,8} x {gate/up, down}; MMQ at M=512 on
+                gate/up in int8 TOPS against 5.0 POPS; with --full also
+                configs 3-5 (all seven projections, M=2048 + LM head, the
+                64-layer decode stream)
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--full] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "sera.c_amd"))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "MMVQ HBM GB/s @M=1; MMQ int8 TOPS @M=512; % of MI355X roofline"
+SHAPES = {  # name: (N, K) as (output features, input features)
+    "q": (8192, 5120), "k": (1024, 5120), "v": (1024, 5120), "o": (5120, 8192),
+    "gate": (25600, 5120), "up": (25600, 5120), "down": (5120, 25600),
+    "lm_head": (151936, 5120),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def alg_bytes(M, N, K):
+    return N * K * 144 // 256 + M * K * 36 // 32 + M * N * 4
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--full", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the Q4_K linear path has no multi-GPU split here)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import q3q4
+
+    L = q3q4.load()
+    dev = torch.device("cuda:0")
+    lin = q3q4.Linear(device=0, max_tokens=2048, max_features=151936, max_k=25600)
+    stream = torch.cuda.current_stream()
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+
+    def quantized(N, K, seed):
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        w = torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32) * 0.02
+        out = torch.empty((N, K // 256 * 144), dtype=torch.uint8, device=dev)
+        q3q4.quantize_weights(w, out)
+        del w
+        return out
+
+    def weight_set(N, K, seed, copies):
+        ws = [quantized(N, K, seed + i) for i in range(copies)]
+        arr = (ctypes.c_void_p * copies)(*[w.data_ptr() for w in ws])
+        return ws, arr
+
+    def activations(M, K, seed):
+        rng = np.random.default_rng(seed)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        ch = np.random.default_rng(K).choice(K, int(np.ceil(0.01 * K)), replace=False)
+        x[:, ch] *= 20.0
+        return torch.from_numpy(x).to(dev)
+
+    def bench_linear(geo, arr, n, x, y, warmup, iters):
+        ms = ctypes.c_double()
+        rc = L.sera_q4k_bench_linear(ctypes.byref(geo), arr, n, ctypes.c_void_p(x.data_ptr()),
+                                     x.shape[0], ctypes.c_void_p(y.data_ptr()), sptr, warmup, iters,
+                                     ctypes.byref(ms))
+        if rc != 0:
+            raise RuntimeError(f"bench_linear rc={rc}")
+        return ms.value / iters
+
+    def bench_kernel(path, arr, n, stage, y, partial, M, N, K, param, warmup, iters):
+        avg, tot = ctypes.c_double(), ctypes.c_double()
+        rc = L.sera_q4k_bench_kernel(path, arr, n, ctypes.c_void_p(stage.data_ptr()),
+                                     ctypes.c_void_p(y.data_ptr()),
+                                     ctypes.c_void_p(partial.data_ptr() if partial is not None else 0),
+                                     M, N, K, param, sptr, warmup, iters, ctypes.byref(avg),
+                                     ctypes.byref(tot))
+        if rc != 0:
+            raise RuntimeError(f"bench_kernel rc={rc}: {L.sera_q4k_last_error().decode()}")
+        return avg.value, tot.value / iters
+
+    results = {}
+
+    # ---------------- config 2: MMVQ decode sweep --------------------------
+    log("[bench] building weights: gate/up and down, "
+        f"{args.copies} copies each ({args.copies * 73.7 * 2:.0f} MB)")
+    t0 = time.time()
+    sets = {"gate_up": (25600, 5120, weight_set(25600, 5120, 0, args.copies)),
+            "down": (5120, 25600, weight_set(5120, 25600, 100, args.copies))}
+    torch.cuda.synchronize()
+    log(f"[bench] weights ready in {time.time() - t0:.1f}s")
+
+    sweep = []
+    headline = None
+    for name, (N, K, (ws, arr)) in sets.items():
+        geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+        for M in (1, 2, 4, 8):
+            x = activations(M, K, 1 + M)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            step_ms = bench_linear(geo, arr, args.copies, x, y, args.warmup, args.steps)
+            stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
+            q3q4.quantize_row(x, stage)
+            rpw = L.sera_q4k_mmvq_rows_per_wave(N, K)
+            kavg, kb2b = bench_kernel(0, arr, args.copies, stage, y, None, M, N, K, 0,
+                                      args.warmup, args.steps)
+            b = alg_bytes(M, N, K)
+            row = {"proj": name, "M": M, "N": N, "K": K, "rows_per_wave": rpw,
+                   "step_us": round(step_ms * 1e3, 3),
+                   "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),
+                   "kernel_us": round(kavg * 1e3, 3),
+                   "kernel_GBps": round(b / (kavg * 1e-3) / 1e9, 1),
+                   "kernel_frac_hbm": round(b / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "kernel_b2b_us": round(kb2b * 1e3, 3)}
+            log(f"[bench] mmvq {name} M={M}: step {row['step_us']} us ({row['step_GBps']} GB/s), "
+                f"kernel {row['kernel_us']} us ({row['kernel_GBps']} GB/s, "
+                f"{100 * row['kernel_frac_hbm']:.1f}% of HBM)")
+            sweep.append(row)
+            if name == "gate_up" and M == 1:
+                headline = (row, step_ms, b)
+    results["mmvq_sweep"] = sweep
+
+    # ---------------- config 3 (gate/up only unless --full): MMQ M=512 -----
+    def mmq_case(label, N, K, M, arr, ncopies, iters):
+        x = activations(M, K, 7)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+        step_ms = bench_linear(geo, arr, ncopies, x, y, 3, iters)
+        stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
+        q3q4.quantize_mmq(x, stage)
+        splits = q3q4.mmq_splits(M, N, K)
+        partial = (torch.empty(splits * M * N, dtype=torch.float32, device=dev)
+                   if splits > 1 else None)
+        kavg, _ = bench_kernel(1, arr, ncopies, stage, y, partial, M, N, K, splits, 3, iters)
+        ops = 2.0 * M * N * K
+        row = {"case": label, "M": M, "N": N, "K": K, "splits": splits,
+               "step_us": round(step_ms * 1e3, 2), "kernel_us": round(kavg * 1e3, 2),
+               "kernel_TOPS": round(ops / (kavg * 1e-3) / 1e12, 1),
+               "step_TOPS": round(ops / (step_ms * 1e-3) / 1e12, 1),
+               "kernel_frac_int8": round(ops / (kavg * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+               "kernel_GBps": round(alg_bytes(M, N, K) / (kavg * 1e-3) / 1e9, 1)}
+        log(f"[bench] mmq {label} M={M} N={N} K={K}: kernel {row['kernel_us']} us, "
+            f"{row['kernel_TOPS']} TOPS ({100 * row['kernel_frac_int8']:.1f}% of int8 peak)")
+        return row
+
+    gN, gK, (gws, garr) = sets["gate_up"]
+    results["mmq_m512_gate"] = mmq_case("gate", gN, gK, 512, garr, args.copies, 20)
+
+    if args.full:
+        full = []
+        for name in ("q", "k", "v", "o", "down"):
+            N, K = SHAPES[name]
+            ws, arr = (sets["down"][2] if name == "down" else weight_set(N, K, 300, 2))
+            full.append(mmq_case(name, N, K, 512, arr, len(ws), 20))
+        results["config3_m512"] = full
+        results["config4_m2048"] = [mmq_case("gate_up", gN, gK, 2048, garr, args.copies, 5),
+                                    mmq_case("down", 5120, 25600, 2048, sets["down"][2][1],
+                                             args.copies, 5)]
+        lmw, lmarr = weight_set(151936, 5120, 500, 1)
+        results["config4_lm_head_m16"] = mmq_case("lm_head", 151936, 5120, 16, lmarr, 1, 20)
+        del lmw
+        results["config5_decode_stream"] = decode_stream(torch, q3q4, L, lin, quantized, activations, dev)
+
+    # ---------------- roofline of the dominant kernel (MMVQ, M=1 gate/up) ---
+    row, step_ms, b = headline
+    kernel_ms = row["kernel_us"] * 1e-3
+    achieved = b / (kernel_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"sera_q4k_mmvq_kernel<1,{row['rows_per_wave']},4>",
+                "avg_launch_us": row["kernel_us"], "algorithmic_bytes_per_launch": b}
+
+    # ---------------- CPU baseline ------------------------------------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(np, torch, gws[0], gN, gK, activations(1, gK, 2).cpu().numpy())
+
+    value = b / (step_ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": (f"synthetic: seeded N(0,0.02) fp32 weights quantized to Q4_K on the GPU "
+                 f"({args.copies} copies round robin, {args.copies * 73.728:.0f} MB > 256 MB MALL); "
+                 "N(0,1) activations with 1% of channels x20"),
+        "config": {"workload": "config 2 headline: q3_cuda_q4k_linear (Q8_1 quantize + MMVQ), "
+                               "Qwen3-32B gate/up 5120->25600, M=1",
+                   "N": gN, "K": gK, "M": 1, "bytes_per_step": b},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "results": results,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(np, torch, w_dev, N, K, x):
+    """Stage A: Q4_K dequant of the whole matrix (reference q3_quant.c when
+    built into oracle/_ref, else this repo's C restatement), one thread.
+    Stage B: numpy fp32 X @ W_deq^T on the BLAS threads. Repeated until
+    ~10 s of CPU work."""
+    from oracle import oracle
+    W = w_dev.cpu().numpy()
+    kind = "reference" if oracle.ref_lib() is not None else "port"
+    deq = oracle.ref_dequant if kind == "reference" else oracle.dequant
+    try:
+        import threadpoolctl
+        blas = max([i.get("num_threads", 1) for i in threadpoolctl.threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        blas = os.cpu_count() or 1
+    ta = tb = 0.0
+    reps = 0
+    t_start = time.time()
+    while reps < 20 and (reps < 2 or time.time() - t_start < 10.0):
+        t0 = time.perf_counter()
+        Wd = deq(W, N, K)
+        t1 = time.perf_counter()
+        y = x @ Wd.T
+        t2 = time.perf_counter()
+        ta += t1 - t0
+        tb += t2 - t1
+        reps += 1
+        del Wd, y
+    ta /= reps
+    tb /= reps
+    wbytes = N * K // 256 * 144
+    return {"value": round(wbytes / (ta + tb) / 1e9, 3), "unit": "GB/s", "cores": int(blas),
+            "kind": kind,
+            "sample": (f"full gate/up matrix {N}x{K} Q4_K ({wbytes} B) at M=1, {reps} reps: "
+                       f"dequant {ta * 1e3:.1f} ms on 1 thread + numpy matmul {tb * 1e3:.1f} ms "
+                       f"on {blas} BLAS threads; nproc={os.cpu_count()}"),
+            "dequant_ms": round(ta * 1e3, 2), "matmul_ms": round(tb * 1e3, 2)}
+
+
+def decode_stream(torch, q3q4, L, lin, quantized, activations, dev):
+    """Config 5: 64 layers x 7 projections at M=1 plus the LM head, all
+    resident (~18 GB); one token = 449 q3_cuda_q4k_linear calls."""
+    order = ["q", "k", "v", "o", "gate", "up", "down"]
+    layers = []
+    total_w = 0
+    for layer in range(64):
+        ws = {}
+        for name in order:
+            N, K = SHAPES[name]
+            ws[name] = quantized(N, K, 10_000 + layer * 7 + order.index(name))
+            total_w += N * K // 256 * 144
+        layers.append(ws)
+    lm = quantized(151936, 5120, 99_999)
+    total_w += 151936 * 5120 // 256 * 144
+    geos = {n: q3q4.bind_geometry(q3q4.QTYPE_Q4_K, SHAPES[n][1], SHAPES[n][0]) for n in SHAPES}
+    xs = {K: activations(1, K, K) for K in (5120, 8192, 25600)}
+    ys = {n: torch.empty((1, SHAPES[n][0]), dtype=torch.float32, device=dev) for n in SHAPES}
+
+    def token():
+        for ws in layers:
+            for n in order:
+                lin(geos[n], ws[n], xs[SHAPES[n][1]], ys[n])
+        lin(geos["lm_head"], lm, xs[5120], ys["lm_head"])
+
+    token()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 5
+    a.record()
+    for _ in range(reps):
+        token()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    del layers, lm
+    return {"ms_per_token": round(ms, 3), "weight_bytes": total_w,
+            "sustained_GBps": round(total_w / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(total_w / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "Python issues the 449 calls; host launch cost is inside the time"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,134 @@
+/*
+ * sera_q4k.h - C ABI of the MI355X (gfx950) Q4_K linear kernels.
+ *
+ * This is the layer the q3_q4_linear boundary (q3_q4_linear.h) calls; it
+ * plays the role of the reference's internal host glue cuda/q3_mmq.h:35-94
+ * and of the test-oracle device decode src/q3_cuda_primitives.h. Plain C
+ * types only: device pointers are void* / float*, a stream is a hipStream_t
+ * passed as void* (NULL = the null stream). Every function enqueues on the
+ * given stream and returns without synchronizing; none allocates device
+ * memory.
+ *
+ * Return codes (as in cuda/q3_mmq.h): 0 success, -1 invalid arguments or
+ * state, -2 activation-quantization launch failed, -3 matmul launch failed.
+ * sera_q4k_last_error() gives the message of the last failure on the
+ * calling thread.
+ *
+ * Layouts:
+ *   W  GGUF Q4_K, N rows of K/256 blocks of 144 bytes (K % 256 == 0)
+ *   X  fp32 [M][K] row-major, 16-byte aligned
+ *   Y  fp32 [M][N] row-major: Y[token*N + feature]
+ *   stages: see sera_q8_1_row_stage_offsets / sera_q8_1_mmq_stage_offsets
+ */
+#ifndef SERA_Q4K_H
+#define SERA_Q4K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SERA_Q4K_MMVQ_MAX_BATCH 8   /* cuda/q3_mmq.h:77 Q3_MMVQ_MAX_BATCH */
+
+/* ---- set-up (cuda/q3_mmq.h:35-38, 84-94) ------------------------------ */
+
+/* Select `device` and create the library's timing events. Returns 0. */
+int sera_q4k_init(int device);
+
+/* Persistent scratch bytes for calls with up to max_tokens rows, up to
+ * max_features output features and contraction length up to max_k
+ * (q3_mmq_arena_bytes, cuda/q3_mmq.cu:213-243). Holds the Q8_1 stage and
+ * the split-K partial sums. */
+size_t sera_q4k_arena_bytes(size_t max_tokens, int64_t max_features, int64_t max_k);
+
+/* Attach caller-owned device scratch (q3_mmq_set_arena, cuda/q3_mmq.h:84). */
+int sera_q4k_set_arena(void *device_ptr, size_t bytes);
+
+/* ---- whole linear: quantize + kernel (cuda/q3_mmq.h:52-63) ------------ */
+
+/* Y[M][N] = X[M][K] . W^T through the MMQ tile path (any M >= 1).
+ * Replaces q3_mmq_q4_K_dense (cuda/q3_mmq.cu:258-379); note M = tokens,
+ * N = features here (the donor ABI had them swapped). */
+int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
+                   void *stream);
+
+/* Same contract through the MMVQ path, 1 <= M <= 8.
+ * Replaces q3_mmq_q4_K_dense_vec (cuda/q3_mmq.cu:408-506). */
+int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
+                       void *stream);
+
+/* Event timings of the last dense call, valid after the caller synchronized
+ * its stream (q3_mmq_read_timings, cuda/q3_mmq.h:48-50). */
+void sera_q4k_read_timings(double *quant_ms, double *kernel_ms, double *total_ms);
+
+/* ---- building blocks -------------------------------------------------- */
+
+/* Row-layout Q8_1 stage (MMVQ activations): qs int8 [M][K], ds half2
+ * [M][K/32] = (fp16 d, fp16 sum), dsf float4 [M][K/64] =
+ * (d_2p, d_2p+1, d_2p*S_2p, d_2p+1*S_2p+1) with S the int sum of 32 quants.
+ * Quantizer of cuda/mmq/quantize.cu:4-48 (quantize_row_q8_1_cuda, :369-383). */
+size_t sera_q8_1_row_stage_bytes(int M, int K);
+void sera_q8_1_row_stage_offsets(int M, int K, size_t *qs, size_t *ds, size_t *dsf);
+int sera_q8_1_quantize_row(const float *X, int M, int K, void *stage, void *stream);
+
+/* MMQ-layout Q8_1 stage: qs int8 [Mpad][K], ds half2 [Mpad][K/32], rows
+ * M..Mpad-1 zero. Quantizer of cuda/mmq/quantize.cu:271-367
+ * (quantize_mmq_q8_1<DS4>, launcher :385-413). */
+int sera_q8_1_mmq_padded_rows(int M);
+size_t sera_q8_1_mmq_stage_bytes(int M, int K);
+void sera_q8_1_mmq_stage_offsets(int M, int K, size_t *qs, size_t *ds);
+int sera_q8_1_quantize_mmq(const float *X, int M, int K, void *stage, void *stream);
+
+/* MMVQ kernel on a row stage (mul_mat_vec_q<Q4_K>, cuda/mmq/mmvq.cu:393-587).
+ * rows_per_wave in {1,2,4,8}, or 0 for the built-in choice. */
+int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
+                  int rows_per_wave, void *stream);
+int sera_q4k_mmvq_rows_per_wave(int N, int K);
+
+/* MMQ kernel on an MMQ stage (mul_mat_q<Q4_K> + stream-K fixup,
+ * cuda/mmq/mmq.cuh:3641-4352). `splits` > 1 splits K; then `partial` must
+ * hold splits*M*N floats (M*N % 4 == 0). splits = 0 picks the built-in
+ * choice (sera_q4k_mmq_splits). */
+int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, float *partial, int M, int N,
+                 int K, int splits, void *stream);
+int sera_q4k_mmq_splits(int M, int N, int K);
+
+/* Device Q4_K dequant, w = (d*sc)*q - (dmin*m) per weight; replaces
+ * q3_cuda_dequantize_row (src/q3_cuda_primitives.h, cuda/q3_cuda_primitives.cu:13-95). */
+int sera_q4k_dequantize(const void *W, size_t nblocks, float *out, void *stream);
+
+/* Exact per-32 int32 dots I[m][n][b] = sum q4*q8 for the first M rows of a
+ * stage's qs array (int8 [rows][K]). Test hook for the integer core shared
+ * by both kernels (cuda/mmq/vecdotq.cuh:505-555). */
+int sera_q4k_subblock_dots(const void *W, const void *stage_qs, int32_t *I, int M, int N, int K,
+                           void *stream);
+
+/* fp32 [rows][K] -> GGUF Q4_K bytes, bit-exact with the repo's quantizer
+ * quantize_q4_k_matrix (tools/qwen3_q4.py:410-481). */
+int sera_q4k_quantize(const float *X, int64_t rows, int64_t K, void *out, void *stream);
+
+const char *sera_q4k_last_error(void);
+
+/* ---- bench loops (the role of src/q3_bench_q4_linear.cu:181-226) ------- */
+
+/* `warmup` untimed and `iters` timed q3_cuda_q4k_linear calls on weight
+ * copies weights[i % nweights]; *elapsed_ms spans the timed calls.
+ * `geometry` is a q3_q4_linear_geometry* (include/q3_q4_linear.h). */
+int sera_q4k_bench_linear(const void *geometry, const void *const *weights, int nweights,
+                          const float *X, size_t M, float *Y, void *stream, int warmup,
+                          int iters, double *elapsed_ms);
+
+/* Kernel-only loop on a prepared stage (path 0 = MMVQ with param =
+ * rows_per_wave, 1 = MMQ with param = splits). *avg_kernel_ms averages an
+ * event pair around each launch; *elapsed_ms spans all launches. */
+int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, const void *stage,
+                          float *Y, float *partial, int M, int N, int K, int param, void *stream,
+                          int warmup, int iters, double *avg_kernel_ms, double *elapsed_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

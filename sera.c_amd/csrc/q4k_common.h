@@ -1,0 +1,97 @@
+/*
+ * q4k_common.h - shared definitions for the gfx950 Q4_K linear kernels.
+ *
+ * GGUF Q4_K super-block (256 weights, 144 bytes), as in the reference's
+ * src/q3_quant.h:28-33 and cuda/mmq/ggml-common.h:313-328:
+ *   bytes 0-1   d     fp16  scale of the 6-bit sub-block scales
+ *   bytes 2-3   dmin  fp16  scale of the 6-bit sub-block mins
+ *   bytes 4-15  12 bytes of packed 6-bit (scale, min) for 8 sub-blocks
+ *   bytes 16-143 qs[128]: sub-block j uses qs[(j/2)*32 + l], low nibble for
+ *                even j, high nibble for odd j
+ * Weight of sub-block j, element l: d*sc_j*q - dmin*m_j.
+ *
+ * Q8_1 activation stages (this library's device layout; the values are the
+ * reference's block_q8_1 {half2 ds; int8 qs[32]} values, stored split):
+ *   row stage (MMVQ):  qs  int8   [M][K]
+ *                      ds  half2  [M][K/32]   (fp16 d, fp16 sum of x)
+ *                      dsf float4 [M][K/64]   (d_2p, d_2p+1, d_2p*S_2p, d_2p+1*S_2p+1)
+ *                                               S = sum of the 32 int8 quants
+ *   mmq stage (MMQ):   qs  int8   [Mpad][K]
+ *                      ds  half2  [Mpad][K/32]
+ */
+#ifndef SERA_Q4K_COMMON_H
+#define SERA_Q4K_COMMON_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define Q4K_QK 256
+#define Q4K_BLOCK_BYTES 144
+#define Q8_QK 32
+
+/* Byte offsets of the sub-arrays of a stage, 256-byte aligned. */
+static inline size_t sera_align256(size_t v) { return (v + 255u) & ~(size_t)255u; }
+
+typedef struct {
+    size_t qs;      /* int8  [rows][K]      */
+    size_t ds;      /* half2 [rows][K/32]   */
+    size_t dsf;     /* float4 [rows][K/64]  (row stage only, else 0) */
+    size_t total;
+} sera_stage_layout;
+
+static inline sera_stage_layout sera_row_stage_layout(size_t rows, size_t K) {
+    sera_stage_layout L;
+    L.qs = 0;
+    L.ds = sera_align256(rows * K);
+    L.dsf = sera_align256(L.ds + rows * (K / 32) * 4);
+    L.total = sera_align256(L.dsf + rows * (K / 64) * 16);
+    return L;
+}
+
+static inline sera_stage_layout sera_mmq_stage_layout(size_t rows_padded, size_t K) {
+    sera_stage_layout L;
+    L.qs = 0;
+    L.ds = sera_align256(rows_padded * K);
+    L.dsf = 0;
+    L.total = sera_align256(L.ds + rows_padded * (K / 32) * 4);
+    return L;
+}
+
+#ifdef __HIPCC__
+typedef _Float16 f16;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f_bits(uint32_t bits16) {
+    union { uint16_t u; f16 h; } c;
+    c.u = (uint16_t)bits16;
+    return (float)c.h;
+}
+
+__device__ __forceinline__ uint32_t f2h_bits(float f) {
+    union { uint16_t u; f16 h; } c;
+    c.h = (f16)f;             /* v_cvt_f16_f32: round to nearest even */
+    return c.u;
+}
+
+/* 6-bit (scale, min) of sub-block j from the 12 scale bytes held as three
+ * little-endian dwords s0 = bytes 0-3, s1 = bytes 4-7, s2 = bytes 8-11
+ * (src/q3_quant.c:44-55). */
+__device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                              uint32_t *sc, uint32_t *m) {
+    if (j < 4) {
+        *sc = (s0 >> (8 * j)) & 63u;
+        *m = (s1 >> (8 * j)) & 63u;
+    } else {
+        const int jj = j - 4;
+        const uint32_t b8 = (s2 >> (8 * jj)) & 0xffu;        /* scales[j+4] */
+        *sc = (b8 & 0xfu) | (((s0 >> (8 * jj)) >> 6 & 3u) << 4);  /* scales[j-4] >> 6 */
+        *m = (b8 >> 4) | (((s1 >> (8 * jj)) >> 6 & 3u) << 4);     /* scales[j] >> 6 */
+    }
+}
+#endif
+
+#endif

@@ -1,0 +1,122 @@
+/*
+ * q8_quantize.hip - fp32 activations -> Q8_1 (32 values per scale).
+ *
+ * Two quantizers, each bit-exact with one of the reference's formulas:
+ *
+ *  row (MMVQ activations), cuda/mmq/quantize.cu:4-48
+ *     amax = max|x|, sum = xor-butterfly over offsets 16,8,4,2,1 of the 32
+ *     values, d = amax/127, q = amax == 0 ? 0 : roundf(x/d),
+ *     ds = (fp16(d), fp16(sum))
+ *
+ *  mmq (MMQ activations, DS4 layout), cuda/mmq/quantize.cu:271-367
+ *     8 lanes hold 4 consecutive values each, lane sum ((x0+x1)+x2)+x3,
+ *     then xor 4,2,1 across the 8 lanes; d_inv = 127/amax,
+ *     q = roundf(x*d_inv), d = 1/d_inv; amax == 0 gives q = 0, d = 0.
+ *
+ * Division is IEEE correctly rounded (hipcc default), roundf rounds half
+ * away from zero, fp16 conversion rounds to nearest even. The float sums are
+ * pure additions in a fixed pairing, so they cannot be contracted or
+ * reassociated by the compiler.
+ */
+#include "q4k_common.h"
+
+/* One wave-64 handles two consecutive Q8_1 blocks (lanes 0-31 and 32-63);
+ * a 256-thread workgroup covers 256 values of one activation row.
+ * grid = (K/256, M). Writes qs, ds and the MMVQ helper dsf. */
+__global__ __launch_bounds__(256) void sera_q8_1_row_kernel(
+        const float *__restrict__ x, int K, int8_t *__restrict__ qs,
+        uint32_t *__restrict__ ds, float4 *__restrict__ dsf) {
+    const int row = blockIdx.y;
+    const int k = blockIdx.x * 256 + threadIdx.x;
+    const float xi = x[(size_t)row * K + k];
+
+    float amax = fabsf(xi);
+    float sum = xi;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        sum = sum + __shfl_xor(sum, off, 64);
+    }
+    const float d = amax / 127.0f;
+    const float qf = amax == 0.0f ? 0.0f : roundf(xi / d);
+    const int q = (int)qf;
+    qs[(size_t)row * K + k] = (int8_t)q;
+
+    /* S = sum of the 32 quants (exact integer), for the MMVQ min term. */
+    int s = q;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+
+    const uint32_t dh = f2h_bits(d);
+    const uint32_t sh = f2h_bits(sum);
+    const int lane = threadIdx.x & 63;
+    const size_t blk = (size_t)row * (K / 32) + (k >> 5);
+    if ((lane & 31) == 0) ds[blk] = dh | (sh << 16);
+
+    /* dsf pairs block 2p (lanes 0-31) with block 2p+1 (lanes 32-63). */
+    const float d8 = h2f_bits(dh);
+    const float dS = d8 * (float)s;
+    const float d8_hi = __shfl(d8, 32, 64);
+    const float dS_hi = __shfl(dS, 32, 64);
+    if (lane == 0) {
+        dsf[(size_t)row * (K / 64) + (k >> 6)] = make_float4(d8, d8_hi, dS, dS_hi);
+    }
+}
+
+/* DS4 quantizer. Each thread holds 4 consecutive values (one float4); a
+ * 256-thread workgroup covers 1024 values of one row. grid = (ceil(K/1024),
+ * Mpad). Rows >= M (padding up to the MMQ tile) are written as zeros. */
+__global__ __launch_bounds__(256) void sera_q8_1_mmq_kernel(
+        const float *__restrict__ x, int M, int K, int8_t *__restrict__ qs,
+        uint32_t *__restrict__ ds) {
+    const int row = blockIdx.y;
+    const int k = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (k >= K) return;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (row < M) v = *(const float4 *)(x + (size_t)row * K + k);
+
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    float sum = ((v.x + v.y) + v.z) + v.w;
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        sum = sum + __shfl_xor(sum, off, 64);
+    }
+    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+    float d = 0.0f;
+    if (amax != 0.0f) {
+        const float d_inv = 127.0f / amax;
+        q0 = (int)roundf(v.x * d_inv);
+        q1 = (int)roundf(v.y * d_inv);
+        q2 = (int)roundf(v.z * d_inv);
+        q3 = (int)roundf(v.w * d_inv);
+        d = 1.0f / d_inv;
+    }
+    const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                            ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+    *(uint32_t *)(qs + (size_t)row * K + k) = packed;
+    if ((threadIdx.x & 7) == 0) {
+        ds[(size_t)row * (K / 32) + (k >> 5)] = f2h_bits(d) | (f2h_bits(sum) << 16);
+    }
+}
+
+extern "C" hipError_t sera_launch_q8_1_row(const float *x, int M, int K, void *stage,
+                                           hipStream_t stream) {
+    const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
+    char *base = (char *)stage;
+    dim3 grid(K / 256, M);
+    hipLaunchKernelGGL(sera_q8_1_row_kernel, grid, dim3(256), 0, stream, x, K,
+                       (int8_t *)(base + L.qs), (uint32_t *)(base + L.ds),
+                       (float4 *)(base + L.dsf));
+    return hipGetLastError();
+}
+
+extern "C" hipError_t sera_launch_q8_1_mmq(const float *x, int M, int Mpad, int K, void *stage,
+                                           hipStream_t stream) {
+    const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
+    char *base = (char *)stage;
+    dim3 grid((K + 1023) / 1024, Mpad);
+    hipLaunchKernelGGL(sera_q8_1_mmq_kernel, grid, dim3(256), 0, stream, x, M, K,
+                       (int8_t *)(base + L.qs), (uint32_t *)(base + L.ds));
+    return hipGetLastError();
+}

@@ -1,0 +1,88 @@
+/*
+ * sera_q4k_bench.hip - timing loops for the bench driver, the counterpart
+ * of the reference's --bench-q4-linear mode (src/q3_bench_q4_linear.cu:
+ * 181-226), kept in C so host launch cost stays out of the GPU timings.
+ *
+ * Both loops walk a list of resident weight copies round robin, so a
+ * working set larger than the 256 MB last-level (MALL) cache keeps every
+ * weight read an HBM read.
+ */
+#include "q4k_common.h"
+#include "../../include/q3_q4_linear.h"
+#include "../../include/sera_q4k.h"
+
+#include <stdlib.h>
+
+extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y, int M, int N,
+                                           int K, int rpw, hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
+                                          int M, int N, int K, int splits, hipStream_t s);
+
+/* `warmup` untimed then `iters` timed calls of q3_cuda_q4k_linear; weight i
+ * of the call is weights[i % nweights]. elapsed_ms: first-to-last event of
+ * the timed calls (host launch overlaps GPU work). */
+extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *weights,
+                                     int nweights, const float *x, size_t M, float *y, void *stream,
+                                     int warmup, int iters, double *elapsed_ms) {
+    const q3_q4_linear_geometry *g = (const q3_q4_linear_geometry *)geometry;
+    if (!g || !weights || nweights <= 0 || iters <= 0 || !elapsed_ms) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    char err[256];
+    for (int i = 0; i < warmup; i++)
+        if (!q3_cuda_q4k_linear(g, weights[i % nweights], x, M, y, stream, NULL, err, sizeof(err))) return -3;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return -1;
+    (void)hipEventRecord(a, s);
+    for (int i = 0; i < iters; i++)
+        if (!q3_cuda_q4k_linear(g, weights[i % nweights], x, M, y, stream, NULL, err, sizeof(err))) return -3;
+    (void)hipEventRecord(b, s);
+    (void)hipEventSynchronize(b);
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, a, b);
+    *elapsed_ms = ms;
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return 0;
+}
+
+/* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ.
+ * avg_kernel_ms: mean over launches of an event pair recorded right before
+ * and after each launch on `stream` (the launch's own duration);
+ * elapsed_ms: first-to-last event over all back-to-back launches. */
+extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights,
+                                     const void *stage, float *y, float *partial, int M, int N, int K,
+                                     int param, void *stream, int warmup, int iters,
+                                     double *avg_kernel_ms, double *elapsed_ms) {
+    if (!weights || nweights <= 0 || iters <= 0) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    auto launch = [&](int i) -> hipError_t {
+        const void *w = weights[i % nweights];
+        return path == 0 ? sera_launch_q4k_mmvq(w, stage, y, M, N, K, param, s)
+                         : sera_launch_q4k_mmq(w, stage, y, partial, M, N, K, param, s);
+    };
+    for (int i = 0; i < warmup; i++)
+        if (launch(i) != hipSuccess) return -3;
+    hipEvent_t *ev = (hipEvent_t *)malloc(sizeof(hipEvent_t) * 2 * (size_t)iters);
+    if (!ev) return -1;
+    for (int i = 0; i < 2 * iters; i++)
+        if (hipEventCreate(&ev[i]) != hipSuccess) { free(ev); return -1; }
+    for (int i = 0; i < iters; i++) {
+        (void)hipEventRecord(ev[2 * i], s);
+        if (launch(i) != hipSuccess) { free(ev); return -3; }
+        (void)hipEventRecord(ev[2 * i + 1], s);
+    }
+    (void)hipEventSynchronize(ev[2 * iters - 1]);
+    double sum = 0.0;
+    for (int i = 0; i < iters; i++) {
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
+        sum += ms;
+    }
+    float tot = 0.0f;
+    (void)hipEventElapsedTime(&tot, ev[0], ev[2 * iters - 1]);
+    for (int i = 0; i < 2 * iters; i++) (void)hipEventDestroy(ev[i]);
+    free(ev);
+    if (avg_kernel_ms) *avg_kernel_ms = sum / iters;
+    if (elapsed_ms) *elapsed_ms = tot;
+    return 0;
+}

@@ -1,0 +1,260 @@
+/*
+ * sera_q4k_runtime.hip - host side of include/sera_q4k.h: argument checks,
+ * the caller-owned scratch arena, hipEvent timings and kernel launches.
+ *
+ * Replaces the reference's host glue cuda/q3_mmq.cu (arena :95-137,
+ * sizing :170-243, dense paths :258-379 and :408-506, timings :45-83).
+ * Nothing here allocates device memory or synchronizes: the arena is
+ * attached once by the caller, every launch is enqueued on the caller's
+ * stream, and timings are read only after the caller has synchronized.
+ */
+#include "q4k_common.h"
+#include "../../include/sera_q4k.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+extern "C" hipError_t sera_launch_q8_1_row(const float *x, int M, int K, void *stage, hipStream_t s);
+extern "C" hipError_t sera_launch_q8_1_mmq(const float *x, int M, int Mpad, int K, void *stage,
+                                           hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y, int M, int N,
+                                           int K, int rpw, hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
+                                          int M, int N, int K, int splits, hipStream_t s);
+extern "C" int sera_mmvq_rows_per_wave(int N, int K);
+extern "C" int sera_mmq_splits(int M, int N, int K);
+extern "C" int sera_mmq_padded_rows(int M);
+extern "C" int sera_mmq_bm(int M);
+extern "C" hipError_t sera_launch_q4k_quantize(const float *x, int64_t rows, int64_t K, void *out,
+                                               hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_dequant(const void *W, int64_t nblocks, float *out, hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_subblock_dots(const void *W, const int8_t *xq, int32_t *I, int M,
+                                                    int N, int K, hipStream_t s);
+
+namespace {
+
+thread_local char g_err[256];
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+struct Events {
+    hipEvent_t quant_begin, quant_end, kernel_begin, kernel_end;
+    bool valid;
+};
+
+int g_device = -1;
+Events g_ev = {};
+unsigned char *g_arena = nullptr;
+size_t g_arena_bytes = 0;
+
+/* Split-K partial floats never exceed this: the split count stops doubling
+ * once tiles*splits >= 512, so splits*Mpad*N < 1024 * BM * 128. */
+size_t partial_floats_bound(size_t max_tokens, int64_t max_features) {
+    const size_t bm = (size_t)sera_mmq_bm((int)(max_tokens > 0x7fffffff ? 0x7fffffff : max_tokens));
+    const size_t by_tiles = (size_t)1024 * bm * 128;
+    const size_t by_shape = (size_t)16 * max_tokens * (size_t)(max_features > 0 ? max_features : 0);
+    return by_tiles < by_shape ? by_tiles : by_shape;
+}
+
+bool check_shape(const char *tag, const void *W, const float *X, const float *Y, int M, int N, int K) {
+    if (!W || !X || !Y) { fail(-1, "%s: null pointer", tag); return false; }
+    if (M <= 0 || N <= 0 || K <= 0) { fail(-1, "%s: bad shape M=%d N=%d K=%d", tag, M, N, K); return false; }
+    if (K % Q4K_QK != 0) { fail(-1, "%s: K=%d must be a multiple of 256", tag, K); return false; }
+    if (((uintptr_t)X & 15u) != 0) { fail(-1, "%s: X must be 16-byte aligned", tag); return false; }
+    if (((uintptr_t)W & 15u) != 0) { fail(-1, "%s: W must be 16-byte aligned", tag); return false; }
+    return true;
+}
+
+void record(hipEvent_t e, hipStream_t s) {
+    if (g_ev.valid) hipEventRecord(e, s);
+}
+
+}  // namespace
+
+extern "C" const char *sera_q4k_last_error(void) { return g_err; }
+
+extern "C" int sera_q4k_init(int device) {
+    if (device < 0) return fail(-1, "sera_q4k_init: invalid device %d", device);
+    if (hipSetDevice(device) != hipSuccess) return fail(-1, "sera_q4k_init: hipSetDevice(%d) failed", device);
+    if (!g_ev.valid || g_device != device) {
+        if (hipEventCreate(&g_ev.quant_begin) != hipSuccess ||
+            hipEventCreate(&g_ev.quant_end) != hipSuccess ||
+            hipEventCreate(&g_ev.kernel_begin) != hipSuccess ||
+            hipEventCreate(&g_ev.kernel_end) != hipSuccess)
+            return fail(-1, "sera_q4k_init: hipEventCreate failed");
+        g_ev.valid = true;
+    }
+    g_device = device;
+    return 0;
+}
+
+extern "C" size_t sera_q8_1_row_stage_bytes(int M, int K) {
+    if (M <= 0 || K <= 0) return 0;
+    return sera_row_stage_layout((size_t)M, (size_t)K).total;
+}
+
+extern "C" void sera_q8_1_row_stage_offsets(int M, int K, size_t *qs, size_t *ds, size_t *dsf) {
+    const sera_stage_layout L = sera_row_stage_layout((size_t)(M > 0 ? M : 0), (size_t)(K > 0 ? K : 0));
+    if (qs) *qs = L.qs;
+    if (ds) *ds = L.ds;
+    if (dsf) *dsf = L.dsf;
+}
+
+extern "C" int sera_q8_1_mmq_padded_rows(int M) { return M > 0 ? sera_mmq_padded_rows(M) : 0; }
+
+extern "C" size_t sera_q8_1_mmq_stage_bytes(int M, int K) {
+    if (M <= 0 || K <= 0) return 0;
+    return sera_mmq_stage_layout((size_t)sera_mmq_padded_rows(M), (size_t)K).total;
+}
+
+extern "C" void sera_q8_1_mmq_stage_offsets(int M, int K, size_t *qs, size_t *ds) {
+    const size_t mp = M > 0 ? (size_t)sera_mmq_padded_rows(M) : 0;
+    const sera_stage_layout L = sera_mmq_stage_layout(mp, (size_t)(K > 0 ? K : 0));
+    if (qs) *qs = L.qs;
+    if (ds) *ds = L.ds;
+}
+
+extern "C" size_t sera_q4k_arena_bytes(size_t max_tokens, int64_t max_features, int64_t max_k) {
+    if (max_tokens == 0 || max_k <= 0) return (size_t)1 << 21;  /* unspecified geometry floor */
+    const int mt = (int)(max_tokens > 0x7fffffff ? 0x7fffffff : max_tokens);
+    const size_t row = sera_row_stage_layout((size_t)(mt < SERA_Q4K_MMVQ_MAX_BATCH ? mt : SERA_Q4K_MMVQ_MAX_BATCH),
+                                             (size_t)max_k).total;
+    const size_t mmq = sera_mmq_stage_layout((size_t)sera_mmq_padded_rows(mt), (size_t)max_k).total;
+    const size_t stage = row > mmq ? row : mmq;
+    const size_t partial = sera_align256(partial_floats_bound(max_tokens, max_features) * sizeof(float));
+    return stage + partial;
+}
+
+extern "C" int sera_q4k_set_arena(void *device_ptr, size_t bytes) {
+    if (!device_ptr || bytes == 0) return fail(-1, "sera_q4k_set_arena: null arena");
+    if (((uintptr_t)device_ptr & 255u) != 0) return fail(-1, "sera_q4k_set_arena: arena must be 256-byte aligned");
+    g_arena = (unsigned char *)device_ptr;
+    g_arena_bytes = bytes;
+    return 0;
+}
+
+extern "C" int sera_q8_1_quantize_row(const float *X, int M, int K, void *stage, void *stream) {
+    if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q8_1_quantize_row: bad arguments");
+    return sera_launch_q8_1_row(X, M, K, stage, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-2, "sera_q8_1_quantize_row: launch failed");
+}
+
+extern "C" int sera_q8_1_quantize_mmq(const float *X, int M, int K, void *stage, void *stream) {
+    if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q8_1_quantize_mmq: bad arguments");
+    if (((uintptr_t)X & 15u) != 0) return fail(-1, "sera_q8_1_quantize_mmq: X must be 16-byte aligned");
+    return sera_launch_q8_1_mmq(X, M, sera_mmq_padded_rows(M), K, stage, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-2, "sera_q8_1_quantize_mmq: launch failed");
+}
+
+extern "C" int sera_q4k_mmvq_rows_per_wave(int N, int K) { return sera_mmvq_rows_per_wave(N, K); }
+
+extern "C" int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
+                             int rows_per_wave, void *stream) {
+    if (!W || !row_stage || !Y) return fail(-1, "sera_q4k_mmvq: null pointer");
+    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q4k_mmvq: batch M=%d outside 1..8", M);
+    if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_mmvq: bad shape N=%d K=%d", N, K);
+    if (rows_per_wave != 0 && rows_per_wave != 1 && rows_per_wave != 2 && rows_per_wave != 4 &&
+        rows_per_wave != 8)
+        return fail(-1, "sera_q4k_mmvq: rows_per_wave=%d not in {0,1,2,4,8}", rows_per_wave);
+    return sera_launch_q4k_mmvq(W, row_stage, Y, M, N, K, rows_per_wave, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_q4k_mmvq: launch failed");
+}
+
+extern "C" int sera_q4k_mmq_splits(int M, int N, int K) { return sera_mmq_splits(M, N, K); }
+
+extern "C" int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, float *partial, int M, int N,
+                            int K, int splits, void *stream) {
+    if (!W || !mmq_stage || !Y) return fail(-1, "sera_q4k_mmq: null pointer");
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_mmq: bad shape M=%d N=%d K=%d", M, N, K);
+    if (splits == 0) splits = sera_mmq_splits(M, N, K);
+    if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q4k_mmq: splits=%d outside 1..K/256", splits);
+    if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
+        return fail(-1, "sera_q4k_mmq: split-K needs a partial buffer and M*N %% 4 == 0");
+    return sera_launch_q4k_mmq(W, mmq_stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_q4k_mmq: launch failed");
+}
+
+extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream) {
+    if (!check_shape("sera_q4k_dense", W, X, Y, M, N, K)) return -1;
+    if (!g_arena) return fail(-1, "sera_q4k_dense: no arena attached");
+    hipStream_t s = (hipStream_t)stream;
+    const int Mpad = sera_mmq_padded_rows(M);
+    const size_t stage_bytes = sera_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
+    int splits = sera_mmq_splits(M, N, K);
+    if (((size_t)M * N) % 4 != 0) splits = 1;
+    const size_t partial_bytes = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+    if (stage_bytes + partial_bytes > g_arena_bytes)
+        return fail(-1, "sera_q4k_dense: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
+                    g_arena_bytes);
+    void *stage = g_arena;
+    float *partial = splits > 1 ? (float *)(g_arena + stage_bytes) : nullptr;
+    record(g_ev.quant_begin, s);
+    if (sera_launch_q8_1_mmq(X, M, Mpad, K, stage, s) != hipSuccess)
+        return fail(-2, "sera_q4k_dense: quantize launch failed");
+    record(g_ev.quant_end, s);
+    record(g_ev.kernel_begin, s);
+    if (sera_launch_q4k_mmq(W, stage, Y, partial, M, N, K, splits, s) != hipSuccess)
+        return fail(-3, "sera_q4k_dense: mmq launch failed");
+    record(g_ev.kernel_end, s);
+    return 0;
+}
+
+extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K, void *stream) {
+    if (!check_shape("sera_q4k_dense_vec", W, X, Y, M, N, K)) return -1;
+    if (M > SERA_Q4K_MMVQ_MAX_BATCH)
+        return fail(-1, "sera_q4k_dense_vec: batch M=%d exceeds MMVQ cap %d", M, SERA_Q4K_MMVQ_MAX_BATCH);
+    if (!g_arena) return fail(-1, "sera_q4k_dense_vec: no arena attached");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
+    if (stage_bytes > g_arena_bytes)
+        return fail(-1, "sera_q4k_dense_vec: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
+    record(g_ev.quant_begin, s);
+    if (sera_launch_q8_1_row(X, M, K, g_arena, s) != hipSuccess)
+        return fail(-2, "sera_q4k_dense_vec: quantize launch failed");
+    record(g_ev.quant_end, s);
+    record(g_ev.kernel_begin, s);
+    if (sera_launch_q4k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess)
+        return fail(-3, "sera_q4k_dense_vec: mmvq launch failed");
+    record(g_ev.kernel_end, s);
+    return 0;
+}
+
+extern "C" void sera_q4k_read_timings(double *quant_ms, double *kernel_ms, double *total_ms) {
+    float q = 0.0f, k = 0.0f, t = 0.0f;
+    if (g_ev.valid) {
+        if (hipEventElapsedTime(&q, g_ev.quant_begin, g_ev.quant_end) != hipSuccess) q = 0.0f;
+        if (hipEventElapsedTime(&k, g_ev.kernel_begin, g_ev.kernel_end) != hipSuccess) k = 0.0f;
+        if (hipEventElapsedTime(&t, g_ev.quant_begin, g_ev.kernel_end) != hipSuccess) t = 0.0f;
+    }
+    if (quant_ms) *quant_ms = q;
+    if (kernel_ms) *kernel_ms = k;
+    if (total_ms) *total_ms = t;
+}
+
+extern "C" int sera_q4k_dequantize(const void *W, size_t nblocks, float *out, void *stream) {
+    if (!W || !out || nblocks == 0) return fail(-1, "sera_q4k_dequantize: bad arguments");
+    return sera_launch_q4k_dequant(W, (int64_t)nblocks, out, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_q4k_dequantize: launch failed");
+}
+
+extern "C" int sera_q4k_subblock_dots(const void *W, const void *stage_qs, int32_t *I, int M, int N, int K,
+                                      void *stream) {
+    if (!W || !stage_qs || !I || M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK)
+        return fail(-1, "sera_q4k_subblock_dots: bad arguments");
+    return sera_launch_q4k_subblock_dots(W, (const int8_t *)stage_qs, I, M, N, K, (hipStream_t)stream) ==
+                   hipSuccess
+               ? 0 : fail(-3, "sera_q4k_subblock_dots: launch failed");
+}
+
+extern "C" int sera_q4k_quantize(const float *X, int64_t rows, int64_t K, void *out, void *stream) {
+    if (!X || !out || rows <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_quantize: bad arguments");
+    return sera_launch_q4k_quantize(X, rows, K, out, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_q4k_quantize: launch failed");
+}

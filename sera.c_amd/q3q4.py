@@ -1,0 +1,252 @@
+"""Python binding of libsera_q4k.so (ctypes), the host-side mirror of the
+reference's q3_q4_linear interface used by the tests and the bench driver.
+
+The C ABI is the product (include/q3_q4_linear.h, include/sera_q4k.h); this
+module only declares its signatures and wraps device buffers that PyTorch
+allocates. Import torch before loading the library so that both use the one
+HIP runtime in the process (same soname, libamdhip64.so.7).
+
+There is no CPU fallback: load() raises if the library is missing, and the
+GPU entry points need a visible device.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsera_q4k.so")
+ROOT = os.path.dirname(HERE)
+HEADERS = [os.path.join(ROOT, "include", "q3_q4_linear.h"),
+           os.path.join(ROOT, "include", "sera_q4k.h")]
+
+QTYPE_Q4_K = 12
+QTYPE_Q6_K = 14
+MMVQ_MAX_BATCH = 8
+
+_lib = None
+
+
+class Stats(ctypes.Structure):
+    """q3_q4_linear_stats (src/q3_q4_linear.h:32-44)."""
+    _fields_ = [("total_ms", ctypes.c_double),
+                ("activation_quant_ms", ctypes.c_double),
+                ("kernel_ms", ctypes.c_double),
+                ("weight_bytes", ctypes.c_uint64),
+                ("activation_read_bytes", ctypes.c_uint64),
+                ("activation_write_bytes", ctypes.c_uint64),
+                ("kernel_launches", ctypes.c_uint64),
+                ("cuda_allocations", ctypes.c_uint64),
+                ("host_syncs", ctypes.c_uint64)]
+
+
+class Geometry(ctypes.Structure):
+    """q3_q4_linear_geometry (src/q3_q4_linear.h:49-55)."""
+    _fields_ = [("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32),
+                ("qtype", ctypes.c_uint32), ("weight_bytes", ctypes.c_uint64)]
+
+
+class Q3Q4Error(RuntimeError):
+    pass
+
+
+def build():
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def load():
+    """Load libsera_q4k.so and declare every exported signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise Q3Q4Error(f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                        "(there is no fallback path)")
+    try:  # share torch's HIP runtime when torch is present
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    L = ctypes.CDLL(LIB_PATH)
+    P, I, I64, SZ, B = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t,
+                        ctypes.c_bool)
+    CP = ctypes.c_char_p
+    sigs = {
+        # q3_q4_linear.h
+        "q3_q4_linear_bind_geometry": ([ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                        ctypes.POINTER(Geometry), CP, SZ], B),
+        "q3_cuda_q4k_linear_init": ([I, SZ, I64, I64, CP, SZ], B),
+        "q3_cuda_q4k_linear_workspace_bytes": ([], SZ),
+        "q3_cuda_q4k_linear_set_workspace": ([P, SZ, CP, SZ], B),
+        "q3_cuda_q4k_linear_path_for_batch": ([SZ], CP),
+        "q3_cuda_q4k_linear": ([ctypes.POINTER(Geometry), P, P, SZ, P, P,
+                                ctypes.POINTER(Stats), CP, SZ], B),
+        "q3_cuda_q4k_linear_read_stats": ([ctypes.POINTER(Stats), P], None),
+        # sera_q4k.h
+        "sera_q4k_init": ([I], I),
+        "sera_q4k_arena_bytes": ([SZ, I64, I64], SZ),
+        "sera_q4k_set_arena": ([P, SZ], I),
+        "sera_q4k_dense": ([P, P, P, I, I, I, P], I),
+        "sera_q4k_dense_vec": ([P, P, P, I, I, I, P], I),
+        "sera_q4k_read_timings": ([ctypes.POINTER(ctypes.c_double)] * 3, None),
+        "sera_q8_1_row_stage_bytes": ([I, I], SZ),
+        "sera_q8_1_row_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ),
+                                         ctypes.POINTER(SZ)], None),
+        "sera_q8_1_quantize_row": ([P, I, I, P, P], I),
+        "sera_q8_1_mmq_padded_rows": ([I], I),
+        "sera_q8_1_mmq_stage_bytes": ([I, I], SZ),
+        "sera_q8_1_mmq_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ)], None),
+        "sera_q8_1_quantize_mmq": ([P, I, I, P, P], I),
+        "sera_q4k_mmvq": ([P, P, P, I, I, I, I, P], I),
+        "sera_q4k_mmvq_rows_per_wave": ([I, I], I),
+        "sera_q4k_mmq": ([P, P, P, P, I, I, I, I, P], I),
+        "sera_q4k_mmq_splits": ([I, I, I], I),
+        "sera_q4k_dequantize": ([P, SZ, P, P], I),
+        "sera_q4k_subblock_dots": ([P, P, P, I, I, I, P], I),
+        "sera_q4k_quantize": ([P, I64, I64, P, P], I),
+        "sera_q4k_last_error": ([], CP),
+        "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
+        "sera_q4k_bench_kernel": ([I, P, I, P, P, P, I, I, I, I, P, I, I,
+                                   ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], I),
+    }
+    for name, (args, res) in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def header_symbols():
+    """Function names declared in include/*.h (for the export check)."""
+    import re
+    names = []
+    for h in HEADERS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b([a-z_][a-z0-9_]*)\s*\(", text):
+            n = m.group(1)
+            if n.startswith(("q3_", "sera_")) and n not in names:
+                names.append(n)
+    return names
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise Q3Q4Error(f"{what} failed (rc={rc}): {load().sera_q4k_last_error().decode()}")
+
+
+# ---------------------------------------------------------------------------
+# The q3_q4_linear boundary
+# ---------------------------------------------------------------------------
+
+def bind_geometry(qtype, dim0, dim1):
+    L = load()
+    g = Geometry()
+    err = ctypes.create_string_buffer(256)
+    ok = L.q3_q4_linear_bind_geometry(qtype, dim0, dim1, ctypes.byref(g), err, 256)
+    if not ok:
+        raise Q3Q4Error(err.value.decode())
+    return g
+
+
+class Linear:
+    """One process-wide q3_q4_linear context: init + caller-owned workspace
+    (src/q3_forward.cu:1050-1116 does the same for the reference runtime)."""
+
+    def __init__(self, device=0, max_tokens=16, max_features=25600, max_k=25600):
+        import torch
+        L = load()
+        err = ctypes.create_string_buffer(256)
+        if not L.q3_cuda_q4k_linear_init(device, max_tokens, max_features, max_k, err, 256):
+            raise Q3Q4Error(err.value.decode())
+        nbytes = L.q3_cuda_q4k_linear_workspace_bytes()
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=f"cuda:{device}")
+        if not L.q3_cuda_q4k_linear_set_workspace(_ptr(self.workspace), nbytes, err, 256):
+            raise Q3Q4Error(err.value.decode())
+        self.workspace_bytes = nbytes
+
+    def __call__(self, geometry, weight, x, out, stream=None, stats=None):
+        L = load()
+        err = ctypes.create_string_buffer(512)
+        st = stats if stats is not None else Stats()
+        ok = L.q3_cuda_q4k_linear(ctypes.byref(geometry), _ptr(weight), _ptr(x), x.shape[0],
+                                  _ptr(out), _stream(stream), ctypes.byref(st), err, 512)
+        if not ok:
+            raise Q3Q4Error(err.value.decode())
+        return st
+
+    @staticmethod
+    def read_stats(stats, stream=None):
+        load().q3_cuda_q4k_linear_read_stats(ctypes.byref(stats), _stream(stream))
+        return stats
+
+
+# ---------------------------------------------------------------------------
+# Building blocks (sera_q4k.h)
+# ---------------------------------------------------------------------------
+
+def row_stage_layout(M, K):
+    L = load()
+    qs, ds, dsf = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+    L.sera_q8_1_row_stage_offsets(M, K, ctypes.byref(qs), ctypes.byref(ds), ctypes.byref(dsf))
+    return {"qs": qs.value, "ds": ds.value, "dsf": dsf.value,
+            "total": L.sera_q8_1_row_stage_bytes(M, K)}
+
+
+def mmq_stage_layout(M, K):
+    L = load()
+    qs, ds = ctypes.c_size_t(), ctypes.c_size_t()
+    L.sera_q8_1_mmq_stage_offsets(M, K, ctypes.byref(qs), ctypes.byref(ds))
+    return {"qs": qs.value, "ds": ds.value, "rows": L.sera_q8_1_mmq_padded_rows(M),
+            "total": L.sera_q8_1_mmq_stage_bytes(M, K)}
+
+
+def quantize_row(x, stage, stream=None):
+    M, K = x.shape
+    _check(load().sera_q8_1_quantize_row(_ptr(x), M, K, _ptr(stage), _stream(stream)),
+           "sera_q8_1_quantize_row")
+
+
+def quantize_mmq(x, stage, stream=None):
+    M, K = x.shape
+    _check(load().sera_q8_1_quantize_mmq(_ptr(x), M, K, _ptr(stage), _stream(stream)),
+           "sera_q8_1_quantize_mmq")
+
+
+def mmvq(W, stage, out, M, N, K, rows_per_wave=0, stream=None):
+    _check(load().sera_q4k_mmvq(_ptr(W), _ptr(stage), _ptr(out), M, N, K, rows_per_wave,
+                                _stream(stream)), "sera_q4k_mmvq")
+
+
+def mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None):
+    _check(load().sera_q4k_mmq(_ptr(W), _ptr(stage), _ptr(out), _ptr(partial), M, N, K, splits,
+                               _stream(stream)), "sera_q4k_mmq")
+
+
+def mmq_splits(M, N, K):
+    return load().sera_q4k_mmq_splits(M, N, K)
+
+
+def dequantize(W, nblocks, out, stream=None):
+    _check(load().sera_q4k_dequantize(_ptr(W), nblocks, _ptr(out), _stream(stream)),
+           "sera_q4k_dequantize")
+
+
+def subblock_dots(W, stage_qs, out, M, N, K, stream=None):
+    _check(load().sera_q4k_subblock_dots(_ptr(W), _ptr(stage_qs), _ptr(out), M, N, K,
+                                         _stream(stream)), "sera_q4k_subblock_dots")
+
+
+def quantize_weights(x, out, stream=None):
+    rows, K = x.shape
+    _check(load().sera_q4k_quantize(_ptr(x), rows, K, _ptr(out), _stream(stream)),
+           "sera_q4k_quantize")

@@ -1,0 +1,127 @@
+"""Host-side checks of the C ABI (no GPU): the library loads, exports every
+function that include/*.h declares, and the host-only argument handling
+follows the reference's contracts (src/q3_q4_linear.cu:48-91,93-228)."""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+import q3q4
+
+
+@pytest.fixture(scope="module")
+def L():
+    return q3q4.load()
+
+
+def test_library_exports_every_header_symbol(L):
+    names = q3q4.header_symbols()
+    assert len(names) >= 25
+    out = subprocess.run(["nm", "-D", "--defined-only", q3q4.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    for n in names:
+        getattr(L, n)
+
+
+def test_reference_boundary_symbols_present():
+    """The seven entry points of src/q3_q4_linear.h:65-116 that a caller binds."""
+    names = set(q3q4.header_symbols())
+    for n in ["q3_q4_linear_bind_geometry", "q3_cuda_q4k_linear_init",
+              "q3_cuda_q4k_linear_workspace_bytes", "q3_cuda_q4k_linear_set_workspace",
+              "q3_cuda_q4k_linear_path_for_batch", "q3_cuda_q4k_linear",
+              "q3_cuda_q4k_linear_read_stats"]:
+        assert n in names
+
+
+def test_struct_layouts_match_reference():
+    assert ctypes.sizeof(q3q4.Stats) == 3 * 8 + 6 * 8
+    assert ctypes.sizeof(q3q4.Geometry) == 24
+    assert q3q4.Geometry.weight_bytes.offset == 16
+
+
+@pytest.mark.parametrize("qtype,dim0,dim1,wbytes", [
+    (12, 5120, 25600, 73_728_000),     # gate/up
+    (12, 25600, 5120, 73_728_000),     # down
+    (12, 5120, 151936, 437_575_680),   # LM head
+    (14, 5120, 1024, 1024 * 20 * 210), # Q6_K geometry is bound (kernel path is Q4_K only)
+])
+def test_bind_geometry(qtype, dim0, dim1, wbytes):
+    g = q3q4.bind_geometry(qtype, dim0, dim1)
+    assert (g.M, g.N, g.K, g.qtype, g.weight_bytes) == (0, dim1, dim0, qtype, wbytes)
+
+
+@pytest.mark.parametrize("qtype,dim0,dim1,msg", [
+    (2, 5120, 100, "not Q4_K/Q6_K"),
+    (12, 0, 100, "degenerate"),
+    (12, 512, 0, "degenerate"),
+    (12, 5000, 100, "multiple of 256"),
+    (12, 2 ** 31 + 256, 4, "exceeds int32"),
+])
+def test_bind_geometry_errors(qtype, dim0, dim1, msg):
+    with pytest.raises(q3q4.Q3Q4Error, match=msg):
+        q3q4.bind_geometry(qtype, dim0, dim1)
+
+
+def test_bind_geometry_null_out(L):
+    assert not L.q3_q4_linear_bind_geometry(12, 256, 4, None, None, 0)
+
+
+def test_path_for_batch(L):
+    assert L.q3_cuda_q4k_linear_path_for_batch(1) == b"MMVQ"
+    assert L.q3_cuda_q4k_linear_path_for_batch(8) == b"MMVQ"
+    assert L.q3_cuda_q4k_linear_path_for_batch(9) == b"MMQ"
+    assert L.q3_cuda_q4k_linear_path_for_batch(2048) == b"MMQ"
+
+
+def test_host_error_paths_without_device(L):
+    err = ctypes.create_string_buffer(256)
+    assert not L.q3_cuda_q4k_linear_init(-1, 16, 1024, 5120, err, 256)
+    assert b"invalid device" in err.value
+    g = q3q4.bind_geometry(12, 256, 4)
+    st = q3q4.Stats()
+    # null arguments are rejected before anything else
+    assert not L.q3_cuda_q4k_linear(ctypes.byref(g), None, None, 1, None, None, ctypes.byref(st), err, 256)
+    assert b"null argument" in err.value
+    # nothing initialised in this process
+    dummy = ctypes.c_void_p(16)
+    assert not L.q3_cuda_q4k_linear(ctypes.byref(g), dummy, dummy, 1, dummy, None, ctypes.byref(st), err, 256)
+    assert b"not initialized" in err.value
+    assert not L.q3_cuda_q4k_linear_set_workspace(None, 0, err, 256)
+    assert b"workspace too small" in err.value
+
+
+def test_kernel_entry_points_validate_on_host(L):
+    d = ctypes.c_void_p(256)
+    assert L.sera_q4k_mmvq(d, d, d, 9, 128, 256, 0, None) == -1
+    assert b"outside 1..8" in L.sera_q4k_last_error()
+    assert L.sera_q4k_mmvq(d, d, d, 1, 128, 256, 3, None) == -1
+    assert L.sera_q4k_dense(d, d, d, 16, 128, 300, None) == -1
+    assert b"multiple of 256" in L.sera_q4k_last_error()
+    assert L.sera_q4k_dense(None, d, d, 16, 128, 256, None) == -1
+    assert L.sera_q4k_dense(d, ctypes.c_void_p(258), d, 16, 128, 256, None) == -1
+    assert b"16-byte aligned" in L.sera_q4k_last_error()
+    assert L.sera_q4k_mmq(d, d, d, None, 64, 128, 1024, 2, None) == -1
+    assert b"partial" in L.sera_q4k_last_error()
+    assert L.sera_q4k_set_arena(ctypes.c_void_p(100), 1024) == -1
+
+
+def test_stage_layouts_and_workspace_sizing():
+    r = q3q4.row_stage_layout(8, 25600)
+    assert r["qs"] == 0 and r["ds"] >= 8 * 25600 and r["dsf"] >= r["ds"] + 8 * 800 * 4
+    assert r["total"] >= r["dsf"] + 8 * 400 * 16 and r["total"] % 256 == 0
+    m = q3q4.mmq_stage_layout(100, 5120)
+    assert m["rows"] == 128 and m["ds"] >= 128 * 5120 and m["total"] >= m["ds"] + 128 * 160 * 4
+    L = q3q4.load()
+    small = L.sera_q4k_arena_bytes(16, 25600, 25600)
+    big = L.sera_q4k_arena_bytes(2048, 25600, 25600)
+    assert big > small > q3q4.mmq_stage_layout(16, 25600)["total"]
+    # every split-K choice for shapes the arena was sized for fits in it
+    for M in (9, 16, 64, 100, 512, 2048):
+        for N, K in ((1024, 5120), (5120, 25600), (25600, 5120), (151936, 5120)):
+            s = q3q4.mmq_splits(M, N, K)
+            need = q3q4.mmq_stage_layout(M, K)["total"] + (s * M * N * 4 if s > 1 else 0)
+            assert need <= L.sera_q4k_arena_bytes(2048, 151936, 25600), (M, N, K, s)

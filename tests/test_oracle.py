@@ -1,0 +1,364 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+
+Each check is one of: a golden vector produced by the reference itself
+(tests/golden/, see make_golden.py), a known answer derived by hand in the
+comment next to it, an independent IEEE implementation (numpy float16 /
+float32 arithmetic), an exact closed form, or brute force on tiny inputs.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+RNG = np.random.default_rng(1234)
+
+
+def fp16_bits(v):
+    return int(np.float16(v).view(np.uint16))
+
+
+# ---------------------------------------------------------------------------
+# fp16 conversions
+# ---------------------------------------------------------------------------
+
+def test_h2f_exhaustive_vs_numpy_float16():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = ((h >> 10) & 0x1F) != 0x1F
+    got = oracle.h2f(h)
+    exp = h.view(np.float16).astype(np.float32)
+    assert np.array_equal(got[finite].view(np.uint32), exp[finite].view(np.uint32))
+    inf = h[~finite & ((h & 0x3FF) == 0)]
+    assert np.all(np.isinf(oracle.h2f(inf)))
+
+
+def test_f2h_rne_vs_numpy_float16_including_ties():
+    f = np.concatenate([
+        (RNG.standard_normal(20000) * np.exp2(RNG.uniform(-30, 17, 20000))).astype(np.float32),
+        # exact ties between neighbouring halves: normal range and subnormal range
+        (np.float32(1.0) + np.arange(1, 200, dtype=np.float32) * np.float32(2.0 ** -11)),
+        (np.arange(1, 200, dtype=np.float32) * np.float32(2.0 ** -25)),
+        np.array([65504, 65519.99, 65520, -65520, 1e-9, -0.0, 0.0], np.float32),
+    ])
+    with np.errstate(over="ignore"):
+        exp = f.astype(np.float16).view(np.uint16)
+    assert np.array_equal(oracle.f2h(f), exp)
+
+
+def test_numpy_bit_trick_conversions_match_reference_vectors(golden_dir):
+    g = np.load(f"{golden_dir}/fp16_helpers.npz")
+    assert np.array_equal(oracle.np_f32_to_f16(g["f32_in"]), g["f32_to_f16"])
+    got = oracle.np_f16_to_f32(g["f16_in"]).view(np.uint32)
+    assert np.array_equal(got, g["f16_to_f32"].view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# Q4_K dequant
+# ---------------------------------------------------------------------------
+
+def test_dequant_matches_reference_q3_quant_c_vectors(golden_dir):
+    g = np.load(f"{golden_dir}/dequant_ref.npz")
+    lcg = g["lcg_blocks"]
+    got = oracle.dequant(lcg.reshape(1, -1), 1, 1024)
+    assert np.array_equal(got.view(np.uint32), g["lcg_deq"].view(np.uint32))
+    for k in g.files:
+        if k.startswith("w_"):
+            W = g[k]
+            N, K = W.shape[0], W.shape[1] // 144 * 256
+            assert np.array_equal(oracle.dequant(W, N, K).view(np.uint32),
+                                  g["deq_" + k[2:]].view(np.uint32)), k
+
+
+def test_dequant_hand_check_first_nibble(golden_dir):
+    """tests/test_q3_q4_linear.cu:97-107: d*sc0*(q0 & 15) - dmin*m0 from raw fields."""
+    b = np.load(f"{golden_dir}/dequant_ref.npz")["lcg_blocks"][0]
+    d = float(np.frombuffer(b[0:2].tobytes(), np.float16)[0])
+    dmin = float(np.frombuffer(b[2:4].tobytes(), np.float16)[0])
+    sc, mn = b[4] & 63, b[8] & 63
+    expected = d * sc * (b[16] & 0xF) - dmin * mn
+    assert abs(oracle.dequant(b.reshape(1, -1), 1, 256)[0, 0] - expected) < 1e-3
+
+
+def test_dequant_lcg_blocks_are_the_reference_test_inputs(golden_dir):
+    """Regenerates the LCG of tests/test_q3_q4_linear.cu:57-74 (seed 0x12345678)."""
+    state = 0x12345678
+
+    def nxt():
+        nonlocal state
+        state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
+        return state >> 8
+
+    blocks = np.load(f"{golden_dir}/dequant_ref.npz")["lcg_blocks"]
+    for b in blocks:
+        assert int(b[0]) | (int(b[1]) << 8) == 0x2000 + (nxt() & 0x0FFF)
+        assert int(b[2]) | (int(b[3]) << 8) == 0x1800 + (nxt() & 0x0FFF)
+        for i in range(12):
+            assert b[4 + i] == nxt() & 0xFF
+        for i in range(128):
+            lo, hi = nxt() & 0xF, nxt() & 0xF
+            assert b[16 + i] == (hi << 4) | lo
+
+
+def test_ref_build_agrees_when_present():
+    """oracle/_ref holds the reference's q3_quant.c compiled from its sources."""
+    if oracle.ref_lib() is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    x = (RNG.standard_normal((16, 512)) * 0.05).astype(np.float32)
+    W = oracle.quantize_q4k(x)
+    assert np.array_equal(oracle.dequant(W, 16, 512).view(np.uint32),
+                          oracle.ref_dequant(W, 16, 512).view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# Q4_K quantizer (the repo's quantizer, tools/qwen3_q4.py:410-481)
+# ---------------------------------------------------------------------------
+
+def test_quantizer_matches_reference_vectors(golden_dir):
+    g = np.load(f"{golden_dir}/q4k_quantizer.npz")
+    names = [k[2:] for k in g.files if k.startswith("x_")]
+    assert len(names) >= 4
+    for n in names:
+        got = oracle.quantize_q4k(g["x_" + n])
+        assert np.array_equal(got, g["q_" + n]), n
+
+
+def test_quantizer_fixture_detects_a_planted_error(golden_dir):
+    g = np.load(f"{golden_dir}/q4k_quantizer.npz")
+    got = oracle.quantize_q4k(g["x_normal_0p02_8x512"]).copy()
+    got[3, 40] ^= 0x01                      # one flipped nibble bit
+    assert not np.array_equal(got, g["q_normal_0p02_8x512"])
+
+
+def test_quantizer_roundtrip_error_is_small():
+    x = (RNG.standard_normal((32, 1024)) * 0.02).astype(np.float32)
+    W = oracle.quantize_q4k(x)
+    rel = np.linalg.norm(oracle.dequant(W, 32, 1024) - x) / np.linalg.norm(x)
+    assert rel < 0.12   # 4-bit quantization of a Gaussian: ~0.09
+
+
+def test_quantizer_rejects_bad_k():
+    with pytest.raises(ValueError):
+        oracle.quantize_q4k(np.zeros((2, 100), np.float32))
+
+
+# ---------------------------------------------------------------------------
+# Q8_1 quantizers
+# ---------------------------------------------------------------------------
+
+def _tree_input():
+    x = np.ones(32, np.float32)
+    x[0], x[16] = 2.0 ** 24, -(2.0 ** 24)
+    return x
+
+
+def test_q8_row_sum_uses_xor_butterfly_order():
+    """Butterfly 16,8,4,2,1: the first level pairs (i, i+16): (2^24 + -2^24)
+    = 0 and fifteen pairs 1+1 = 2, total 30. A left-to-right sum gives 15
+    (each +1 on 2^24 rounds away)."""
+    _, _, s = oracle.q8_1_row(_tree_input().reshape(1, 32))
+    assert s[0, 0] == fp16_bits(30.0)
+
+
+def test_q8_mmq_sum_uses_ds4_order():
+    """DS4: lane t sums ((x0+x1)+x2)+x3 of x[4t..4t+3]. Lane 0:
+    2^24+1+1+1 -> 2^24 (ties to even); lane 4: -2^24+1+1+1 = -16777213;
+    others 4. xor 4,2,1: (2^24-16777213) + 8 -> 11, 8+8 -> 16, 11+16 = 27."""
+    _, _, s = oracle.q8_1_mmq(_tree_input().reshape(1, 32))
+    assert s[0, 0] == fp16_bits(27.0)
+
+
+@pytest.mark.parametrize("fn", [oracle.q8_1_row, oracle.q8_1_mmq])
+def test_q8_roundf_half_away_from_zero(fn):
+    """amax = 127 gives d = 1 (and d_inv = 1) exactly, so q = roundf(x):
+    2.5 -> 3, -2.5 -> -3, 0.5 -> 1, -0.5 -> -1, 1.5 -> 2 (rint would give
+    2, -2, 0, 0, 2)."""
+    x = np.zeros(32, np.float32)
+    x[:6] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5]
+    q, d, _ = fn(x.reshape(1, 32))
+    assert list(q[0, :6]) == [127, 3, -3, 1, -1, 2]
+    assert d[0, 0] == fp16_bits(1.0)
+
+
+@pytest.mark.parametrize("fn", [oracle.q8_1_row, oracle.q8_1_mmq])
+def test_q8_scale_fp16_ties_to_even(fn):
+    """amax = 127*(1+2^-11) gives d = 1+2^-11 exactly, halfway between
+    0x3C00 and 0x3C01 -> even 0x3C00; amax = 127*(1+3*2^-11) gives
+    1+3*2^-11, halfway between 0x3C01 and 0x3C02 -> 0x3C02."""
+    for amax, bits in [(127.0 * (1 + 2.0 ** -11), 0x3C00), (127.0 * (1 + 3 * 2.0 ** -11), 0x3C02)]:
+        x = np.zeros(32, np.float32)
+        x[5] = amax
+        _, d, _ = fn(x.reshape(1, 32))
+        assert d[0, 0] == bits
+
+
+@pytest.mark.parametrize("fn", [oracle.q8_1_row, oracle.q8_1_mmq])
+def test_q8_zero_block(fn):
+    """amax == 0: every q is 0 and d is 0; the sum of -0.0 values is -0.0
+    (fp16 0x8000), of +0.0 values +0.0."""
+    q, d, s = fn(np.full((1, 32), -0.0, np.float32))
+    assert not q.any() and d[0, 0] == 0 and s[0, 0] == 0x8000
+    q, d, s = fn(np.zeros((1, 32), np.float32))
+    assert not q.any() and d[0, 0] == 0 and s[0, 0] == 0
+
+
+def test_q8_row_and_mmq_formulas_differ_where_ieee_says_so():
+    """x/d (row, d = amax/127) and x*(127/amax) (mmq) round differently for
+    some x; numpy float32 arithmetic (IEEE) decides which q each one must
+    produce, and the oracle must follow its own reference formula."""
+    def roundf(v):  # half away from zero, evaluated exactly in float64
+        v = np.asarray(v, np.float64)
+        return np.sign(v) * np.floor(np.abs(v) + 0.5)
+
+    found = 0
+    for amax in np.float32([3.0, 0.7, 11.3, 1e-3]):
+        d = np.float32(amax) / np.float32(127)
+        d_inv = np.float32(127) / np.float32(amax)
+        cand = (np.arange(1, 127, dtype=np.float32) + np.float32(0.5)) * d
+        cand = np.concatenate([cand, np.nextafter(cand, np.float32(0)),
+                               np.nextafter(cand, np.float32(1e9))]).astype(np.float32)
+        qa = roundf(cand / d)          # float32 division, then exact rounding
+        qb = roundf(cand * d_inv)      # float32 product, then exact rounding
+        diff = np.nonzero(qa != qb)[0]
+        for i in diff[:8]:
+            x = np.zeros(32, np.float32)
+            x[0], x[1] = amax, cand[i]
+            qr, _, _ = oracle.q8_1_row(x.reshape(1, 32))
+            qm, _, _ = oracle.q8_1_mmq(x.reshape(1, 32))
+            assert qr[0, 1] == qa[i] and qm[0, 1] == qb[i]
+            found += 1
+    assert found > 0
+
+
+@pytest.mark.parametrize("fn", [oracle.q8_1_row, oracle.q8_1_mmq])
+def test_q8_invariants_with_outlier_channels(fn):
+    K = 2048
+    x = RNG.standard_normal((4, K)).astype(np.float32)
+    x[:, RNG.choice(K, K // 100, replace=False)] *= 20.0
+    q, d, s = fn(x)
+    xb = x.reshape(4, -1, 32)
+    qb = q.reshape(4, -1, 32).astype(np.int32)
+    amax = np.abs(xb).max(axis=2)
+    d32 = amax / np.float32(127)
+    assert np.abs(qb).max() <= 127
+    # the element holding amax maps to +-127
+    idx = np.abs(xb).argmax(axis=2)
+    assert np.all(np.abs(np.take_along_axis(qb, idx[..., None], 2)) == 127)
+    # reconstruction within half a step (plus fp32 rounding of the step)
+    err = np.abs(xb - qb * d32[..., None])
+    assert np.all(err <= d32[..., None] * (0.5 + 1e-5))
+    # scale and sum are the fp16 roundings of amax/127 and of the block sum
+    assert np.array_equal(d, d32.astype(np.float16).view(np.uint16)) or fn is oracle.q8_1_mmq
+    ssum = xb.astype(np.float64).sum(axis=2)
+    s_f = oracle.h2f(s)
+    assert np.all(np.abs(s_f - ssum) <= 2e-3 * np.abs(xb).sum(axis=2) + 1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Integer dots and the two output formulas
+# ---------------------------------------------------------------------------
+
+def test_subblock_dots_brute_force_tiny():
+    K, N, M = 256, 3, 2
+    W = oracle.quantize_q4k((RNG.standard_normal((N, K)) * 0.1).astype(np.float32))
+    xq = RNG.integers(-127, 128, (M, K)).astype(np.int8)
+    got = oracle.subblock_dots(W, xq, N, K)
+    for n in range(N):
+        qs = W[n, 16:144]
+        for m in range(M):
+            for j in range(8):
+                acc = 0
+                for l in range(32):
+                    byte = int(qs[(j // 2) * 32 + l])
+                    nib = (byte >> 4) if (j % 2) else (byte & 0xF)
+                    acc += nib * int(xq[m, 32 * j + l])
+                assert got[m, n, j] == acc
+
+
+def test_subblock_dot_extreme_is_closed_form():
+    """All nibbles 15 and all quants +-127: I = +-32*15*127 = +-60960."""
+    W = np.zeros((1, 144), np.uint8)
+    W[0, 16:] = 0xFF
+    xq = np.full((2, 256), 127, np.int8)
+    xq[1] = -127
+    I = oracle.subblock_dots(W, xq, 1, 256)
+    assert np.all(I[0] == 60960) and np.all(I[1] == -60960)
+
+
+def _exact_case(M, N, K, balanced_sums):
+    """Weights with d = 2^-8, dmin = 2^-9 and activations x = q * 2^-5 with a
+    +-127 in every 32-block: every weight, every Q8_1 value and every product
+    is exact, so both path formulas must equal the dequant GEMM exactly."""
+    W = np.zeros((N, K // 256, 144), np.uint8)
+    W[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -8).tobytes(), np.uint8)
+    W[:, :, 2:4] = np.frombuffer(np.float16(2.0 ** -9).tobytes(), np.uint8)
+    W[:, :, 4:16] = RNG.integers(0, 256, (N, K // 256, 12))
+    W[:, :, 16:] = RNG.integers(0, 256, (N, K // 256, 128))
+    W = W.reshape(N, -1)
+    q = RNG.integers(-20, 21, (M, K // 32, 32))
+    q[:, :, 0] = 127
+    q[:, :, 1] = -127
+    if balanced_sums:
+        q[:, :, 2:] -= np.round(q[:, :, 2:].mean(axis=2, keepdims=True)).astype(q.dtype)
+        q = np.clip(q, -127, 127)
+    X = (q.reshape(M, K) * 2.0 ** -5).astype(np.float32)
+    return W, X
+
+
+def test_mmvq_formula_equals_dequant_gemm_when_exact():
+    M, N, K = 3, 5, 512
+    W, X = _exact_case(M, N, K, balanced_sums=False)
+    xq, xd, _ = oracle.q8_1_row(X)
+    assert np.all(xd == fp16_bits(2.0 ** -5))
+    y = oracle.gemm_mmvq(W, xq, xd, N, K)
+    assert np.array_equal(y, oracle.gemm_dequant(W, X, N, K))
+
+
+def test_mmq_formula_equals_dequant_gemm_when_exact():
+    M, N, K = 3, 5, 512
+    W, X = _exact_case(M, N, K, balanced_sums=True)
+    xq, xd, xs = oracle.q8_1_mmq(X)
+    assert np.all(xd == fp16_bits(2.0 ** -5))
+    y = oracle.gemm_mmq(W, xq, xd, xs, N, K)
+    assert np.array_equal(y, oracle.gemm_dequant(W, X, N, K))
+
+
+def test_mmq_formula_rounds_d_times_sc_to_fp16():
+    """With d = 1 + 2^-10 (fp16 0x3C01) and sc = 63: d*sc = 63.0615...,
+    which fp16 rounds to 63.0625; the MMQ formula uses that rounded scale
+    (mmq.cuh:2278-2282), the MMVQ formula the exact one."""
+    W = np.zeros((1, 144), np.uint8)
+    W[0, 0:2] = [0x01, 0x3C]            # d = 1 + 2^-10
+    W[0, 4] = 63                        # sc0 = 63, m0 = 0, other sub-blocks 0
+    W[0, 16:48] = 0x01                  # q = 1 in sub-block 0
+    X = np.zeros((1, 256), np.float32)
+    X[0, :32] = 127.0 / 64              # d8 = 1/64 exactly, q8 = 127
+    xq, xd, xs = oracle.q8_1_mmq(X)
+    y_mmq = oracle.gemm_mmq(W, xq, xd, xs, 1, 256)[0, 0]
+    xr, xdr, _ = oracle.q8_1_row(X)
+    y_mmvq = oracle.gemm_mmvq(W, xr, xdr, 1, 256)[0, 0]
+    I = 32 * 127
+    assert y_mmq == 63.0625 * (1 / 64) * I
+    assert y_mmvq == (1 + 2 ** -10) * 63 * (1 / 64) * I
+
+
+def fill_activation(M, K):
+    """Activations of tests/test_q3_q4_linear.cu:226-233:
+    a = ((k*17 + t*131) % 1009) * 0.1, x = 0.5 sin(a) + 0.25 cos(0.37 a)."""
+    k = np.arange(K)[None, :]
+    t = np.arange(M)[:, None]
+    a = ((k * 17 + t * 131) % 1009).astype(np.float32) * np.float32(0.1)
+    return (np.float32(0.5) * np.sin(a) + np.float32(0.25) * np.cos(a * np.float32(0.37))).astype(np.float32)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_path_oracles_pass_reference_gates_vs_dequant(M):
+    """tests/test_q3_q4_linear.cu:374,379: cos > 0.999 and relL2 < 1% against
+    the fp32 dequant oracle, on the reference test's activations; also
+    catches sign/transpose slips."""
+    N, K = 64, 1024
+    W = oracle.quantize_q4k((RNG.standard_normal((N, K)) * 0.02).astype(np.float32))
+    X = fill_activation(M, K)
+    ref = oracle.gemm_dequant(W, X, N, K)
+    y = oracle.linear_reference(W, X, N, K)
+    cos = (y * ref).sum() / np.sqrt((y * y).sum() * (ref * ref).sum())
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert cos > 0.999 and rel < 0.01
