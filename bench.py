@@ -136,11 +136,11 @@ def main():
             step_ms = bench_linear(geo, arr, args.copies, x, y, args.warmup, args.steps)
             stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
             q3q4.quantize_row(x, stage)
-            rpw = L.sera_q4k_mmvq_rows_per_wave(N, K)
+            rpw = L.sera_q4k_mmvq_rows_per_tile(M, N, K)
             kavg, kb2b = bench_kernel(0, arr, args.copies, stage, y, None, M, N, K, 0,
                                       args.warmup, args.steps)
             b = alg_bytes(M, N, K)
-            row = {"proj": name, "M": M, "N": N, "K": K, "rows_per_wave": rpw,
+            row = {"proj": name, "M": M, "N": N, "K": K, "rows_per_tile": rpw,
                    "step_us": round(step_ms * 1e3, 3),
                    "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),
                    "kernel_us": round(kavg * 1e3, 3),
@@ -202,7 +202,7 @@ def main():
     achieved = b / (kernel_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"sera_q4k_mmvq_kernel<1,{row['rows_per_wave']},4>",
+                "kernel": f"sera_q4k_mmvq_kernel<1,{row['rows_per_tile']},3>",
                 "avg_launch_us": row["kernel_us"], "algorithmic_bytes_per_launch": b}
 
     # ---------------- CPU baseline ------------------------------------------

@@ -50,17 +50,18 @@ int sera_q4k_set_arena(void *device_ptr, size_t bytes);
 
 /* Y[M][N] = X[M][K] . W^T through the MMQ tile path (any M >= 1).
  * Replaces q3_mmq_q4_K_dense (cuda/q3_mmq.cu:258-379); note M = tokens,
- * N = features here (the donor ABI had them swapped). */
+ * N = features here (the donor ABI had them swapped). timed != 0 records
+ * the quantize/kernel event pairs (each costs GPU time per call). */
 int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
-                   void *stream);
+                   void *stream, int timed);
 
 /* Same contract through the MMVQ path, 1 <= M <= 8.
  * Replaces q3_mmq_q4_K_dense_vec (cuda/q3_mmq.cu:408-506). */
 int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
-                       void *stream);
+                       void *stream, int timed);
 
-/* Event timings of the last dense call, valid after the caller synchronized
- * its stream (q3_mmq_read_timings, cuda/q3_mmq.h:48-50). */
+/* Event timings of the last timed dense call, valid after the caller
+ * synchronized its stream (q3_mmq_read_timings, cuda/q3_mmq.h:48-50). */
 void sera_q4k_read_timings(double *quant_ms, double *kernel_ms, double *total_ms);
 
 /* ---- building blocks -------------------------------------------------- */
@@ -82,10 +83,11 @@ void sera_q8_1_mmq_stage_offsets(int M, int K, size_t *qs, size_t *ds);
 int sera_q8_1_quantize_mmq(const float *X, int M, int K, void *stage, void *stream);
 
 /* MMVQ kernel on a row stage (mul_mat_vec_q<Q4_K>, cuda/mmq/mmvq.cu:393-587).
- * rows_per_wave in {1,2,4,8}, or 0 for the built-in choice. */
+ * rows_per_tile = weight rows per workgroup in {2,4,8,16}, or 0 for the
+ * built-in choice (sera_q4k_mmvq_rows_per_tile). */
 int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
-                  int rows_per_wave, void *stream);
-int sera_q4k_mmvq_rows_per_wave(int N, int K);
+                  int rows_per_tile, void *stream);
+int sera_q4k_mmvq_rows_per_tile(int M, int N, int K);
 
 /* MMQ kernel on an MMQ stage (mul_mat_q<Q4_K> + stream-K fixup,
  * cuda/mmq/mmq.cuh:3641-4352). `splits` > 1 splits K; then `partial` must

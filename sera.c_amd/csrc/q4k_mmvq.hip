@@ -6,152 +6,276 @@
  * with I_b = sum of q4*q8 over sub-block b (exact int32, v_dot4_i32_i8) and
  * S_b = sum of q8 over b (precomputed by the row quantizer into dsf).
  *
- * gfx950 mapping (wave64, HBM-bound):
- *   - a Q4_K super-block is 9 x 16 bytes: header (d, dmin, 12 scale bytes)
- *     and 8 pieces of 16 qs bytes. Eight lanes ("a group") take one block:
- *     lane p loads qs piece p with one 16-byte load and the header with a
- *     second 16-byte load (all 8 lanes hit the same address). Piece p holds
- *     elements 16h..16h+15 (h = p&1) of sub-blocks 2*(p>>1) (low nibbles)
- *     and 2*(p>>1)+1 (high nibbles).
- *   - a wave covers RPW weight rows; the 8/RPW groups of a row walk its
- *     blocks with stride 8/RPW, so one wave-wide load touches 8 blocks,
- *     RPW rows x (8/RPW) consecutive blocks each.
- *   - nibbles are unpacked in registers (and/shift), dotted with v_dot4,
- *     scaled in fp32; the per-row partials are reduced across the row's
- *     lanes with xor shuffles (DPP/ds_swizzle) and one lane stores.
+ * gfx950 mapping (wave64, HBM-bound, activation-stationary):
+ *   - a Q4_K super-block is a 16-byte header (d, dmin, 12 scale bytes) and
+ *     128 qs bytes in four 32-byte pairs; pair j holds sub-block 2j (low
+ *     nibbles) and 2j+1 (high nibbles). Four lanes (a quad) take one block,
+ *     lane q loading pair q with two 16-byte loads; a wave-wide load of 64
+ *     lanes covers 8 consecutive blocks of 2 rows (lanes 32-63 take the
+ *     second row).
+ *   - the header is fetched as one dword per lane (lane q loads dword q) and
+ *     broadcast to the quad with DPP quad_perm: 4 bytes per lane through
+ *     the texture path instead of 16.
+ *   - each lane loads the Q8_1 slice matching its pair (64 int8 + one float4
+ *     of scales) once per block group and reuses it for all weight rows the
+ *     lane walks (R/2), so activation traffic per weight byte drops by R/2.
+ *   - buffer loads with loop-invariant 32-bit lane offsets; the block-group
+ *     and row steps live in the scalar offset, so the loop has no address
+ *     arithmetic on the vector ALU.
+ *   - the NW waves of a workgroup split the row's block groups (K). Partial
+ *     sums are reduce-scattered across rows and
+ *     lanes with xor shuffles and summed across waves through LDS in a fixed
+ *     order, so results repeat bit for bit.
  */
 #include "q4k_common.h"
 
-template <int NCOLS, int RPW, int UNROLL>
-__global__ __launch_bounds__(256) void sera_q4k_mmvq_kernel(
-        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
-        const float4 *__restrict__ dsf, float *__restrict__ y, int N, int K) {
-    constexpr int LPR = 64 / RPW;     /* lanes per row */
-    constexpr int GPR = LPR / 8;      /* 8-lane groups per row */
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int p = lane & 7;           /* qs piece */
-    const int j2 = p >> 1;            /* sub-block pair */
-    const int h = p & 1;              /* element half */
-    const int gi = (lane >> 3) % GPR; /* group index within the row */
-    const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
-    if (row >= N) return;             /* whole row-group leaves together */
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+#define SERA_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
 
-    const int nb = K / Q4K_QK;
-    const uint8_t *wrow = W + (size_t)row * nb * Q4K_BLOCK_BYTES;
+/* DPP quad_perm broadcast of one lane of each quad to the whole quad. */
+template <int CTRL>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
 
-    float acc[NCOLS];
-#pragma unroll
-    for (int c = 0; c < NCOLS; c++) acc[c] = 0.0f;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, SERA_RSRC_FLAGS);
+}
 
-    for (int blk0 = gi; blk0 < nb; blk0 += GPR * UNROLL) {
-        uint4 hdr[UNROLL], qv[UNROLL];
+/* One halving step of the row reduce-scatter: lanes with bit `o` set keep
+ * the upper half of v[0..2h) and receive the partner's copy of it. */
+__device__ __forceinline__ void rs_halve(float *v, int h, int lane, int o) {
+    const bool up = (lane & o) != 0;
 #pragma unroll
-        for (int u = 0; u < UNROLL; u++) {
-            const int blk = blk0 + u * GPR;
-            if (blk < nb) {
-                const uint8_t *b = wrow + (size_t)blk * Q4K_BLOCK_BYTES;
-                hdr[u] = *(const uint4 *)b;
-                qv[u] = *(const uint4 *)(b + 16 + 16 * p);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < UNROLL; u++) {
-            const int blk = blk0 + u * GPR;
-            if (blk >= nb) break;
-            const float d = h2f_bits(hdr[u].x & 0xffffu);
-            const float dmin = h2f_bits(hdr[u].x >> 16);
-            uint32_t scA, mA, scB, mB;
-            q4k_scale_min(2 * j2, hdr[u].y, hdr[u].z, hdr[u].w, &scA, &mA);
-            q4k_scale_min(2 * j2 + 1, hdr[u].y, hdr[u].z, hdr[u].w, &scB, &mB);
-            const int lo0 = qv[u].x & 0x0F0F0F0F, hi0 = (qv[u].x >> 4) & 0x0F0F0F0F;
-            const int lo1 = qv[u].y & 0x0F0F0F0F, hi1 = (qv[u].y >> 4) & 0x0F0F0F0F;
-            const int lo2 = qv[u].z & 0x0F0F0F0F, hi2 = (qv[u].z >> 4) & 0x0F0F0F0F;
-            const int lo3 = qv[u].w & 0x0F0F0F0F, hi3 = (qv[u].w >> 4) & 0x0F0F0F0F;
-            const float mh = (float)(h ? mB : mA);
-            const size_t koff = (size_t)blk * Q4K_QK + 64 * j2 + 16 * h;
-#pragma unroll
-            for (int c = 0; c < NCOLS; c++) {
-                const int8_t *xr = xq + (size_t)c * K + koff;
-                const int4 xa = *(const int4 *)xr;
-                const int4 xb = *(const int4 *)(xr + 32);
-                const float4 f = dsf[(size_t)c * (K / 64) + blk * 4 + j2];
-                int ia = __builtin_amdgcn_sdot4(lo0, xa.x, 0, false);
-                ia = __builtin_amdgcn_sdot4(lo1, xa.y, ia, false);
-                ia = __builtin_amdgcn_sdot4(lo2, xa.z, ia, false);
-                ia = __builtin_amdgcn_sdot4(lo3, xa.w, ia, false);
-                int ib = __builtin_amdgcn_sdot4(hi0, xb.x, 0, false);
-                ib = __builtin_amdgcn_sdot4(hi1, xb.y, ib, false);
-                ib = __builtin_amdgcn_sdot4(hi2, xb.z, ib, false);
-                ib = __builtin_amdgcn_sdot4(hi3, xb.w, ib, false);
-                const float sumd = f.x * (float)(ia * (int)scA) + f.y * (float)(ib * (int)scB);
-                const float summ = (h ? f.w : f.z) * mh;
-                acc[c] += d * sumd - dmin * summ;
-            }
-        }
-    }
-
-#pragma unroll
-    for (int c = 0; c < NCOLS; c++) {
-        float v = acc[c];
-#pragma unroll
-        for (int off = LPR / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-        acc[c] = v;
-    }
-    if ((lane % LPR) == 0) {
-#pragma unroll
-        for (int c = 0; c < NCOLS; c++) y[(size_t)c * N + row] = acc[c];
+    for (int i = 0; i < h; i++) {
+        const float send = up ? v[i] : v[i + h];
+        const float keep = up ? v[i + h] : v[i];
+        v[i] = keep + __shfl_xor(send, o, 64);
     }
 }
 
-template <int NCOLS, int RPW>
+template <int NCOLS, int HR>
+struct MmvqRegs {
+    v4i xa0[NCOLS], xa1[NCOLS], xb0[NCOLS], xb1[NCOLS];
+    v4u f[NCOLS];
+    uint32_t hw[HR];
+    v4u qa[HR], qc[HR];
+};
+
+template <int NCOLS, int R, int NW>
+__global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
+        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
+        const float4 *__restrict__ dsf, float *__restrict__ y, int N, int K) {
+    constexpr int HR = R / 2;              /* rows per lane */
+    __shared__ float s_part[NW][R][NCOLS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane & 3;                /* sub-block pair */
+    const int g = (lane >> 2) & 7;         /* block within the group of 8 */
+    const int rs = lane >> 5;              /* row parity */
+    const int row0 = blockIdx.x * R;
+    const int nb = K / Q4K_QK;
+    const int ngroups = (nb + 7) >> 3;
+    const int rowbytes = nb * Q4K_BLOCK_BYTES;
+    const int nrows = min(R, N - row0);
+    /* rows >= N fall outside the descriptor's range and read as zero */
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + (size_t)row0 * rowbytes, (uint32_t)(nrows * rowbytes));
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, (uint32_t)(NCOLS * K));
+    const __amdgpu_buffer_rsrc_t rf = make_rsrc(dsf, (uint32_t)(NCOLS * (K / 64) * 16));
+    const int vo_w = rs * rowbytes + g * Q4K_BLOCK_BYTES;
+    const int vo_hdr = vo_w + 4 * q;
+    const int vo_qs = vo_w + 16 + 32 * q;
+    const int vo_x = g * Q4K_QK + 64 * q;
+    const int vo_f = (g * 4 + q) * 16;
+    const int sh = 16 * (q & 1);
+    const bool hi_pair = q >= 2;
+
+    auto load = [&](int bg, MmvqRegs<NCOLS, HR> &t) {
+#pragma unroll
+        for (int c = 0; c < NCOLS; c++) {
+            const int so = c * K + bg * 2048;
+            t.xa0[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x, so, 0));
+            t.xa1[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x + 16, so, 0));
+            t.xb0[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x + 32, so, 0));
+            t.xb1[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x + 48, so, 0));
+            t.f[c] = __builtin_amdgcn_raw_buffer_load_b128(rf, vo_f, c * (K / 4) + bg * 512, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < HR; r++) {
+            const int so = 2 * r * rowbytes + bg * 8 * Q4K_BLOCK_BYTES;
+            t.hw[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vo_hdr, so, 0);
+            t.qa[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qs, so, 0);
+            t.qc[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qs + 16, so, 0);
+        }
+    };
+
+    float acc[HR][NCOLS];
+#pragma unroll
+    for (int r = 0; r < HR; r++)
+#pragma unroll
+        for (int c = 0; c < NCOLS; c++) acc[r][c] = 0.0f;
+
+    auto compute = [&](const MmvqRegs<NCOLS, HR> &t) {
+#pragma unroll
+        for (int r = 0; r < HR; r++) {
+            const uint32_t h0 = quad_bcast<0x00>(t.hw[r]);
+            const uint32_t s1 = quad_bcast<0x55>(t.hw[r]) >> sh;
+            const uint32_t s2 = quad_bcast<0xAA>(t.hw[r]) >> sh;
+            const uint32_t s3 = quad_bcast<0xFF>(t.hw[r]) >> sh;
+            /* 6-bit (scale, min) of sub-blocks 2q, 2q+1 as byte pairs
+             * (src/q3_quant.c:44-55 evaluated for both at once) */
+            const uint32_t scp = hi_pair ? ((s3 & 0x0F0Fu) | ((s1 >> 2) & 0x3030u)) : (s1 & 0x3F3Fu);
+            const uint32_t mp = hi_pair ? (((s3 >> 4) & 0x0F0Fu) | ((s2 >> 2) & 0x3030u)) : (s2 & 0x3F3Fu);
+            const int scA = (int)(scp & 0xFFu), scB = (int)(scp >> 8);
+            const float mA = (float)(mp & 0xFFu), mB = (float)(mp >> 8);
+            const float d = h2f_bits(h0 & 0xffffu);
+            const float dmin = h2f_bits(h0 >> 16);
+            const uint32_t w[8] = {t.qa[r].x, t.qa[r].y, t.qa[r].z, t.qa[r].w,
+                                   t.qc[r].x, t.qc[r].y, t.qc[r].z, t.qc[r].w};
+            int lo[8], hi[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                lo[i] = (int)(w[i] & 0x0F0F0F0Fu);
+                hi[i] = (int)((w[i] >> 4) & 0x0F0F0F0Fu);
+            }
+#pragma unroll
+            for (int c = 0; c < NCOLS; c++) {
+                int ia = __builtin_amdgcn_sdot4(lo[0], t.xa0[c].x, 0, false);
+                ia = __builtin_amdgcn_sdot4(lo[1], t.xa0[c].y, ia, false);
+                ia = __builtin_amdgcn_sdot4(lo[2], t.xa0[c].z, ia, false);
+                ia = __builtin_amdgcn_sdot4(lo[3], t.xa0[c].w, ia, false);
+                ia = __builtin_amdgcn_sdot4(lo[4], t.xa1[c].x, ia, false);
+                ia = __builtin_amdgcn_sdot4(lo[5], t.xa1[c].y, ia, false);
+                ia = __builtin_amdgcn_sdot4(lo[6], t.xa1[c].z, ia, false);
+                ia = __builtin_amdgcn_sdot4(lo[7], t.xa1[c].w, ia, false);
+                int ib = __builtin_amdgcn_sdot4(hi[0], t.xb0[c].x, 0, false);
+                ib = __builtin_amdgcn_sdot4(hi[1], t.xb0[c].y, ib, false);
+                ib = __builtin_amdgcn_sdot4(hi[2], t.xb0[c].z, ib, false);
+                ib = __builtin_amdgcn_sdot4(hi[3], t.xb0[c].w, ib, false);
+                ib = __builtin_amdgcn_sdot4(hi[4], t.xb1[c].x, ib, false);
+                ib = __builtin_amdgcn_sdot4(hi[5], t.xb1[c].y, ib, false);
+                ib = __builtin_amdgcn_sdot4(hi[6], t.xb1[c].z, ib, false);
+                ib = __builtin_amdgcn_sdot4(hi[7], t.xb1[c].w, ib, false);
+                const float d8A = __uint_as_float(t.f[c].x), d8B = __uint_as_float(t.f[c].y);
+                const float dSA = __uint_as_float(t.f[c].z), dSB = __uint_as_float(t.f[c].w);
+                /* |I| <= 32*15*127 and sc <= 63: the product fits a 24-bit multiply */
+                const float sumd = d8A * (float)__mul24(ia, scA) + d8B * (float)__mul24(ib, scB);
+                const float summ = dSA * mA + dSB * mB;
+                acc[r][c] = fmaf(d, sumd, fmaf(-dmin, summ, acc[r][c]));
+            }
+        }
+    };
+
+    /* groups of this wave: wave, wave+NW, ...; all lanes of a quad share blk.
+     * One group in flight per wave keeps registers low; occupancy (several
+     * waves per SIMD) hides the HBM latency. */
+    for (int bg = wave; bg < ngroups; bg += NW) {
+        if (bg * 8 + g < nb) {
+            MmvqRegs<NCOLS, HR> cur;
+            load(bg, cur);
+            compute(cur);
+        }
+    }
+
+    /* reduce-scatter: after log2(HR) halvings each lane holds one row's
+     * partial; the remaining xor steps finish the 32-lane sum. */
+#pragma unroll
+    for (int c = 0; c < NCOLS; c++) {
+        float v[HR];
+#pragma unroll
+        for (int r = 0; r < HR; r++) v[r] = acc[r][c];
+        int ri = 0;
+        if constexpr (HR >= 8) { rs_halve(v, 4, lane, 16); ri = ri * 2 + ((lane >> 4) & 1); }
+        if constexpr (HR >= 4) {
+            constexpr int o = HR >= 8 ? 8 : 16;
+            rs_halve(v, 2, lane, o);
+            ri = ri * 2 + ((lane & o) ? 1 : 0);
+        }
+        if constexpr (HR >= 2) {
+            constexpr int o = HR >= 8 ? 4 : (HR >= 4 ? 8 : 16);
+            rs_halve(v, 1, lane, o);
+            ri = ri * 2 + ((lane & o) ? 1 : 0);
+        }
+        constexpr int ofirst = HR >= 8 ? 2 : (HR >= 4 ? 4 : (HR >= 2 ? 8 : 16));
+        float s = v[0];
+#pragma unroll
+        for (int o = ofirst; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+        if ((lane & (2 * ofirst - 1)) == 0) s_part[wave][2 * ri + rs][c] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < R * NCOLS) {
+        const int r = threadIdx.x / NCOLS, c = threadIdx.x % NCOLS;
+        float v = s_part[0][r][c];
+#pragma unroll
+        for (int w = 1; w < NW; w++) v += s_part[w][r][c];
+        if (row0 + r < N) y[(size_t)c * N + row0 + r] = v;
+    }
+}
+
+template <int NCOLS, int R, int NW>
 static hipError_t launch_mmvq(const uint8_t *W, const int8_t *xq, const float4 *dsf,
                               float *y, int N, int K, hipStream_t s) {
-    const int rows_per_wg = 4 * RPW;
-    dim3 grid((N + rows_per_wg - 1) / rows_per_wg);
-    hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, RPW, 4>), grid, dim3(256), 0, s,
+    dim3 grid((N + R - 1) / R);
+    hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW>), grid, dim3(NW * 64), 0, s,
                        W, xq, dsf, y, N, K);
     return hipGetLastError();
 }
 
-/* Rows per wave: the largest of 8/4/2/1 that still gives >= 4096 waves
- * (16 per CU on 256 CUs), so short-N shapes split each row across more
- * lanes instead of leaving CUs idle. */
-extern "C" int sera_mmvq_rows_per_wave(int N, int K) {
-    (void)K;
-    int rpw = 8;
-    while (rpw > 1 && (N + rpw - 1) / rpw < 4096) rpw >>= 1;
-    return rpw;
+/* Rows per workgroup (even, 2..16), from a sweep on MI355X over the
+ * Qwen3-32B shapes: 4 for one token; 8 for 2-4 tokens (each loaded
+ * activation slice serves more rows); for 5-8 tokens the R/2 x M partial
+ * sums crowd the registers, so 4 on tall matrices and 2 otherwise. */
+extern "C" int sera_mmvq_rows_per_wave(int N, int M) {
+    if (M <= 1) return 4;
+    if (M <= 4) return 8;
+    return N >= 16384 ? 4 : 2;
+}
+
+template <int NCOLS, int R>
+static hipError_t dispatch_nw(int K, const uint8_t *W, const int8_t *xq, const float4 *dsf,
+                              float *y, int N, hipStream_t s) {
+    const int ngroups = (K / Q4K_QK + 7) / 8;
+    switch (ngroups >= 4 ? 4 : ngroups) {
+        case 1: return launch_mmvq<NCOLS, R, 1>(W, xq, dsf, y, N, K, s);
+        case 2: return launch_mmvq<NCOLS, R, 2>(W, xq, dsf, y, N, K, s);
+        case 3: return launch_mmvq<NCOLS, R, 3>(W, xq, dsf, y, N, K, s);
+        default: return launch_mmvq<NCOLS, R, 4>(W, xq, dsf, y, N, K, s);
+    }
 }
 
 template <int NCOLS>
-static hipError_t dispatch_rpw(int rpw, const uint8_t *W, const int8_t *xq, const float4 *dsf,
-                               float *y, int N, int K, hipStream_t s) {
-    switch (rpw) {
-        case 8: return launch_mmvq<NCOLS, 8>(W, xq, dsf, y, N, K, s);
-        case 4: return launch_mmvq<NCOLS, 4>(W, xq, dsf, y, N, K, s);
-        case 2: return launch_mmvq<NCOLS, 2>(W, xq, dsf, y, N, K, s);
-        default: return launch_mmvq<NCOLS, 1>(W, xq, dsf, y, N, K, s);
+static hipError_t dispatch_r(int r, const uint8_t *W, const int8_t *xq, const float4 *dsf,
+                             float *y, int N, int K, hipStream_t s) {
+    /* register budget: R/2 x M partial sums plus two sets of loads */
+    if (NCOLS > 2 && r > 8) r = 8;
+    if (NCOLS > 4 && r > 4) r = 4;
+    switch (r) {
+        case 16: if constexpr (NCOLS <= 2) return dispatch_nw<NCOLS, 16>(K, W, xq, dsf, y, N, s);
+                 [[fallthrough]];
+        case 8: if constexpr (NCOLS <= 4) return dispatch_nw<NCOLS, 8>(K, W, xq, dsf, y, N, s);
+                [[fallthrough]];
+        case 4: return dispatch_nw<NCOLS, 4>(K, W, xq, dsf, y, N, s);
+        default: return dispatch_nw<NCOLS, 2>(K, W, xq, dsf, y, N, s);
     }
 }
 
 extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y,
-                                           int M, int N, int K, int rpw, hipStream_t s) {
+                                           int M, int N, int K, int rows, hipStream_t s) {
     const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
     const char *base = (const char *)stage;
     const int8_t *xq = (const int8_t *)(base + L.qs);
     const float4 *dsf = (const float4 *)(base + L.dsf);
     const uint8_t *w = (const uint8_t *)W;
-    if (rpw <= 0) rpw = sera_mmvq_rows_per_wave(N, K);
+    if (rows <= 0) rows = sera_mmvq_rows_per_wave(N, M);
     switch (M) {
-        case 1: return dispatch_rpw<1>(rpw, w, xq, dsf, y, N, K, s);
-        case 2: return dispatch_rpw<2>(rpw, w, xq, dsf, y, N, K, s);
-        case 3: return dispatch_rpw<3>(rpw, w, xq, dsf, y, N, K, s);
-        case 4: return dispatch_rpw<4>(rpw, w, xq, dsf, y, N, K, s);
-        case 5: return dispatch_rpw<5>(rpw, w, xq, dsf, y, N, K, s);
-        case 6: return dispatch_rpw<6>(rpw, w, xq, dsf, y, N, K, s);
-        case 7: return dispatch_rpw<7>(rpw, w, xq, dsf, y, N, K, s);
-        case 8: return dispatch_rpw<8>(rpw, w, xq, dsf, y, N, K, s);
+        case 1: return dispatch_r<1>(rows, w, xq, dsf, y, N, K, s);
+        case 2: return dispatch_r<2>(rows, w, xq, dsf, y, N, K, s);
+        case 3: return dispatch_r<3>(rows, w, xq, dsf, y, N, K, s);
+        case 4: return dispatch_r<4>(rows, w, xq, dsf, y, N, K, s);
+        case 5: return dispatch_r<5>(rows, w, xq, dsf, y, N, K, s);
+        case 6: return dispatch_r<6>(rows, w, xq, dsf, y, N, K, s);
+        case 7: return dispatch_r<7>(rows, w, xq, dsf, y, N, K, s);
+        case 8: return dispatch_r<8>(rows, w, xq, dsf, y, N, K, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -22,7 +22,7 @@ extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, flo
                                            int K, int rpw, hipStream_t s);
 extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
                                           int M, int N, int K, int splits, hipStream_t s);
-extern "C" int sera_mmvq_rows_per_wave(int N, int K);
+extern "C" int sera_mmvq_rows_per_wave(int N, int M);
 extern "C" int sera_mmq_splits(int M, int N, int K);
 extern "C" int sera_mmq_padded_rows(int M);
 extern "C" int sera_mmq_bm(int M);
@@ -73,7 +73,7 @@ bool check_shape(const char *tag, const void *W, const float *X, const float *Y,
 }
 
 void record(hipEvent_t e, hipStream_t s) {
-    if (g_ev.valid) hipEventRecord(e, s);
+    if (g_ev.valid) (void)hipEventRecord(e, s);
 }
 
 }  // namespace
@@ -153,17 +153,20 @@ extern "C" int sera_q8_1_quantize_mmq(const float *X, int M, int K, void *stage,
                ? 0 : fail(-2, "sera_q8_1_quantize_mmq: launch failed");
 }
 
-extern "C" int sera_q4k_mmvq_rows_per_wave(int N, int K) { return sera_mmvq_rows_per_wave(N, K); }
+extern "C" int sera_q4k_mmvq_rows_per_tile(int M, int N, int K) {
+    (void)K;
+    return sera_mmvq_rows_per_wave(N, M);
+}
 
 extern "C" int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
-                             int rows_per_wave, void *stream) {
+                             int rows_per_tile, void *stream) {
     if (!W || !row_stage || !Y) return fail(-1, "sera_q4k_mmvq: null pointer");
     if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q4k_mmvq: batch M=%d outside 1..8", M);
     if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_mmvq: bad shape N=%d K=%d", N, K);
-    if (rows_per_wave != 0 && rows_per_wave != 1 && rows_per_wave != 2 && rows_per_wave != 4 &&
-        rows_per_wave != 8)
-        return fail(-1, "sera_q4k_mmvq: rows_per_wave=%d not in {0,1,2,4,8}", rows_per_wave);
-    return sera_launch_q4k_mmvq(W, row_stage, Y, M, N, K, rows_per_wave, (hipStream_t)stream) == hipSuccess
+    if (rows_per_tile != 0 && rows_per_tile != 2 && rows_per_tile != 4 && rows_per_tile != 8 &&
+        rows_per_tile != 16)
+        return fail(-1, "sera_q4k_mmvq: rows_per_tile=%d not in {0,2,4,8,16}", rows_per_tile);
+    return sera_launch_q4k_mmvq(W, row_stage, Y, M, N, K, rows_per_tile, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q4k_mmvq: launch failed");
 }
 
@@ -181,7 +184,8 @@ extern "C" int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, floa
                ? 0 : fail(-3, "sera_q4k_mmq: launch failed");
 }
 
-extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream) {
+extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
+                              int timed) {
     if (!check_shape("sera_q4k_dense", W, X, Y, M, N, K)) return -1;
     if (!g_arena) return fail(-1, "sera_q4k_dense: no arena attached");
     hipStream_t s = (hipStream_t)stream;
@@ -195,18 +199,19 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
                     g_arena_bytes);
     void *stage = g_arena;
     float *partial = splits > 1 ? (float *)(g_arena + stage_bytes) : nullptr;
-    record(g_ev.quant_begin, s);
+    if (timed) record(g_ev.quant_begin, s);
     if (sera_launch_q8_1_mmq(X, M, Mpad, K, stage, s) != hipSuccess)
         return fail(-2, "sera_q4k_dense: quantize launch failed");
-    record(g_ev.quant_end, s);
-    record(g_ev.kernel_begin, s);
+    if (timed) record(g_ev.quant_end, s);
+    if (timed) record(g_ev.kernel_begin, s);
     if (sera_launch_q4k_mmq(W, stage, Y, partial, M, N, K, splits, s) != hipSuccess)
         return fail(-3, "sera_q4k_dense: mmq launch failed");
-    record(g_ev.kernel_end, s);
+    if (timed) record(g_ev.kernel_end, s);
     return 0;
 }
 
-extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K, void *stream) {
+extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
+                                  int timed) {
     if (!check_shape("sera_q4k_dense_vec", W, X, Y, M, N, K)) return -1;
     if (M > SERA_Q4K_MMVQ_MAX_BATCH)
         return fail(-1, "sera_q4k_dense_vec: batch M=%d exceeds MMVQ cap %d", M, SERA_Q4K_MMVQ_MAX_BATCH);
@@ -215,14 +220,14 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
     const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
     if (stage_bytes > g_arena_bytes)
         return fail(-1, "sera_q4k_dense_vec: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
-    record(g_ev.quant_begin, s);
+    if (timed) record(g_ev.quant_begin, s);
     if (sera_launch_q8_1_row(X, M, K, g_arena, s) != hipSuccess)
         return fail(-2, "sera_q4k_dense_vec: quantize launch failed");
-    record(g_ev.quant_end, s);
-    record(g_ev.kernel_begin, s);
+    if (timed) record(g_ev.quant_end, s);
+    if (timed) record(g_ev.kernel_begin, s);
     if (sera_launch_q4k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess)
         return fail(-3, "sera_q4k_dense_vec: mmvq launch failed");
-    record(g_ev.kernel_end, s);
+    if (timed) record(g_ev.kernel_end, s);
     return 0;
 }
 

@@ -84,8 +84,8 @@ def load():
         "sera_q4k_init": ([I], I),
         "sera_q4k_arena_bytes": ([SZ, I64, I64], SZ),
         "sera_q4k_set_arena": ([P, SZ], I),
-        "sera_q4k_dense": ([P, P, P, I, I, I, P], I),
-        "sera_q4k_dense_vec": ([P, P, P, I, I, I, P], I),
+        "sera_q4k_dense": ([P, P, P, I, I, I, P, I], I),
+        "sera_q4k_dense_vec": ([P, P, P, I, I, I, P, I], I),
         "sera_q4k_read_timings": ([ctypes.POINTER(ctypes.c_double)] * 3, None),
         "sera_q8_1_row_stage_bytes": ([I, I], SZ),
         "sera_q8_1_row_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ),
@@ -96,7 +96,7 @@ def load():
         "sera_q8_1_mmq_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ)], None),
         "sera_q8_1_quantize_mmq": ([P, I, I, P, P], I),
         "sera_q4k_mmvq": ([P, P, P, I, I, I, I, P], I),
-        "sera_q4k_mmvq_rows_per_wave": ([I, I], I),
+        "sera_q4k_mmvq_rows_per_tile": ([I, I, I], I),
         "sera_q4k_mmq": ([P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_splits": ([I, I, I], I),
         "sera_q4k_dequantize": ([P, SZ, P, P], I),
@@ -222,8 +222,8 @@ def quantize_mmq(x, stage, stream=None):
            "sera_q8_1_quantize_mmq")
 
 
-def mmvq(W, stage, out, M, N, K, rows_per_wave=0, stream=None):
-    _check(load().sera_q4k_mmvq(_ptr(W), _ptr(stage), _ptr(out), M, N, K, rows_per_wave,
+def mmvq(W, stage, out, M, N, K, rows_per_tile=0, stream=None):
+    _check(load().sera_q4k_mmvq(_ptr(W), _ptr(stage), _ptr(out), M, N, K, rows_per_tile,
                                 _stream(stream)), "sera_q4k_mmvq")
 
 

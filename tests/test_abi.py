@@ -99,10 +99,10 @@ def test_kernel_entry_points_validate_on_host(L):
     assert L.sera_q4k_mmvq(d, d, d, 9, 128, 256, 0, None) == -1
     assert b"outside 1..8" in L.sera_q4k_last_error()
     assert L.sera_q4k_mmvq(d, d, d, 1, 128, 256, 3, None) == -1
-    assert L.sera_q4k_dense(d, d, d, 16, 128, 300, None) == -1
+    assert L.sera_q4k_dense(d, d, d, 16, 128, 300, None, 0) == -1
     assert b"multiple of 256" in L.sera_q4k_last_error()
-    assert L.sera_q4k_dense(None, d, d, 16, 128, 256, None) == -1
-    assert L.sera_q4k_dense(d, ctypes.c_void_p(258), d, 16, 128, 256, None) == -1
+    assert L.sera_q4k_dense(None, d, d, 16, 128, 256, None, 0) == -1
+    assert L.sera_q4k_dense(d, ctypes.c_void_p(258), d, 16, 128, 256, None, 0) == -1
     assert b"16-byte aligned" in L.sera_q4k_last_error()
     assert L.sera_q4k_mmq(d, d, d, None, 64, 128, 1024, 2, None) == -1
     assert b"partial" in L.sera_q4k_last_error()

@@ -202,7 +202,7 @@ def test_weight_quantizer_bit_exact(torch, golden_dir):
 # MMVQ and MMQ kernels vs the path-faithful oracles
 # ---------------------------------------------------------------------------
 
-MMVQ_SHAPES = [(256, 256), (1000, 512), (512, 5120), (64, 25600)]
+MMVQ_SHAPES = [(256, 256), (1000, 512), (512, 5120), (64, 25600), (203, 2304)]
 
 
 @pytest.mark.parametrize("N,K", MMVQ_SHAPES)
@@ -216,12 +216,12 @@ def test_mmvq_parity(torch, N, K):
         q3q4.quantize_row(dev(torch, x), stage)
         xq, xd, _ = oracle.q8_1_row(x)
         ref = oracle.gemm_mmvq(W, xq, xd, N, K)
-        for rpw in (1, 2, 4, 8):
-            say(f"case mmvq M={M} N={N} K={K} rpw={rpw}")
+        for rows in (2, 4, 8, 16):
+            say(f"case mmvq M={M} N={N} K={K} rows={rows}")
             y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-            q3q4.mmvq(Wd, stage, y, M, N, K, rows_per_wave=rpw)
+            q3q4.mmvq(Wd, stage, y, M, N, K, rows_per_tile=rows)
             torch.cuda.synchronize()
-            check_close(y.cpu().numpy(), ref, f"mmvq M={M} N={N} K={K} rpw={rpw}")
+            check_close(y.cpu().numpy(), ref, f"mmvq M={M} N={N} K={K} rows={rows}")
 
 
 MMQ_CASES = [(9, 128, 256), (16, 256, 1024), (33, 1000, 512), (64, 384, 5120),
