@@ -55,10 +55,10 @@ unsigned char *g_arena = nullptr;
 size_t g_arena_bytes = 0;
 
 /* Split-K partial floats never exceed this: the split count stops doubling
- * once tiles*splits >= 512, so splits*Mpad*N < 1024 * BM * 128. */
+ * once tiles*splits >= 512, so tiles*splits < 1024, and every MMQ tile
+ * covers at most 128*128 = 64*256 outputs, so splits*M*N < 1024 * 16384. */
 size_t partial_floats_bound(size_t max_tokens, int64_t max_features) {
-    const size_t bm = (size_t)sera_mmq_bm((int)(max_tokens > 0x7fffffff ? 0x7fffffff : max_tokens));
-    const size_t by_tiles = (size_t)1024 * bm * 128;
+    const size_t by_tiles = (size_t)1024 * 16384;
     const size_t by_shape = (size_t)16 * max_tokens * (size_t)(max_features > 0 ? max_features : 0);
     return by_tiles < by_shape ? by_tiles : by_shape;
 }
