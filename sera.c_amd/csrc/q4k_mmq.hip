@@ -47,10 +47,10 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 template <int BM>
-struct MmqSmem {
-    int8_t xs[2][BM][MMQ_XROW];      /* int8 quants, one 256-wide K step */
-    float d8[2][8][BM];              /* fp16 d8 as float, [sub-block][token] */
-    _Float16 s8[2][BM][8];           /* fp16 s8, [token][sub-block] */
+struct alignas(16) MmqSmem {
+    alignas(16) int8_t xs[2][BM][MMQ_XROW];  /* int8 quants, one 256-wide K step */
+    alignas(16) float d8[2][8][BM];          /* fp16 d8 as float, [sub-block][token] */
+    alignas(16) _Float16 s8[2][BM][8];       /* fp16 s8, [token][sub-block] */
 };
 
 /* Tile order: consecutive workgroup ids go to consecutive XCDs (8 on
@@ -74,6 +74,40 @@ __device__ __forceinline__ v4i unpack_nib(v4u q, int hi) {
     return a;
 }
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) {
+    union { uint32_t u; h2 h; } c;
+    c.u = u;
+    return c.h;
+}
+
+/* The eight (scale, min) pairs of a Q4_K header (dwords: d|dmin, then the
+ * 12 scale bytes), as fp16 products sw[p] = (fp16(d*sc_2p), fp16(d*sc_2p+1))
+ * and mw[p] = (fp16(-dmin*m_2p), fp16(-dmin*m_2p+1)), each a single
+ * round-to-nearest-even rounding of the exact product as in the
+ * reference's half2 scale store (cuda/mmq/mmq.cuh:2269-2283). The 6-bit
+ * fields are unpacked four at a time (src/q3_quant.c:44-55); a byte v < 64
+ * becomes the fp16 1024 + v by placing it under the exponent byte 0x64,
+ * and subtracting 1024 is exact. */
+__device__ __forceinline__ void q4k_scales_f16(v4u hd, h2 sw[4], h2 mw[4]) {
+    const uint32_t sc03 = hd.y & 0x3F3F3F3Fu;
+    const uint32_t m03 = hd.z & 0x3F3F3F3Fu;
+    const uint32_t sc47 = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+    const uint32_t m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const h2 dd = as_h2(__builtin_amdgcn_perm(hd.x, hd.x, 0x01000100u));       /* (d, d) */
+    const h2 nm = -as_h2(__builtin_amdgcn_perm(hd.x, hd.x, 0x03020302u));      /* (-dmin, -dmin) */
+    const uint32_t srcs[4] = {sc03, sc47, m03, m47};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const h2 lo = as_h2(__builtin_amdgcn_perm(0x64646464u, srcs[i], 0x04010400u)) - bias;
+        const h2 hi = as_h2(__builtin_amdgcn_perm(0x64646464u, srcs[i], 0x04030402u)) - bias;
+        if (i < 2) { sw[2 * i] = lo * dd; sw[2 * i + 1] = hi * dd; }
+        else       { mw[2 * (i - 2)] = lo * nm; mw[2 * (i - 2) + 1] = hi * nm; }
+    }
+}
+
 /* TT token tiles (of 32) per wave, WGT x WGN waves (along tokens x rows),
  * two 32-row weight tiles per wave. */
 template <int TT, int WGT, int WGN>
@@ -85,7 +119,7 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
     constexpr int BMW = 32 * TT;        /* tokens per wave */
     constexpr int BM = BMW * WGT;       /* tokens per workgroup */
     constexpr int BN = 64 * WGN;        /* weight rows per workgroup */
-    __shared__ MmqSmem<BM> sm;
+    __shared__ __attribute__((aligned(16))) MmqSmem<BM> sm;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -170,6 +204,9 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
     v4u xr[XCH], dr = {};
     v4u hdr[2] = {}, qw[2][4];
 
+    /* The 16 pad bytes of xs[0][0] stay zero: they are the min-term A
+     * operand of the lanes (h = 1) whose k positions carry no sub-block. */
+    if (tid == 0) *(v4u *)&sm.xs[0][0][Q4K_QK] = (v4u){0u, 0u, 0u, 0u};
     if (nkb > 0) {
         load_x(kb_begin, xr, dr);
         store_x(0, xr, dr);
@@ -182,35 +219,29 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
         const bool more = it + 1 < nkb;
         if (more) load_x(kb_begin + it + 1, xr, dr);
 
-        /* per weight tile: d, -dmin, and the min-term B operand
-         * fp16(-dmin*m_b) for b = 0..7 (lanes h = 0; zeros for h = 1) */
-        _Float16 dh[2];
+        /* per weight tile: fp16(d*sc_b) as fp32 for the epilogue and the
+         * min-term B operand fp16(-dmin*m_b), b = 0..7 */
+        h2 sw[2][4];
         v8h bmin[2];
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
-            union { uint16_t u; _Float16 f; } cd, cm;
-            cd.u = (uint16_t)(hdr[nt].x & 0xffffu);
-            cm.u = (uint16_t)(hdr[nt].x >> 16);
-            dh[nt] = cd.f;
-            const _Float16 ndmin = -cm.f;
+            h2 mw[4];
+            q4k_scales_f16(hdr[nt], sw[nt], mw);
 #pragma unroll
-            for (int b = 0; b < 8; b++) {
-                uint32_t sc, mn;
-                q4k_scale_min(b, hdr[nt].y, hdr[nt].z, hdr[nt].w, &sc, &mn);
-                bmin[nt][b] = h ? (_Float16)0.0f : (_Float16)(ndmin * (_Float16)(float)mn);
+            for (int p = 0; p < 4; p++) {
+                bmin[nt][2 * p] = mw[p].x;
+                bmin[nt][2 * p + 1] = mw[p].y;
             }
         }
 
 #pragma unroll
         for (int b = 0; b < 8; b++) {
-            float swb[2];
             v4i Bw[2];
+            float swb[2];
 #pragma unroll
             for (int nt = 0; nt < 2; nt++) {
-                uint32_t sc, mn;
-                q4k_scale_min(b, hdr[nt].y, hdr[nt].z, hdr[nt].w, &sc, &mn);
-                swb[nt] = (float)(dh[nt] * (_Float16)(float)sc);   /* fp16 product, RNE */
                 Bw[nt] = unpack_nib(qw[nt][b >> 1], b & 1);
+                swb[nt] = (float)((b & 1) ? sw[nt][b >> 1].y : sw[nt][b >> 1].x);
             }
 #pragma unroll
             for (int t = 0; t < TT; t++) {
@@ -236,8 +267,7 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
 #pragma unroll
         for (int t = 0; t < TT; t++) {
             const int tok = BMW * wt + 32 * t + l32;
-            v8h as8 = *(const v8h *)&sm.s8[buf][tok][0];
-            if (h) as8 = (v8h){};
+            const v8h as8 = *(const v8h *)(h ? (const void *)&sm.xs[0][0][Q4K_QK] : (const void *)&sm.s8[buf][tok][0]);
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
                 acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as8, bmin[nt], acc[t][nt], 0, 0, 0);
