@@ -11,8 +11,11 @@ copies (590 MB) are used round robin so that every step reads HBM, not the
 
 Also printed in the same JSON line:
   roofline      the MMVQ kernel alone: algorithmic bytes per launch over its
-                average launch duration (HIP event pair around each launch on
-                the launch stream), against 8 TB/s
+                average launch duration (back-to-back launches between one HIP
+                event pair on the launch stream), against 8 TB/s; `traffic` is
+                the HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE
+                counter summary in profiles/ when one is present for the same
+                kernel, scaled by the copy-kernel calibration it records
   cpu_baseline  the reference's CPU path on this host: Q4_K dequant with the
                 reference's q3_quant.c (oracle/_ref, single thread) plus
                 numpy fp32 matmul, on the full gate/up matrix at M=1
@@ -59,6 +62,10 @@ def main():
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--full", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quick", action="store_true",
+                    help="headline only (gate/up M=1): for counter-collection runs")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="only run a plain device copy of MB megabytes 20 times (counter scale)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -68,6 +75,16 @@ def main():
     import numpy as np
     import torch
     import q3q4
+
+    if args.copy_calibration:
+        n = args.copy_calibration * 1000 * 1000 // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 20 copies of {n * 4} bytes")
+        return
 
     L = q3q4.load()
     dev = torch.device("cuda:0")
@@ -130,23 +147,24 @@ def main():
     headline = None
     for name, (N, K, (ws, arr)) in sets.items():
         geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
-        for M in (1, 2, 4, 8):
+        for M in ((1,) if args.quick else (1, 2, 4, 8)):
+            if args.quick and name != "gate_up":
+                break
             x = activations(M, K, 1 + M)
             y = torch.empty((M, N), dtype=torch.float32, device=dev)
             step_ms = bench_linear(geo, arr, args.copies, x, y, args.warmup, args.steps)
             stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
             q3q4.quantize_row(x, stage)
             rpw = L.sera_q4k_mmvq_rows_per_tile(M, N, K)
-            kavg, kb2b = bench_kernel(0, arr, args.copies, stage, y, None, M, N, K, 0,
-                                      args.warmup, args.steps)
+            kavg, _ = bench_kernel(0, arr, args.copies, stage, y, None, M, N, K, 0,
+                                   args.warmup, args.steps)
             b = alg_bytes(M, N, K)
             row = {"proj": name, "M": M, "N": N, "K": K, "rows_per_tile": rpw,
                    "step_us": round(step_ms * 1e3, 3),
                    "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),
                    "kernel_us": round(kavg * 1e3, 3),
                    "kernel_GBps": round(b / (kavg * 1e-3) / 1e9, 1),
-                   "kernel_frac_hbm": round(b / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                   "kernel_b2b_us": round(kb2b * 1e3, 3)}
+                   "kernel_frac_hbm": round(b / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             log(f"[bench] mmvq {name} M={M}: step {row['step_us']} us ({row['step_GBps']} GB/s), "
                 f"kernel {row['kernel_us']} us ({row['kernel_GBps']} GB/s, "
                 f"{100 * row['kernel_frac_hbm']:.1f}% of HBM)")
@@ -179,7 +197,8 @@ def main():
         return row
 
     gN, gK, (gws, garr) = sets["gate_up"]
-    results["mmq_m512_gate"] = mmq_case("gate", gN, gK, 512, garr, args.copies, 20)
+    if not args.quick:
+        results["mmq_m512_gate"] = mmq_case("gate", gN, gK, 512, garr, args.copies, 20)
 
     if args.full:
         full = []
@@ -200,9 +219,10 @@ def main():
     row, step_ms, b = headline
     kernel_ms = row["kernel_us"] * 1e-3
     achieved = b / (kernel_ms * 1e-3) / 1e9
+    kname = f"sera_q4k_mmvq_kernel<1, {row['rows_per_tile']}, 3>"
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"sera_q4k_mmvq_kernel<1,{row['rows_per_tile']},3>",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(kname),
+                "kernel": kname,
                 "avg_launch_us": row["kernel_us"], "algorithmic_bytes_per_launch": b}
 
     # ---------------- CPU baseline ------------------------------------------
@@ -226,6 +246,24 @@ def main():
         "results": results,
     }
     print(json.dumps(out), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mmvq_gate_up_m1_hbm_traffic.json")
+
+
+def hbm_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary:
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) times the factors that make
+    the same counters read a plain copy of known size correctly. None when
+    the summary is absent or was taken on another kernel."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel:
+        return None
+    return int(round(1024 * (t["fetch_kib"] * t["fetch_factor"] + t["write_kib"] * t["write_factor"])))
 
 
 def cpu_baseline(np, torch, w_dev, N, K, x):

@@ -123,8 +123,9 @@ int sera_q4k_bench_linear(const void *geometry, const void *const *weights, int 
                           int iters, double *elapsed_ms);
 
 /* Kernel-only loop on a prepared stage (path 0 = MMVQ with param =
- * rows_per_wave, 1 = MMQ with param = splits). *avg_kernel_ms averages an
- * event pair around each launch; *elapsed_ms spans all launches. */
+ * rows_per_wave, 1 = MMQ with param = splits): `iters` launches back to back
+ * between one event pair on `stream`; *avg_kernel_ms = pair time / iters,
+ * *elapsed_ms = pair time. */
 int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, const void *stage,
                           float *Y, float *partial, int M, int N, int K, int param, void *stream,
                           int warmup, int iters, double *avg_kernel_ms, double *elapsed_ms);

@@ -11,7 +11,6 @@
 #include "../../include/q3_q4_linear.h"
 #include "../../include/sera_q4k.h"
 
-#include <stdlib.h>
 
 extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y, int M, int N,
                                            int K, int rpw, hipStream_t s);
@@ -46,9 +45,10 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
 }
 
 /* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ.
- * avg_kernel_ms: mean over launches of an event pair recorded right before
- * and after each launch on `stream` (the launch's own duration);
- * elapsed_ms: first-to-last event over all back-to-back launches. */
+ * `iters` launches back to back on `stream` between one pair of events, so
+ * no timing packet sits between two launches; avg_kernel_ms is the pair's
+ * elapsed time over iters (each launch's duration plus the dispatch gap to
+ * the next one), elapsed_ms the pair's elapsed time. */
 extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights,
                                      const void *stage, float *y, float *partial, int M, int N, int K,
                                      int param, void *stream, int warmup, int iters,
@@ -62,27 +62,21 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
     };
     for (int i = 0; i < warmup; i++)
         if (launch(i) != hipSuccess) return -3;
-    hipEvent_t *ev = (hipEvent_t *)malloc(sizeof(hipEvent_t) * 2 * (size_t)iters);
-    if (!ev) return -1;
-    for (int i = 0; i < 2 * iters; i++)
-        if (hipEventCreate(&ev[i]) != hipSuccess) { free(ev); return -1; }
-    for (int i = 0; i < iters; i++) {
-        (void)hipEventRecord(ev[2 * i], s);
-        if (launch(i) != hipSuccess) { free(ev); return -3; }
-        (void)hipEventRecord(ev[2 * i + 1], s);
-    }
-    (void)hipEventSynchronize(ev[2 * iters - 1]);
-    double sum = 0.0;
-    for (int i = 0; i < iters; i++) {
-        float ms = 0.0f;
-        (void)hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
-        sum += ms;
-    }
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess) return -1;
+    if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return -1; }
+    int rc = 0;
+    (void)hipEventRecord(a, s);
+    for (int i = 0; i < iters && rc == 0; i++)
+        if (launch(i) != hipSuccess) rc = -3;
+    (void)hipEventRecord(b, s);
+    (void)hipEventSynchronize(b);
     float tot = 0.0f;
-    (void)hipEventElapsedTime(&tot, ev[0], ev[2 * iters - 1]);
-    for (int i = 0; i < 2 * iters; i++) (void)hipEventDestroy(ev[i]);
-    free(ev);
-    if (avg_kernel_ms) *avg_kernel_ms = sum / iters;
+    (void)hipEventElapsedTime(&tot, a, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    if (rc) return rc;
+    if (avg_kernel_ms) *avg_kernel_ms = (double)tot / iters;
     if (elapsed_ms) *elapsed_ms = tot;
     return 0;
 }
