@@ -38,6 +38,7 @@ sys.path.insert(0, os.path.join(ROOT, "sera.c_amd"))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+VEC_MFMA_MIN_BATCH = 5   # MMVQ-path batches from here run the few-token MFMA kernel
 METRIC = "MMVQ HBM GB/s @M=1; MMQ int8 TOPS @M=512; % of MI355X roofline"
 SHAPES = {  # name: (N, K) as (output features, input features)
     "q": (8192, 5120), "k": (1024, 5120), "v": (1024, 5120), "o": (5120, 8192),
@@ -156,10 +157,20 @@ def main():
             stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
             q3q4.quantize_row(x, stage)
             rpw = L.sera_q4k_mmvq_rows_per_tile(M, N, K)
-            kavg, _ = bench_kernel(0, arr, args.copies, stage, y, None, M, N, K, 0,
-                                   args.warmup, args.steps)
+            if M >= VEC_MFMA_MIN_BATCH:
+                # the MMVQ path's few-token MFMA kernel (MMVQ arithmetic)
+                sp = q3q4.skinny_splits(M, N, K)
+                part = torch.empty(sp * M * N, dtype=torch.float32, device=dev) if sp > 1 else None
+                kavg, _ = bench_kernel(2, arr, args.copies, stage, y, part, M, N, K, sp,
+                                       args.warmup, args.steps)
+                rpw = None
+            else:
+                kavg, _ = bench_kernel(0, arr, args.copies, stage, y, None, M, N, K, 0,
+                                       args.warmup, args.steps)
             b = alg_bytes(M, N, K)
-            row = {"proj": name, "M": M, "N": N, "K": K, "rows_per_tile": rpw,
+            row = {"proj": name, "M": M, "N": N, "K": K,
+                   "kernel": "sera_q4k_skinny_kernel<0, 1, 4>" if rpw is None else
+                             f"sera_q4k_mmvq_kernel<{M}, {rpw}, {min(4, (K // 256 + 7) // 8)}>",
                    "step_us": round(step_ms * 1e3, 3),
                    "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),
                    "kernel_us": round(kavg * 1e3, 3),
@@ -219,7 +230,7 @@ def main():
     row, step_ms, b = headline
     kernel_ms = row["kernel_us"] * 1e-3
     achieved = b / (kernel_ms * 1e-3) / 1e9
-    kname = f"sera_q4k_mmvq_kernel<1, {row['rows_per_tile']}, 3>"
+    kname = row["kernel"]
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(kname),
                 "kernel": kname,

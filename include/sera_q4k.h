@@ -30,7 +30,8 @@
 extern "C" {
 #endif
 
-#define SERA_Q4K_MMVQ_MAX_BATCH 8   /* cuda/q3_mmq.h:77 Q3_MMVQ_MAX_BATCH */
+#define SERA_Q4K_MMVQ_MAX_BATCH 8    /* cuda/q3_mmq.h:77 Q3_MMVQ_MAX_BATCH */
+#define SERA_Q4K_SKINNY_MAX_BATCH 16 /* token tile of the few-token MFMA kernel */
 
 /* ---- set-up (cuda/q3_mmq.h:35-38, 84-94) ------------------------------ */
 
@@ -55,10 +56,15 @@ int sera_q4k_set_arena(void *device_ptr, size_t bytes);
 int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
                    void *stream, int timed);
 
-/* Same contract through the MMVQ path, 1 <= M <= 8.
- * Replaces q3_mmq_q4_K_dense_vec (cuda/q3_mmq.cu:408-506). */
+/* Same contract through the MMVQ path (MMVQ arithmetic), 1 <= M <= 8:
+ * the dot4 MMVQ kernel up to 4 tokens, the few-token MFMA kernel (form 0)
+ * from 5. Replaces q3_mmq_q4_K_dense_vec (cuda/q3_mmq.cu:408-506). */
 int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
+
+/* Kernel launches (quantize + matmul + split-K reduce if any) one dense or
+ * dense_vec call makes for this shape; 0 for an invalid shape. */
+int sera_q4k_kernel_launches(int M, int N, int K);
 
 /* Event timings of the last timed dense call, valid after the caller
  * synchronized its stream (q3_mmq_read_timings, cuda/q3_mmq.h:48-50). */
@@ -96,6 +102,18 @@ int sera_q4k_mmvq_rows_per_tile(int M, int N, int K);
 int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, float *partial, int M, int N,
                  int K, int splits, void *stream);
 int sera_q4k_mmq_splits(int M, int N, int K);
+
+/* Few-token kernel (1 <= M <= 16) on 16x16 int8 MFMA tiles. form 0 takes a
+ * row stage and computes the MMVQ formula (the same arithmetic as
+ * sera_q4k_mmvq, vec_dot_q4_K_q8_1, cuda/mmq/vecdotq.cuh:505-527); form 1
+ * takes an MMQ stage and computes the MMQ formula (as sera_q4k_mmq,
+ * cuda/mmq/mmq.cuh:2269-2283,1440-1472). No reference counterpart as a
+ * kernel: it is this build's tiling for the reference's small-batch cases.
+ * splits > 1 splits K; partial then holds splits*M*N floats (M*N % 4 == 0);
+ * 0 picks the built-in choice (sera_q4k_skinny_splits). */
+int sera_q4k_skinny(int form, const void *W, const void *stage, float *Y, float *partial, int M, int N,
+                    int K, int splits, void *stream);
+int sera_q4k_skinny_splits(int M, int N, int K);
 
 /* Device Q4_K dequant, w = (d*sc)*q - (dmin*m) per weight; replaces
  * q3_cuda_dequantize_row (src/q3_cuda_primitives.h, cuda/q3_cuda_primitives.cu:13-95). */

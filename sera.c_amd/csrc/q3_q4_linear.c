@@ -148,12 +148,11 @@ bool q3_cuda_q4k_linear(const q3_q4_linear_geometry *geometry, const void *weigh
     if (tokens <= SERA_Q4K_MMVQ_MAX_BATCH) {
         rc = sera_q4k_dense_vec(weight, device_input, device_output, tokens, features, K, stream,
                                 stats != NULL);
-        s->kernel_launches = 2;  /* quantize + MMVQ */
+        s->kernel_launches = (uint64_t)sera_q4k_kernel_launches(tokens, features, K);
     } else {
         rc = sera_q4k_dense(weight, device_input, device_output, tokens, features, K, stream,
                             stats != NULL);
-        s->kernel_launches = sera_q4k_mmq_splits(tokens, features, K) > 1 &&
-                                     ((size_t)tokens * features) % 4 == 0 ? 3 : 2;
+        s->kernel_launches = (uint64_t)sera_q4k_kernel_launches(tokens, features, K);
     }
     if (rc != 0) {
         char buffer[400];

@@ -309,6 +309,15 @@ __global__ __launch_bounds__(256) void sera_splitk_reduce_kernel(
     y[i] = s;
 }
 
+/* y[i] = sum over k of partial[k*n + i], k = 0..splits-1 in order; n % 4 == 0. */
+extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits,
+                                                hipStream_t s) {
+    const size_t n4 = n / 4;
+    hipLaunchKernelGGL(sera_splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                       (const float4 *)partial, (float4 *)y, n4, splits);
+    return hipGetLastError();
+}
+
 /* Token-tile width of the workgroup for M tokens: 32 (one token tile per
  * wave, 4 waves along weight rows), 64 (two per wave) or 128 (two per wave,
  * 2 x 2 waves). */
@@ -350,10 +359,7 @@ static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint3
                        splits > 1 ? partial : nullptr, M, N, K, per);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
-    const size_t n4 = (size_t)M * N / 4;
-    hipLaunchKernelGGL(sera_splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
-                       (const float4 *)partial, (float4 *)y, n4, splits);
-    return hipGetLastError();
+    return sera_launch_splitk_reduce(partial, y, (size_t)M * N, splits, s);
 }
 
 /* partial: M*N*splits floats of scratch when splits > 1 (M*N % 4 == 0). */

@@ -73,12 +73,17 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
     const int q = lane & 3;                /* sub-block pair */
     const int g = (lane >> 2) & 7;         /* block within the group of 8 */
     const int rs = lane >> 5;              /* row parity */
-    const int row0 = blockIdx.x * R;
+    /* The last tile is shifted back to end at row N (it recomputes rows of
+     * its neighbour and stores only its own): the range check of a raw
+     * buffer load covers the vector offset but not the scalar row step, so
+     * no row past N may be addressed. The launcher keeps R <= N, or R = 2
+     * where row 1 sits in the vector offset. */
+    const int tile0 = blockIdx.x * R;
+    const int row0 = tile0 + R > N && N >= R ? N - R : tile0;
     const int nb = K / Q4K_QK;
     const int ngroups = (nb + 7) >> 3;
     const int rowbytes = nb * Q4K_BLOCK_BYTES;
     const int nrows = min(R, N - row0);
-    /* rows >= N fall outside the descriptor's range and read as zero */
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + (size_t)row0 * rowbytes, (uint32_t)(nrows * rowbytes));
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, (uint32_t)(NCOLS * K));
     const __amdgpu_buffer_rsrc_t rf = make_rsrc(dsf, (uint32_t)(NCOLS * (K / 64) * 16));
@@ -208,7 +213,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
         float v = s_part[0][r][c];
 #pragma unroll
         for (int w = 1; w < NW; w++) v += s_part[w][r][c];
-        if (row0 + r < N) y[(size_t)c * N + row0 + r] = v;
+        if (row0 + r >= tile0 && row0 + r < N) y[(size_t)c * N + row0 + r] = v;
     }
 }
 
@@ -267,6 +272,7 @@ extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, flo
     const float4 *dsf = (const float4 *)(base + L.dsf);
     const uint8_t *w = (const uint8_t *)W;
     if (rows <= 0) rows = sera_mmvq_rows_per_wave(N, M);
+    while (rows > 2 && rows > N) rows >>= 1;   /* the shifted last tile needs R <= N */
     switch (M) {
         case 1: return dispatch_r<1>(rows, w, xq, dsf, y, N, K, s);
         case 2: return dispatch_r<2>(rows, w, xq, dsf, y, N, K, s);

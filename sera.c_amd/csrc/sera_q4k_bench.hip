@@ -16,6 +16,8 @@ extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, flo
                                            int K, int rpw, hipStream_t s);
 extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
                                           int M, int N, int K, int splits, hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
+                                             int M, int N, int K, int splits, hipStream_t s);
 
 /* `warmup` untimed then `iters` timed calls of q3_cuda_q4k_linear; weight i
  * of the call is weights[i % nweights]. elapsed_ms: first-to-last event of
@@ -44,7 +46,8 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
     return 0;
 }
 
-/* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ.
+/* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ, 2 / 3 = few-token
+ * kernel with the MMVQ / MMQ formula.
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
  * elapsed time over iters (each launch's duration plus the dispatch gap to
@@ -57,8 +60,11 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
     hipStream_t s = (hipStream_t)stream;
     auto launch = [&](int i) -> hipError_t {
         const void *w = weights[i % nweights];
-        return path == 0 ? sera_launch_q4k_mmvq(w, stage, y, M, N, K, param, s)
-                         : sera_launch_q4k_mmq(w, stage, y, partial, M, N, K, param, s);
+        switch (path) {
+            case 0: return sera_launch_q4k_mmvq(w, stage, y, M, N, K, param, s);
+            case 1: return sera_launch_q4k_mmq(w, stage, y, partial, M, N, K, param, s);
+            default: return sera_launch_q4k_skinny(path - 2, w, stage, y, partial, M, N, K, param, s);
+        }
     };
     for (int i = 0; i < warmup; i++)
         if (launch(i) != hipSuccess) return -3;

@@ -24,6 +24,9 @@ extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, floa
                                           int M, int N, int K, int splits, hipStream_t s);
 extern "C" int sera_mmvq_rows_per_wave(int N, int M);
 extern "C" int sera_mmq_splits(int M, int N, int K);
+extern "C" int sera_skinny_splits(int M, int N, int K);
+extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
+                                             int M, int N, int K, int splits, hipStream_t s);
 extern "C" int sera_mmq_padded_rows(int M);
 extern "C" int sera_mmq_bm(int M);
 extern "C" hipError_t sera_launch_q4k_quantize(const float *x, int64_t rows, int64_t K, void *out,
@@ -172,6 +175,22 @@ extern "C" int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int
 
 extern "C" int sera_q4k_mmq_splits(int M, int N, int K) { return sera_mmq_splits(M, N, K); }
 
+extern "C" int sera_q4k_skinny_splits(int M, int N, int K) { return sera_skinny_splits(M, N, K); }
+
+extern "C" int sera_q4k_skinny(int form, const void *W, const void *stage, float *Y, float *partial, int M,
+                               int N, int K, int splits, void *stream) {
+    if (!W || !stage || !Y) return fail(-1, "sera_q4k_skinny: null pointer");
+    if (form != 0 && form != 1) return fail(-1, "sera_q4k_skinny: form=%d not 0 (row stage) or 1 (MMQ stage)", form);
+    if (M < 1 || M > SERA_Q4K_SKINNY_MAX_BATCH) return fail(-1, "sera_q4k_skinny: batch M=%d outside 1..16", M);
+    if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_skinny: bad shape N=%d K=%d", N, K);
+    if (splits == 0) splits = sera_skinny_splits(M, N, K);
+    if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q4k_skinny: splits=%d outside 1..K/256", splits);
+    if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
+        return fail(-1, "sera_q4k_skinny: split-K needs a partial buffer and M*N %% 4 == 0");
+    return sera_launch_q4k_skinny(form, W, stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_q4k_skinny: launch failed");
+}
+
 extern "C" int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, float *partial, int M, int N,
                             int K, int splits, void *stream) {
     if (!W || !mmq_stage || !Y) return fail(-1, "sera_q4k_mmq: null pointer");
@@ -210,6 +229,25 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
     return 0;
 }
 
+/* Batches from this size up to the MMVQ cap run the few-token MFMA kernel
+ * (MMVQ formula) instead of the dot4 MMVQ kernel: on MI355X it is about
+ * twice as fast at 8 tokens, while dot4 wins up to 4 tokens. */
+#define SERA_Q4K_VEC_MFMA_MIN_BATCH 5
+
+namespace {
+int vec_splits(int M, int N, int K) {
+    if (M < SERA_Q4K_VEC_MFMA_MIN_BATCH) return 1;
+    const int sp = sera_skinny_splits(M, N, K);
+    return ((size_t)M * N) % 4 == 0 ? sp : 1;
+}
+}  // namespace
+
+extern "C" int sera_q4k_kernel_launches(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
+    if (M <= SERA_Q4K_MMVQ_MAX_BATCH) return vec_splits(M, N, K) > 1 ? 3 : 2;
+    return sera_mmq_splits(M, N, K) > 1 && ((size_t)M * N) % 4 == 0 ? 3 : 2;
+}
+
 extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
                                   int timed) {
     if (!check_shape("sera_q4k_dense_vec", W, X, Y, M, N, K)) return -1;
@@ -218,15 +256,23 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
     if (!g_arena) return fail(-1, "sera_q4k_dense_vec: no arena attached");
     hipStream_t s = (hipStream_t)stream;
     const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
-    if (stage_bytes > g_arena_bytes)
-        return fail(-1, "sera_q4k_dense_vec: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
+    const int splits = vec_splits(M, N, K);
+    const size_t partial_bytes = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+    if (stage_bytes + partial_bytes > g_arena_bytes)
+        return fail(-1, "sera_q4k_dense_vec: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
+                    g_arena_bytes);
     if (timed) record(g_ev.quant_begin, s);
     if (sera_launch_q8_1_row(X, M, K, g_arena, s) != hipSuccess)
         return fail(-2, "sera_q4k_dense_vec: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    if (sera_launch_q4k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess)
+    if (M >= SERA_Q4K_VEC_MFMA_MIN_BATCH) {
+        float *partial = splits > 1 ? (float *)(g_arena + stage_bytes) : nullptr;
+        if (sera_launch_q4k_skinny(0, W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
+            return fail(-3, "sera_q4k_dense_vec: few-token kernel launch failed");
+    } else if (sera_launch_q4k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
         return fail(-3, "sera_q4k_dense_vec: mmvq launch failed");
+    }
     if (timed) record(g_ev.kernel_end, s);
     return 0;
 }

@@ -99,6 +99,9 @@ def load():
         "sera_q4k_mmvq_rows_per_tile": ([I, I, I], I),
         "sera_q4k_mmq": ([P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_splits": ([I, I, I], I),
+        "sera_q4k_skinny": ([I, P, P, P, P, I, I, I, I, P], I),
+        "sera_q4k_skinny_splits": ([I, I, I], I),
+        "sera_q4k_kernel_launches": ([I, I, I], I),
         "sera_q4k_dequantize": ([P, SZ, P, P], I),
         "sera_q4k_subblock_dots": ([P, P, P, I, I, I, P], I),
         "sera_q4k_quantize": ([P, I64, I64, P, P], I),
@@ -234,6 +237,17 @@ def mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None):
 
 def mmq_splits(M, N, K):
     return load().sera_q4k_mmq_splits(M, N, K)
+
+
+def skinny(form, W, stage, out, M, N, K, splits=0, partial=None, stream=None):
+    """Few-token MFMA kernel: form 0 on a row stage (MMVQ formula), form 1 on
+    an MMQ stage (MMQ formula); 1 <= M <= 16."""
+    _check(load().sera_q4k_skinny(form, _ptr(W), _ptr(stage), _ptr(out), _ptr(partial), M, N, K, splits,
+                                  _stream(stream)), "sera_q4k_skinny")
+
+
+def skinny_splits(M, N, K):
+    return load().sera_q4k_skinny_splits(M, N, K)
 
 
 def dequantize(W, nblocks, out, stream=None):

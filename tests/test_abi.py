@@ -107,6 +107,13 @@ def test_kernel_entry_points_validate_on_host(L):
     assert L.sera_q4k_mmq(d, d, d, None, 64, 128, 1024, 2, None) == -1
     assert b"partial" in L.sera_q4k_last_error()
     assert L.sera_q4k_set_arena(ctypes.c_void_p(100), 1024) == -1
+    assert L.sera_q4k_skinny(0, d, d, d, None, 17, 128, 256, 1, None) == -1
+    assert b"outside 1..16" in L.sera_q4k_last_error()
+    assert L.sera_q4k_skinny(2, d, d, d, None, 4, 128, 256, 1, None) == -1
+    assert L.sera_q4k_skinny(1, d, d, d, None, 4, 128, 512, 3, None) == -1
+    assert b"splits" in L.sera_q4k_last_error()
+    assert L.sera_q4k_skinny(1, d, d, d, None, 4, 128, 512, 2, None) == -1
+    assert b"partial" in L.sera_q4k_last_error()
 
 
 def test_stage_layouts_and_workspace_sizing():
@@ -125,3 +132,14 @@ def test_stage_layouts_and_workspace_sizing():
             s = q3q4.mmq_splits(M, N, K)
             need = q3q4.mmq_stage_layout(M, K)["total"] + (s * M * N * 4 if s > 1 else 0)
             assert need <= L.sera_q4k_arena_bytes(2048, 151936, 25600), (M, N, K, s)
+
+
+def test_kernel_launch_counts(L):
+    """quantize + matmul (+ the split-K reduce when K is split)."""
+    assert L.sera_q4k_kernel_launches(1, 25600, 5120) == 2          # dot4 MMVQ
+    assert L.sera_q4k_kernel_launches(8, 25600, 5120) == 2          # few-token kernel, no split
+    assert L.sera_q4k_kernel_launches(8, 5120, 25600) == 3          # few-token kernel, split K
+    assert L.sera_q4k_kernel_launches(512, 25600, 5120) == 2        # MMQ, enough tiles
+    assert L.sera_q4k_kernel_launches(16, 5120, 25600) == 3         # MMQ, split K
+    assert L.sera_q4k_kernel_launches(0, 5120, 25600) == 0
+    assert L.sera_q4k_kernel_launches(4, 5120, 300) == 0
