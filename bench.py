@@ -192,12 +192,22 @@ def main():
         step_ms = bench_linear(geo, arr, ncopies, x, y, 3, iters)
         stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
         q3q4.quantize_mmq(x, stage)
-        splits = q3q4.mmq_splits(M, N, K)
-        partial = (torch.empty(splits * M * N, dtype=torch.float32, device=dev)
-                   if splits > 1 else None)
-        kavg, _ = bench_kernel(1, arr, ncopies, stage, y, partial, M, N, K, splits, 3, iters)
+        wgs = L.sera_q4k_mmq_streamk_wgs(M)
+        tiles = L.sera_q4k_mmq_tiles(M, N)
+        if wgs < tiles < 4 * wgs and tiles * (K // 256) >= wgs:
+            # stream-K schedule: slots, then the zeroed tile counters
+            splits = 0
+            nslot = 2 * wgs * L.sera_q4k_mmq_slot_floats(M)
+            partial = torch.zeros(nslot + tiles, dtype=torch.float32, device=dev)
+            kavg, _ = bench_kernel(4, arr, ncopies, stage, y, partial, M, N, K, wgs, 3, iters)
+        else:
+            splits = q3q4.mmq_splits(M, N, K)
+            partial = (torch.empty(splits * M * N, dtype=torch.float32, device=dev)
+                       if splits > 1 else None)
+            kavg, _ = bench_kernel(1, arr, ncopies, stage, y, partial, M, N, K, splits, 3, iters)
         ops = 2.0 * M * N * K
-        row = {"case": label, "M": M, "N": N, "K": K, "splits": splits,
+        row = {"case": label, "M": M, "N": N, "K": K,
+               "schedule": "stream-K" if splits == 0 else f"split-K x{splits}",
                "step_us": round(step_ms * 1e3, 2), "kernel_us": round(kavg * 1e3, 2),
                "kernel_TOPS": round(ops / (kavg * 1e-3) / 1e12, 1),
                "step_TOPS": round(ops / (step_ms * 1e-3) / 1e12, 1),

@@ -44,7 +44,9 @@ int sera_q4k_init(int device);
  * the split-K partial sums. */
 size_t sera_q4k_arena_bytes(size_t max_tokens, int64_t max_features, int64_t max_k);
 
-/* Attach caller-owned device scratch (q3_mmq_set_arena, cuda/q3_mmq.h:84). */
+/* Attach caller-owned device scratch (q3_mmq_set_arena, cuda/q3_mmq.h:84).
+ * The first 256 KB hold the stream-K tile counters, which this call clears
+ * (a synchronous memset) and every call leaves zero again. */
 int sera_q4k_set_arena(void *device_ptr, size_t bytes);
 
 /* ---- whole linear: quantize + kernel (cuda/q3_mmq.h:52-63) ------------ */
@@ -103,6 +105,21 @@ int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, float *partial,
                  int K, int splits, void *stream);
 int sera_q4k_mmq_splits(int M, int N, int K);
 
+/* MMQ kernel under a stream-K schedule (the role of mul_mat_q's stream-K
+ * decomposition and mul_mat_q_stream_k_fixup, cuda/mmq/mmq.cuh:3641-4352):
+ * `wgs` persistent workgroups (a multiple of 8; 0 = the device's resident
+ * count) split the (tile, 256-wide K step) units evenly; split tiles are
+ * summed in a fixed order by their last contributor, found with a per-tile
+ * counter, so results repeat bit for bit and no workgroup waits on another.
+ * slots: 2*wgs*sera_q4k_mmq_slot_floats(M) floats; counters:
+ * sera_q4k_mmq_tiles(M, N) ints that must be zero and are zero again after
+ * the kernel. Needs tiles*K/256 >= wgs. */
+int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
+                         int M, int N, int K, int wgs, void *stream);
+int sera_q4k_mmq_streamk_wgs(int M);   /* resident workgroups for M tokens (after init) */
+int sera_q4k_mmq_tiles(int M, int N);
+int sera_q4k_mmq_slot_floats(int M);
+
 /* Few-token kernel (1 <= M <= 16) on 16x16 int8 MFMA tiles. form 0 takes a
  * row stage and computes the MMVQ formula (the same arithmetic as
  * sera_q4k_mmvq, vec_dot_q4_K_q8_1, cuda/mmq/vecdotq.cuh:505-527); form 1
@@ -141,7 +158,10 @@ int sera_q4k_bench_linear(const void *geometry, const void *const *weights, int 
                           int iters, double *elapsed_ms);
 
 /* Kernel-only loop on a prepared stage (path 0 = MMVQ with param =
- * rows_per_wave, 1 = MMQ with param = splits): `iters` launches back to back
+ * rows_per_wave, 1 = MMQ with param = splits, 2/3 = few-token kernel form
+ * 0/1 with param = splits, 4 = stream-K MMQ with param = workgroups and
+ * `partial` holding the slots followed by the zeroed tile counters): `iters`
+ * launches back to back
  * between one event pair on `stream`; *avg_kernel_ms = pair time / iters,
  * *elapsed_ms = pair time. */
 int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, const void *stage,

@@ -40,7 +40,8 @@
  */
 #include "q4k_common.h"
 
-#define MMQ_XROW 272          /* LDS bytes per staged token row (256 + 16 pad) */
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_cvoid_t;
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
@@ -48,9 +49,13 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 template <int BM>
 struct alignas(16) MmqSmem {
-    alignas(16) int8_t xs[2][BM][MMQ_XROW];  /* int8 quants, one 256-wide K step */
+    /* int8 quants of one 256-wide K step; the 16-byte piece c of token t
+     * sits in column c ^ (t & 15), so 16 consecutive tokens reading the same
+     * piece hit 16 different bank groups */
+    alignas(16) int8_t xs[2][BM][Q4K_QK];
     alignas(16) float d8[2][8][BM];          /* fp16 d8 as float, [sub-block][token] */
     alignas(16) _Float16 s8[2][BM][8];       /* fp16 s8, [token][sub-block] */
+    alignas(16) _Float16 zero8[8];           /* a zero min-term operand */
 };
 
 /* Tile order: consecutive workgroup ids go to consecutive XCDs (8 on
@@ -108,19 +113,25 @@ __device__ __forceinline__ void q4k_scales_f16(v4u hd, h2 sw[4], h2 mw[4]) {
     }
 }
 
-/* TT token tiles (of 32) per wave, WGT x WGN waves (along tokens x rows),
- * two 32-row weight tiles per wave. */
 template <int TT, int WGT, int WGN>
-__global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
-        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
-        const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ partial,
-        int M, int N, int K, int kb_per_split) {
-    static_assert(WGT * WGN == 4, "4 waves per workgroup");
-    constexpr int BMW = 32 * TT;        /* tokens per wave */
-    constexpr int BM = BMW * WGT;       /* tokens per workgroup */
-    constexpr int BN = 64 * WGN;        /* weight rows per workgroup */
-    __shared__ __attribute__((aligned(16))) MmqSmem<BM> sm;
+struct MmqShape {
+    static constexpr int BMW = 32 * TT;     /* tokens per wave */
+    static constexpr int BM = BMW * WGT;    /* tokens per workgroup */
+    static constexpr int BN = 64 * WGN;     /* weight rows per workgroup */
+    static constexpr int NACC = TT * 2 * 16; /* accumulator floats per lane */
+};
 
+/* One output tile (tokens m0.., weight rows n0..) over super-blocks
+ * [kb_begin, kb_end): TT token tiles (of 32) per wave, WGT x WGN waves
+ * (along tokens x rows), two 32-row weight tiles per wave. Starts and ends
+ * with all threads past a barrier, so consecutive calls may restage. */
+template <int TT, int WGT, int WGN>
+__device__ __forceinline__ void mmq_segment(
+        MmqSmem<MmqShape<TT, WGT, WGN>::BM> &sm, const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
+        const uint32_t *__restrict__ xds, int N, int K, int m0, int n0, int kb_begin, int kb_end,
+        v16f (&acc)[TT][2]) {
+    using S = MmqShape<TT, WGT, WGN>;
+    constexpr int BMW = S::BMW, BM = S::BM;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -128,16 +139,7 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
     const int h = lane >> 5;
     const int wt = wave % WGT;
     const int wn = wave / WGT;
-
-    const int ntt = (M + BM - 1) / BM;
-    const int nrt = (N + BN - 1) / BN;
-    const int tile = mmq_tile_of(blockIdx.x, ntt * nrt);
-    const int n0 = (tile / ntt) * BN;
-    const int m0 = (tile % ntt) * BM;
-
     const int nkb_total = K / Q4K_QK;
-    const int kb_begin = blockIdx.y * kb_per_split;
-    const int kb_end = min(nkb_total, kb_begin + kb_per_split);
     const int nkb = kb_end - kb_begin;
 
     /* the two weight rows this lane feeds as B operand (column l32) */
@@ -149,27 +151,27 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
         wbase[nt] = W + (size_t)row * nkb_total * Q4K_BLOCK_BYTES;
     }
 
-    /* --- activation staging: BM tokens x 256 int8, d8 and s8 per step --- */
-    constexpr int XCH = BM * 16 / 256;         /* 16-byte quant chunks per thread */
-    auto load_x = [&](int kb, v4u *xr, v4u &dr) {
+    /* --- activation staging: BM tokens x 256 int8 go global -> LDS directly
+     * (16-byte loads to LDS, one KB per wave-instruction, XOR-swizzled
+     * columns); d8 and s8 go through registers (fp16 -> fp32 for d8) --- */
+    constexpr int XCH = BM * 16 / 256;         /* 16-byte pieces per thread */
+    auto issue_x = [&](int kb, int buf) {
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
-            const int c = tid + 256 * i;
-            const int tok = c >> 4, piece = c & 15;
-            xr[i] = *(const v4u *)(xq + (size_t)(m0 + tok) * K + (size_t)kb * Q4K_QK + 16 * piece);
+            const int inst = wave + 4 * i;        /* wave-instruction index: 64 pieces each */
+            const int c = inst * 64 + lane;       /* LDS piece: token c/16, column c%16 */
+            const int tok = c >> 4, col = c & 15;
+            const int8_t *src = xq + (size_t)(m0 + tok) * K + (size_t)kb * Q4K_QK + 16 * (col ^ (tok & 15));
+            __builtin_amdgcn_global_load_lds((global_cvoid_t *)src, (lds_void_t *)&sm.xs[buf][0][inst * 1024], 16, 0, 0);
         }
+    };
+    auto load_x = [&](int kb, v4u &dr) {
         if (tid < BM * 2) {
             const int tok = tid >> 1, part = tid & 1;
             dr = *(const v4u *)(xds + (size_t)(m0 + tok) * (K / 32) + kb * 8 + 4 * part);
         }
     };
-    auto store_x = [&](int buf, const v4u *xr, const v4u &dr) {
-#pragma unroll
-        for (int i = 0; i < XCH; i++) {
-            const int c = tid + 256 * i;
-            const int tok = c >> 4, piece = c & 15;
-            *(v4u *)&sm.xs[buf][tok][16 * piece] = xr[i];
-        }
+    auto store_x = [&](int buf, const v4u &dr) {
         if (tid < BM * 2) {
             const int tok = tid >> 1, part = tid & 1;
             const uint32_t dw[4] = {dr.x, dr.y, dr.z, dr.w};
@@ -193,7 +195,6 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
         }
     };
 
-    v16f acc[TT][2];
 #pragma unroll
     for (int t = 0; t < TT; t++)
 #pragma unroll
@@ -201,23 +202,28 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[t][nt][r] = 0.0f;
 
-    v4u xr[XCH], dr = {};
+    v4u dr = {};
     v4u hdr[2] = {}, qw[2][4];
 
-    /* The 16 pad bytes of xs[0][0] stay zero: they are the min-term A
-     * operand of the lanes (h = 1) whose k positions carry no sub-block. */
-    if (tid == 0) *(v4u *)&sm.xs[0][0][Q4K_QK] = (v4u){0u, 0u, 0u, 0u};
+    /* zero8 is the min-term A operand of the lanes (h = 1) whose k
+     * positions carry no sub-block */
+    if (tid == 0) *(v4u *)&sm.zero8[0] = (v4u){0u, 0u, 0u, 0u};
     if (nkb > 0) {
-        load_x(kb_begin, xr, dr);
-        store_x(0, xr, dr);
+        issue_x(kb_begin, 0);
+        load_x(kb_begin, dr);
+        store_x(0, dr);
         load_w(kb_begin, hdr, qw);
     }
+    __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads to LDS have landed */
     __syncthreads();
 
     for (int it = 0; it < nkb; it++) {
         const int buf = it & 1;
         const bool more = it + 1 < nkb;
-        if (more) load_x(kb_begin + it + 1, xr, dr);
+        if (more) {
+            issue_x(kb_begin + it + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
+            load_x(kb_begin + it + 1, dr);
+        }
 
         /* per weight tile: fp16(d*sc_b) as fp32 for the epilogue and the
          * min-term B operand fp16(-dmin*m_b), b = 0..7 */
@@ -246,7 +252,7 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
 #pragma unroll
             for (int t = 0; t < TT; t++) {
                 const int tok = BMW * wt + 32 * t + l32;
-                const v4i A = *(const v4i *)&sm.xs[buf][tok][32 * b + 16 * h];
+                const v4i A = *(const v4i *)&sm.xs[buf][tok][16 * ((2 * b + h) ^ (tok & 15))];
                 float d8v[16];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -267,21 +273,29 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
 #pragma unroll
         for (int t = 0; t < TT; t++) {
             const int tok = BMW * wt + 32 * t + l32;
-            const v8h as8 = *(const v8h *)(h ? (const void *)&sm.xs[0][0][Q4K_QK] : (const void *)&sm.s8[buf][tok][0]);
+            const v8h as8 = *(const v8h *)(h ? (const void *)&sm.zero8[0] : (const void *)&sm.s8[buf][tok][0]);
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
                 acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as8, bmin[nt], acc[t][nt], 0, 0, 0);
         }
         if (more) {
             load_w(kb_begin + it + 1, hdr, qw);
-            store_x(buf ^ 1, xr, dr);
+            store_x(buf ^ 1, dr);
         }
+        __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads to LDS have landed */
         __syncthreads();
     }
+}
 
-    /* Store: lane holds weight row n0+64*wn+32*nt+l32 for tokens
-     * m0+BMW*wt+32*t + 8*(r/4) + 4*h + r%4. */
-    float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
+/* Store an output tile: lane holds weight row n0+64*wn+32*nt+l32 for tokens
+ * m0+BMW*wt+32*t + 8*(r/4) + 4*h + r%4. */
+template <int TT, int WGT, int WGN>
+__device__ __forceinline__ void mmq_store(float *__restrict__ out, int M, int N, int m0, int n0,
+                                          const v16f (&acc)[TT][2]) {
+    constexpr int BMW = MmqShape<TT, WGT, WGN>::BMW;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wt = wave % WGT, wn = wave / WGT;
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) {
         const int n = n0 + 64 * wn + 32 * nt + l32;
@@ -293,6 +307,118 @@ __global__ __launch_bounds__(256, 2) void sera_q4k_mmq_kernel(
                 const int m = m0 + BMW * wt + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (m < M) out[(size_t)m * N + n] = acc[t][nt][r];
             }
+    }
+}
+
+/* Grid over (tile, K split); splits > 1 write fp32 partials per split.
+ * WPE: waves per SIMD the register budget is cut for. */
+template <int TT, int WGT, int WGN, int WPE = 2>
+__global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
+        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
+        const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ partial,
+        int M, int N, int K, int kb_per_split) {
+    static_assert(WGT * WGN == 4, "4 waves per workgroup");
+    using S = MmqShape<TT, WGT, WGN>;
+    __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
+    const int ntt = (M + S::BM - 1) / S::BM;
+    const int nrt = (N + S::BN - 1) / S::BN;
+    const int tile = mmq_tile_of(blockIdx.x, ntt * nrt);
+    const int n0 = (tile / ntt) * S::BN;
+    const int m0 = (tile % ntt) * S::BM;
+    const int nkb_total = K / Q4K_QK;
+    const int kb_begin = blockIdx.y * kb_per_split;
+    const int kb_end = min(nkb_total, kb_begin + kb_per_split);
+    v16f acc[TT][2];
+    mmq_segment<TT, WGT, WGN>(sm, W, xq, xds, N, K, m0, n0, kb_begin, kb_end, acc);
+    float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
+    mmq_store<TT, WGT, WGN>(out, M, N, m0, n0, acc);
+}
+
+/* Stream-K schedule: P persistent workgroups split the ntiles x nkb
+ * (tile, super-block) units evenly, so the last round of tiles does not
+ * leave workgroup slots idle. Workgroup w owns units [w*U/P, (w+1)*U/P)
+ * and walks them in order; a tile whose units are not all its own is a
+ * split tile. Each contributor of a split tile writes its accumulators to
+ * its own slot, then bumps the tile's counter; the contributor that brings
+ * the counter to the contributor count sums all slots in contributor order
+ * (deterministic), stores the tile and resets the counter to zero for the
+ * next call. No workgroup ever waits on another. Logical ids are remapped
+ * so each XCD runs a contiguous range of units (the tiles sharing weight
+ * rows meet in one L2). */
+__device__ __forceinline__ int64_t sk_u0(int w, int64_t U, int P) { return (int64_t)w * U / P; }
+__device__ __forceinline__ int sk_owner(int64_t u, int64_t U, int P) { return (int)(((u + 1) * P - 1) / U); }
+
+template <int TT, int WGT, int WGN, int WPE = 2>
+__global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
+        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
+        const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ slots,
+        int *__restrict__ counters, int M, int N, int K) {
+    static_assert(WGT * WGN == 4, "4 waves per workgroup");
+    using S = MmqShape<TT, WGT, WGN>;
+    __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+    const int P = gridDim.x;                       /* multiple of 8 */
+    const int w = (blockIdx.x & 7) * (P >> 3) + (blockIdx.x >> 3);
+    const int ntt = (M + S::BM - 1) / S::BM;
+    const int nrt = (N + S::BN - 1) / S::BN;
+    const int nkb = K / Q4K_QK;
+    const int64_t U = (int64_t)ntt * nrt * nkb;
+    const int64_t myu0 = sk_u0(w, U, P), myu1 = sk_u0(w + 1, U, P);
+
+    for (int64_t u = myu0; u < myu1;) {
+        const int t = (int)(u / nkb);
+        const int kb0 = (int)(u - (int64_t)t * nkb);
+        const int kb1 = (int)min<int64_t>(nkb, kb0 + (myu1 - u));
+        const int m0 = (t % ntt) * S::BM, n0 = (t / ntt) * S::BN;
+        v16f acc[TT][2];
+        mmq_segment<TT, WGT, WGN>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc);
+        if (kb0 == 0 && kb1 == nkb) {
+            mmq_store<TT, WGT, WGN>(y, M, N, m0, n0, acc);
+        } else {
+            /* slot rule: 2c for a contributor c whose range starts inside the
+             * tile, 2c + 1 for one that started before it (then the tile is
+             * its last); each contributor has at most one of each */
+            const int64_t a = (int64_t)t * nkb;
+            const int c0 = sk_owner(a, U, P), c1 = sk_owner(a + nkb - 1, U, P);
+            float *mine = slots + (size_t)(2 * w + (myu0 <= a ? 1 : 0)) * (S::NACC * 256);
+            /* Slot traffic uses device-scope (write-through, cache-bypassing)
+             * stores and loads, so the hand-off needs no cache-wide fence:
+             * each thread's stores have reached the coherence point when its
+             * wait returns, before the counter moves; the last contributor
+             * reads the slots back from that point. */
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        __hip_atomic_store(&mine[(size_t)((tt * 2 + nt) * 16 + r) * 256 + tid], acc[tt][nt][r],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0)
+                s_last = __hip_atomic_fetch_add(&counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c1 - c0;
+            __syncthreads();
+            if (s_last) {
+                if (tid == 0) __hip_atomic_store(&counters[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int c = c0; c <= c1; c++) {
+                    const float *src = slots + (size_t)(2 * c + (sk_u0(c, U, P) <= a ? 1 : 0)) * (S::NACC * 256);
+#pragma unroll
+                    for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                            for (int r = 0; r < 16; r++) {
+                                const float v = __hip_atomic_load(&src[(size_t)((tt * 2 + nt) * 16 + r) * 256 + tid],
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                acc[tt][nt][r] = c == c0 ? v : acc[tt][nt][r] + v;
+                            }
+                }
+                mmq_store<TT, WGT, WGN>(y, M, N, m0, n0, acc);
+            }
+        }
+        u += kb1 - kb0;
     }
 }
 
@@ -319,15 +445,17 @@ extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, 
 }
 
 /* Token-tile width of the workgroup for M tokens: 32 (one token tile per
- * wave, 4 waves along weight rows), 64 (two per wave) or 128 (two per wave,
- * 2 x 2 waves). */
-extern "C" int sera_mmq_bm(int M) {
-    if (M <= 32) return 32;
-    if (M <= 64) return 64;
-    return 128;
-}
+ * wave, 4 waves along weight rows, registers cut for 3 waves per SIMD) or
+ * 64 (two per wave, 2 waves per SIMD); both tiles span 256 weight rows.
+ * Measured on MI355X against 128 x 128 tiles: the 64 x 256 tile under the
+ * stream-K schedule is the fastest at 512 tokens for both the 5120 -> 25600
+ * and the 25600 -> 5120 shapes. */
+extern "C" int sera_mmq_bm(int M) { return M <= 32 ? 32 : 64; }
 
-static int mmq_bn(int bm) { return bm == 128 ? 128 : 256; }
+static int mmq_bn(int bm) { (void)bm; return 256; }
+
+/* Workgroups of the MMQ kernel one CU keeps resident. */
+extern "C" int sera_mmq_wgs_per_cu(int M) { return sera_mmq_bm(M) == 32 ? 3 : 2; }
 
 /* Split-K factor: enough workgroups to give every CU at least two, but
  * never fewer than 2 super-blocks per split. */
@@ -347,7 +475,7 @@ extern "C" int sera_mmq_padded_rows(int M) {
     return (M + bm - 1) / bm * bm;
 }
 
-template <int TT, int WGT, int WGN>
+template <int TT, int WGT, int WGN, int WPE>
 static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
                                  float *partial, int M, int N, int K, int splits, hipStream_t s) {
     constexpr int BM = 32 * TT * WGT, BN = 64 * WGN;
@@ -355,7 +483,7 @@ static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint3
     const int nkb = K / Q4K_QK;
     const int per = (nkb + splits - 1) / splits;
     dim3 grid(tiles, splits);
-    hipLaunchKernelGGL((sera_q4k_mmq_kernel<TT, WGT, WGN>), grid, dim3(256), 0, s, W, xq, xds, y,
+    hipLaunchKernelGGL((sera_q4k_mmq_kernel<TT, WGT, WGN, WPE>), grid, dim3(256), 0, s, W, xq, xds, y,
                        splits > 1 ? partial : nullptr, M, N, K, per);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
@@ -371,9 +499,44 @@ extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, floa
     const int8_t *xq = (const int8_t *)(base + L.qs);
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
-    switch (sera_mmq_bm(M)) {
-        case 32: return launch_mmq_cfg<1, 1, 4>(w, xq, xds, y, partial, M, N, K, splits, s);
-        case 64: return launch_mmq_cfg<2, 1, 4>(w, xq, xds, y, partial, M, N, K, splits, s);
-        default: return launch_mmq_cfg<2, 2, 2>(w, xq, xds, y, partial, M, N, K, splits, s);
-    }
+    if (sera_mmq_bm(M) == 32) return launch_mmq_cfg<1, 1, 4, 3>(w, xq, xds, y, partial, M, N, K, splits, s);
+    return launch_mmq_cfg<2, 1, 4, 2>(w, xq, xds, y, partial, M, N, K, splits, s);
+}
+
+/* ---- stream-K schedule ---------------------------------------------------- */
+
+/* Output tiles of the MMQ grid for M tokens. */
+extern "C" int sera_mmq_tiles(int M, int N) {
+    const int bm = sera_mmq_bm(M);
+    const int bn = mmq_bn(bm);
+    return ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+}
+
+/* Floats of one stream-K partial slot (a whole tile's accumulators). */
+extern "C" int sera_mmq_slot_floats(int M) { return sera_mmq_bm(M) * mmq_bn(sera_mmq_bm(M)); }
+
+template <int TT, int WGT, int WGN, int WPE>
+static hipError_t launch_mmq_streamk_cfg(const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
+                                         float *slots, int *counters, int M, int N, int K, int P,
+                                         hipStream_t s) {
+    hipLaunchKernelGGL((sera_q4k_mmq_streamk_kernel<TT, WGT, WGN, WPE>), dim3(P), dim3(256), 0, s, W, xq, xds, y,
+                       slots, counters, M, N, K);
+    return hipGetLastError();
+}
+
+/* Stream-K MMQ over P persistent workgroups (P a multiple of 8, at most the
+ * workgroups the device keeps resident, and ntiles*K/256 >= P).
+ * slots: 2*P*sera_mmq_slot_floats(M) floats; counters: sera_mmq_tiles(M,N)
+ * ints, zero on entry and zero again on exit. */
+extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots,
+                                                  int *counters, int M, int N, int K, int P, hipStream_t s) {
+    const int Mpad = sera_mmq_padded_rows(M);
+    const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
+    const char *base = (const char *)stage;
+    const int8_t *xq = (const int8_t *)(base + L.qs);
+    const uint32_t *xds = (const uint32_t *)(base + L.ds);
+    const uint8_t *w = (const uint8_t *)W;
+    if (sera_mmq_bm(M) == 32)
+        return launch_mmq_streamk_cfg<1, 1, 4, 3>(w, xq, xds, y, slots, counters, M, N, K, P, s);
+    return launch_mmq_streamk_cfg<2, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, s);
 }

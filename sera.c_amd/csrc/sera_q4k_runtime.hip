@@ -28,6 +28,11 @@ extern "C" int sera_skinny_splits(int M, int N, int K);
 extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
                                              int M, int N, int K, int splits, hipStream_t s);
 extern "C" int sera_mmq_padded_rows(int M);
+extern "C" int sera_mmq_tiles(int M, int N);
+extern "C" int sera_mmq_slot_floats(int M);
+extern "C" int sera_mmq_wgs_per_cu(int M);
+extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots,
+                                                  int *counters, int M, int N, int K, int P, hipStream_t s);
 extern "C" int sera_mmq_bm(int M);
 extern "C" hipError_t sera_launch_q4k_quantize(const float *x, int64_t rows, int64_t K, void *out,
                                                hipStream_t s);
@@ -53,15 +58,30 @@ struct Events {
 };
 
 int g_device = -1;
+int g_cus = 0;                    /* compute units of the device */
 Events g_ev = {};
-unsigned char *g_arena = nullptr;
+unsigned char *g_arena = nullptr; /* stage and partial sums (after the counter region) */
+int *g_counters = nullptr;        /* stream-K tile counters, zero between calls */
 size_t g_arena_bytes = 0;
 
-/* Split-K partial floats never exceed this: the split count stops doubling
- * once tiles*splits >= 512, so tiles*splits < 1024, and every MMQ tile
- * covers at most 128*128 = 64*256 outputs, so splits*M*N < 1024 * 16384. */
+/* The arena starts with the stream-K tile counters (zeroed when the arena
+ * is attached; each call leaves them zero again). */
+constexpr size_t kCounterBytes = (size_t)256 << 10;
+constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(int));
+
+/* Workgroups the stream-K MMQ schedule runs for M tokens: the resident
+ * count, a multiple of 8. */
+int streamk_wgs(int M) { return g_cus > 0 ? sera_mmq_wgs_per_cu(M) * g_cus / 8 * 8 : 0; }
+
+/* Partial-sum floats never exceed this. Split-K: the split count stops
+ * doubling once tiles*splits >= 512, so tiles*splits < 1024, and an MMQ
+ * tile holds at most 64*256 outputs, so splits*M*N < 1024 * 16384.
+ * Stream-K: two tile slots per resident workgroup, at most 2*(2*CUs)*16384
+ * = 4*CUs*16384 (64 x 256 tiles) or 2*(3*CUs)*8192 (32 x 256 tiles). */
 size_t partial_floats_bound(size_t max_tokens, int64_t max_features) {
-    const size_t by_tiles = (size_t)1024 * 16384;
+    size_t by_tiles = (size_t)1024 * 16384;
+    const size_t by_slots = (size_t)4 * (g_cus > 0 ? g_cus : 256) * 16384;
+    if (by_slots > by_tiles) by_tiles = by_slots;
     const size_t by_shape = (size_t)16 * max_tokens * (size_t)(max_features > 0 ? max_features : 0);
     return by_tiles < by_shape ? by_tiles : by_shape;
 }
@@ -94,6 +114,10 @@ extern "C" int sera_q4k_init(int device) {
             return fail(-1, "sera_q4k_init: hipEventCreate failed");
         g_ev.valid = true;
     }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+        return fail(-1, "sera_q4k_init: cannot read the compute-unit count of device %d", device);
+    g_cus = cus;
     g_device = device;
     return 0;
 }
@@ -132,14 +156,17 @@ extern "C" size_t sera_q4k_arena_bytes(size_t max_tokens, int64_t max_features, 
     const size_t mmq = sera_mmq_stage_layout((size_t)sera_mmq_padded_rows(mt), (size_t)max_k).total;
     const size_t stage = row > mmq ? row : mmq;
     const size_t partial = sera_align256(partial_floats_bound(max_tokens, max_features) * sizeof(float));
-    return stage + partial;
+    return kCounterBytes + stage + partial;
 }
 
 extern "C" int sera_q4k_set_arena(void *device_ptr, size_t bytes) {
-    if (!device_ptr || bytes == 0) return fail(-1, "sera_q4k_set_arena: null arena");
+    if (!device_ptr || bytes <= kCounterBytes) return fail(-1, "sera_q4k_set_arena: null or too small arena");
     if (((uintptr_t)device_ptr & 255u) != 0) return fail(-1, "sera_q4k_set_arena: arena must be 256-byte aligned");
-    g_arena = (unsigned char *)device_ptr;
-    g_arena_bytes = bytes;
+    if (hipMemset(device_ptr, 0, kCounterBytes) != hipSuccess)
+        return fail(-1, "sera_q4k_set_arena: clearing the tile counters failed");
+    g_counters = (int *)device_ptr;
+    g_arena = (unsigned char *)device_ptr + kCounterBytes;
+    g_arena_bytes = bytes - kCounterBytes;
     return 0;
 }
 
@@ -203,6 +230,19 @@ extern "C" int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, floa
                ? 0 : fail(-3, "sera_q4k_mmq: launch failed");
 }
 
+namespace {
+/* Stream-K pays when the tile grid needs more than one round of resident
+ * workgroups; it needs its counters and two partial slots per workgroup. */
+bool use_streamk(int M, int N, int K) {
+    const int P = streamk_wgs(M);
+    if (P < 8 || !g_counters) return false;
+    const int tiles = sera_mmq_tiles(M, N);
+    /* between one and four rounds of tiles: beyond that the last round's
+     * idle share is small and plain tiles measured faster */
+    return tiles > P && tiles < 4 * P && tiles <= kMaxCounters && (int64_t)tiles * (K / Q4K_QK) >= P;
+}
+}  // namespace
+
 extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
                               int timed) {
     if (!check_shape("sera_q4k_dense", W, X, Y, M, N, K)) return -1;
@@ -210,24 +250,47 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
     hipStream_t s = (hipStream_t)stream;
     const int Mpad = sera_mmq_padded_rows(M);
     const size_t stage_bytes = sera_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
-    int splits = sera_mmq_splits(M, N, K);
+    const size_t slot_bytes = (size_t)2 * streamk_wgs(M) * sera_mmq_slot_floats(M) * sizeof(float);
+    const bool sk = use_streamk(M, N, K) && stage_bytes + slot_bytes <= g_arena_bytes;
+    int splits = sk ? 1 : sera_mmq_splits(M, N, K);
     if (((size_t)M * N) % 4 != 0) splits = 1;
-    const size_t partial_bytes = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+    const size_t partial_bytes = sk ? slot_bytes : splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
     if (stage_bytes + partial_bytes > g_arena_bytes)
         return fail(-1, "sera_q4k_dense: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
                     g_arena_bytes);
     void *stage = g_arena;
-    float *partial = splits > 1 ? (float *)(g_arena + stage_bytes) : nullptr;
+    float *partial = partial_bytes ? (float *)(g_arena + stage_bytes) : nullptr;
     if (timed) record(g_ev.quant_begin, s);
     if (sera_launch_q8_1_mmq(X, M, Mpad, K, stage, s) != hipSuccess)
         return fail(-2, "sera_q4k_dense: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    if (sera_launch_q4k_mmq(W, stage, Y, partial, M, N, K, splits, s) != hipSuccess)
-        return fail(-3, "sera_q4k_dense: mmq launch failed");
+    const hipError_t e = sk ? sera_launch_q4k_mmq_streamk(W, stage, Y, partial, g_counters, M, N, K, streamk_wgs(M), s)
+                            : sera_launch_q4k_mmq(W, stage, Y, partial, M, N, K, splits, s);
+    if (e != hipSuccess) return fail(-3, "sera_q4k_dense: mmq launch failed");
     if (timed) record(g_ev.kernel_end, s);
     return 0;
 }
+
+extern "C" int sera_q4k_mmq_streamk_wgs(int M) { return M > 0 ? streamk_wgs(M) : 0; }
+
+extern "C" int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
+                                    int M, int N, int K, int wgs, void *stream) {
+    if (!W || !mmq_stage || !Y || !slots || !counters) return fail(-1, "sera_q4k_mmq_streamk: null pointer");
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK)
+        return fail(-1, "sera_q4k_mmq_streamk: bad shape M=%d N=%d K=%d", M, N, K);
+    if (wgs == 0) wgs = streamk_wgs(M);
+    if (wgs < 8 || wgs % 8)
+        return fail(-1, "sera_q4k_mmq_streamk: workgroups=%d must be a positive multiple of 8", wgs);
+    if ((int64_t)sera_mmq_tiles(M, N) * (K / Q4K_QK) < wgs)
+        return fail(-1, "sera_q4k_mmq_streamk: fewer (tile, super-block) units than workgroups=%d", wgs);
+    return sera_launch_q4k_mmq_streamk(W, mmq_stage, Y, slots, counters, M, N, K, wgs, (hipStream_t)stream) ==
+                   hipSuccess
+               ? 0 : fail(-3, "sera_q4k_mmq_streamk: launch failed");
+}
+
+extern "C" int sera_q4k_mmq_tiles(int M, int N) { return M > 0 && N > 0 ? sera_mmq_tiles(M, N) : 0; }
+extern "C" int sera_q4k_mmq_slot_floats(int M) { return M > 0 ? sera_mmq_slot_floats(M) : 0; }
 
 /* Batches from this size up to the MMVQ cap run the few-token MFMA kernel
  * (MMVQ formula) instead of the dot4 MMVQ kernel: on MI355X it is about
@@ -245,6 +308,7 @@ int vec_splits(int M, int N, int K) {
 extern "C" int sera_q4k_kernel_launches(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
     if (M <= SERA_Q4K_MMVQ_MAX_BATCH) return vec_splits(M, N, K) > 1 ? 3 : 2;
+    if (use_streamk(M, N, K)) return 2;
     return sera_mmq_splits(M, N, K) > 1 && ((size_t)M * N) % 4 == 0 ? 3 : 2;
 }
 

@@ -102,6 +102,10 @@ def load():
         "sera_q4k_skinny": ([I, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_skinny_splits": ([I, I, I], I),
         "sera_q4k_kernel_launches": ([I, I, I], I),
+        "sera_q4k_mmq_streamk": ([P, P, P, P, P, I, I, I, I, P], I),
+        "sera_q4k_mmq_streamk_wgs": ([I], I),
+        "sera_q4k_mmq_tiles": ([I, I], I),
+        "sera_q4k_mmq_slot_floats": ([I], I),
         "sera_q4k_dequantize": ([P, SZ, P, P], I),
         "sera_q4k_subblock_dots": ([P, P, P, I, I, I, P], I),
         "sera_q4k_quantize": ([P, I64, I64, P, P], I),
@@ -237,6 +241,13 @@ def mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None):
 
 def mmq_splits(M, N, K):
     return load().sera_q4k_mmq_splits(M, N, K)
+
+
+def mmq_streamk(W, stage, out, M, N, K, slots, counters, wgs=0, stream=None):
+    """MMQ under a stream-K schedule; counters (int32, sera_q4k_mmq_tiles)
+    must be zero and are zero again afterwards."""
+    _check(load().sera_q4k_mmq_streamk(_ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N, K,
+                                       wgs, _stream(stream)), "sera_q4k_mmq_streamk")
 
 
 def skinny(form, W, stage, out, M, N, K, splits=0, partial=None, stream=None):

@@ -251,6 +251,38 @@ def test_mmq_parity(torch, M, N, K):
         check_close(y.cpu().numpy(), ref, f"mmq M={M} N={N} K={K} splits={s}")
 
 
+STREAMK_CASES = [(512, 256, 5120, 8), (512, 256, 5120, 24), (300, 640, 1024, 16), (128, 128, 25600, 8),
+                 (64, 384, 5120, 8), (20, 1000, 2304, 8), (200, 640, 1024, 40)]
+
+
+@pytest.mark.parametrize("M,N,K,wgs", STREAMK_CASES)
+def test_mmq_streamk_parity(torch, M, N, K, wgs):
+    """Stream-K MMQ: split tiles with 2 or more contributors, summed by the
+    last one; results against the MMQ oracle, bit-identical on repeat, and
+    the tile counters back at zero."""
+    rng = np.random.default_rng(M * 13 + N + K + wgs)
+    W = rand_weights(rng, N, K)
+    x = outlier_activations(rng, M, K)
+    Wd = dev(torch, W)
+    stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+    q3q4.quantize_mmq(dev(torch, x), stage)
+    xq, xd, xs = oracle.q8_1_mmq(x)
+    ref = oracle.gemm_mmq(W, xq, xd, xs, N, K)
+    L = q3q4.load()
+    slots = torch.empty(2 * wgs * L.sera_q4k_mmq_slot_floats(M), dtype=torch.float32, device="cuda")
+    counters = torch.zeros(L.sera_q4k_mmq_tiles(M, N), dtype=torch.int32, device="cuda")
+    outs = []
+    for rep in range(2):
+        say(f"case mmq stream-K M={M} N={N} K={K} wgs={wgs} rep={rep}")
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        q3q4.mmq_streamk(Wd, stage, y, M, N, K, slots, counters, wgs=wgs)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+        assert int(counters.abs().sum()) == 0
+    check_close(outs[0], ref, f"mmq stream-K M={M} N={N} K={K} wgs={wgs}")
+    assert np.array_equal(outs[0], outs[1])
+
+
 SKINNY_SHAPES = [(16, 256), (1000, 512), (300, 5120), (64, 25600), (203, 2304)]
 
 
