@@ -194,7 +194,7 @@ def main():
         q3q4.quantize_mmq(x, stage)
         wgs = L.sera_q4k_mmq_streamk_wgs(M)
         tiles = L.sera_q4k_mmq_tiles(M, N)
-        if wgs < tiles < 4 * wgs and tiles * (K // 256) >= wgs:
+        if L.sera_q4k_mmq_schedule(M, N, K) == 1:
             # stream-K schedule: slots, then the zeroed tile counters
             splits = 0
             nslot = 2 * wgs * L.sera_q4k_mmq_slot_floats(M)
@@ -234,7 +234,7 @@ def main():
         lmw, lmarr = weight_set(151936, 5120, 500, 1)
         results["config4_lm_head_m16"] = mmq_case("lm_head", 151936, 5120, 16, lmarr, 1, 20)
         del lmw
-        results["config5_decode_stream"] = decode_stream(torch, q3q4, L, lin, quantized, activations, dev)
+        results["config5_decode_stream"] = decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr)
 
     # ---------------- roofline of the dominant kernel (MMVQ, M=1 gate/up) ---
     row, step_ms, b = headline
@@ -325,46 +325,45 @@ def cpu_baseline(np, torch, w_dev, N, K, x):
             "dequant_ms": round(ta * 1e3, 2), "matmul_ms": round(tb * 1e3, 2)}
 
 
-def decode_stream(torch, q3q4, L, lin, quantized, activations, dev):
+def decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr):
     """Config 5: 64 layers x 7 projections at M=1 plus the LM head, all
-    resident (~18 GB); one token = 449 q3_cuda_q4k_linear calls."""
+    resident (~18 GB); one token = 449 q3_cuda_q4k_linear calls, issued from
+    C (sera_q4k_bench_stream) so no host language sits in the loop."""
     order = ["q", "k", "v", "o", "gate", "up", "down"]
-    layers = []
-    total_w = 0
-    for layer in range(64):
-        ws = {}
-        for name in order:
-            N, K = SHAPES[name]
-            ws[name] = quantized(N, K, 10_000 + layer * 7 + order.index(name))
-            total_w += N * K // 256 * 144
-        layers.append(ws)
-    lm = quantized(151936, 5120, 99_999)
-    total_w += 151936 * 5120 // 256 * 144
+    keep = []
     geos = {n: q3q4.bind_geometry(q3q4.QTYPE_Q4_K, SHAPES[n][1], SHAPES[n][0]) for n in SHAPES}
     xs = {K: activations(1, K, K) for K in (5120, 8192, 25600)}
     ys = {n: torch.empty((1, SHAPES[n][0]), dtype=torch.float32, device=dev) for n in SHAPES}
-
-    def token():
-        for ws in layers:
-            for n in order:
-                lin(geos[n], ws[n], xs[SHAPES[n][1]], ys[n])
-        lin(geos["lm_head"], lm, xs[5120], ys["lm_head"])
-
-    token()
+    calls = []
+    total_w = 0
+    for layer in range(64):
+        for name in order:
+            N, K = SHAPES[name]
+            w = quantized(N, K, 10_000 + layer * 7 + order.index(name))
+            keep.append(w)
+            calls.append((name, w))
+            total_w += N * K // 256 * 144
+    lm = quantized(151936, 5120, 99_999)
+    keep.append(lm)
+    calls.append(("lm_head", lm))
+    total_w += 151936 * 5120 // 256 * 144
+    n = len(calls)
+    g_arr = (ctypes.c_void_p * n)(*[ctypes.addressof(geos[c[0]]) for c in calls])
+    w_arr = (ctypes.c_void_p * n)(*[c[1].data_ptr() for c in calls])
+    x_arr = (ctypes.c_void_p * n)(*[xs[SHAPES[c[0]][1]].data_ptr() for c in calls])
+    m_arr = (ctypes.c_size_t * n)(*([1] * n))
+    y_arr = (ctypes.c_void_p * n)(*[ys[c[0]].data_ptr() for c in calls])
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 5
-    a.record()
-    for _ in range(reps):
-        token()
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / reps
-    del layers, lm
-    return {"ms_per_token": round(ms, 3), "weight_bytes": total_w,
-            "sustained_GBps": round(total_w / (ms * 1e-3) / 1e9, 1),
-            "frac_hbm": round(total_w / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "note": "Python issues the 449 calls; host launch cost is inside the time"}
+    ms = ctypes.c_double()
+    rc = L.sera_q4k_bench_stream(g_arr, w_arr, x_arr, m_arr, y_arr, n, sptr, 2, 10, ctypes.byref(ms))
+    if rc != 0:
+        raise RuntimeError(f"bench_stream rc={rc}: {L.sera_q4k_last_error().decode()}")
+    del keep, lm
+    t = ms.value
+    return {"ms_per_token": round(t, 3), "calls_per_token": n, "weight_bytes": total_w,
+            "sustained_GBps": round(total_w / (t * 1e-3) / 1e9, 1),
+            "frac_hbm": round(total_w / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "449 q3_cuda_q4k_linear calls (Q8_1 quantize + MMVQ each) issued from C, 10 timed tokens"}
 
 
 if __name__ == "__main__":

@@ -117,6 +117,9 @@ int sera_q4k_mmq_splits(int M, int N, int K);
 int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
                          int M, int N, int K, int wgs, void *stream);
 int sera_q4k_mmq_streamk_wgs(int M);   /* resident workgroups for M tokens (after init) */
+/* Schedule sera_q4k_dense picks for this shape (after init): 1 = stream-K,
+ * 0 = plain tiles / split-K (sera_q4k_mmq_splits); -1 for a bad shape. */
+int sera_q4k_mmq_schedule(int M, int N, int K);
 int sera_q4k_mmq_tiles(int M, int N);
 int sera_q4k_mmq_slot_floats(int M);
 
@@ -167,6 +170,13 @@ int sera_q4k_bench_linear(const void *geometry, const void *const *weights, int 
 int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, const void *stage,
                           float *Y, float *partial, int M, int N, int K, int param, void *stream,
                           int warmup, int iters, double *avg_kernel_ms, double *elapsed_ms);
+
+/* `reps` timed passes (after `warmup`) over a sequence of
+ * q3_cuda_q4k_linear calls: geometries[i] (q3_q4_linear_geometry*),
+ * weights[i], xs[i] with Ms[i] rows, ys[i]. *ms_per_rep: one pass. */
+int sera_q4k_bench_stream(const void *const *geometries, const void *const *weights,
+                          const float *const *xs, const size_t *Ms, float *const *ys, int ncalls,
+                          void *stream, int warmup, int reps, double *ms_per_rep);
 
 #ifdef __cplusplus
 }

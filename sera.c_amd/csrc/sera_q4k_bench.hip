@@ -93,3 +93,41 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
     if (elapsed_ms) *elapsed_ms = tot;
     return 0;
 }
+
+/* A sequence of q3_cuda_q4k_linear calls (call i: geometries[i], weights[i],
+ * xs[i] with Ms[i] rows, ys[i]), issued from C back to back, `warmup` times
+ * untimed and `reps` times between one event pair; *ms_per_rep is the pair
+ * time over reps. The decode-stream measurement: a token's 64 x 7
+ * projections and the LM head without a host language in the loop. */
+extern "C" int sera_q4k_bench_stream(const void *const *geometries, const void *const *weights,
+                                     const float *const *xs, const size_t *Ms, float *const *ys, int ncalls,
+                                     void *stream, int warmup, int reps, double *ms_per_rep) {
+    if (!geometries || !weights || !xs || !Ms || !ys || ncalls <= 0 || reps <= 0 || !ms_per_rep) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    char err[256];
+    auto pass = [&]() -> bool {
+        for (int i = 0; i < ncalls; i++)
+            if (!q3_cuda_q4k_linear((const q3_q4_linear_geometry *)geometries[i], weights[i], xs[i], Ms[i], ys[i],
+                                    stream, NULL, err, sizeof(err)))
+                return false;
+        return true;
+    };
+    for (int i = 0; i < warmup; i++)
+        if (!pass()) return -3;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess) return -1;
+    if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return -1; }
+    int rc = 0;
+    (void)hipEventRecord(a, s);
+    for (int i = 0; i < reps && rc == 0; i++)
+        if (!pass()) rc = -3;
+    (void)hipEventRecord(b, s);
+    (void)hipEventSynchronize(b);
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    if (rc) return rc;
+    *ms_per_rep = (double)ms / reps;
+    return 0;
+}

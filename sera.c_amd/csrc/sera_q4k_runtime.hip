@@ -231,16 +231,19 @@ extern "C" int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, floa
 }
 
 namespace {
-/* Stream-K pays when the tile grid needs more than one round of resident
- * workgroups; it needs its counters and two partial slots per workgroup. */
-bool use_streamk(int M, int N, int K) {
+/* The schedule rule, from MI355X measurements over the Qwen3-32B shapes:
+ * stream-K for 64-token tiles when there are at least 64 tiles and fewer
+ * than four rounds of resident workgroups (beyond that the last round's idle
+ * share is small and plain tiles are faster); split-K (or plain tiles) for
+ * 32-token tiles and for grids of a few dozen tiles, where each tile would
+ * be cut into many short pieces. */
+bool streamk_rule(int M, int N, int K) {
     const int P = streamk_wgs(M);
-    if (P < 8 || !g_counters) return false;
+    if (P < 8 || M <= 32) return false;
     const int tiles = sera_mmq_tiles(M, N);
-    /* between one and four rounds of tiles: beyond that the last round's
-     * idle share is small and plain tiles measured faster */
-    return tiles > P && tiles < 4 * P && tiles <= kMaxCounters && (int64_t)tiles * (K / Q4K_QK) >= P;
+    return tiles >= 64 && tiles < 4 * P && tiles <= kMaxCounters && (int64_t)tiles * (K / Q4K_QK) >= P;
 }
+bool use_streamk(int M, int N, int K) { return g_counters && streamk_rule(M, N, K); }
 }  // namespace
 
 extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
@@ -273,6 +276,11 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
 }
 
 extern "C" int sera_q4k_mmq_streamk_wgs(int M) { return M > 0 ? streamk_wgs(M) : 0; }
+
+extern "C" int sera_q4k_mmq_schedule(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return -1;
+    return streamk_rule(M, N, K) ? 1 : 0;
+}
 
 extern "C" int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
                                     int M, int N, int K, int wgs, void *stream) {

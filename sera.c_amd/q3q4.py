@@ -104,6 +104,7 @@ def load():
         "sera_q4k_kernel_launches": ([I, I, I], I),
         "sera_q4k_mmq_streamk": ([P, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_streamk_wgs": ([I], I),
+        "sera_q4k_mmq_schedule": ([I, I, I], I),
         "sera_q4k_mmq_tiles": ([I, I], I),
         "sera_q4k_mmq_slot_floats": ([I], I),
         "sera_q4k_dequantize": ([P, SZ, P, P], I),
@@ -111,6 +112,7 @@ def load():
         "sera_q4k_quantize": ([P, I64, I64, P, P], I),
         "sera_q4k_last_error": ([], CP),
         "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
+        "sera_q4k_bench_stream": ([P, P, P, P, P, I, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_kernel": ([I, P, I, P, P, P, I, I, I, I, P, I, I,
                                    ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], I),
     }
