@@ -173,10 +173,12 @@ int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, co
 
 /* `reps` timed passes (after `warmup`) over a sequence of
  * q3_cuda_q4k_linear calls: geometries[i] (q3_q4_linear_geometry*),
- * weights[i], xs[i] with Ms[i] rows, ys[i]. *ms_per_rep: one pass. */
+ * weights[i], xs[i] with Ms[i] rows, ys[i]. *ms_per_rep: one pass.
+ * use_graph != 0: the pass is captured once into a HIP graph and replayed
+ * (stream must not be the null stream). */
 int sera_q4k_bench_stream(const void *const *geometries, const void *const *weights,
                           const float *const *xs, const size_t *Ms, float *const *ys, int ncalls,
-                          void *stream, int warmup, int reps, double *ms_per_rep);
+                          void *stream, int warmup, int reps, int use_graph, double *ms_per_rep);
 
 #ifdef __cplusplus
 }

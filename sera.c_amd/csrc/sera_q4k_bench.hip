@@ -98,12 +98,15 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
  * xs[i] with Ms[i] rows, ys[i]), issued from C back to back, `warmup` times
  * untimed and `reps` times between one event pair; *ms_per_rep is the pair
  * time over reps. The decode-stream measurement: a token's 64 x 7
- * projections and the LM head without a host language in the loop. */
+ * projections and the LM head without a host language in the loop. With
+ * use_graph != 0 the sequence is captured once into a HIP graph (stream
+ * must not be the null stream) and the graph is replayed instead. */
 extern "C" int sera_q4k_bench_stream(const void *const *geometries, const void *const *weights,
                                      const float *const *xs, const size_t *Ms, float *const *ys, int ncalls,
-                                     void *stream, int warmup, int reps, double *ms_per_rep) {
+                                     void *stream, int warmup, int reps, int use_graph, double *ms_per_rep) {
     if (!geometries || !weights || !xs || !Ms || !ys || ncalls <= 0 || reps <= 0 || !ms_per_rep) return -1;
     hipStream_t s = (hipStream_t)stream;
+    if (use_graph && !s) return -1;
     char err[256];
     auto pass = [&]() -> bool {
         for (int i = 0; i < ncalls; i++)
@@ -112,22 +115,36 @@ extern "C" int sera_q4k_bench_stream(const void *const *geometries, const void *
                 return false;
         return true;
     };
-    for (int i = 0; i < warmup; i++)
-        if (!pass()) return -3;
-    hipEvent_t a, b;
-    if (hipEventCreate(&a) != hipSuccess) return -1;
-    if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return -1; }
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (use_graph) {
+        if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return -1;
+        const bool ok = pass();
+        if (hipStreamEndCapture(s, &graph) != hipSuccess || !ok) return -3;
+        if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            return -3;
+        }
+    }
+    auto run = [&]() -> bool { return use_graph ? hipGraphLaunch(exec, s) == hipSuccess : pass(); };
     int rc = 0;
-    (void)hipEventRecord(a, s);
-    for (int i = 0; i < reps && rc == 0; i++)
-        if (!pass()) rc = -3;
-    (void)hipEventRecord(b, s);
-    (void)hipEventSynchronize(b);
-    float ms = 0.0f;
-    (void)hipEventElapsedTime(&ms, a, b);
-    (void)hipEventDestroy(a);
-    (void)hipEventDestroy(b);
-    if (rc) return rc;
-    *ms_per_rep = (double)ms / reps;
-    return 0;
+    for (int i = 0; i < warmup && rc == 0; i++)
+        if (!run()) rc = -3;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (rc == 0 && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)) rc = -1;
+    if (rc == 0) {
+        (void)hipEventRecord(a, s);
+        for (int i = 0; i < reps && rc == 0; i++)
+            if (!run()) rc = -3;
+        (void)hipEventRecord(b, s);
+        (void)hipEventSynchronize(b);
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, a, b);
+        *ms_per_rep = (double)ms / reps;
+    }
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
 }

@@ -112,7 +112,7 @@ def load():
         "sera_q4k_quantize": ([P, I64, I64, P, P], I),
         "sera_q4k_last_error": ([], CP),
         "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
-        "sera_q4k_bench_stream": ([P, P, P, P, P, I, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
+        "sera_q4k_bench_stream": ([P, P, P, P, P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_kernel": ([I, P, I, P, P, P, I, I, I, I, P, I, I,
                                    ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], I),
     }
