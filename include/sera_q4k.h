@@ -151,6 +151,59 @@ int sera_q4k_quantize(const float *X, int64_t rows, int64_t K, void *out, void *
 
 const char *sera_q4k_last_error(void);
 
+/* ---- Q6_K weights (GGUF type 14): N rows of K/256 blocks of 210 bytes ---
+ * Block: ql[128] low nibbles, qh[64] high 2 bits, sc[16] int8 scales of
+ * 16-wide groups, fp16 d (cuda/mmq/ggml-common.h:348-357, src/q3_quant.c:78-103).
+ * Rows are 2-byte aligned only; W itself must be 16-byte aligned and
+ * readable up to the next 16-byte boundary past its last byte (any hipMalloc
+ * allocation is). */
+
+/* Y = X . W^T through the MMVQ path, 1 <= M <= 8, on the row-layout Q8_1
+ * stage (the reference quantizes Q6_K decode activations with the same
+ * quantize_row_q8_1_cuda call as Q4_K). Replaces q3_mmq_q6_K_dense_vec
+ * (cuda/q3_mmq.cu:515-519 over q3_mmq_dense_vec_impl, :408-506). */
+int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
+                       void *stream, int timed);
+
+/* Same contract through the MMQ path, any M >= 1 (the ABI uses it for
+ * M > 8). Replaces q3_mmq_q6_K_dense (cuda/q3_mmq.cu:388-393 over
+ * q3_mmq_dense_impl, :258-379). Activations go through the D4 MMQ quantizer
+ * (fp32 scale per 32 values, cuda/mmq/quantize.cu:271-367,
+ * mmq.cuh:64-103). */
+int sera_q6k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
+                   void *stream, int timed);
+
+/* Kernel launches one sera_q6k_dense / sera_q6k_dense_vec call makes. */
+int sera_q6k_kernel_launches(int M, int N, int K);
+
+/* MMVQ kernel on a row stage (mul_mat_vec_q<Q6_K>, cuda/mmq/mmvq.cu:907-911,
+ * with vec_dot_q6_K_q8_1, cuda/mmq/vecdotq.cuh:624-643,956-980):
+ * y = sum_blk d * sum_g d8[g/2] * (I_g * sc_g), I_g the exact int dot of a
+ * 16-wide group. rows_per_wave in {1, 2, 4} (4 only for M <= 4), or 0 for
+ * the built-in choice (sera_q6k_mmvq_rows_per_wave). */
+int sera_q6k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
+                  int rows_per_wave, void *stream);
+int sera_q6k_mmvq_rows_per_wave(int M, int N);
+
+/* Q6_K MMQ activation stage (D4 quantizer of cuda/mmq/quantize.cu:271-367
+ * with the layout mmq_get_q8_1_ds_layout selects for Q6_K,
+ * cuda/mmq/mmq.cuh:64-103): quants as fp16 [Mpad][K] (exact integers), fp32
+ * d = 1/d_inv as [K/256][8][Mpad]; rows M..Mpad-1 zero, Mpad a multiple of
+ * 64. */
+int sera_q8_1_q6k_mmq_padded_rows(int M);
+size_t sera_q8_1_q6k_mmq_stage_bytes(int M, int K);
+void sera_q8_1_q6k_mmq_stage_offsets(int M, int K, size_t *qs, size_t *d);
+int sera_q8_1_quantize_mmq_d4(const float *X, int M, int K, void *stage, void *stream);
+
+/* MMQ kernel on a Q6_K MMQ stage (mul_mat_q<Q6_K>, cuda/mmq/mmq.cuh:3570-3575
+ * with load_tiles_q6_K :2512-2596 and vec_dot_q6_K_q8_1_mma :2634-2786):
+ * y = sum_blk d * sum_b d8_b * (sc_2b*I_2b + sc_2b+1*I_2b+1). splits > 1
+ * splits K (partial: splits*M*N floats, M*N % 4 == 0); 0 = built-in choice
+ * (sera_q6k_mmq_splits_for). */
+int sera_q6k_mmq(const void *W, const void *q6k_mmq_stage, float *Y, float *partial, int M, int N, int K,
+                 int splits, void *stream);
+int sera_q6k_mmq_splits_for(int M, int N, int K);
+
 /* ---- bench loops (the role of src/q3_bench_q4_linear.cu:181-226) ------- */
 
 /* `warmup` untimed and `iters` timed q3_cuda_q4k_linear calls on weight

@@ -53,6 +53,12 @@ def lib():
             ("orc_gemm_mmvq", [P, P, P, I64, I64, I64, P], None),
             ("orc_gemm_mmq", [P, P, P, P, I64, I64, I64, P], None),
             ("orc_gemm_dequant", [P, P, I64, I64, I64, P], None),
+            ("orc_q6k_unpack", [P, P, P, P], None),
+            ("orc_dequant_q6k", [P, SZ, P], None),
+            ("orc_q8_1_mmq_d4", [P, I64, P, P], None),
+            ("orc_q6k_group_dots", [P, P, I64, I64, I64, P], None),
+            ("orc_gemm_q6k", [P, P, P, I64, I64, I64, P], None),
+            ("orc_gemm_dequant_q6k", [P, P, I64, I64, I64, P], None),
         ]:
             fn = getattr(L, name)
             fn.argtypes = args
@@ -116,15 +122,16 @@ def dequant(W, N, K):
     return out
 
 
-def ref_dequant(W, N, K):
-    """Dequant through the reference's compiled q3_quant.c (None if absent)."""
+def ref_dequant(W, N, K, qtype=12):
+    """Dequant through the reference's compiled q3_quant.c (None if absent);
+    qtype 12 = Q4_K, 14 = Q6_K."""
     R = ref_lib()
     if R is None:
         return None
     W = np.ascontiguousarray(W, dtype=np.uint8)
     out = np.empty((N, K), np.float32)
     err = ctypes.create_string_buffer(256)
-    ok = R.q3_quant_dequantize_row(12, _p(W), N * (K // 256), _p(out), N * K, err, 256)
+    ok = R.q3_quant_dequantize_row(qtype, _p(W), N * (K // 256), _p(out), N * K, err, 256)
     assert ok, err.value
     return out
 
@@ -211,3 +218,93 @@ def linear_reference(W, X, N, K):
         return gemm_mmvq(W, xq, xd, N, K)
     xq, xd, xs = q8_1_mmq(X)
     return gemm_mmq(W, xq, xd, xs, N, K)
+
+
+# ---------------------------------------------------------------------------
+# Q6_K (210-byte blocks; layouts: W uint8 [N, K/256*210])
+# ---------------------------------------------------------------------------
+
+Q6K_BYTES = 210
+
+
+def q6k_blocks(rng, nblocks, d_scale=2.0e-5, scales=None):
+    """Synthetic Q6_K blocks: uniform ql/qh bytes, int8 group scales uniform
+    in [-128, 127] (or the given array), fp16 d of magnitude ~d_scale with a
+    random sign. Any such bytes are a valid Q6_K block (the reference repo
+    ships no Q6_K quantizer)."""
+    b = rng.integers(0, 256, (nblocks, Q6K_BYTES), dtype=np.uint8)
+    if scales is not None:
+        b[:, 192:208] = np.asarray(scales, np.int8).view(np.uint8)
+    d = (rng.uniform(0.5, 1.5, nblocks) * d_scale * rng.choice([-1.0, 1.0], nblocks)).astype(np.float16)
+    b[:, 208:210] = d.view(np.uint8).reshape(nblocks, 2)
+    return b
+
+
+def q6k_weights(rng, N, K, **kw):
+    return q6k_blocks(rng, N * (K // 256), **kw).reshape(N, K // 256 * Q6K_BYTES)
+
+
+def q6k_unpack(block):
+    """(q - 32 as int8 [256], int8 scales [16], d as float32) of one block."""
+    block = np.ascontiguousarray(block, dtype=np.uint8)
+    q = np.empty(256, np.int8)
+    sc = np.empty(16, np.int8)
+    d = ctypes.c_float()
+    lib().orc_q6k_unpack(_p(block), _p(q), _p(sc), ctypes.byref(d))
+    return q, sc, np.float32(d.value)
+
+
+def dequant_q6k(W, N, K):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    assert W.size == N * (K // 256) * Q6K_BYTES
+    out = np.empty((N, K), np.float32)
+    lib().orc_dequant_q6k(_p(W), N * (K // 256), _p(out))
+    return out
+
+
+def q8_1_mmq_d4(X):
+    """MMQ D4 activation quantizer (Q6_K): int8 quants and fp32 d [M, K/32]."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    M, K = X.shape
+    xq = np.empty((M, K), np.int8)
+    d = np.empty((M, K // 32), np.float32)
+    for m in range(M):
+        lib().orc_q8_1_mmq_d4(_p(X[m]), K, _p(xq[m]), _p(d[m]))
+    return xq, d
+
+
+def q6k_group_dots(W, xq, N, K):
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    M = xq.shape[0]
+    out = np.empty((M, N, K // 16), np.int32)
+    lib().orc_q6k_group_dots(_p(np.ascontiguousarray(W)), _p(xq), M, N, K, _p(out))
+    return out
+
+
+def gemm_q6k(W, xq, d8, N, K):
+    """y = sum_blk d * sum_g sc_g * d8[g/2] * I_g (double); d8 float [M, K/32]."""
+    M = xq.shape[0]
+    Y = np.empty((M, N), np.float64)
+    lib().orc_gemm_q6k(_p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(xq)),
+                       _p(np.ascontiguousarray(d8, dtype=np.float32)), M, N, K, _p(Y))
+    return Y
+
+
+def gemm_dequant_q6k(W, X, N, K):
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    M = X.shape[0]
+    Y = np.empty((M, N), np.float64)
+    lib().orc_gemm_dequant_q6k(_p(np.ascontiguousarray(W)), _p(X), M, N, K, _p(Y))
+    return Y
+
+
+def linear_reference_q6k(W, X, N, K):
+    """Output the reference path produces for Q6_K weights: row Q8_1 with
+    fp16 d8 when M <= 8 (MMVQ), D4 Q8_1 with fp32 d8 otherwise (MMQ)
+    (src/q3_q4_linear.cu:198-210, cuda/q3_mmq.cu:303-316,408-470)."""
+    M = X.shape[0]
+    if M <= 8:
+        xq, xd, _ = q8_1_row(X)
+        return gemm_q6k(W, xq, h2f(xd), N, K)
+    xq, d = q8_1_mmq_d4(X)
+    return gemm_q6k(W, xq, d, N, K)

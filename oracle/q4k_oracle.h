@@ -1,5 +1,5 @@
 /*
- * q4k_oracle.h - CPU oracle for the Q4_K quantized-linear path.
+ * q4k_oracle.h - CPU oracle for the Q4_K / Q6_K quantized-linear path.
  *
  * TEST INFRASTRUCTURE ONLY. This library is the checker that the HIP path is
  * compared against; nothing in the product (sera.c_amd/, include/) links,
@@ -22,6 +22,10 @@
  *   MMVQ output formula ...... cuda/mmq/vecdotq.cuh:505-527,864-908
  *   MMQ output formula ....... cuda/mmq/mmq.cuh:2269-2283,1440-1472
  *   dequant x fp32 GEMM ...... tests/test_q3_q4_linear.cu:236-277
+ *   Q6_K block + dequant ..... src/q3_quant.c:78-103 (q6k_oracle.c)
+ *   Q8_1 MMQ D4 quantizer .... cuda/mmq/quantize.cu:271-367 (Q6_K MMQ)
+ *   Q6_K output formula ...... cuda/mmq/vecdotq.cuh:624-643,956-980 (MMVQ),
+ *                              cuda/mmq/mmq.cuh:2687-2786 (MMQ)
  *
  * Pinning status of every function is listed in the comment above it and in
  * tests/test_oracle.py, which holds the checks.
@@ -109,6 +113,34 @@ void orc_gemm_mmq(const uint8_t *W, const int8_t *xq, const uint16_t *xd,
  * double accumulation (tests/test_q3_q4_linear.cu:236-277). */
 void orc_gemm_dequant(const uint8_t *W, const float *X, int64_t M, int64_t N,
                       int64_t K, double *Y);
+
+/* ---- Q6_K (q6k_oracle.c): W is uint8 [N][K/256][210] GGUF Q6_K ---- */
+#define ORC_Q6K_BYTES 210
+
+/* One block -> q[256] = quant - 32, sc[16] int8 group scales, d fp32.
+ * src/q3_quant.c:78-103. */
+void orc_q6k_unpack(const uint8_t *blk, int8_t *q, int8_t *sc, float *d);
+
+/* Q6_K dequant, (d*sc)*q in fp32 (src/q3_quant.c:78-103). */
+void orc_dequant_q6k(const uint8_t *blocks, size_t nblocks, float *out);
+
+/* Q8_1 MMQ quantizer, D4 layout (the one the reference uses for Q6_K):
+ * quants as orc_q8_1_mmq, fp32 scale d = 1/d_inv per 32 values, no sum.
+ * cuda/mmq/quantize.cu:271-367, cuda/mmq/mmq.cuh:64-103. */
+void orc_q8_1_mmq_d4(const float *x, int64_t K, int8_t *qs, float *d);
+
+/* Exact per-16 dots I[m][n][g] = sum (q-32)*q8 over group g (K/16 per row). */
+void orc_q6k_group_dots(const uint8_t *W, const int8_t *xq, int64_t M, int64_t N, int64_t K,
+                        int32_t *I);
+
+/* y = sum_blk d * sum_g sc_g * d8[g/2] * I_g in double, d8 floats [M][K/32]
+ * (fp16 row-quantizer scales for MMVQ, fp32 D4 scales for MMQ). */
+void orc_gemm_q6k(const uint8_t *W, const int8_t *xq, const float *d8, int64_t M, int64_t N,
+                  int64_t K, double *Y);
+
+/* Dequantized Q6_K W (fp32) x fp32 X, double accumulation. */
+void orc_gemm_dequant_q6k(const uint8_t *W, const float *X, int64_t M, int64_t N, int64_t K,
+                          double *Y);
 
 #ifdef __cplusplus
 }

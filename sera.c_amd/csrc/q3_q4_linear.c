@@ -128,10 +128,11 @@ bool q3_cuda_q4k_linear(const q3_q4_linear_geometry *geometry, const void *weigh
         set_error(error, error_len, "q3_q4_linear: unresolved geometry");
         return false;
     }
-    if (geometry->qtype != QTYPE_Q4_K) {
-        set_error(error, error_len, "q3_q4_linear: only Q4_K weights are implemented in this build");
+    if (geometry->qtype != QTYPE_Q4_K && geometry->qtype != QTYPE_Q6_K) {
+        set_error(error, error_len, "q3_q4_linear: tensor qtype is not Q4_K/Q6_K");
         return false;
     }
+    const bool q6 = geometry->qtype == QTYPE_Q6_K;
 
     q3_q4_linear_stats local;
     q3_q4_linear_stats *s = stats ? stats : &local;
@@ -146,14 +147,18 @@ bool q3_cuda_q4k_linear(const q3_q4_linear_geometry *geometry, const void *weigh
 
     int rc;
     if (tokens <= SERA_Q4K_MMVQ_MAX_BATCH) {
-        rc = sera_q4k_dense_vec(weight, device_input, device_output, tokens, features, K, stream,
-                                stats != NULL);
-        s->kernel_launches = (uint64_t)sera_q4k_kernel_launches(tokens, features, K);
+        rc = q6 ? sera_q6k_dense_vec(weight, device_input, device_output, tokens, features, K, stream,
+                                     stats != NULL)
+                : sera_q4k_dense_vec(weight, device_input, device_output, tokens, features, K, stream,
+                                     stats != NULL);
     } else {
-        rc = sera_q4k_dense(weight, device_input, device_output, tokens, features, K, stream,
-                            stats != NULL);
-        s->kernel_launches = (uint64_t)sera_q4k_kernel_launches(tokens, features, K);
+        rc = q6 ? sera_q6k_dense(weight, device_input, device_output, tokens, features, K, stream,
+                                 stats != NULL)
+                : sera_q4k_dense(weight, device_input, device_output, tokens, features, K, stream,
+                                 stats != NULL);
     }
+    s->kernel_launches = (uint64_t)(q6 ? sera_q6k_kernel_launches(tokens, features, K)
+                                       : sera_q4k_kernel_launches(tokens, features, K));
     if (rc != 0) {
         char buffer[400];
         snprintf(buffer, sizeof(buffer), "q3_q4_linear: %s path failed (rc=%d) for M=%d N=%d K=%d: %s",

@@ -18,6 +18,9 @@
  *                                               S = sum of the 32 int8 quants
  *   mmq stage (MMQ):   qs  int8   [Mpad][K]
  *                      ds  half2  [Mpad][K/32]
+ *   Q6_K mmq stage:    qs  fp16   [Mpad][K]          (the int8 quants, exact)
+ *                      ds  float  [K/256][8][Mpad]   (fp32 D4 scale d, per
+ *                                  256-wide K step, sub-block, token)
  */
 #ifndef SERA_Q4K_COMMON_H
 #define SERA_Q4K_COMMON_H
@@ -57,6 +60,18 @@ static inline sera_stage_layout sera_mmq_stage_layout(size_t rows_padded, size_t
     L.total = sera_align256(L.ds + rows_padded * (K / 32) * 4);
     return L;
 }
+
+/* Q6_K MMQ stage: Mpad is a multiple of 64. */
+static inline sera_stage_layout sera_q6k_mmq_stage_layout(size_t rows_padded, size_t K) {
+    sera_stage_layout L;
+    L.qs = 0;
+    L.ds = sera_align256(rows_padded * K * 2);
+    L.dsf = 0;
+    L.total = sera_align256(L.ds + rows_padded * (K / 32) * 4);
+    return L;
+}
+
+static inline int sera_q6k_mmq_padded_rows(int M) { return (M + 63) / 64 * 64; }
 
 #ifdef __HIPCC__
 typedef _Float16 f16;

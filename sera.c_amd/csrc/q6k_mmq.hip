@@ -1,0 +1,327 @@
+/*
+ * q6k_mmq.hip - Q6_K x Q8_1 tiled GEMM on CDNA4 fp16 MFMA (prefill, M > 8).
+ *
+ * Arithmetic of the reference MMQ for Q6_K (tensor-core branch of
+ * vec_dot_q6_K_q8_1_mma, cuda/mmq/mmq.cuh:2687-2786, tiles from
+ * load_tiles_q6_K :2512-2596, D4 activations): per 32-wide sub-block b of a
+ * super-block with its two 16-wide groups,
+ *   J_b = sc_2b * I_2b + sc_2b+1 * I_2b+1       (exact integer, :2775)
+ *   y   = sum_blk d * sum_b d8_b * J_b           (fp32 d8, d per block, :2784)
+ * where I_g = sum (q - 32) * q8 over group g.
+ *
+ * gfx950 mapping. The int8 group scales change every 16 weights, so an int8
+ * MFMA result would need two scale multiplies, a convert and an FMA per
+ * element and sub-block on the VALU. Instead the scales go into the weight
+ * operand, exactly: with sc = 16*sh + sl (sh in [-8, 7], sl in [0, 15]),
+ * (q-32)*sl and 16*(q-32)*sh are integers of at most 13 significant bits,
+ * exact in fp16, and the int8 activation quants are exact in fp16 too. Two
+ * v_mfma_f32_32x32x16_f16 per 16 K (one per part) accumulate
+ * sum q8 * (q-32) * sc, every product and partial sum an integer below 2^24,
+ * so the fp32 result IS the integer J_b, bit for bit. The epilogue is then
+ * one FMA per element and sub-block (J_b * d8_b), plus one per block (d).
+ *   - weights are the B operand: lane = weight row (MFMA column), so d and
+ *     the group scales are per-lane values. A lane of half h takes, for
+ *     sub-block (j, q), weights l = 16h + [0, 16) of the quarter: one 16-wide
+ *     group, one scale. Its bytes (4 ql runs, 2 qh runs, the 16 scales and d
+ *     of the block) are loaded straight from HBM with dword-aligned buffer
+ *     loads and funnel-shifted into place (rows are only 2-byte aligned),
+ *     one block ahead of use. The raw quant bytes become fp16 (1024 + q) by
+ *     v_perm under exponent byte 0x64, and one packed fp16 FMA per pair
+ *     gives (q-32)*s.
+ *   - activations (fp16 quants, fp32 d8) for the workgroup's tokens go
+ *     global -> LDS directly (16-byte loads to LDS, 1 KB per wave
+ *     instruction), double buffered per 256-wide K step; 16-byte chunk c of
+ *     token t sits in column c ^ (t & 31) so a half-wave's 32 tokens reading
+ *     one chunk hit distinct banks. The quantizer writes d8 transposed per K
+ *     step so it lands in LDS as [sub-block][token].
+ *   - tile: 32*TT tokens x 128 weight rows per workgroup, 4 waves along the
+ *     rows; split-K with a fixed-order reduce when tiles are few.
+ */
+#include "q4k_common.h"
+
+typedef __attribute__((address_space(3))) void q6m_lds_void;
+typedef __attribute__((address_space(1))) const void q6m_global_cvoid;
+typedef _Float16 q6h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 q6v8h __attribute__((ext_vector_type(8)));
+typedef uint32_t q6v4u __attribute__((ext_vector_type(4)));
+typedef float q6v4f __attribute__((ext_vector_type(4)));
+
+#define Q6K_BLOCK_BYTES 210
+#define Q6M_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
+#define Q6M_BN 128
+
+template <int BM>
+struct alignas(16) Q6MmqSmem {
+    alignas(16) _Float16 xs[2][BM][Q4K_QK];
+    alignas(16) float d8[2][8][BM];
+};
+
+namespace {
+
+/* Consecutive workgroup ids go to consecutive XCDs (8 on MI355X); give each
+ * XCD a contiguous run of tiles, token tiles fastest, so workgroups on one
+ * XCD share weight rows in its L2. */
+__device__ __forceinline__ int q6m_tile_of(int wg, int ntiles) {
+    const int nx = 8;
+    const int full = (ntiles / nx) * nx;
+    if (wg >= full) return wg;
+    const int per = ntiles / nx;
+    return (wg % nx) * per + wg / nx;
+}
+
+__device__ __forceinline__ q6h2 q6m_h2(uint32_t u) { return __builtin_bit_cast(q6h2, u); }
+
+/* 16 bytes that start `sh` bits into the 5 dwords (a.x .. a.w, b) */
+__device__ __forceinline__ q6v4u q6m_align16(q6v4u a, uint32_t b, uint32_t sh) {
+    q6v4u r;
+    r.x = __builtin_amdgcn_alignbit(a.y, a.x, sh);
+    r.y = __builtin_amdgcn_alignbit(a.z, a.y, sh);
+    r.z = __builtin_amdgcn_alignbit(a.w, a.z, sh);
+    r.w = __builtin_amdgcn_alignbit(b, a.w, sh);
+    return r;
+}
+
+/* raw 6-bit quants of quarter Q (bits 2Q..2Q+1 of qh, low nibble of ql for
+ * Q < 2, high nibble for Q >= 2), four per dword (src/q3_quant.c:88-95) */
+template <int Q>
+__device__ __forceinline__ uint32_t q6m_raw(uint32_t ql, uint32_t qh) {
+    const uint32_t nib = (Q >= 2 ? (ql >> 4) : ql) & 0x0F0F0F0Fu;
+    const uint32_t hi = Q == 0 ? (qh << 4) : Q == 1 ? (qh << 2) : Q == 2 ? qh : (qh >> 2);
+    return nib | (hi & 0x30303030u);
+}
+
+__device__ __forceinline__ int q6m_sext8(uint32_t w, int sh) { return (int)(w << (24 - sh)) >> 24; }
+
+struct Q6WRaw {
+    q6v4u a[7];
+    uint32_t b[7];
+};
+
+}  // namespace
+
+/* Grid (tiles, K splits); splits > 1 write fp32 partials per split. */
+template <int TT, int WPE>
+__global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
+        const uint8_t *__restrict__ W, uint64_t wbytes, const _Float16 *__restrict__ xh,
+        const float *__restrict__ d8t, float *__restrict__ y, float *__restrict__ partial, int M, int Mpad,
+        int N, int K, int kb_per_split) {
+    constexpr int BM = 32 * TT;
+    __shared__ __attribute__((aligned(16))) Q6MmqSmem<BM> sm;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int ntt = Mpad / BM, nrt = (N + Q6M_BN - 1) / Q6M_BN;
+    const int tile = q6m_tile_of(blockIdx.x, ntt * nrt);
+    const int n0 = (tile / ntt) * Q6M_BN, m0 = (tile % ntt) * BM;
+    const int nb = K / Q4K_QK;
+    const int kb0 = blockIdx.y * kb_per_split, kb1 = min(nb, kb0 + kb_per_split);
+    const uint32_t rb = (uint32_t)nb * Q6K_BLOCK_BYTES;
+
+    /* weights: resource from the tile's first row (16-byte aligned down) to
+     * the end of the matrix, rounded up to 16 bytes (a dword that straddles
+     * the end must not read as zero); the lane's row, clamped (rows >= N are
+     * never stored) */
+    const uint64_t gbase = ((uint64_t)n0 * rb) & ~(uint64_t)15;
+    const uint64_t rem = ((wbytes - gbase) + 15) & ~(uint64_t)15;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(W + gbase), (short)0, (int)(rem > 0x7fffffffu ? 0x7fffffffu : rem), Q6M_RSRC_FLAGS);
+    const int n = min(n0 + 32 * wave + l32, N - 1);
+    const uint32_t rowoff = (uint32_t)((uint64_t)n * rb - gbase);
+
+    /* the lane's runs of a block: ql[64j + 32p + 16h + 0..15] (j, p = 0, 1),
+     * qh[32j + 16h + 0..15], and bytes 192..209 (scales, d) */
+    auto load_w = [&](int kb, Q6WRaw &w) {
+        const uint32_t o = rowoff + (uint32_t)kb * Q6K_BLOCK_BYTES;
+        const uint32_t X[7] = {16u * h, 32u + 16u * h, 64u + 16u * h, 96u + 16u * h, 128u + 16u * h,
+                               160u + 16u * h, 192u};
+#pragma unroll
+        for (int i = 0; i < 7; i++) {
+            const uint32_t a4 = (o + X[i]) & ~3u;
+            w.a[i] = __builtin_bit_cast(q6v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, a4, 0, 0));
+            w.b[i] = __builtin_amdgcn_raw_buffer_load_b32(rw, a4 + 16, 0, 0);
+        }
+    };
+
+    /* activations of K step kb: BM tokens x 256 fp16 and 8 x BM fp32 d8 */
+    auto issue_x = [&](int kb, int buf) {
+#pragma unroll
+        for (int i = 0; i < BM / 8; i++) {
+            const int inst = wave + 4 * i;          /* 1 KB = two tokens */
+            const int tok = 2 * inst + (lane >> 5), col = lane & 31;
+            const _Float16 *src = xh + (size_t)(m0 + tok) * K + (size_t)kb * Q4K_QK + 8 * (col ^ (tok & 31));
+            __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src, (q6m_lds_void *)&sm.xs[buf][2 * inst][0], 16,
+                                             0, 0);
+        }
+        if (wave < BM / 32) {
+            const int f = wave * 256 + lane * 4;    /* float index in [8][BM] */
+            const int b = f / BM, t = f % BM;
+            const float *src = d8t + ((size_t)kb * 8 + b) * Mpad + m0 + t;
+            __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src, (q6m_lds_void *)&sm.d8[buf][0][wave * 256],
+                                             16, 0, 0);
+        }
+    };
+
+    v16f acc[TT], tmp[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            acc[t][r] = 0.0f;
+            tmp[t][r] = 0.0f;
+        }
+
+    auto step = [&](int kb, int buf, const Q6WRaw &wc, Q6WRaw &wn) {
+        if (kb + 1 < kb1) {
+            issue_x(kb + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
+            load_w(kb + 1, wn);
+        }
+        const uint32_t sh = ((rowoff + (uint32_t)kb * Q6K_BLOCK_BYTES) & 2u) * 8u;
+        q6v4u QL[4], QH[2];
+#pragma unroll
+        for (int i = 0; i < 4; i++) QL[i] = q6m_align16(wc.a[i], wc.b[i], sh);
+#pragma unroll
+        for (int i = 0; i < 2; i++) QH[i] = q6m_align16(wc.a[4 + i], wc.b[4 + i], sh);
+        const q6v4u SC = q6m_align16(wc.a[6], wc.b[6], sh);
+        const float d = h2f_bits((wc.b[6] >> sh) & 0xffffu);
+
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                /* the lane's group 8j + 2q + h: scale byte of the 16 */
+                const uint32_t scw = SC[2 * j + (q >> 1)];
+                const int sc = q6m_sext8(scw, 8 * (2 * (q & 1) + h));
+                const int shi = sc >> 4, slo = sc & 15;        /* sc = 16*shi + slo */
+                const _Float16 fh = (_Float16)shi, fl = (_Float16)slo;
+                const _Float16 ch = (_Float16)(-1056 * shi), cl = (_Float16)(-1056 * slo);
+                const q6h2 s_hi = {fh, fh}, s_lo = {fl, fl}, c_hi = {ch, ch}, c_lo = {cl, cl};
+                const q6h2 x16 = {(_Float16)16.0f, (_Float16)16.0f};
+                v16f C[TT];
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    uint32_t v[2];
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t ql = QL[2 * j + (q & 1)][2 * u + e], qh = QH[j][2 * u + e];
+                        v[e] = q == 0 ? q6m_raw<0>(ql, qh) : q == 1 ? q6m_raw<1>(ql, qh)
+                             : q == 2 ? q6m_raw<2>(ql, qh) : q6m_raw<3>(ql, qh);
+                    }
+                    q6v8h Blo, Bhi;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        /* fp16 (1024 + q) pairs from bytes 2(k&1), 2(k&1)+1 of v[k>>1] */
+                        const q6h2 t = q6m_h2(__builtin_amdgcn_perm(0x64646464u, v[k >> 1],
+                                                                    (k & 1) ? 0x04030402u : 0x04010400u));
+                        const q6h2 lo = __builtin_elementwise_fma(t, s_lo, c_lo);          /* (q-32)*sl */
+                        const q6h2 hi = __builtin_elementwise_fma(t, s_hi, c_hi) * x16;    /* 16(q-32)*sh */
+                        Blo[2 * k] = lo.x;
+                        Blo[2 * k + 1] = lo.y;
+                        Bhi[2 * k] = hi.x;
+                        Bhi[2 * k + 1] = hi.y;
+                    }
+#pragma unroll
+                    for (int t = 0; t < TT; t++) {
+                        const int tok = 32 * t + l32;
+                        const int chunk = (16 * j + 4 * q + 2 * h + u) ^ (tok & 31);
+                        const q6v8h A = *(const q6v8h *)&sm.xs[buf][tok][8 * chunk];
+                        const v16f zero = {};
+                        C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Blo, u == 0 ? zero : C[t], 0, 0, 0);
+                        C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bhi, C[t], 0, 0, 0);
+                    }
+                }
+                /* C is the exact integer J_b; scale by the tokens' d8 */
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const q6v4f f4 = *(const q6v4f *)&sm.d8[buf][4 * j + q][32 * t + 8 * g + 4 * h];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) tmp[t][4 * g + e] = fmaf(C[t][4 * g + e], f4[e], tmp[t][4 * g + e]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                acc[t][r] = fmaf(tmp[t][r], d, acc[t][r]);
+                tmp[t][r] = 0.0f;
+            }
+        __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads (to LDS and registers) have landed */
+        __syncthreads();
+    };
+
+    Q6WRaw w0, w1;
+    if (kb0 < kb1) {
+        issue_x(kb0, 0);
+        load_w(kb0, w0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int kb = kb0; kb < kb1; kb += 2) {
+        step(kb, 0, w0, w1);
+        if (kb + 1 < kb1) step(kb + 1, 1, w1, w0);
+    }
+
+    /* lane holds weight row n0 + 32*wave + l32 for tokens
+     * m0 + 32t + 8(r/4) + 4h + r%4 */
+    float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
+    const int col = n0 + 32 * wave + l32;
+    if (col < N) {
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < M) out[(size_t)m * N + col] = acc[t][r];
+            }
+    }
+}
+
+extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits,
+                                                hipStream_t s);
+
+/* Token tile: 32 for up to 32 tokens, else 64. */
+extern "C" int sera_q6k_mmq_bm(int M) { return M <= 32 ? 32 : 64; }
+
+/* K splits: double while the grid holds fewer than 512 tiles and each split
+ * keeps at least 2 super-blocks. */
+extern "C" int sera_q6k_mmq_splits(int M, int N, int K) {
+    const int bm = sera_q6k_mmq_bm(M);
+    const int tiles = ((M + bm - 1) / bm) * ((N + Q6M_BN - 1) / Q6M_BN);
+    const int nkb = K / Q4K_QK;
+    int s = 1;
+    while (tiles * s < 512 && nkb / (s * 2) >= 2 && s < 16) s *= 2;
+    return s;
+}
+
+template <int TT, int WPE>
+static hipError_t launch_q6k_mmq(const uint8_t *W, uint64_t wbytes, const _Float16 *xh, const float *d8t, float *y,
+                                 float *partial, int M, int Mpad, int N, int K, int splits, hipStream_t s) {
+    constexpr int BM = 32 * TT;
+    const int tiles = (Mpad / BM) * ((N + Q6M_BN - 1) / Q6M_BN);
+    const int nkb = K / Q4K_QK;
+    const int per = (nkb + splits - 1) / splits;
+    splits = (nkb + per - 1) / per;
+    hipLaunchKernelGGL((sera_q6k_mmq_kernel<TT, WPE>), dim3(tiles, splits), dim3(256), 0, s, W, wbytes, xh, d8t, y,
+                       splits > 1 ? partial : nullptr, M, Mpad, N, K, per);
+    if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
+    if (splits == 1) return hipSuccess;
+    return sera_launch_splitk_reduce(partial, y, (size_t)M * N, splits, s);
+}
+
+/* stage: the Q6_K MMQ stage for Mpad = sera_q6k_mmq_padded_rows(M) rows;
+ * partial: splits*M*N floats when splits > 1 (M*N % 4 == 0). */
+extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
+                                          int K, int splits, hipStream_t s) {
+    const int Mpad = sera_q6k_mmq_padded_rows(M);
+    const sera_stage_layout L = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K);
+    const char *base = (const char *)stage;
+    const _Float16 *xh = (const _Float16 *)(base + L.qs);
+    const float *d8t = (const float *)(base + L.ds);
+    const uint8_t *w = (const uint8_t *)W;
+    const uint64_t wbytes = (uint64_t)N * (uint64_t)(K / Q4K_QK) * Q6K_BLOCK_BYTES;
+    if (splits < 1) splits = 1;
+    if (sera_q6k_mmq_bm(M) == 32) return launch_q6k_mmq<1, 2>(w, wbytes, xh, d8t, y, partial, M, Mpad, N, K, splits, s);
+    return launch_q6k_mmq<2, 1>(w, wbytes, xh, d8t, y, partial, M, Mpad, N, K, splits, s);
+}

@@ -13,6 +13,12 @@
  *     then xor 4,2,1 across the 8 lanes; d_inv = 127/amax,
  *     q = roundf(x*d_inv), d = 1/d_inv; amax == 0 gives q = 0, d = 0.
  *
+ *  mmq D4 (MMQ activations for Q6_K weights), the same kernel with the D4
+ *     layout the reference selects for Q6_K (cuda/mmq/mmq.cuh:64-103,
+ *     cuda/q3_mmq.cu:303-316): quants as above, fp32 d = 1/d_inv, no sum.
+ *     This library stores the quants as fp16 (exact) for the fp16-MFMA
+ *     Q6_K kernel and d transposed per 256-wide K step (see q4k_common.h).
+ *
  * Division is IEEE correctly rounded (hipcc default), roundf rounds half
  * away from zero, fp16 conversion rounds to nearest even. The float sums are
  * pure additions in a fixed pairing, so they cannot be contracted or
@@ -98,6 +104,46 @@ __global__ __launch_bounds__(256) void sera_q8_1_mmq_kernel(
     if ((threadIdx.x & 7) == 0) {
         ds[(size_t)row * (K / 32) + (k >> 5)] = f2h_bits(d) | (f2h_bits(sum) << 16);
     }
+}
+
+/* D4 quantizer for the Q6_K MMQ stage: quants as fp16 [Mpad][K], fp32 d
+ * as [K/256][8][Mpad]. grid = (ceil(K/1024), Mpad); rows >= M are zero. */
+__global__ __launch_bounds__(256) void sera_q8_1_mmq_d4_kernel(
+        const float *__restrict__ x, int M, int Mpad, int K, _Float16 *__restrict__ xh,
+        float *__restrict__ d8t) {
+    const int row = blockIdx.y;
+    const int k = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (k >= K) return;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (row < M) v = *(const float4 *)(x + (size_t)row * K + k);
+
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    float q0 = 0.0f, q1 = 0.0f, q2 = 0.0f, q3 = 0.0f, d = 0.0f;
+    if (amax != 0.0f) {
+        const float d_inv = 127.0f / amax;
+        q0 = roundf(v.x * d_inv);
+        q1 = roundf(v.y * d_inv);
+        q2 = roundf(v.z * d_inv);
+        q3 = roundf(v.w * d_inv);
+        d = 1.0f / d_inv;
+    }
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 hq = {(_Float16)q0, (_Float16)q1, (_Float16)q2, (_Float16)q3};   /* |q| <= 127: exact */
+    *(h4 *)(xh + (size_t)row * K + k) = hq;
+    if ((threadIdx.x & 7) == 0)
+        d8t[((size_t)(k >> 8) * 8 + ((k >> 5) & 7)) * Mpad + row] = d;
+}
+
+extern "C" hipError_t sera_launch_q8_1_mmq_d4(const float *x, int M, int Mpad, int K, void *stage,
+                                              hipStream_t stream) {
+    const sera_stage_layout L = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K);
+    char *base = (char *)stage;
+    dim3 grid((K + 1023) / 1024, Mpad);
+    hipLaunchKernelGGL(sera_q8_1_mmq_d4_kernel, grid, dim3(256), 0, stream, x, M, Mpad, K,
+                       (_Float16 *)(base + L.qs), (float *)(base + L.ds));
+    return hipGetLastError();
 }
 
 extern "C" hipError_t sera_launch_q8_1_row(const float *x, int M, int K, void *stage,

@@ -23,6 +23,13 @@ extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, flo
 extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
                                           int M, int N, int K, int splits, hipStream_t s);
 extern "C" int sera_mmvq_rows_per_wave(int N, int M);
+extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K,
+                                           int rows, hipStream_t s);
+extern "C" int sera_q6k_mmvq_rows(int N, int M);
+extern "C" hipError_t sera_launch_q8_1_mmq_d4(const float *x, int M, int Mpad, int K, void *stage, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
+                                          int K, int splits, hipStream_t s);
+extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
 extern "C" int sera_mmq_splits(int M, int N, int K);
 extern "C" int sera_skinny_splits(int M, int N, int K);
 extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
@@ -154,7 +161,9 @@ extern "C" size_t sera_q4k_arena_bytes(size_t max_tokens, int64_t max_features, 
     const size_t row = sera_row_stage_layout((size_t)(mt < SERA_Q4K_MMVQ_MAX_BATCH ? mt : SERA_Q4K_MMVQ_MAX_BATCH),
                                              (size_t)max_k).total;
     const size_t mmq = sera_mmq_stage_layout((size_t)sera_mmq_padded_rows(mt), (size_t)max_k).total;
-    const size_t stage = row > mmq ? row : mmq;
+    const size_t q6 = sera_q6k_mmq_stage_layout((size_t)sera_q6k_mmq_padded_rows(mt), (size_t)max_k).total;
+    size_t stage = row > mmq ? row : mmq;
+    if (q6 > stage) stage = q6;
     const size_t partial = sera_align256(partial_floats_bound(max_tokens, max_features) * sizeof(float));
     return kCounterBytes + stage + partial;
 }
@@ -345,6 +354,140 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
     } else if (sera_launch_q4k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
         return fail(-3, "sera_q4k_dense_vec: mmvq launch failed");
     }
+    if (timed) record(g_ev.kernel_end, s);
+    return 0;
+}
+
+/* ---- Q6_K ---------------------------------------------------------------- */
+
+namespace {
+/* Q6_K rows are K/256 * 210 bytes; the kernels address a row's bytes with
+ * 32-bit offsets from the start of a group of rows. */
+bool q6k_shape_ok(const char *tag, int N, int K) {
+    if ((uint64_t)(K / Q4K_QK) * 210u * 256u >= (1ull << 31)) {
+        fail(-1, "%s: K=%d too long for 32-bit row offsets", tag, K);
+        return false;
+    }
+    (void)N;
+    return true;
+}
+}  // namespace
+
+extern "C" int sera_q6k_mmvq_rows_per_wave(int M, int N) {
+    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH || N <= 0) return 0;
+    return sera_q6k_mmvq_rows(N, M);
+}
+
+extern "C" int sera_q6k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
+                             int rows_per_wave, void *stream) {
+    if (!W || !row_stage || !Y) return fail(-1, "sera_q6k_mmvq: null pointer");
+    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q6k_mmvq: batch M=%d outside 1..8", M);
+    if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q6k_mmvq: bad shape N=%d K=%d", N, K);
+    if (rows_per_wave != 0 && rows_per_wave != 1 && rows_per_wave != 2 && rows_per_wave != 4)
+        return fail(-1, "sera_q6k_mmvq: rows_per_wave=%d not in {0,1,2,4}", rows_per_wave);
+    if (rows_per_wave == 4 && M > 4) return fail(-1, "sera_q6k_mmvq: rows_per_wave=4 needs M <= 4");
+    if (((uintptr_t)W & 15u) != 0) return fail(-1, "sera_q6k_mmvq: W must be 16-byte aligned");
+    if (!q6k_shape_ok("sera_q6k_mmvq", N, K)) return -1;
+    return sera_launch_q6k_mmvq(W, row_stage, Y, M, N, K, rows_per_wave, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_q6k_mmvq: launch failed");
+}
+
+extern "C" int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
+                                  int timed) {
+    if (!check_shape("sera_q6k_dense_vec", W, X, Y, M, N, K)) return -1;
+    if (M > SERA_Q4K_MMVQ_MAX_BATCH)
+        return fail(-1, "sera_q6k_dense_vec: batch M=%d exceeds MMVQ cap %d", M, SERA_Q4K_MMVQ_MAX_BATCH);
+    if (!q6k_shape_ok("sera_q6k_dense_vec", N, K)) return -1;
+    if (!g_arena) return fail(-1, "sera_q6k_dense_vec: no arena attached");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
+    if (stage_bytes > g_arena_bytes)
+        return fail(-1, "sera_q6k_dense_vec: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
+    if (timed) record(g_ev.quant_begin, s);
+    if (sera_launch_q8_1_row(X, M, K, g_arena, s) != hipSuccess)
+        return fail(-2, "sera_q6k_dense_vec: quantize launch failed");
+    if (timed) record(g_ev.quant_end, s);
+    if (timed) record(g_ev.kernel_begin, s);
+    if (sera_launch_q6k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess)
+        return fail(-3, "sera_q6k_dense_vec: mmvq launch failed");
+    if (timed) record(g_ev.kernel_end, s);
+    return 0;
+}
+
+namespace {
+int q6k_splits(int M, int N, int K) {
+    return ((size_t)M * N) % 4 == 0 ? sera_q6k_mmq_splits(M, N, K) : 1;
+}
+}  // namespace
+
+extern "C" int sera_q6k_kernel_launches(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
+    if (M <= SERA_Q4K_MMVQ_MAX_BATCH) return 2;
+    return q6k_splits(M, N, K) > 1 ? 3 : 2;
+}
+
+extern "C" int sera_q8_1_q6k_mmq_padded_rows(int M) { return M > 0 ? sera_q6k_mmq_padded_rows(M) : 0; }
+
+extern "C" size_t sera_q8_1_q6k_mmq_stage_bytes(int M, int K) {
+    if (M <= 0 || K <= 0) return 0;
+    return sera_q6k_mmq_stage_layout((size_t)sera_q6k_mmq_padded_rows(M), (size_t)K).total;
+}
+
+extern "C" void sera_q8_1_q6k_mmq_stage_offsets(int M, int K, size_t *qs, size_t *d) {
+    const size_t mp = M > 0 ? (size_t)sera_q6k_mmq_padded_rows(M) : 0;
+    const sera_stage_layout L = sera_q6k_mmq_stage_layout(mp, (size_t)(K > 0 ? K : 0));
+    if (qs) *qs = L.qs;
+    if (d) *d = L.ds;
+}
+
+extern "C" int sera_q8_1_quantize_mmq_d4(const float *X, int M, int K, void *stage, void *stream) {
+    if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK)
+        return fail(-1, "sera_q8_1_quantize_mmq_d4: bad arguments");
+    if (((uintptr_t)X & 15u) != 0) return fail(-1, "sera_q8_1_quantize_mmq_d4: X must be 16-byte aligned");
+    return sera_launch_q8_1_mmq_d4(X, M, sera_q6k_mmq_padded_rows(M), K, stage, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-2, "sera_q8_1_quantize_mmq_d4: launch failed");
+}
+
+extern "C" int sera_q6k_mmq_splits_for(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
+    return q6k_splits(M, N, K);
+}
+
+extern "C" int sera_q6k_mmq(const void *W, const void *q6k_mmq_stage, float *Y, float *partial, int M, int N, int K,
+                            int splits, void *stream) {
+    if (!W || !q6k_mmq_stage || !Y) return fail(-1, "sera_q6k_mmq: null pointer");
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q6k_mmq: bad shape M=%d N=%d K=%d", M, N, K);
+    if (((uintptr_t)W & 15u) != 0) return fail(-1, "sera_q6k_mmq: W must be 16-byte aligned");
+    if (!q6k_shape_ok("sera_q6k_mmq", N, K)) return -1;
+    if (splits == 0) splits = q6k_splits(M, N, K);
+    if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q6k_mmq: splits=%d outside 1..K/256", splits);
+    if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
+        return fail(-1, "sera_q6k_mmq: split-K needs a partial buffer and M*N %% 4 == 0");
+    return sera_launch_q6k_mmq(W, q6k_mmq_stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_q6k_mmq: launch failed");
+}
+
+extern "C" int sera_q6k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
+                              int timed) {
+    if (!check_shape("sera_q6k_dense", W, X, Y, M, N, K)) return -1;
+    if (!q6k_shape_ok("sera_q6k_dense", N, K)) return -1;
+    if (!g_arena) return fail(-1, "sera_q6k_dense: no arena attached");
+    hipStream_t s = (hipStream_t)stream;
+    const int Mpad = sera_q6k_mmq_padded_rows(M);
+    const size_t stage_bytes = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
+    const int splits = q6k_splits(M, N, K);
+    const size_t partial_bytes = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+    if (stage_bytes + partial_bytes > g_arena_bytes)
+        return fail(-1, "sera_q6k_dense: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
+                    g_arena_bytes);
+    float *partial = partial_bytes ? (float *)(g_arena + stage_bytes) : nullptr;
+    if (timed) record(g_ev.quant_begin, s);
+    if (sera_launch_q8_1_mmq_d4(X, M, Mpad, K, g_arena, s) != hipSuccess)
+        return fail(-2, "sera_q6k_dense: quantize launch failed");
+    if (timed) record(g_ev.quant_end, s);
+    if (timed) record(g_ev.kernel_begin, s);
+    if (sera_launch_q6k_mmq(W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
+        return fail(-3, "sera_q6k_dense: mmq launch failed");
     if (timed) record(g_ev.kernel_end, s);
     return 0;
 }

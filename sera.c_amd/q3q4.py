@@ -111,6 +111,17 @@ def load():
         "sera_q4k_subblock_dots": ([P, P, P, I, I, I, P], I),
         "sera_q4k_quantize": ([P, I64, I64, P, P], I),
         "sera_q4k_last_error": ([], CP),
+        "sera_q6k_dense": ([P, P, P, I, I, I, P, I], I),
+        "sera_q6k_dense_vec": ([P, P, P, I, I, I, P, I], I),
+        "sera_q6k_kernel_launches": ([I, I, I], I),
+        "sera_q6k_mmvq": ([P, P, P, I, I, I, I, P], I),
+        "sera_q6k_mmvq_rows_per_wave": ([I, I], I),
+        "sera_q8_1_q6k_mmq_padded_rows": ([I], I),
+        "sera_q8_1_q6k_mmq_stage_bytes": ([I, I], SZ),
+        "sera_q8_1_q6k_mmq_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ)], None),
+        "sera_q8_1_quantize_mmq_d4": ([P, I, I, P, P], I),
+        "sera_q6k_mmq": ([P, P, P, P, I, I, I, I, P], I),
+        "sera_q6k_mmq_splits_for": ([I, I, I], I),
         "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_stream": ([P, P, P, P, P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_kernel": ([I, P, I, P, P, P, I, I, I, I, P, I, I,
@@ -277,3 +288,35 @@ def quantize_weights(x, out, stream=None):
     rows, K = x.shape
     _check(load().sera_q4k_quantize(_ptr(x), rows, K, _ptr(out), _stream(stream)),
            "sera_q4k_quantize")
+
+
+# ---------------------------------------------------------------------------
+# Q6_K (GGUF type 14)
+# ---------------------------------------------------------------------------
+
+def q6k_mmq_stage_layout(M, K):
+    L = load()
+    qs, d = ctypes.c_size_t(), ctypes.c_size_t()
+    L.sera_q8_1_q6k_mmq_stage_offsets(M, K, ctypes.byref(qs), ctypes.byref(d))
+    return {"qs": qs.value, "d": d.value, "rows": L.sera_q8_1_q6k_mmq_padded_rows(M),
+            "total": L.sera_q8_1_q6k_mmq_stage_bytes(M, K)}
+
+
+def quantize_mmq_d4(x, stage, stream=None):
+    M, K = x.shape
+    _check(load().sera_q8_1_quantize_mmq_d4(_ptr(x), M, K, _ptr(stage), _stream(stream)),
+           "sera_q8_1_quantize_mmq_d4")
+
+
+def q6k_mmvq(W, stage, out, M, N, K, rows_per_wave=0, stream=None):
+    _check(load().sera_q6k_mmvq(_ptr(W), _ptr(stage), _ptr(out), M, N, K, rows_per_wave,
+                                _stream(stream)), "sera_q6k_mmvq")
+
+
+def q6k_mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None):
+    _check(load().sera_q6k_mmq(_ptr(W), _ptr(stage), _ptr(out), _ptr(partial), M, N, K, splits,
+                               _stream(stream)), "sera_q6k_mmq")
+
+
+def q6k_mmq_splits(M, N, K):
+    return load().sera_q6k_mmq_splits_for(M, N, K)

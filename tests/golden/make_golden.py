@@ -15,7 +15,12 @@ Outputs (data only: inputs and expected outputs):
                      f16_to_f32 values
   dequant_ref.npz    Q4_K bytes (LCG blocks + quantized matrices) and the
                      reference dequant of each
-Run:  python tests/golden/make_golden.py
+  dequant_q6k_ref.npz  seeded Q6_K blocks (plus edge blocks: extreme group
+                     scales, all-low / all-high quants, d = 0, negative and
+                     subnormal d) and the reference dequant (src/q3_quant.c:78-103,
+                     qtype 14) of each; needs only oracle/_ref
+Run:  python tests/golden/make_golden.py            (all fixtures)
+      python tests/golden/make_golden.py --q6k      (Q6_K fixture only)
 """
 import importlib.util
 import os
@@ -87,8 +92,31 @@ def quantizer_inputs():
     return mats
 
 
+def q6k_vectors():
+    """Q6_K blocks and their dequant through the compiled reference."""
+    rng = np.random.default_rng(60606)
+    blocks = [oracle.q6k_blocks(rng, 24)]
+    edge = oracle.q6k_blocks(rng, 8)
+    edge[0, 192:208] = np.array([-128, 127] * 8, np.int8).view(np.uint8)   # extreme scales
+    edge[1, 0:192] = 0x00                                                   # all quants 0 -> -32
+    edge[2, 0:192] = 0xFF                                                   # all quants 63 -> +31
+    edge[3, 208:210] = np.array([0], np.uint16).view(np.uint8)              # d = 0
+    edge[4, 208:210] = np.array([0x8001], np.uint16).view(np.uint8)         # negative subnormal d
+    edge[5, 208:210] = np.array([0x7BFF], np.uint16).view(np.uint8)         # largest finite d
+    edge[6, 192:208] = np.arange(16, dtype=np.int8).view(np.uint8)          # scale = group index
+    blocks.append(edge)
+    W = np.concatenate(blocks).reshape(4, -1)                               # 4 rows x 2048 weights
+    deq = oracle.ref_dequant(W, 4, 2048, qtype=14)
+    assert deq is not None, "oracle/_ref not built (reference tree not mounted?)"
+    np.savez_compressed(os.path.join(HERE, "dequant_q6k_ref.npz"), w=W, deq=deq)
+    print("dequant_q6k_ref.npz", os.path.getsize(os.path.join(HERE, "dequant_q6k_ref.npz")), "bytes")
+
+
 def main():
     oracle.build()
+    if "--q6k" in sys.argv[1:]:
+        q6k_vectors()
+        return
     q = load_ref_quantizer()
 
     # --- quantizer ---
@@ -128,6 +156,7 @@ def main():
     np.savez_compressed(os.path.join(HERE, "dequant_ref.npz"), **dq)
     for fn in ("q4k_quantizer.npz", "fp16_helpers.npz", "dequant_ref.npz"):
         print(fn, os.path.getsize(os.path.join(HERE, fn)), "bytes")
+    q6k_vectors()
 
 
 if __name__ == "__main__":

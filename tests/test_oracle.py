@@ -362,3 +362,158 @@ def test_path_oracles_pass_reference_gates_vs_dequant(M):
     cos = (y * ref).sum() / np.sqrt((y * y).sum() * (ref * ref).sum())
     rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
     assert cos > 0.999 and rel < 0.01
+
+
+# ---------------------------------------------------------------------------
+# Q6_K
+# ---------------------------------------------------------------------------
+
+def test_q6k_dequant_matches_reference_q3_quant_c_vectors(golden_dir):
+    """Bytes and outputs of the reference's own dequant (src/q3_quant.c:78-103,
+    built from its sources into oracle/_ref by make_golden.py --q6k), seeded
+    blocks plus edge blocks (scales -128/127, quants 0 and 63, d = 0,
+    subnormal and largest d)."""
+    g = np.load(f"{golden_dir}/dequant_q6k_ref.npz")
+    W, deq = g["w"], g["deq"]
+    got = oracle.dequant_q6k(W, W.shape[0], deq.shape[1])
+    assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))
+
+
+def test_q6k_ref_build_agrees_when_present():
+    W = oracle.q6k_weights(RNG, 3, 768)
+    ref = oracle.ref_dequant(W, 3, 768, qtype=14)
+    if ref is None:
+        pytest.skip("reference tree not mounted: oracle/_ref not built")
+    assert np.array_equal(oracle.dequant_q6k(W, 3, 768).view(np.uint32), ref.view(np.uint32))
+
+
+def test_q6k_dequant_hand_check():
+    """One block worked by hand from the loop of src/q3_quant.c:88-98 with
+    d = 1 and sc[g] = g + 1:
+      ql[0] = 0x5A, ql[32] = 0x3C, qh[0] = 0x9C = 0b10_01_11_00
+      w[0]  = sc[0] * ((0xA | 0<<4) - 32) = 1 * -22
+      w[32] = sc[2] * ((0xC | 3<<4) - 32) = 3 * 28
+      w[64] = sc[4] * ((0x5 | 1<<4) - 32) = 5 * -11
+      w[96] = sc[6] * ((0x3 | 2<<4) - 32) = 7 * 3
+      w[16] uses ql[16] = 0x00, qh[16] = 0x00 and sc[1]: 2 * -32
+      w[128] uses ql[64] = 0xF1, qh[32] = 0x03, sc[8]: 9 * ((1 | 3<<4) - 32) = 9 * 17
+      w[255] = ql[127] high nibble 0xF, qh[63] bits 6-7 = 3, sc[15]: 16 * 31"""
+    b = np.zeros((1, 210), np.uint8)
+    b[0, 0], b[0, 32], b[0, 128] = 0x5A, 0x3C, 0x9C
+    b[0, 64], b[0, 128 + 32] = 0xF1, 0x03
+    b[0, 127], b[0, 128 + 63] = 0xF0, 0xC0
+    b[0, 192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8)
+    b[0, 208:210] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    w = oracle.dequant_q6k(b, 1, 256)[0]
+    assert (w[0], w[32], w[64], w[96]) == (-22.0, 84.0, -55.0, 21.0)
+    assert w[16] == -64.0 and w[128] == 153.0 and w[255] == 496.0
+    ref = oracle.ref_dequant(b, 1, 256, qtype=14)
+    if ref is not None:
+        assert np.array_equal(ref[0], w)
+
+
+def _q6k_exact_case(M, N, K):
+    """Q6_K weights with d = 2^-8 and activations x = q * 2^-5 with a +-127
+    in every 32-block: every weight (d*sc*(q-32)), every Q8_1 value and every
+    product is exact, so the formula must equal the dequant GEMM exactly."""
+    W = oracle.q6k_weights(RNG, N, K).reshape(N, K // 256, 210)
+    W[:, :, 208:210] = np.frombuffer(np.float16(2.0 ** -8).tobytes(), np.uint8)
+    W = W.reshape(N, -1)
+    q = RNG.integers(-60, 61, (M, K // 32, 32))
+    q[:, :, 0] = 127
+    q[:, :, 1] = -127
+    X = (q.reshape(M, K) * 2.0 ** -5).astype(np.float32)
+    return W, X
+
+
+def test_q6k_formula_equals_dequant_gemm_when_exact():
+    """Pins the weight -> (group scale, quant) mapping and which d8 scales
+    which weights against the dequant (itself pinned to the reference's)."""
+    M, N, K = 3, 5, 768
+    W, X = _q6k_exact_case(M, N, K)
+    ref = oracle.gemm_dequant_q6k(W, X, N, K)
+    xq, xd, _ = oracle.q8_1_row(X)
+    assert np.all(xd == fp16_bits(2.0 ** -5))
+    assert np.array_equal(oracle.gemm_q6k(W, xq, oracle.h2f(xd), N, K), ref)
+    xq4, d4 = oracle.q8_1_mmq_d4(X)
+    assert np.all(d4 == np.float32(2.0 ** -5))
+    assert np.array_equal(oracle.gemm_q6k(W, xq4, d4, N, K), ref)
+
+
+def test_q6k_formula_matches_reference_dequant_on_golden_blocks(golden_dir):
+    """Random quants and d8 on the golden blocks: the formula equals
+    sum_k w_ref[n,k] * d8[k/32] * q8[k] up to the fp32 roundings inside the
+    reference dequant ((d*sc)*q)."""
+    g = np.load(f"{golden_dir}/dequant_q6k_ref.npz")
+    W, deq = g["w"], g["deq"].astype(np.float64)
+    N, K = deq.shape
+    keep = np.isfinite(deq).all(axis=1) & (np.abs(deq).max(axis=1) < 1e3)   # drop the huge-d row
+    xq = RNG.integers(-127, 128, (2, K)).astype(np.int8)
+    d8 = RNG.uniform(0.001, 0.02, (2, K // 32)).astype(np.float32)
+    y = oracle.gemm_q6k(W, xq, d8, N, K)
+    x = np.repeat(d8.astype(np.float64), 32, axis=1) * xq
+    ref = x @ deq.T
+    scale = np.abs(x) @ np.abs(deq).T
+    assert np.all(np.abs(y - ref)[:, keep] <= 1e-6 * scale[:, keep] + 1e-30)
+    # a planted mistake (d8 of the neighbouring 32-block) must not pass
+    bad = oracle.gemm_q6k(W, xq, np.roll(d8, 1, axis=1), N, K)
+    assert not np.all(np.abs(bad - ref)[:, keep] <= 1e-6 * scale[:, keep] + 1e-30)
+
+
+def test_q6k_group_dots_brute_force_tiny():
+    N, K, M = 2, 512, 2
+    W = oracle.q6k_weights(RNG, N, K)
+    xq = RNG.integers(-127, 128, (M, K)).astype(np.int8)
+    got = oracle.q6k_group_dots(W, xq, N, K)
+    for n in range(N):
+        for b in range(K // 256):
+            blk = W[n, 210 * b:210 * (b + 1)]
+            ql, qh = blk[:128].astype(int), blk[128:192].astype(int)
+            for m in range(M):
+                for g in range(16):
+                    acc = 0
+                    for i in range(16):
+                        e = 16 * g + i
+                        j, k, l = e // 128, (e % 128) // 32, e % 32
+                        lo = ql[64 * j + 32 * (k & 1) + l]
+                        nib = (lo >> 4) if k >= 2 else (lo & 0xF)
+                        q = nib | (((qh[32 * j + l] >> (2 * k)) & 3) << 4)
+                        acc += (q - 32) * int(xq[m, 256 * b + e])
+                    assert got[m, n, 16 * b + g] == acc
+
+
+def test_q6k_group_dot_extreme_is_closed_form():
+    """All quants 0 (value -32) against +-127: I = -+16*32*127 = -+65024."""
+    W = np.zeros((1, 210), np.uint8)
+    xq = np.full((2, 256), 127, np.int8)
+    xq[1] = -127
+    I = oracle.q6k_group_dots(W, xq, 1, 256)
+    assert np.all(I[0] == -65024) and np.all(I[1] == 65024)
+
+
+def test_q8_mmq_d4_quants_and_fp32_scale():
+    """D4 keeps the DS4 quants and stores d = 1/(127/amax) in fp32
+    (cuda/mmq/quantize.cu:326-366), checked against numpy float32 IEEE
+    arithmetic; an all-zero block gives q = 0, d = 0."""
+    X = (RNG.standard_normal((3, 512)) * np.exp2(RNG.integers(-8, 8, (3, 1)))).astype(np.float32)
+    X[1, 64:96] = 0.0
+    xq, d = oracle.q8_1_mmq_d4(X)
+    eq, _, _ = oracle.q8_1_mmq(X)
+    assert np.array_equal(xq, eq)
+    amax = np.abs(X.reshape(3, 16, 32)).max(axis=2)
+    with np.errstate(divide="ignore"):
+        exp = np.where(amax == 0, np.float32(0), np.float32(1) / (np.float32(127) / amax)).astype(np.float32)
+    assert np.array_equal(d.view(np.uint32), exp.view(np.uint32))
+    assert d[1, 2] == 0.0 and np.all(xq[1, 64:96] == 0)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_q6k_path_oracle_passes_reference_gates_vs_dequant(M):
+    N, K = 48, 1024
+    W = oracle.q6k_weights(RNG, N, K)
+    X = fill_activation(M, K)
+    ref = oracle.gemm_dequant_q6k(W, X, N, K)
+    y = oracle.linear_reference_q6k(W, X, N, K)
+    cos = (y * ref).sum() / np.sqrt((y * y).sum() * (ref * ref).sum())
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert cos > 0.999 and rel < 0.01
