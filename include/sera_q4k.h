@@ -158,10 +158,12 @@ const char *sera_q4k_last_error(void);
  * readable up to the next 16-byte boundary past its last byte (any hipMalloc
  * allocation is). */
 
-/* Y = X . W^T through the MMVQ path, 1 <= M <= 8, on the row-layout Q8_1
- * stage (the reference quantizes Q6_K decode activations with the same
- * quantize_row_q8_1_cuda call as Q4_K). Replaces q3_mmq_q6_K_dense_vec
- * (cuda/q3_mmq.cu:515-519 over q3_mmq_dense_vec_impl, :408-506). */
+/* Y = X . W^T through the MMVQ path (MMVQ arithmetic), 1 <= M <= 8: the
+ * reference quantizes Q6_K decode activations with the same
+ * quantize_row_q8_1_cuda call as Q4_K. Up to 4 tokens the dot4 MMVQ kernel
+ * on the row stage, from 5 the fp16-MFMA tile kernel on a row-formula Q6_K
+ * stage. Replaces q3_mmq_q6_K_dense_vec (cuda/q3_mmq.cu:515-519 over
+ * q3_mmq_dense_vec_impl, :408-506). */
 int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
 
@@ -187,13 +189,17 @@ int sera_q6k_mmvq_rows_per_wave(int M, int N);
 
 /* Q6_K MMQ activation stage (D4 quantizer of cuda/mmq/quantize.cu:271-367
  * with the layout mmq_get_q8_1_ds_layout selects for Q6_K,
- * cuda/mmq/mmq.cuh:64-103): quants as fp16 [Mpad][K] (exact integers), fp32
- * d = 1/d_inv as [K/256][8][Mpad]; rows M..Mpad-1 zero, Mpad a multiple of
- * 64. */
+ * cuda/mmq/mmq.cuh:64-103): 16 * quant as fp16 [Mpad][K] (exact integers),
+ * fp32 d = 1/d_inv as [K/256][8][Mpad]; rows M..Mpad-1 zero, Mpad a
+ * multiple of 32. sera_q8_1_quantize_row_q6k fills the same layout with the
+ * row quantizer's values (cuda/mmq/quantize.cu:4-48, d8 = fp32(fp16 d)):
+ * the MMVQ arithmetic on the tile kernel, which sera_q6k_dense_vec uses
+ * from 5 tokens. */
 int sera_q8_1_q6k_mmq_padded_rows(int M);
 size_t sera_q8_1_q6k_mmq_stage_bytes(int M, int K);
 void sera_q8_1_q6k_mmq_stage_offsets(int M, int K, size_t *qs, size_t *d);
 int sera_q8_1_quantize_mmq_d4(const float *X, int M, int K, void *stage, void *stream);
+int sera_q8_1_quantize_row_q6k(const float *X, int M, int K, void *stage, void *stream);
 
 /* MMQ kernel on a Q6_K MMQ stage (mul_mat_q<Q6_K>, cuda/mmq/mmq.cuh:3570-3575
  * with load_tiles_q6_K :2512-2596 and vec_dot_q6_K_q8_1_mma :2634-2786):
@@ -216,10 +222,10 @@ int sera_q4k_bench_linear(const void *geometry, const void *const *weights, int 
 /* Kernel-only loop on a prepared stage (path 0 = MMVQ with param =
  * rows_per_wave, 1 = MMQ with param = splits, 2/3 = few-token kernel form
  * 0/1 with param = splits, 4 = stream-K MMQ with param = workgroups and
- * `partial` holding the slots followed by the zeroed tile counters): `iters`
- * launches back to back
- * between one event pair on `stream`; *avg_kernel_ms = pair time / iters,
- * *elapsed_ms = pair time. */
+ * `partial` holding the slots followed by the zeroed tile counters, 5 =
+ * Q6_K MMVQ with param = rows per wave, 6 = Q6_K MMQ with param = splits on
+ * a Q6_K MMQ stage): `iters` launches back to back between one event pair
+ * on `stream`; *avg_kernel_ms = pair time / iters, *elapsed_ms = pair time. */
 int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, const void *stage,
                           float *Y, float *partial, int M, int N, int K, int param, void *stream,
                           int warmup, int iters, double *avg_kernel_ms, double *elapsed_ms);

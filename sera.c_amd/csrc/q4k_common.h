@@ -18,7 +18,7 @@
  *                                               S = sum of the 32 int8 quants
  *   mmq stage (MMQ):   qs  int8   [Mpad][K]
  *                      ds  half2  [Mpad][K/32]
- *   Q6_K mmq stage:    qs  fp16   [Mpad][K]          (the int8 quants, exact)
+ *   Q6_K mmq stage:    qs  fp16   [Mpad][K]          (16 x the int8 quants, exact)
  *                      ds  float  [K/256][8][Mpad]   (fp32 D4 scale d, per
  *                                  256-wide K step, sub-block, token)
  */
@@ -61,7 +61,7 @@ static inline sera_stage_layout sera_mmq_stage_layout(size_t rows_padded, size_t
     return L;
 }
 
-/* Q6_K MMQ stage: Mpad is a multiple of 64. */
+/* Q6_K MMQ stage: Mpad is a multiple of the 32-token tile. */
 static inline sera_stage_layout sera_q6k_mmq_stage_layout(size_t rows_padded, size_t K) {
     sera_stage_layout L;
     L.qs = 0;
@@ -71,7 +71,7 @@ static inline sera_stage_layout sera_q6k_mmq_stage_layout(size_t rows_padded, si
     return L;
 }
 
-static inline int sera_q6k_mmq_padded_rows(int M) { return (M + 63) / 64 * 64; }
+static inline int sera_q6k_mmq_padded_rows(int M) { return (M + 31) / 32 * 32; }
 
 #ifdef __HIPCC__
 typedef _Float16 f16;

@@ -34,8 +34,9 @@
  *     token t sits in column c ^ (t & 31) so a half-wave's 32 tokens reading
  *     one chunk hit distinct banks. The quantizer writes d8 transposed per K
  *     step so it lands in LDS as [sub-block][token].
- *   - tile: 32*TT tokens x 128 weight rows per workgroup, 4 waves along the
- *     rows; split-K with a fixed-order reduce when tiles are few.
+ *   - tile: 32 tokens x 128 weight rows per workgroup, 4 waves along the
+ *     rows (one 32 x 32 MFMA tile each), two workgroups per CU; split-K
+ *     with a fixed-order reduce when tiles are few.
  */
 #include "q4k_common.h"
 
@@ -49,11 +50,14 @@ typedef float q6v4f __attribute__((ext_vector_type(4)));
 #define Q6K_BLOCK_BYTES 210
 #define Q6M_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
 #define Q6M_BN 128
+#define Q6M_WCH 15    /* 16-byte LDS chunks per weight row and K step: a 210-byte block at any
+                         2-byte phase needs 14; the 15th spreads row starts over more banks */
 
 template <int BM>
 struct alignas(16) Q6MmqSmem {
     alignas(16) _Float16 xs[2][BM][Q4K_QK];
     alignas(16) float d8[2][8][BM];
+    alignas(16) uint8_t w[Q6M_BN * Q6M_WCH * 16];
 };
 
 namespace {
@@ -71,13 +75,13 @@ __device__ __forceinline__ int q6m_tile_of(int wg, int ntiles) {
 
 __device__ __forceinline__ q6h2 q6m_h2(uint32_t u) { return __builtin_bit_cast(q6h2, u); }
 
-/* 16 bytes that start `sh` bits into the 5 dwords (a.x .. a.w, b) */
-__device__ __forceinline__ q6v4u q6m_align16(q6v4u a, uint32_t b, uint32_t sh) {
+/* 16 bytes that start `sh` bits into the 5 dwords p[0..4] */
+__device__ __forceinline__ q6v4u q6m_align16(const uint32_t *p, uint32_t sh) {
     q6v4u r;
-    r.x = __builtin_amdgcn_alignbit(a.y, a.x, sh);
-    r.y = __builtin_amdgcn_alignbit(a.z, a.y, sh);
-    r.z = __builtin_amdgcn_alignbit(a.w, a.z, sh);
-    r.w = __builtin_amdgcn_alignbit(b, a.w, sh);
+    r.x = __builtin_amdgcn_alignbit(p[1], p[0], sh);
+    r.y = __builtin_amdgcn_alignbit(p[2], p[1], sh);
+    r.z = __builtin_amdgcn_alignbit(p[3], p[2], sh);
+    r.w = __builtin_amdgcn_alignbit(p[4], p[3], sh);
     return r;
 }
 
@@ -92,11 +96,6 @@ __device__ __forceinline__ uint32_t q6m_raw(uint32_t ql, uint32_t qh) {
 
 __device__ __forceinline__ int q6m_sext8(uint32_t w, int sh) { return (int)(w << (24 - sh)) >> 24; }
 
-struct Q6WRaw {
-    q6v4u a[7];
-    uint32_t b[7];
-};
-
 }  // namespace
 
 /* Grid (tiles, K splits); splits > 1 write fp32 partials per split. */
@@ -106,6 +105,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
         const float *__restrict__ d8t, float *__restrict__ y, float *__restrict__ partial, int M, int Mpad,
         int N, int K, int kb_per_split) {
     constexpr int BM = 32 * TT;
+    constexpr int WINST = Q6M_BN * Q6M_WCH * 16 / 1024;   /* load-to-LDS instructions per weight tile */
     __shared__ __attribute__((aligned(16))) Q6MmqSmem<BM> sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
@@ -117,30 +117,28 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
     const uint32_t rb = (uint32_t)nb * Q6K_BLOCK_BYTES;
 
     /* weights: resource from the tile's first row (16-byte aligned down) to
-     * the end of the matrix, rounded up to 16 bytes (a dword that straddles
-     * the end must not read as zero); the lane's row, clamped (rows >= N are
-     * never stored) */
+     * the end of the matrix rounded up to 16 bytes (a chunk that straddles the
+     * end must not read as zero); rows >= N are clamped (never stored) */
     const uint64_t gbase = ((uint64_t)n0 * rb) & ~(uint64_t)15;
     const uint64_t rem = ((wbytes - gbase) + 15) & ~(uint64_t)15;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(W + gbase), (short)0, (int)(rem > 0x7fffffffu ? 0x7fffffffu : rem), Q6M_RSRC_FLAGS);
-    const int n = min(n0 + 32 * wave + l32, N - 1);
-    const uint32_t rowoff = (uint32_t)((uint64_t)n * rb - gbase);
 
-    /* the lane's runs of a block: ql[64j + 32p + 16h + 0..15] (j, p = 0, 1),
-     * qh[32j + 16h + 0..15], and bytes 192..209 (scales, d) */
-    auto load_w = [&](int kb, Q6WRaw &w) {
-        const uint32_t o = rowoff + (uint32_t)kb * Q6K_BLOCK_BYTES;
-        const uint32_t X[7] = {16u * h, 32u + 16u * h, 64u + 16u * h, 96u + 16u * h, 128u + 16u * h,
-                               160u + 16u * h, 192u};
+    /* weight tile of K step kb -> LDS: row r's block from its 16-byte-aligned
+     * start, chunks 0..13 at w[r*240 + 16c]; 1 KB per wave-instruction */
+    auto issue_w = [&](int kb) {
 #pragma unroll
-        for (int i = 0; i < 7; i++) {
-            const uint32_t a4 = (o + X[i]) & ~3u;
-            w.a[i] = __builtin_bit_cast(q6v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, a4, 0, 0));
-            w.b[i] = __builtin_amdgcn_raw_buffer_load_b32(rw, a4 + 16, 0, 0);
+        for (int i = 0; i < (WINST + 3) / 4; i++) {
+            const int inst = wave + 4 * i;
+            if (inst < WINST) {
+                const int f = inst * 64 + lane;
+                const int r = f / Q6M_WCH, c = f - r * Q6M_WCH;
+                const uint32_t g = (uint32_t)((uint64_t)min(n0 + r, N - 1) * rb - gbase) + (uint32_t)kb * Q6K_BLOCK_BYTES;
+                const uint32_t vo = c < 14 ? (g & ~15u) + 16u * (uint32_t)c : 0x80000000u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, vo, 0, 0, 0);
+            }
         }
     };
-
     /* activations of K step kb: BM tokens x 256 fp16 and 8 x BM fp32 d8 */
     auto issue_x = [&](int kb, int buf) {
 #pragma unroll
@@ -160,6 +158,10 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
         }
     };
 
+    /* this lane's weight row (B column) and its phase in the LDS window */
+    const int wr = 32 * wave + l32;
+    const uint32_t rowg = (uint32_t)((uint64_t)min(n0 + wr, N - 1) * rb - gbase);
+
     v16f acc[TT], tmp[TT];
 #pragma unroll
     for (int t = 0; t < TT; t++)
@@ -169,77 +171,141 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             tmp[t][r] = 0.0f;
         }
 
-    auto step = [&](int kb, int buf, const Q6WRaw &wc, Q6WRaw &wn) {
-        if (kb + 1 < kb1) {
-            issue_x(kb + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
-            load_w(kb + 1, wn);
-        }
-        const uint32_t sh = ((rowoff + (uint32_t)kb * Q6K_BLOCK_BYTES) & 2u) * 8u;
-        q6v4u QL[4], QH[2];
-#pragma unroll
-        for (int i = 0; i < 4; i++) QL[i] = q6m_align16(wc.a[i], wc.b[i], sh);
-#pragma unroll
-        for (int i = 0; i < 2; i++) QH[i] = q6m_align16(wc.a[4 + i], wc.b[4 + i], sh);
-        const q6v4u SC = q6m_align16(wc.a[6], wc.b[6], sh);
-        const float d = h2f_bits((wc.b[6] >> sh) & 0xffffu);
+    if (kb0 < kb1) {
+        issue_w(kb0);
+        issue_x(kb0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 
+    for (int kb = kb0; kb < kb1; kb++) {
+        const int buf = (kb - kb0) & 1;
+        /* the lane's runs of this block from LDS: ql[64j + 32p + 16h + 0..15],
+         * qh[32j + 16h + 0..15], bytes 192..207 (scales) and d */
+        const uint32_t base = (uint32_t)wr * (Q6M_WCH * 16) + (((rowg + (uint32_t)kb * Q6K_BLOCK_BYTES)) & 15u);
+        const uint32_t sh = (base & 2u) * 8u;
+        q6v4u QL[4], QH[2], SC;
+        uint32_t dword;
+        {
+            const uint32_t X[6] = {16u * h, 32u + 16u * h, 64u + 16u * h, 96u + 16u * h, 128u + 16u * h,
+                                   160u + 16u * h};
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+            for (int i = 0; i < 6; i++) {
+                const uint32_t *p = (const uint32_t *)&sm.w[(base + X[i]) & ~3u];
+                const uint32_t v[5] = {p[0], p[1], p[2], p[3], p[4]};
+                if (i < 4) QL[i] = q6m_align16(v, sh);
+                else QH[i - 4] = q6m_align16(v, sh);
+            }
+            const uint32_t *p = (const uint32_t *)&sm.w[(base + 192u) & ~3u];
+            const uint32_t v[5] = {p[0], p[1], p[2], p[3], p[4]};
+            SC = q6m_align16(v, sh);
+            dword = v[4];
+        }
+        const float d = h2f_bits((dword >> sh) & 0xffffu);
+        __syncthreads();   /* every wave has its runs: the weight buffer is free */
+        if (kb + 1 < kb1) {
+            issue_w(kb + 1);
+            issue_x(kb + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
+        }
+
+        /* The lane's group scales sc = 16*sh + sl of sub-blocks b = 2m, 2m+1
+         * (scale bytes 2b + h, all in dword m), as fp16 pairs: sl/16, -66*sl,
+         * sh and -1056*sh. A byte v < 64 becomes the fp16 1024 + v under
+         * exponent byte 0x64; sh + 8 = (high nibble) ^ 8 for sh = sc >> 4. */
+        q6h2 SL16[4], CL[4], SH[4], CH[4];
+        {
+            const uint32_t sel = h ? 0x04030401u : 0x04020400u;
+            const q6h2 b1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+            const q6h2 b1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
+            const q6h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+            const q6h2 k66 = {(_Float16)-66.0f, (_Float16)-66.0f};
+            const q6h2 k1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                /* the lane's group 8j + 2q + h: scale byte of the 16 */
-                const uint32_t scw = SC[2 * j + (q >> 1)];
-                const int sc = q6m_sext8(scw, 8 * (2 * (q & 1) + h));
-                const int shi = sc >> 4, slo = sc & 15;        /* sc = 16*shi + slo */
-                const _Float16 fh = (_Float16)shi, fl = (_Float16)slo;
-                const _Float16 ch = (_Float16)(-1056 * shi), cl = (_Float16)(-1056 * slo);
-                const q6h2 s_hi = {fh, fh}, s_lo = {fl, fl}, c_hi = {ch, ch}, c_lo = {cl, cl};
-                const q6h2 x16 = {(_Float16)16.0f, (_Float16)16.0f};
-                v16f C[TT];
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    uint32_t v[2];
-#pragma unroll
-                    for (int e = 0; e < 2; e++) {
-                        const uint32_t ql = QL[2 * j + (q & 1)][2 * u + e], qh = QH[j][2 * u + e];
-                        v[e] = q == 0 ? q6m_raw<0>(ql, qh) : q == 1 ? q6m_raw<1>(ql, qh)
-                             : q == 2 ? q6m_raw<2>(ql, qh) : q6m_raw<3>(ql, qh);
-                    }
-                    q6v8h Blo, Bhi;
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        /* fp16 (1024 + q) pairs from bytes 2(k&1), 2(k&1)+1 of v[k>>1] */
-                        const q6h2 t = q6m_h2(__builtin_amdgcn_perm(0x64646464u, v[k >> 1],
-                                                                    (k & 1) ? 0x04030402u : 0x04010400u));
-                        const q6h2 lo = __builtin_elementwise_fma(t, s_lo, c_lo);          /* (q-32)*sl */
-                        const q6h2 hi = __builtin_elementwise_fma(t, s_hi, c_hi) * x16;    /* 16(q-32)*sh */
-                        Blo[2 * k] = lo.x;
-                        Blo[2 * k + 1] = lo.y;
-                        Bhi[2 * k] = hi.x;
-                        Bhi[2 * k + 1] = hi.y;
-                    }
-#pragma unroll
-                    for (int t = 0; t < TT; t++) {
-                        const int tok = 32 * t + l32;
-                        const int chunk = (16 * j + 4 * q + 2 * h + u) ^ (tok & 31);
-                        const q6v8h A = *(const q6v8h *)&sm.xs[buf][tok][8 * chunk];
-                        const v16f zero = {};
-                        C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Blo, u == 0 ? zero : C[t], 0, 0, 0);
-                        C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bhi, C[t], 0, 0, 0);
-                    }
-                }
-                /* C is the exact integer J_b; scale by the tokens' d8 */
-#pragma unroll
-                for (int t = 0; t < TT; t++) {
-#pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const q6v4f f4 = *(const q6v4f *)&sm.d8[buf][4 * j + q][32 * t + 8 * g + 4 * h];
-#pragma unroll
-                        for (int e = 0; e < 4; e++) tmp[t][4 * g + e] = fmaf(C[t][4 * g + e], f4[e], tmp[t][4 * g + e]);
-                    }
-                }
+            for (int m = 0; m < 4; m++) {
+                const uint32_t lo = SC[m] & 0x0F0F0F0Fu;
+                const uint32_t hi = ((SC[m] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+                const q6h2 sl = q6m_h2(__builtin_amdgcn_perm(0x64646464u, lo, sel)) - b1024;
+                const q6h2 shv = q6m_h2(__builtin_amdgcn_perm(0x64646464u, hi, sel)) - b1032;
+                SL16[m] = sl * k16;      /* exact: sl <= 15 */
+                CL[m] = sl * k66;
+                SH[m] = shv;
+                CH[m] = shv * k1056;
             }
         }
+
+        /* sub-block (j, q): 2 x 2 MFMAs per token tile (K halves u, scale
+         * parts). The activations are 16*q8, so the parts are
+         * (q-32)*sh and (q-32)*sl/16, both exact in fp16: fma(1024+q, s, c)
+         * with c = -1056*sh or -66*sl. */
+        auto mfma_sb = [&](int j, int q, v16f (&C)[TT]) {
+            const int b = 4 * j + q, m = b >> 1, odd = b & 1;
+            const _Float16 sl16 = odd ? SL16[m].y : SL16[m].x, cl = odd ? CL[m].y : CL[m].x;
+            const _Float16 shh = odd ? SH[m].y : SH[m].x, ch = odd ? CH[m].y : CH[m].x;
+            const q6h2 s_hi = {shh, shh}, s_lo = {sl16, sl16}, c_hi = {ch, ch}, c_lo = {cl, cl};
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                uint32_t v[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint32_t ql = QL[2 * j + (q & 1)][2 * u + e], qh = QH[j][2 * u + e];
+                    v[e] = q == 0 ? q6m_raw<0>(ql, qh) : q == 1 ? q6m_raw<1>(ql, qh)
+                         : q == 2 ? q6m_raw<2>(ql, qh) : q6m_raw<3>(ql, qh);
+                }
+                q6v8h Blo, Bhi;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    /* fp16 (1024 + q) pairs from bytes 2(k&1), 2(k&1)+1 of v[k>>1] */
+                    const q6h2 t = q6m_h2(__builtin_amdgcn_perm(0x64646464u, v[k >> 1],
+                                                                (k & 1) ? 0x04030402u : 0x04010400u));
+                    const q6h2 lo = __builtin_elementwise_fma(t, s_lo, c_lo);   /* (q-32)*sl/16 */
+                    const q6h2 hi = __builtin_elementwise_fma(t, s_hi, c_hi);   /* (q-32)*sh */
+                    Blo[2 * k] = lo.x;
+                    Blo[2 * k + 1] = lo.y;
+                    Bhi[2 * k] = hi.x;
+                    Bhi[2 * k + 1] = hi.y;
+                }
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const int tok = 32 * t + l32;
+                    const int chunk = (16 * j + 4 * q + 2 * h + u) ^ (tok & 31);
+                    const q6v8h A = *(const q6v8h *)&sm.xs[buf][tok][8 * chunk];
+                    const v16f zero = {};
+                    C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Blo, u == 0 ? zero : C[t], 0, 0, 0);
+                    C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bhi, C[t], 0, 0, 0);
+                }
+            }
+        };
+        /* C is the exact integer J_b; scale by the tokens' d8 */
+        auto epi_sb = [&](int j, int q, const v16f (&C)[TT]) {
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const q6v4f f4 = *(const q6v4f *)&sm.d8[buf][4 * j + q][32 * t + 8 * g + 4 * h];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) tmp[t][4 * g + e] = fmaf(C[t][4 * g + e], f4[e], tmp[t][4 * g + e]);
+                }
+            }
+        };
+        /* software pipeline: the MFMAs of sub-block b+1 run while the VALU
+         * scales sub-block b */
+        v16f Ca[TT], Cb[TT];
+        mfma_sb(0, 0, Ca);
+        mfma_sb(0, 1, Cb);
+        epi_sb(0, 0, Ca);
+        mfma_sb(0, 2, Ca);
+        epi_sb(0, 1, Cb);
+        mfma_sb(0, 3, Cb);
+        epi_sb(0, 2, Ca);
+        mfma_sb(1, 0, Ca);
+        epi_sb(0, 3, Cb);
+        mfma_sb(1, 1, Cb);
+        epi_sb(1, 0, Ca);
+        mfma_sb(1, 2, Ca);
+        epi_sb(1, 1, Cb);
+        mfma_sb(1, 3, Cb);
+        epi_sb(1, 2, Ca);
+        epi_sb(1, 3, Cb);
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
@@ -247,20 +313,8 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                 acc[t][r] = fmaf(tmp[t][r], d, acc[t][r]);
                 tmp[t][r] = 0.0f;
             }
-        __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads (to LDS and registers) have landed */
+        __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads to LDS have landed */
         __syncthreads();
-    };
-
-    Q6WRaw w0, w1;
-    if (kb0 < kb1) {
-        issue_x(kb0, 0);
-        load_w(kb0, w0);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int kb = kb0; kb < kb1; kb += 2) {
-        step(kb, 0, w0, w1);
-        if (kb + 1 < kb1) step(kb + 1, 1, w1, w0);
     }
 
     /* lane holds weight row n0 + 32*wave + l32 for tokens
@@ -281,13 +335,11 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
 extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits,
                                                 hipStream_t s);
 
-/* Token tile: 32 for up to 32 tokens, else 64. */
-extern "C" int sera_q6k_mmq_bm(int M) { return M <= 32 ? 32 : 64; }
 
 /* K splits: double while the grid holds fewer than 512 tiles and each split
  * keeps at least 2 super-blocks. */
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K) {
-    const int bm = sera_q6k_mmq_bm(M);
+    const int bm = 32;
     const int tiles = ((M + bm - 1) / bm) * ((N + Q6M_BN - 1) / Q6M_BN);
     const int nkb = K / Q4K_QK;
     int s = 1;
@@ -322,6 +374,5 @@ extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, floa
     const uint8_t *w = (const uint8_t *)W;
     const uint64_t wbytes = (uint64_t)N * (uint64_t)(K / Q4K_QK) * Q6K_BLOCK_BYTES;
     if (splits < 1) splits = 1;
-    if (sera_q6k_mmq_bm(M) == 32) return launch_q6k_mmq<1, 2>(w, wbytes, xh, d8t, y, partial, M, Mpad, N, K, splits, s);
-    return launch_q6k_mmq<2, 1>(w, wbytes, xh, d8t, y, partial, M, Mpad, N, K, splits, s);
+    return launch_q6k_mmq<1, 2>(w, wbytes, xh, d8t, y, partial, M, Mpad, N, K, splits, s);
 }

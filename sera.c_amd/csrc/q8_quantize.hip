@@ -16,7 +16,7 @@
  *  mmq D4 (MMQ activations for Q6_K weights), the same kernel with the D4
  *     layout the reference selects for Q6_K (cuda/mmq/mmq.cuh:64-103,
  *     cuda/q3_mmq.cu:303-316): quants as above, fp32 d = 1/d_inv, no sum.
- *     This library stores the quants as fp16 (exact) for the fp16-MFMA
+ *     This library stores 16 * quant as fp16 (exact) for the fp16-MFMA
  *     Q6_K kernel and d transposed per 256-wide K step (see q4k_common.h).
  *
  * Division is IEEE correctly rounded (hipcc default), roundf rounds half
@@ -106,9 +106,15 @@ __global__ __launch_bounds__(256) void sera_q8_1_mmq_kernel(
     }
 }
 
-/* D4 quantizer for the Q6_K MMQ stage: quants as fp16 [Mpad][K], fp32 d
- * as [K/256][8][Mpad]. grid = (ceil(K/1024), Mpad); rows >= M are zero. */
-__global__ __launch_bounds__(256) void sera_q8_1_mmq_d4_kernel(
+/* Q6_K MMQ-layout stage: 16 * quant as fp16 [Mpad][K], fp32 d as
+ * [K/256][8][Mpad]; grid = (ceil(K/1024), Mpad); rows >= M are zero.
+ * ROW = false: the D4 quantizer (MMQ arithmetic): d_inv = 127/amax,
+ *   q = roundf(x*d_inv), d = 1/d_inv in fp32.
+ * ROW = true: the row quantizer's values (MMVQ arithmetic, the same as
+ *   sera_q8_1_row_kernel): d = amax/127, q = roundf(x/d), and the scale
+ *   kept as fp32(fp16(d)), the d8 the MMVQ formula multiplies by. */
+template <bool ROW>
+__global__ __launch_bounds__(256) void sera_q8_1_q6k_stage_kernel(
         const float *__restrict__ x, int M, int Mpad, int K, _Float16 *__restrict__ xh,
         float *__restrict__ d8t) {
     const int row = blockIdx.y;
@@ -122,27 +128,42 @@ __global__ __launch_bounds__(256) void sera_q8_1_mmq_d4_kernel(
     for (int off = 4; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
     float q0 = 0.0f, q1 = 0.0f, q2 = 0.0f, q3 = 0.0f, d = 0.0f;
     if (amax != 0.0f) {
-        const float d_inv = 127.0f / amax;
-        q0 = roundf(v.x * d_inv);
-        q1 = roundf(v.y * d_inv);
-        q2 = roundf(v.z * d_inv);
-        q3 = roundf(v.w * d_inv);
-        d = 1.0f / d_inv;
+        if (ROW) {
+            const float dr = amax / 127.0f;
+            q0 = roundf(v.x / dr);
+            q1 = roundf(v.y / dr);
+            q2 = roundf(v.z / dr);
+            q3 = roundf(v.w / dr);
+            d = h2f_bits(f2h_bits(dr));
+        } else {
+            const float d_inv = 127.0f / amax;
+            q0 = roundf(v.x * d_inv);
+            q1 = roundf(v.y * d_inv);
+            q2 = roundf(v.z * d_inv);
+            q3 = roundf(v.w * d_inv);
+            d = 1.0f / d_inv;
+        }
     }
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    const h4 hq = {(_Float16)q0, (_Float16)q1, (_Float16)q2, (_Float16)q3};   /* |q| <= 127: exact */
+    /* stored as 16*q: |16q| <= 2032 is exact in fp16 */
+    const h4 hq = {(_Float16)(16.0f * q0), (_Float16)(16.0f * q1), (_Float16)(16.0f * q2), (_Float16)(16.0f * q3)};
     *(h4 *)(xh + (size_t)row * K + k) = hq;
     if ((threadIdx.x & 7) == 0)
         d8t[((size_t)(k >> 8) * 8 + ((k >> 5) & 7)) * Mpad + row] = d;
 }
 
-extern "C" hipError_t sera_launch_q8_1_mmq_d4(const float *x, int M, int Mpad, int K, void *stage,
-                                              hipStream_t stream) {
+/* row_formula = 0: D4 (MMQ) values, 1: row-quantizer (MMVQ) values. */
+extern "C" hipError_t sera_launch_q8_1_q6k_stage(const float *x, int M, int Mpad, int K, int row_formula,
+                                                 void *stage, hipStream_t stream) {
     const sera_stage_layout L = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K);
     char *base = (char *)stage;
     dim3 grid((K + 1023) / 1024, Mpad);
-    hipLaunchKernelGGL(sera_q8_1_mmq_d4_kernel, grid, dim3(256), 0, stream, x, M, Mpad, K,
-                       (_Float16 *)(base + L.qs), (float *)(base + L.ds));
+    if (row_formula)
+        hipLaunchKernelGGL(sera_q8_1_q6k_stage_kernel<true>, grid, dim3(256), 0, stream, x, M, Mpad, K,
+                           (_Float16 *)(base + L.qs), (float *)(base + L.ds));
+    else
+        hipLaunchKernelGGL(sera_q8_1_q6k_stage_kernel<false>, grid, dim3(256), 0, stream, x, M, Mpad, K,
+                           (_Float16 *)(base + L.qs), (float *)(base + L.ds));
     return hipGetLastError();
 }
 

@@ -21,6 +21,10 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *sta
 extern "C" int sera_mmq_slot_floats(int M);
 extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
                                              int M, int N, int K, int splits, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K,
+                                           int rows, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
+                                          int K, int splits, hipStream_t s);
 
 /* `warmup` untimed then `iters` timed calls of q3_cuda_q4k_linear; weight i
  * of the call is weights[i % nweights]. elapsed_ms: first-to-last event of
@@ -51,7 +55,8 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
 
 /* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ, 2 / 3 = few-token
  * kernel with the MMVQ / MMQ formula, 4 = stream-K MMQ (partial = slots, then
- * the zeroed tile counters).
+ * the zeroed tile counters), 5 = Q6_K MMVQ (param = rows per wave), 6 = Q6_K
+ * MMQ (param = splits).
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
  * elapsed time over iters (each launch's duration plus the dispatch gap to
@@ -67,6 +72,8 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
         switch (path) {
             case 0: return sera_launch_q4k_mmvq(w, stage, y, M, N, K, param, s);
             case 1: return sera_launch_q4k_mmq(w, stage, y, partial, M, N, K, param, s);
+            case 5: return sera_launch_q6k_mmvq(w, stage, y, M, N, K, param, s);
+            case 6: return sera_launch_q6k_mmq(w, stage, y, partial, M, N, K, param, s);
             case 4: return sera_launch_q4k_mmq_streamk(
                         w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),
                         M, N, K, param, s);

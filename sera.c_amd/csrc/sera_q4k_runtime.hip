@@ -26,7 +26,8 @@ extern "C" int sera_mmvq_rows_per_wave(int N, int M);
 extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K,
                                            int rows, hipStream_t s);
 extern "C" int sera_q6k_mmvq_rows(int N, int M);
-extern "C" hipError_t sera_launch_q8_1_mmq_d4(const float *x, int M, int Mpad, int K, void *stage, hipStream_t s);
+extern "C" hipError_t sera_launch_q8_1_q6k_stage(const float *x, int M, int Mpad, int K, int row_formula,
+                                                 void *stage, hipStream_t s);
 extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
                                           int K, int splits, hipStream_t s);
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
@@ -392,6 +393,13 @@ extern "C" int sera_q6k_mmvq(const void *W, const void *row_stage, float *Y, int
                ? 0 : fail(-3, "sera_q6k_mmvq: launch failed");
 }
 
+/* Q6_K batches from this size up to the MMVQ cap run the MFMA tile kernel
+ * on a row-formula stage (the MMVQ arithmetic) instead of the dot4 MMVQ
+ * kernel, which is VALU-bound there. */
+#define SERA_Q6K_VEC_MFMA_MIN_BATCH 5
+
+extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
+
 extern "C" int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
                                   int timed) {
     if (!check_shape("sera_q6k_dense_vec", W, X, Y, M, N, K)) return -1;
@@ -400,16 +408,28 @@ extern "C" int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M
     if (!q6k_shape_ok("sera_q6k_dense_vec", N, K)) return -1;
     if (!g_arena) return fail(-1, "sera_q6k_dense_vec: no arena attached");
     hipStream_t s = (hipStream_t)stream;
-    const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
-    if (stage_bytes > g_arena_bytes)
-        return fail(-1, "sera_q6k_dense_vec: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
+    const bool mfma = M >= SERA_Q6K_VEC_MFMA_MIN_BATCH;
+    const int Mpad = sera_q6k_mmq_padded_rows(M);
+    const size_t stage_bytes = mfma ? sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K).total
+                                    : sera_row_stage_layout((size_t)M, (size_t)K).total;
+    const int splits = mfma && ((size_t)M * N) % 4 == 0 ? sera_q6k_mmq_splits(M, N, K) : 1;
+    const size_t partial_bytes = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+    if (stage_bytes + partial_bytes > g_arena_bytes)
+        return fail(-1, "sera_q6k_dense_vec: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
+                    g_arena_bytes);
     if (timed) record(g_ev.quant_begin, s);
-    if (sera_launch_q8_1_row(X, M, K, g_arena, s) != hipSuccess)
-        return fail(-2, "sera_q6k_dense_vec: quantize launch failed");
+    const hipError_t qe = mfma ? sera_launch_q8_1_q6k_stage(X, M, Mpad, K, 1, g_arena, s)
+                               : sera_launch_q8_1_row(X, M, K, g_arena, s);
+    if (qe != hipSuccess) return fail(-2, "sera_q6k_dense_vec: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    if (sera_launch_q6k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess)
+    if (mfma) {
+        float *partial = partial_bytes ? (float *)(g_arena + stage_bytes) : nullptr;
+        if (sera_launch_q6k_mmq(W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
+            return fail(-3, "sera_q6k_dense_vec: tile kernel launch failed");
+    } else if (sera_launch_q6k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
         return fail(-3, "sera_q6k_dense_vec: mmvq launch failed");
+    }
     if (timed) record(g_ev.kernel_end, s);
     return 0;
 }
@@ -422,7 +442,7 @@ int q6k_splits(int M, int N, int K) {
 
 extern "C" int sera_q6k_kernel_launches(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
-    if (M <= SERA_Q4K_MMVQ_MAX_BATCH) return 2;
+    if (M < SERA_Q6K_VEC_MFMA_MIN_BATCH) return 2;
     return q6k_splits(M, N, K) > 1 ? 3 : 2;
 }
 
@@ -444,8 +464,18 @@ extern "C" int sera_q8_1_quantize_mmq_d4(const float *X, int M, int K, void *sta
     if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK)
         return fail(-1, "sera_q8_1_quantize_mmq_d4: bad arguments");
     if (((uintptr_t)X & 15u) != 0) return fail(-1, "sera_q8_1_quantize_mmq_d4: X must be 16-byte aligned");
-    return sera_launch_q8_1_mmq_d4(X, M, sera_q6k_mmq_padded_rows(M), K, stage, (hipStream_t)stream) == hipSuccess
+    return sera_launch_q8_1_q6k_stage(X, M, sera_q6k_mmq_padded_rows(M), K, 0, stage, (hipStream_t)stream) ==
+                   hipSuccess
                ? 0 : fail(-2, "sera_q8_1_quantize_mmq_d4: launch failed");
+}
+
+extern "C" int sera_q8_1_quantize_row_q6k(const float *X, int M, int K, void *stage, void *stream) {
+    if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK)
+        return fail(-1, "sera_q8_1_quantize_row_q6k: bad arguments");
+    if (((uintptr_t)X & 15u) != 0) return fail(-1, "sera_q8_1_quantize_row_q6k: X must be 16-byte aligned");
+    return sera_launch_q8_1_q6k_stage(X, M, sera_q6k_mmq_padded_rows(M), K, 1, stage, (hipStream_t)stream) ==
+                   hipSuccess
+               ? 0 : fail(-2, "sera_q8_1_quantize_row_q6k: launch failed");
 }
 
 extern "C" int sera_q6k_mmq_splits_for(int M, int N, int K) {
@@ -482,7 +512,7 @@ extern "C" int sera_q6k_dense(const void *W, const float *X, float *Y, int M, in
                     g_arena_bytes);
     float *partial = partial_bytes ? (float *)(g_arena + stage_bytes) : nullptr;
     if (timed) record(g_ev.quant_begin, s);
-    if (sera_launch_q8_1_mmq_d4(X, M, Mpad, K, g_arena, s) != hipSuccess)
+    if (sera_launch_q8_1_q6k_stage(X, M, Mpad, K, 0, g_arena, s) != hipSuccess)
         return fail(-2, "sera_q6k_dense: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);

@@ -120,6 +120,7 @@ def load():
         "sera_q8_1_q6k_mmq_stage_bytes": ([I, I], SZ),
         "sera_q8_1_q6k_mmq_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ)], None),
         "sera_q8_1_quantize_mmq_d4": ([P, I, I, P, P], I),
+        "sera_q8_1_quantize_row_q6k": ([P, I, I, P, P], I),
         "sera_q6k_mmq": ([P, P, P, P, I, I, I, I, P], I),
         "sera_q6k_mmq_splits_for": ([I, I, I], I),
         "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
@@ -306,6 +307,13 @@ def quantize_mmq_d4(x, stage, stream=None):
     M, K = x.shape
     _check(load().sera_q8_1_quantize_mmq_d4(_ptr(x), M, K, _ptr(stage), _stream(stream)),
            "sera_q8_1_quantize_mmq_d4")
+
+
+def quantize_row_q6k(x, stage, stream=None):
+    """Row-quantizer values (MMVQ arithmetic) in the Q6_K tile-kernel layout."""
+    M, K = x.shape
+    _check(load().sera_q8_1_quantize_row_q6k(_ptr(x), M, K, _ptr(stage), _stream(stream)),
+           "sera_q8_1_quantize_row_q6k")
 
 
 def q6k_mmvq(W, stage, out, M, N, K, rows_per_wave=0, stream=None):

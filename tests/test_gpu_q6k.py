@@ -96,9 +96,50 @@ def test_q8_mmq_d4_bit_exact(torch, M, K):
     torch.cuda.synchronize()
     xh, d = decode_d4_stage(stage, M, K)
     eq, ed = oracle.q8_1_mmq_d4(x)
-    assert np.array_equal(xh[:M].astype(np.int32), eq.astype(np.int32))
+    assert np.array_equal(xh[:M].astype(np.int32), 16 * eq.astype(np.int32))   # stored as 16 * q
     assert np.array_equal(d[:M].view(np.uint32), ed.view(np.uint32))
     assert not xh[M:].any() and not d[M:].any()
+
+
+@pytest.mark.parametrize("M,K", [(1, 256), (5, 5120), (8, 25600), (33, 768)])
+def test_q8_row_q6k_stage_bit_exact(torch, M, K):
+    """The row quantizer's values (MMVQ arithmetic) in the tile-kernel layout:
+    16 * quant, and d8 = fp32 of the fp16 scale."""
+    say(f"case q8_row_q6k M={M} K={K}")
+    rng = np.random.default_rng(M * 5 + K)
+    x = outlier_activations(rng, M, K)
+    x[0, 32:64] = 0.0
+    stage = torch.empty(q3q4.q6k_mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+    stage.fill_(0x5A)
+    q3q4.quantize_row_q6k(dev(torch, x), stage)
+    torch.cuda.synchronize()
+    xh, d = decode_d4_stage(stage, M, K)
+    eq, ed, _ = oracle.q8_1_row(x)
+    assert np.array_equal(xh[:M].astype(np.int32), 16 * eq.astype(np.int32))
+    assert np.array_equal(d[:M].view(np.uint32), oracle.h2f(ed).view(np.uint32))
+    assert not xh[M:].any() and not d[M:].any()
+
+
+@pytest.mark.parametrize("N,K", [(256, 256), (515, 5120), (64, 25600), (203, 2304)])
+def test_q6k_tile_kernel_mmvq_formula_parity(torch, N, K):
+    """The tile kernel on a row-formula stage computes the MMVQ formula
+    (what sera_q6k_dense_vec runs for 5..8 tokens)."""
+    rng = np.random.default_rng(N * 7 + K)
+    W = q6k_weights_with_edges(rng, N, K)
+    Wd = dev(torch, W)
+    for M in (1, 3, 5, 6, 7, 8, 16):
+        say(f"case q6k tile mmvq-formula M={M} N={N} K={K}")
+        x = outlier_activations(rng, M, K)
+        stage = torch.empty(q3q4.q6k_mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+        q3q4.quantize_row_q6k(dev(torch, x), stage)
+        xq, xd, _ = oracle.q8_1_row(x)
+        ref = oracle.gemm_q6k(W, xq, oracle.h2f(xd), N, K)
+        s = q3q4.q6k_mmq_splits(M, N, K)
+        partial = torch.empty(s * M * N, dtype=torch.float32, device="cuda") if s > 1 else None
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        q3q4.q6k_mmq(Wd, stage, y, M, N, K, splits=s, partial=partial)
+        torch.cuda.synchronize()
+        check_close(y.cpu().numpy(), ref, f"q6k tile mmvq-formula M={M} N={N} K={K} splits={s}")
 
 
 # ---------------------------------------------------------------------------
