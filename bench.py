@@ -20,7 +20,9 @@ Also printed in the same JSON line:
                 reference's q3_quant.c (oracle/_ref, single thread) plus
                 numpy fp32 matmul, on the full gate/up matrix at M=1
   results       MMVQ sweep M in {1,2,4,8} x {gate/up, down}; MMQ at M=512 on
-                gate/up in int8 TOPS against 5.0 POPS; with --full also
+                gate/up in int8 TOPS against 5.0 POPS; Q6_K (GGUF type 14)
+                through the same ABI on the 25600 -> 5120 down shape (a Q6_K
+                tensor in stock Q4_K_M files): M in {1,4,8} and M=512; with --full also
                 configs 3-5 (all seven projections, M=2048 + LM head, the
                 64-layer decode stream)
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--full] [--no-cpu]
@@ -51,8 +53,8 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def alg_bytes(M, N, K):
-    return N * K * 144 // 256 + M * K * 36 // 32 + M * N * 4
+def alg_bytes(M, N, K, block_bytes=144):
+    return N * K * block_bytes // 256 + M * K * 36 // 32 + M * N * 4
 
 
 def main():
@@ -221,6 +223,10 @@ def main():
     if not args.quick:
         results["mmq_m512_gate"] = mmq_case("gate", gN, gK, 512, garr, args.copies, 20)
 
+    if not args.quick:
+        results["q6k_down"] = q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel,
+                                        args)
+
     if args.full:
         full = []
         for name in ("q", "k", "v", "o", "down"):
@@ -267,6 +273,57 @@ def main():
         "results": results,
     }
     print(json.dumps(out), flush=True)
+
+
+def q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel, args):
+    """Q6_K weights (random ql/qh/scale bytes, fp16 d ~2e-5: the reference
+    repo has no Q6_K quantizer) on the down shape 25600 -> 5120, 4 copies
+    (430 MB) round robin: the whole q3_cuda_q4k_linear call and the kernel
+    alone (MMVQ kernel up to 4 tokens, the fp16-MFMA tile kernel from 5)."""
+    N, K, copies = 5120, 25600, 4
+    ws = []
+    for i in range(copies):
+        gen = torch.Generator(device=dev).manual_seed(700 + i)
+        w = torch.randint(0, 256, (N, K // 256, 210), generator=gen, device=dev, dtype=torch.uint8)
+        d = (torch.rand((N, K // 256), generator=gen, device=dev) + 0.5) * 2e-5
+        w[:, :, 208:210] = d.to(torch.float16).view(torch.uint8).view(N, K // 256, 2)
+        ws.append(w.view(N, -1))
+    arr = (ctypes.c_void_p * copies)(*[w.data_ptr() for w in ws])
+    geo = q3q4.bind_geometry(q3q4.QTYPE_Q6_K, K, N)
+    rows = []
+    iters = max(20, args.steps // 5)
+    for M in (1, 4, 8, 512):
+        x = activations(M, K, 40 + M)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        step_ms = bench_linear(geo, arr, copies, x, y, 5, iters if M < 512 else 10)
+        tile = M >= 5
+        if tile:
+            stage = torch.empty(q3q4.q6k_mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
+            (q3q4.quantize_row_q6k if M <= 8 else q3q4.quantize_mmq_d4)(x, stage)
+            sp = q3q4.q6k_mmq_splits(M, N, K)
+            part = torch.empty(sp * M * N, dtype=torch.float32, device=dev) if sp > 1 else None
+            kavg, _ = bench_kernel(6, arr, copies, stage, y, part, M, N, K, sp, 5, iters if M < 512 else 10)
+            kname = "sera_q6k_mmq_kernel<1, 2>"
+        else:
+            stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
+            q3q4.quantize_row(x, stage)
+            rpw = L.sera_q6k_mmvq_rows_per_wave(M, N)
+            kavg, _ = bench_kernel(5, arr, copies, stage, y, None, M, N, K, rpw, 5, iters)
+            kname = f"sera_q6k_mmvq_kernel<{M}, {rpw}>"
+        b = alg_bytes(M, N, K, 210)
+        ops = 2.0 * M * N * K
+        row = {"M": M, "N": N, "K": K, "kernel": kname,
+               "step_us": round(step_ms * 1e3, 2), "kernel_us": round(kavg * 1e3, 2),
+               "kernel_GBps": round(b / (kavg * 1e-3) / 1e9, 1),
+               "kernel_frac_hbm": round(b / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "kernel_TOPS": round(ops / (kavg * 1e-3) / 1e12, 1),
+               "kernel_frac_int8": round(ops / (kavg * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+        log(f"[bench] q6k down M={M}: step {row['step_us']} us, kernel {row['kernel_us']} us "
+            f"({row['kernel_GBps']} GB/s, {row['kernel_TOPS']} TOPS)")
+        rows.append(row)
+    del ws
+    torch.cuda.empty_cache()
+    return rows
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mmvq_gate_up_m1_hbm_traffic.json")

@@ -336,14 +336,15 @@ extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, 
                                                 hipStream_t s);
 
 
-/* K splits: double while the grid holds fewer than 512 tiles and each split
+/* K splits: double while the grid holds fewer than 1024 (tile, split)
+ * workgroups (two resident per CU, two rounds on 256 CUs) and each split
  * keeps at least 2 super-blocks. */
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K) {
     const int bm = 32;
     const int tiles = ((M + bm - 1) / bm) * ((N + Q6M_BN - 1) / Q6M_BN);
     const int nkb = K / Q4K_QK;
     int s = 1;
-    while (tiles * s < 512 && nkb / (s * 2) >= 2 && s < 16) s *= 2;
+    while (tiles * s < 1024 && nkb / (s * 2) >= 2 && s < 16) s *= 2;
     return s;
 }
 
