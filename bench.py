@@ -224,6 +224,7 @@ def main():
         results["mmq_m512_gate"] = mmq_case("gate", gN, gK, 512, garr, args.copies, 20)
 
     if not args.quick:
+        results["selected_row_lm_head"] = lm_head_rows(torch, dev, bench_kernel)
         results["q6k_down"] = q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel,
                                         args)
 
@@ -273,6 +274,30 @@ def main():
         "results": results,
     }
     print(json.dumps(out), flush=True)
+
+
+def lm_head_rows(torch, dev, bench_kernel):
+    """Selected-row LM head (sera_candidate_logits) on a Q6_K 151936 x 5120
+    output.weight (random Q6_K bytes, fp16 d ~2e-5): 16 branches x 128
+    candidates per call, fp32 hidden; bytes = candidate rows read."""
+    N, K, branches, per = 151936, 5120, 16, 128
+    gen = torch.Generator(device=dev).manual_seed(900)
+    w = torch.randint(0, 256, (N, K // 256, 210), generator=gen, device=dev, dtype=torch.uint8)
+    d = (torch.rand((N, K // 256), generator=gen, device=dev) + 0.5) * 2e-5
+    w[:, :, 208:210] = d.to(torch.float16).view(torch.uint8).view(N, K // 256, 2)
+    arr = (ctypes.c_void_p * 1)(w.data_ptr())
+    hidden = torch.randn((branches, K), generator=gen, device=dev)
+    ids = torch.randint(0, N, (branches * per,), generator=gen, device=dev, dtype=torch.int32)
+    logits = torch.empty(branches * per, dtype=torch.float32, device=dev)
+    kavg, _ = bench_kernel(7, arr, 1, hidden, logits, ids, branches, N, K, per, 10, 200)
+    b = branches * per * (K // 256 * 210) + branches * K * 4 + branches * per * 4
+    row = {"qtype": "Q6_K", "N": N, "K": K, "branches": branches, "candidates_per_branch": per,
+           "kernel": "sera_candidate_logits_kernel<14>", "kernel_us": round(kavg * 1e3, 2),
+           "rows_GBps": round(b / (kavg * 1e-3) / 1e9, 1)}
+    log(f"[bench] selected-row LM head {branches}x{per} Q6_K rows: {row['kernel_us']} us "
+        f"({row['rows_GBps']} GB/s of candidate rows)")
+    del w
+    return row
 
 
 def q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel, args):

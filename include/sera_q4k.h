@@ -210,6 +210,31 @@ int sera_q6k_mmq(const void *W, const void *q6k_mmq_stage, float *Y, float *part
                  int splits, void *stream);
 int sera_q6k_mmq_splits_for(int M, int N, int K);
 
+/* ---- gathered rows of a Q4_K (12) / Q6_K (14) matrix ------------------
+ * fp32 dequant with the expression order of src/q3_quant.c:57-103 (Q4_K
+ * (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32)) and the GGUF Q6_K byte mapping of
+ * q3_quant.c. The reference's device twin q6_value_dev
+ * (src/q3_forward.cu:86-110) indexes ql/qh and the group scale differently
+ * from its own q3_quant.c for most weights of a block; these functions
+ * follow q3_quant.c. hidden must be 16-byte aligned; W as for the linear
+ * calls. */
+
+/* Selected-row LM head: logits[b*C + c] = sum_k w[ids[b*C + c]][k] *
+ * hidden[b][k] for b < branches, c < C = per_branch; fp32 weights times
+ * fp32 hidden (no Q8_1). Replaces candidate_logits_kernel and
+ * candidate_logits_batched_kernel (src/q3_forward.cu:329-370,566-607); the
+ * reference's host wrappers q3_candidate_logits / _batched (:1826-1900)
+ * copy host ids to the device first, here ids are device memory. ids >= N
+ * give NaN logits. */
+int sera_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden, int branches,
+                          const uint32_t *ids, int per_branch, float *logits, void *stream);
+
+/* Embedding row gather: hidden[t][k] = w[ids[t]][k]; ids >= N leave the
+ * row untouched. Replaces q3_cuda_embedding / embedding_kernel
+ * (src/q3_forward.cu:291-322,757-774). */
+int sera_embedding(int qtype, const void *W, int N, int K, const uint32_t *ids, int tokens, float *hidden,
+                   void *stream);
+
 /* ---- bench loops (the role of src/q3_bench_q4_linear.cu:181-226) ------- */
 
 /* `warmup` untimed and `iters` timed q3_cuda_q4k_linear calls on weight
@@ -224,7 +249,9 @@ int sera_q4k_bench_linear(const void *geometry, const void *const *weights, int 
  * 0/1 with param = splits, 4 = stream-K MMQ with param = workgroups and
  * `partial` holding the slots followed by the zeroed tile counters, 5 =
  * Q6_K MMVQ with param = rows per wave, 6 = Q6_K MMQ with param = splits on
- * a Q6_K MMQ stage): `iters` launches back to back between one event pair
+ * a Q6_K MMQ stage, 7 / 8 = selected-row LM head on Q6_K / Q4_K rows with
+ * stage = fp32 hidden [M][K], partial = the M*param candidate ids, param =
+ * candidates per branch): `iters` launches back to back between one event pair
  * on `stream`; *avg_kernel_ms = pair time / iters, *elapsed_ms = pair time. */
 int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, const void *stage,
                           float *Y, float *partial, int M, int N, int K, int param, void *stream,

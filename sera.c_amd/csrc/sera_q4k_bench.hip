@@ -25,6 +25,9 @@ extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, flo
                                            int rows, hipStream_t s);
 extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
                                           int K, int splits, hipStream_t s);
+extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
+                                                   const uint32_t *ids, int branches, int per_branch,
+                                                   float *logits, hipStream_t s);
 
 /* `warmup` untimed then `iters` timed calls of q3_cuda_q4k_linear; weight i
  * of the call is weights[i % nweights]. elapsed_ms: first-to-last event of
@@ -56,7 +59,9 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
 /* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ, 2 / 3 = few-token
  * kernel with the MMVQ / MMQ formula, 4 = stream-K MMQ (partial = slots, then
  * the zeroed tile counters), 5 = Q6_K MMVQ (param = rows per wave), 6 = Q6_K
- * MMQ (param = splits).
+ * MMQ (param = splits), 7 / 8 = selected-row LM head on Q6_K / Q4_K rows
+ * (stage = fp32 hidden [M][K], partial = the M*param candidate ids,
+ * param = candidates per branch, y = logits).
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
  * elapsed time over iters (each launch's duration plus the dispatch gap to
@@ -74,6 +79,9 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
             case 1: return sera_launch_q4k_mmq(w, stage, y, partial, M, N, K, param, s);
             case 5: return sera_launch_q6k_mmvq(w, stage, y, M, N, K, param, s);
             case 6: return sera_launch_q6k_mmq(w, stage, y, partial, M, N, K, param, s);
+            case 7:
+            case 8: return sera_launch_candidate_logits(path == 7 ? 14 : 12, w, N, K, (const float *)stage,
+                                                        (const uint32_t *)partial, M, param, y, s);
             case 4: return sera_launch_q4k_mmq_streamk(
                         w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),
                         M, N, K, param, s);

@@ -31,6 +31,11 @@ extern "C" hipError_t sera_launch_q8_1_q6k_stage(const float *x, int M, int Mpad
 extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
                                           int K, int splits, hipStream_t s);
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
+extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
+                                                   const uint32_t *ids, int branches, int per_branch,
+                                                   float *logits, hipStream_t s);
+extern "C" hipError_t sera_launch_embedding(int qtype, const void *W, int N, int K, const uint32_t *ids, int tokens,
+                                            float *hidden, hipStream_t s);
 extern "C" int sera_mmq_splits(int M, int N, int K);
 extern "C" int sera_skinny_splits(int M, int N, int K);
 extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
@@ -520,6 +525,40 @@ extern "C" int sera_q6k_dense(const void *W, const float *X, float *Y, int M, in
         return fail(-3, "sera_q6k_dense: mmq launch failed");
     if (timed) record(g_ev.kernel_end, s);
     return 0;
+}
+
+/* ---- gathered rows ----------------------------------------------------- */
+
+namespace {
+bool rows_shape_ok(const char *tag, int qtype, const void *W, int N, int K) {
+    if (!W) { fail(-1, "%s: null weight pointer", tag); return false; }
+    if (qtype != 12 && qtype != 14) { fail(-1, "%s: qtype %d is not Q4_K (12) or Q6_K (14)", tag, qtype); return false; }
+    if (N <= 0 || K <= 0 || K % Q4K_QK) { fail(-1, "%s: bad shape N=%d K=%d", tag, N, K); return false; }
+    if (((uintptr_t)W & 15u) != 0) { fail(-1, "%s: W must be 16-byte aligned", tag); return false; }
+    if ((uint64_t)(K / Q4K_QK) * 210u >= (1ull << 30)) { fail(-1, "%s: K=%d too long", tag, K); return false; }
+    return true;
+}
+}  // namespace
+
+extern "C" int sera_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden, int branches,
+                                     const uint32_t *ids, int per_branch, float *logits, void *stream) {
+    if (!rows_shape_ok("sera_candidate_logits", qtype, W, N, K)) return -1;
+    if (!hidden || !ids || !logits) return fail(-1, "sera_candidate_logits: null pointer");
+    if (branches <= 0 || per_branch <= 0 || (int64_t)branches * per_branch > (1 << 28))
+        return fail(-1, "sera_candidate_logits: bad counts branches=%d per_branch=%d", branches, per_branch);
+    if (((uintptr_t)hidden & 15u) != 0) return fail(-1, "sera_candidate_logits: hidden must be 16-byte aligned");
+    return sera_launch_candidate_logits(qtype, W, N, K, hidden, ids, branches, per_branch, logits,
+                                        (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_candidate_logits: launch failed");
+}
+
+extern "C" int sera_embedding(int qtype, const void *W, int N, int K, const uint32_t *ids, int tokens, float *hidden,
+                              void *stream) {
+    if (!rows_shape_ok("sera_embedding", qtype, W, N, K)) return -1;
+    if (!ids || !hidden || tokens <= 0) return fail(-1, "sera_embedding: bad arguments");
+    if (((uintptr_t)hidden & 15u) != 0) return fail(-1, "sera_embedding: hidden must be 16-byte aligned");
+    return sera_launch_embedding(qtype, W, N, K, ids, tokens, hidden, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_embedding: launch failed");
 }
 
 extern "C" void sera_q4k_read_timings(double *quant_ms, double *kernel_ms, double *total_ms) {

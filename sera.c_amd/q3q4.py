@@ -123,6 +123,8 @@ def load():
         "sera_q8_1_quantize_row_q6k": ([P, I, I, P, P], I),
         "sera_q6k_mmq": ([P, P, P, P, I, I, I, I, P], I),
         "sera_q6k_mmq_splits_for": ([I, I, I], I),
+        "sera_candidate_logits": ([I, P, I, I, P, I, P, I, P, P], I),
+        "sera_embedding": ([I, P, I, I, P, I, P, P], I),
         "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_stream": ([P, P, P, P, P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_kernel": ([I, P, I, P, P, P, I, I, I, I, P, I, I,
@@ -328,3 +330,19 @@ def q6k_mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None):
 
 def q6k_mmq_splits(M, N, K):
     return load().sera_q6k_mmq_splits_for(M, N, K)
+
+
+# ---------------------------------------------------------------------------
+# Gathered rows: selected-row LM head, embedding
+# ---------------------------------------------------------------------------
+
+def candidate_logits(qtype, W, N, K, hidden, ids, per_branch, logits, stream=None):
+    """hidden [branches, K] fp32, ids uint32/int32 [branches*per_branch] (device)."""
+    branches = hidden.shape[0]
+    _check(load().sera_candidate_logits(qtype, _ptr(W), N, K, _ptr(hidden), branches, _ptr(ids), per_branch,
+                                        _ptr(logits), _stream(stream)), "sera_candidate_logits")
+
+
+def embedding(qtype, W, N, K, ids, hidden, stream=None):
+    _check(load().sera_embedding(qtype, _ptr(W), N, K, _ptr(ids), ids.numel(), _ptr(hidden), _stream(stream)),
+           "sera_embedding")

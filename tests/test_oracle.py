@@ -517,3 +517,39 @@ def test_q6k_path_oracle_passes_reference_gates_vs_dequant(M):
     cos = (y * ref).sum() / np.sqrt((y * y).sum() * (ref * ref).sum())
     rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
     assert cos > 0.999 and rel < 0.01
+
+
+def test_reference_q6_value_dev_disagrees_with_its_own_dequant(golden_dir):
+    """The reference's device twin for Q6_K gathers (q6_value_dev,
+    src/q3_forward.cu:86-110, used by its embedding and candidate-logit
+    kernels) is restated here only as index arithmetic, to record why this
+    build's gathered-row kernels follow q3_quant.c:78-103 instead: on the
+    reference's own golden blocks the two agree only on the weights where
+    the index maps coincide (16 of each 256). Its group index can also pass
+    the 16 scale bytes and read d and the next block's bytes."""
+    g = np.load(f"{golden_dir}/dequant_q6k_ref.npz")
+    W, deq = g["w"], g["deq"]
+    raw = W.reshape(-1)                             # the blocks back to back
+    ref_rows = deq.reshape(-1, 256)
+    nblk = 24                                       # the seeded blocks
+
+    def q6_value_dev(i, e):
+        b = raw[210 * i:]
+        ql, qh = b[:128].astype(int), b[128:192].astype(int)
+        d = np.float32(b[208:210].view(np.float16)[0])
+        j, l = e // 128, e % 128
+        isx = l // 16
+        if l < 32:
+            q = (ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)
+        elif l < 64:
+            q = (ql[l] & 15) | (((qh[l] >> 2) & 3) << 4)
+        elif l < 96:
+            q = (ql[l - 64] >> 4) | (((qh[l - 64] >> 4) & 3) << 4)
+        else:
+            q = (ql[l - 64] >> 4) | (((qh[l - 64] >> 6) & 3) << 4)
+        s = int(np.int8(b[192 + j * 8 + isx * 2 + (1 if l % 32 >= 16 else 0)].astype(np.int8)))
+        return np.float32(np.float32(d * np.float32(s)) * np.float32(q - 32))
+
+    same = np.array([all(q6_value_dev(i, e) == ref_rows[i, e] for i in range(nblk)) for e in range(256)])
+    assert same[:16].all()                       # weights 0..15: both maps read ql[l], qh[l], sc[0]
+    assert same.sum() <= 32 and not same[16:64].any()
