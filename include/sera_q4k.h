@@ -210,6 +210,35 @@ int sera_q6k_mmq(const void *W, const void *q6k_mmq_stage, float *Y, float *part
                  int splits, void *stream);
 int sera_q6k_mmq_splits_for(int M, int N, int K);
 
+/* ---- fused linear group (the path's edges) -----------------------------
+ * No single reference counterpart: one call replaces the sequence the
+ * reference's forward pass makes around its q3_cuda_q4k_linear calls
+ * (src/q3_forward.cu:1204-1351):
+ *   outputs[i] = op(X) . W_i^T          for i < count (1..4)
+ *   outputs[i] += op(X) . W_i^T         with SERA_LIN_ACCUMULATE, the
+ *       residual add (q3_cuda_residual_add, :167-171,688-700) fused into
+ *       the product's store: bit-identical to product-then-add;
+ *   op(X) = X, or with SERA_LIN_RMSNORM (x * inv_rms) * gamma,
+ *       inv_rms = 1/sqrt(mean(x^2) + eps) (q3_cuda_rms_norm, :117-146,
+ *       659-672; sum order and IEEE sqrt/div as documented in
+ *       q8_quantize.hip), or with SERA_LIN_SILU_MUL (x / (1 + exp(-x))) * X2
+ *       (q3_cuda_silu_mul, :154-161,674-686), computed inside the Q8_1
+ *       quantize (no materialized op(X)).
+ * All weights share K and qtype (geometries are q3_q4_linear_geometry*);
+ * the activations are quantized once for the group (q/k/v and gate/up read
+ * the same normed input), and at decode (Q4_K, M <= 4) the group runs as
+ * one MMVQ launch. Arithmetic per product as q3_cuda_q4k_linear (MMVQ
+ * formula for M <= 8, MMQ above). gamma and X2 must be 16-byte aligned.
+ * Uses the arena of sera_q4k_set_arena / q3_cuda_q4k_linear_set_workspace;
+ * enqueue only. */
+#define SERA_LINEAR_GROUP_MAX 4
+#define SERA_LIN_ACCUMULATE 1u
+#define SERA_LIN_RMSNORM 2u
+#define SERA_LIN_SILU_MUL 4u
+int sera_linear_group(int count, const void *const *geometries, const void *const *weights, float *const *outputs,
+                      const float *X, const float *X2, const float *gamma, float eps, size_t M, unsigned flags,
+                      void *stream);
+
 /* ---- gathered rows of a Q4_K (12) / Q6_K (14) matrix ------------------
  * fp32 dequant with the expression order of src/q3_quant.c:57-103 (Q4_K
  * (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32)) and the GGUF Q6_K byte mapping of

@@ -308,3 +308,50 @@ def linear_reference_q6k(W, X, N, K):
         return gemm_q6k(W, xq, h2f(xd), N, K)
     xq, d = q8_1_mmq_d4(X)
     return gemm_q6k(W, xq, d, N, K)
+
+
+# ---------------------------------------------------------------------------
+# Producers fused into the quantize (numpy float32, IEEE)
+# ---------------------------------------------------------------------------
+
+def rmsnorm_fused_order(H, gamma, eps):
+    """RMSNorm of each row in the order the fused quantizer uses: thread t of
+    256 sums x[t + 256 i]^2 in i order (square exact in double, each sum
+    rounded to float32, as the reference's `float += double` in
+    rms_norm_batched_kernel, src/q3_forward.cu:131-132); an xor butterfly
+    over each 64-thread wave (offsets 32..1); the four wave sums left to
+    right; inv = 1 / sqrt(sum / K + eps) with IEEE float32 division and
+    square root (the reference uses rsqrtf, :143); x = (h * inv) * gamma
+    (:144-145)."""
+    H = np.ascontiguousarray(H, dtype=np.float32)
+    gamma = np.asarray(gamma, np.float32)
+    M, K = H.shape
+    out = np.empty_like(H)
+    eps = np.float32(eps)
+    for m in range(M):
+        h = H[m]
+        part = np.zeros(256, np.float32)
+        for t in range(256):
+            acc = np.float32(0.0)
+            for v in h[t::256].astype(np.float64):
+                acc = np.float32(np.float64(acc) + v * v)
+            part[t] = acc
+        waves = part.reshape(4, 64).copy()
+        idx = np.arange(64)
+        for o in (32, 16, 8, 4, 2, 1):
+            waves = (waves + waves[:, idx ^ o]).astype(np.float32)
+        tot = np.float32(np.float32(np.float32(waves[0, 0] + waves[1, 0]) + waves[2, 0]) + waves[3, 0])
+        inv = np.float32(np.float32(1.0) / np.sqrt(np.float32(np.float32(tot / np.float32(K)) + eps)))
+        out[m] = ((h * inv).astype(np.float32) * gamma).astype(np.float32)
+    return out
+
+
+def silu_mul(G, U):
+    """(g / (1 + exp(-g))) * u in float32 (silu_mul_kernel,
+    src/q3_forward.cu:154-161); numpy's float32 exp may differ from the
+    device expf in the last place."""
+    G = np.asarray(G, np.float32)
+    U = np.asarray(U, np.float32)
+    with np.errstate(over="ignore"):
+        den = (np.float32(1.0) + np.exp(-G)).astype(np.float32)
+    return ((G / den).astype(np.float32) * U).astype(np.float32)

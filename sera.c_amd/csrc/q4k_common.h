@@ -61,6 +61,17 @@ static inline sera_stage_layout sera_mmq_stage_layout(size_t rows_padded, size_t
     return L;
 }
 
+/* What a quantizer reads as its activation row (the producer fused into
+ * the Q8_1 quantize): kind 0 x itself; 1 RMSNorm, (x * inv_rms) * gamma
+ * with inv_rms = 1 / sqrt(mean(x^2) + eps); 2 SiLU-mul,
+ * (x / (1 + exp(-x))) * x2. */
+typedef struct {
+    int kind;
+    const float *x2;
+    const float *gamma;
+    float eps;
+} sera_producer;
+
 /* Q6_K MMQ stage: Mpad is a multiple of the 32-token tile. */
 static inline sera_stage_layout sera_q6k_mmq_stage_layout(size_t rows_padded, size_t K) {
     sera_stage_layout L;

@@ -291,7 +291,7 @@ __device__ __forceinline__ void mmq_segment(
  * m0+BMW*wt+32*t + 8*(r/4) + 4*h + r%4. */
 template <int TT, int WGT, int WGN>
 __device__ __forceinline__ void mmq_store(float *__restrict__ out, int M, int N, int m0, int n0,
-                                          const v16f (&acc)[TT][2]) {
+                                          const v16f (&acc)[TT][2], int accum) {
     constexpr int BMW = MmqShape<TT, WGT, WGN>::BMW;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l32 = lane & 31, h = lane >> 5;
@@ -305,7 +305,10 @@ __device__ __forceinline__ void mmq_store(float *__restrict__ out, int M, int N,
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + BMW * wt + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m < M) out[(size_t)m * N + n] = acc[t][nt][r];
+                if (m < M) {
+                    float *dst = out + (size_t)m * N + n;
+                    *dst = accum ? *dst + acc[t][nt][r] : acc[t][nt][r];
+                }
             }
     }
 }
@@ -316,7 +319,7 @@ template <int TT, int WGT, int WGN, int WPE = 2>
 __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ partial,
-        int M, int N, int K, int kb_per_split) {
+        int M, int N, int K, int kb_per_split, int accum) {
     static_assert(WGT * WGN == 4, "4 waves per workgroup");
     using S = MmqShape<TT, WGT, WGN>;
     __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
@@ -331,7 +334,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
     v16f acc[TT][2];
     mmq_segment<TT, WGT, WGN>(sm, W, xq, xds, N, K, m0, n0, kb_begin, kb_end, acc);
     float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
-    mmq_store<TT, WGT, WGN>(out, M, N, m0, n0, acc);
+    mmq_store<TT, WGT, WGN>(out, M, N, m0, n0, acc, partial ? 0 : accum);
 }
 
 /* Stream-K schedule: P persistent workgroups split the ntiles x nkb
@@ -352,7 +355,7 @@ template <int TT, int WGT, int WGN, int WPE = 2>
 __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ slots,
-        int *__restrict__ counters, int M, int N, int K) {
+        int *__restrict__ counters, int M, int N, int K, int accum) {
     static_assert(WGT * WGN == 4, "4 waves per workgroup");
     using S = MmqShape<TT, WGT, WGN>;
     __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         v16f acc[TT][2];
         mmq_segment<TT, WGT, WGN>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc);
         if (kb0 == 0 && kb1 == nkb) {
-            mmq_store<TT, WGT, WGN>(y, M, N, m0, n0, acc);
+            mmq_store<TT, WGT, WGN>(y, M, N, m0, n0, acc, accum);
         } else {
             /* slot rule: 2c for a contributor c whose range starts inside the
              * tile, 2c + 1 for one that started before it (then the tile is
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
                                 acc[tt][nt][r] = c == c0 ? v : acc[tt][nt][r] + v;
                             }
                 }
-                mmq_store<TT, WGT, WGN>(y, M, N, m0, n0, acc);
+                mmq_store<TT, WGT, WGN>(y, M, N, m0, n0, acc, accum);
             }
         }
         u += kb1 - kb0;
@@ -424,7 +427,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
 
 /* Sums the split-K partials in split order: y = ((p0 + p1) + p2) + ... */
 __global__ __launch_bounds__(256) void sera_splitk_reduce_kernel(
-        const float4 *__restrict__ partial, float4 *__restrict__ y, size_t n4, int splits) {
+        const float4 *__restrict__ partial, float4 *__restrict__ y, size_t n4, int splits, int accum) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n4) return;
     float4 s = partial[i];
@@ -432,16 +435,26 @@ __global__ __launch_bounds__(256) void sera_splitk_reduce_kernel(
         const float4 v = partial[(size_t)k * n4 + i];
         s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
+    if (accum) {
+        const float4 o = y[i];
+        s = make_float4(o.x + s.x, o.y + s.y, o.z + s.z, o.w + s.w);
+    }
     y[i] = s;
 }
 
-/* y[i] = sum over k of partial[k*n + i], k = 0..splits-1 in order; n % 4 == 0. */
-extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits,
-                                                hipStream_t s) {
+/* y[i] (+)= sum over k of partial[k*n + i], k = 0..splits-1 in order, added
+ * to y[i] when accum != 0; n % 4 == 0. */
+extern "C" hipError_t sera_launch_splitk_reduce_acc(const float *partial, float *y, size_t n, int splits, int accum,
+                                                    hipStream_t s) {
     const size_t n4 = n / 4;
     hipLaunchKernelGGL(sera_splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
-                       (const float4 *)partial, (float4 *)y, n4, splits);
+                       (const float4 *)partial, (float4 *)y, n4, splits, accum);
     return hipGetLastError();
+}
+
+extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits,
+                                                hipStream_t s) {
+    return sera_launch_splitk_reduce_acc(partial, y, n, splits, 0, s);
 }
 
 /* Token-tile width of the workgroup for M tokens: 32 (one token tile per
@@ -477,30 +490,40 @@ extern "C" int sera_mmq_padded_rows(int M) {
 
 template <int TT, int WGT, int WGN, int WPE>
 static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
-                                 float *partial, int M, int N, int K, int splits, hipStream_t s) {
+                                 float *partial, int M, int N, int K, int splits, int accum, hipStream_t s) {
     constexpr int BM = 32 * TT * WGT, BN = 64 * WGN;
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     const int nkb = K / Q4K_QK;
     const int per = (nkb + splits - 1) / splits;
     dim3 grid(tiles, splits);
     hipLaunchKernelGGL((sera_q4k_mmq_kernel<TT, WGT, WGN, WPE>), grid, dim3(256), 0, s, W, xq, xds, y,
-                       splits > 1 ? partial : nullptr, M, N, K, per);
+                       splits > 1 ? partial : nullptr, M, N, K, per, accum);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
-    return sera_launch_splitk_reduce(partial, y, (size_t)M * N, splits, s);
+    return sera_launch_splitk_reduce_acc(partial, y, (size_t)M * N, splits, accum, s);
 }
 
-/* partial: M*N*splits floats of scratch when splits > 1 (M*N % 4 == 0). */
+/* partial: M*N*splits floats of scratch when splits > 1 (M*N % 4 == 0);
+ * accum != 0 adds the product to y. */
+extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, float *y, float *partial,
+                                              int M, int N, int K, int splits, int accum, hipStream_t s);
+
 extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
                                           int M, int N, int K, int splits, hipStream_t s) {
+    return sera_launch_q4k_mmq_acc(W, stage, y, partial, M, N, K, splits, 0, s);
+}
+
+extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, float *y, float *partial,
+                                              int M, int N, int K, int splits, int accum, hipStream_t s) {
     const int Mpad = sera_mmq_padded_rows(M);
     const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
     const char *base = (const char *)stage;
     const int8_t *xq = (const int8_t *)(base + L.qs);
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
-    if (sera_mmq_bm(M) == 32) return launch_mmq_cfg<1, 1, 4, 3>(w, xq, xds, y, partial, M, N, K, splits, s);
-    return launch_mmq_cfg<2, 1, 4, 2>(w, xq, xds, y, partial, M, N, K, splits, s);
+    if (sera_mmq_bm(M) == 32)
+        return launch_mmq_cfg<1, 1, 4, 3>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
+    return launch_mmq_cfg<2, 1, 4, 2>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
 }
 
 /* ---- stream-K schedule ---------------------------------------------------- */
@@ -517,10 +540,10 @@ extern "C" int sera_mmq_slot_floats(int M) { return sera_mmq_bm(M) * mmq_bn(sera
 
 template <int TT, int WGT, int WGN, int WPE>
 static hipError_t launch_mmq_streamk_cfg(const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
-                                         float *slots, int *counters, int M, int N, int K, int P,
+                                         float *slots, int *counters, int M, int N, int K, int P, int accum,
                                          hipStream_t s) {
     hipLaunchKernelGGL((sera_q4k_mmq_streamk_kernel<TT, WGT, WGN, WPE>), dim3(P), dim3(256), 0, s, W, xq, xds, y,
-                       slots, counters, M, N, K);
+                       slots, counters, M, N, K, accum);
     return hipGetLastError();
 }
 
@@ -528,8 +551,18 @@ static hipError_t launch_mmq_streamk_cfg(const uint8_t *W, const int8_t *xq, con
  * workgroups the device keeps resident, and ntiles*K/256 >= P).
  * slots: 2*P*sera_mmq_slot_floats(M) floats; counters: sera_mmq_tiles(M,N)
  * ints, zero on entry and zero again on exit. */
+extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots,
+                                                      int *counters, int M, int N, int K, int P, int accum,
+                                                      hipStream_t s);
+
 extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots,
                                                   int *counters, int M, int N, int K, int P, hipStream_t s) {
+    return sera_launch_q4k_mmq_streamk_acc(W, stage, y, slots, counters, M, N, K, P, 0, s);
+}
+
+extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots,
+                                                      int *counters, int M, int N, int K, int P, int accum,
+                                                      hipStream_t s) {
     const int Mpad = sera_mmq_padded_rows(M);
     const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
     const char *base = (const char *)stage;
@@ -537,6 +570,6 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *sta
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
     if (sera_mmq_bm(M) == 32)
-        return launch_mmq_streamk_cfg<1, 1, 4, 3>(w, xq, xds, y, slots, counters, M, N, K, P, s);
-    return launch_mmq_streamk_cfg<2, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, s);
+        return launch_mmq_streamk_cfg<1, 1, 4, 3>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
+    return launch_mmq_streamk_cfg<2, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
 }

@@ -62,10 +62,30 @@ struct MmvqRegs {
     v4u qa[HR], qc[HR];
 };
 
+/* Up to SERA_MMVQ_GROUP weight matrices of one K that read the same
+ * activations (q/k/v, gate/up): workgroups [tile_end[g-1], tile_end[g])
+ * take matrix g. accum != 0 adds to y instead of overwriting it. */
+#define SERA_MMVQ_GROUP 4
+struct MmvqGroup {
+    const uint8_t *W[SERA_MMVQ_GROUP];
+    float *y[SERA_MMVQ_GROUP];
+    int N[SERA_MMVQ_GROUP];
+    int tile_end[SERA_MMVQ_GROUP];
+    int count;
+    int accum;
+};
+
 template <int NCOLS, int R, int NW>
 __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
-        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
-        const float4 *__restrict__ dsf, float *__restrict__ y, int N, int K) {
+        MmvqGroup grp, const int8_t *__restrict__ xq, const float4 *__restrict__ dsf, int K) {
+    int gi = 0;
+#pragma unroll
+    for (int i = 1; i < SERA_MMVQ_GROUP; i++)
+        if (i < grp.count && (int)blockIdx.x >= grp.tile_end[i - 1]) gi = i;
+    const uint8_t *__restrict__ W = grp.W[gi];
+    float *__restrict__ y = grp.y[gi];
+    const int N = grp.N[gi];
+    const int tile = (int)blockIdx.x - (gi ? grp.tile_end[gi - 1] : 0);
     constexpr int HR = R / 2;              /* rows per lane */
     __shared__ float s_part[NW][R][NCOLS];
     const int lane = threadIdx.x & 63;
@@ -78,7 +98,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
      * buffer load covers the vector offset but not the scalar row step, so
      * no row past N may be addressed. The launcher keeps R <= N, or R = 2
      * where row 1 sits in the vector offset. */
-    const int tile0 = blockIdx.x * R;
+    const int tile0 = tile * R;
     const int row0 = tile0 + R > N && N >= R ? N - R : tile0;
     const int nb = K / Q4K_QK;
     const int ngroups = (nb + 7) >> 3;
@@ -213,16 +233,21 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
         float v = s_part[0][r][c];
 #pragma unroll
         for (int w = 1; w < NW; w++) v += s_part[w][r][c];
-        if (row0 + r >= tile0 && row0 + r < N) y[(size_t)c * N + row0 + r] = v;
+        if (row0 + r >= tile0 && row0 + r < N) {
+            float *dst = y + (size_t)c * N + row0 + r;
+            *dst = grp.accum ? *dst + v : v;
+        }
     }
 }
 
 template <int NCOLS, int R, int NW>
-static hipError_t launch_mmvq(const uint8_t *W, const int8_t *xq, const float4 *dsf,
-                              float *y, int N, int K, hipStream_t s) {
-    dim3 grid((N + R - 1) / R);
-    hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW>), grid, dim3(NW * 64), 0, s,
-                       W, xq, dsf, y, N, K);
+static hipError_t launch_mmvq(MmvqGroup grp, const int8_t *xq, const float4 *dsf, int K, hipStream_t s) {
+    int tiles = 0;
+    for (int i = 0; i < grp.count; i++) {
+        tiles += (grp.N[i] + R - 1) / R;
+        grp.tile_end[i] = tiles;
+    }
+    hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW>), dim3(tiles), dim3(NW * 64), 0, s, grp, xq, dsf, K);
     return hipGetLastError();
 }
 
@@ -237,51 +262,68 @@ extern "C" int sera_mmvq_rows_per_wave(int N, int M) {
 }
 
 template <int NCOLS, int R>
-static hipError_t dispatch_nw(int K, const uint8_t *W, const int8_t *xq, const float4 *dsf,
-                              float *y, int N, hipStream_t s) {
+static hipError_t dispatch_nw(int K, const MmvqGroup &grp, const int8_t *xq, const float4 *dsf, hipStream_t s) {
     const int ngroups = (K / Q4K_QK + 7) / 8;
     switch (ngroups >= 4 ? 4 : ngroups) {
-        case 1: return launch_mmvq<NCOLS, R, 1>(W, xq, dsf, y, N, K, s);
-        case 2: return launch_mmvq<NCOLS, R, 2>(W, xq, dsf, y, N, K, s);
-        case 3: return launch_mmvq<NCOLS, R, 3>(W, xq, dsf, y, N, K, s);
-        default: return launch_mmvq<NCOLS, R, 4>(W, xq, dsf, y, N, K, s);
+        case 1: return launch_mmvq<NCOLS, R, 1>(grp, xq, dsf, K, s);
+        case 2: return launch_mmvq<NCOLS, R, 2>(grp, xq, dsf, K, s);
+        case 3: return launch_mmvq<NCOLS, R, 3>(grp, xq, dsf, K, s);
+        default: return launch_mmvq<NCOLS, R, 4>(grp, xq, dsf, K, s);
     }
 }
 
 template <int NCOLS>
-static hipError_t dispatch_r(int r, const uint8_t *W, const int8_t *xq, const float4 *dsf,
-                             float *y, int N, int K, hipStream_t s) {
+static hipError_t dispatch_r(int r, const MmvqGroup &grp, const int8_t *xq, const float4 *dsf, int K,
+                             hipStream_t s) {
     /* register budget: R/2 x M partial sums plus two sets of loads */
     if (NCOLS > 2 && r > 8) r = 8;
     if (NCOLS > 4 && r > 4) r = 4;
     switch (r) {
-        case 16: if constexpr (NCOLS <= 2) return dispatch_nw<NCOLS, 16>(K, W, xq, dsf, y, N, s);
+        case 16: if constexpr (NCOLS <= 2) return dispatch_nw<NCOLS, 16>(K, grp, xq, dsf, s);
                  [[fallthrough]];
-        case 8: if constexpr (NCOLS <= 4) return dispatch_nw<NCOLS, 8>(K, W, xq, dsf, y, N, s);
+        case 8: if constexpr (NCOLS <= 4) return dispatch_nw<NCOLS, 8>(K, grp, xq, dsf, s);
                 [[fallthrough]];
-        case 4: return dispatch_nw<NCOLS, 4>(K, W, xq, dsf, y, N, s);
-        default: return dispatch_nw<NCOLS, 2>(K, W, xq, dsf, y, N, s);
+        case 4: return dispatch_nw<NCOLS, 4>(K, grp, xq, dsf, s);
+        default: return dispatch_nw<NCOLS, 2>(K, grp, xq, dsf, s);
+    }
+}
+
+/* count weight matrices (W[i], N[i] rows, output y[i]) of one K on one row
+ * stage; rows = 0 picks the rows per workgroup from the smallest N. */
+extern "C" hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W, float *const *y, const int *N,
+                                                 const void *stage, int M, int K, int rows, int accum,
+                                                 hipStream_t s) {
+    if (count < 1 || count > SERA_MMVQ_GROUP) return hipErrorInvalidValue;
+    const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
+    const char *base = (const char *)stage;
+    const int8_t *xq = (const int8_t *)(base + L.qs);
+    const float4 *dsf = (const float4 *)(base + L.dsf);
+    MmvqGroup grp = {};
+    int nmin = N[0];
+    for (int i = 0; i < count; i++) {
+        grp.W[i] = (const uint8_t *)W[i];
+        grp.y[i] = y[i];
+        grp.N[i] = N[i];
+        if (N[i] < nmin) nmin = N[i];
+    }
+    grp.count = count;
+    grp.accum = accum;
+    if (rows <= 0) rows = sera_mmvq_rows_per_wave(nmin, M);
+    while (rows > 2 && rows > nmin) rows >>= 1;   /* the shifted last tile needs R <= N */
+    switch (M) {
+        case 1: return dispatch_r<1>(rows, grp, xq, dsf, K, s);
+        case 2: return dispatch_r<2>(rows, grp, xq, dsf, K, s);
+        case 3: return dispatch_r<3>(rows, grp, xq, dsf, K, s);
+        case 4: return dispatch_r<4>(rows, grp, xq, dsf, K, s);
+        case 5: return dispatch_r<5>(rows, grp, xq, dsf, K, s);
+        case 6: return dispatch_r<6>(rows, grp, xq, dsf, K, s);
+        case 7: return dispatch_r<7>(rows, grp, xq, dsf, K, s);
+        case 8: return dispatch_r<8>(rows, grp, xq, dsf, K, s);
+        default: return hipErrorInvalidValue;
     }
 }
 
 extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y,
                                            int M, int N, int K, int rows, hipStream_t s) {
-    const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
-    const char *base = (const char *)stage;
-    const int8_t *xq = (const int8_t *)(base + L.qs);
-    const float4 *dsf = (const float4 *)(base + L.dsf);
-    const uint8_t *w = (const uint8_t *)W;
-    if (rows <= 0) rows = sera_mmvq_rows_per_wave(N, M);
-    while (rows > 2 && rows > N) rows >>= 1;   /* the shifted last tile needs R <= N */
-    switch (M) {
-        case 1: return dispatch_r<1>(rows, w, xq, dsf, y, N, K, s);
-        case 2: return dispatch_r<2>(rows, w, xq, dsf, y, N, K, s);
-        case 3: return dispatch_r<3>(rows, w, xq, dsf, y, N, K, s);
-        case 4: return dispatch_r<4>(rows, w, xq, dsf, y, N, K, s);
-        case 5: return dispatch_r<5>(rows, w, xq, dsf, y, N, K, s);
-        case 6: return dispatch_r<6>(rows, w, xq, dsf, y, N, K, s);
-        case 7: return dispatch_r<7>(rows, w, xq, dsf, y, N, K, s);
-        case 8: return dispatch_r<8>(rows, w, xq, dsf, y, N, K, s);
-        default: return hipErrorInvalidValue;
-    }
+    return sera_launch_q4k_mmvq_group(1, &W, &y, &N, stage, M, K, rows, 0, s);
 }

@@ -55,7 +55,7 @@ __device__ __forceinline__ h2 sk_as_h2(uint32_t u) {
 template <int FORM, int CT>
 __global__ __launch_bounds__(256) void sera_q4k_skinny_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq, const void *__restrict__ xsc,
-        float *__restrict__ y, float *__restrict__ partial, int M, int N, int K, int kb_per_split) {
+        float *__restrict__ y, float *__restrict__ partial, int M, int N, int K, int kb_per_split, int accum) {
     __shared__ SkinnySmem sm;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -244,13 +244,16 @@ __global__ __launch_bounds__(256) void sera_q4k_skinny_kernel(
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int t = 4 * gk + r;
-            if (t < M) out[(size_t)t * N + n0 + 16 * c + j] = acc[c][r];
+            if (t < M) {
+                float *dst = out + (size_t)t * N + n0 + 16 * c + j;
+                *dst = !partial && accum ? *dst + acc[c][r] : acc[c][r];
+            }
         }
     }
 }
 
-extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits,
-                                                hipStream_t s);
+extern "C" hipError_t sera_launch_splitk_reduce_acc(const float *partial, float *y, size_t n, int splits, int accum,
+                                                    hipStream_t s);
 extern "C" int sera_mmq_padded_rows(int M);
 
 #define SK_CT 2   /* 16-row tiles per wave: 128 weight rows per workgroup */
@@ -268,29 +271,40 @@ extern "C" int sera_skinny_splits(int M, int N, int K) {
 
 template <int FORM>
 static hipError_t launch_skinny(const uint8_t *W, const int8_t *xq, const void *xsc, float *y, float *partial,
-                                int M, int N, int K, int splits, hipStream_t s) {
+                                int M, int N, int K, int splits, int accum, hipStream_t s) {
     const int nkb = K / Q4K_QK;
     const int per = (nkb + splits - 1) / splits;
     dim3 grid((N + 64 * SK_CT - 1) / (64 * SK_CT), splits);
     hipLaunchKernelGGL((sera_q4k_skinny_kernel<FORM, SK_CT>), grid, dim3(256), 0, s, W, xq, xsc, y,
-                       splits > 1 ? partial : nullptr, M, N, K, per);
+                       splits > 1 ? partial : nullptr, M, N, K, per, accum);
     return hipGetLastError();
 }
+
+extern "C" hipError_t sera_launch_q4k_skinny_acc(int form, const void *W, const void *stage, float *y,
+                                                 float *partial, int M, int N, int K, int splits, int accum,
+                                                 hipStream_t s);
 
 /* form 0: row stage (MMVQ formula), form 1: MMQ stage (MMQ formula).
  * partial: splits*M*N floats when splits > 1 (M*N % 4 == 0). */
 extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
                                              int M, int N, int K, int splits, hipStream_t s) {
+    return sera_launch_q4k_skinny_acc(form, W, stage, y, partial, M, N, K, splits, 0, s);
+}
+
+/* accum != 0 adds the product to y. */
+extern "C" hipError_t sera_launch_q4k_skinny_acc(int form, const void *W, const void *stage, float *y,
+                                                 float *partial, int M, int N, int K, int splits, int accum,
+                                                 hipStream_t s) {
     const char *base = (const char *)stage;
     const uint8_t *w = (const uint8_t *)W;
     hipError_t e;
     if (form == 0) {
         const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
-        e = launch_skinny<0>(w, (const int8_t *)(base + L.qs), base + L.dsf, y, partial, M, N, K, splits, s);
+        e = launch_skinny<0>(w, (const int8_t *)(base + L.qs), base + L.dsf, y, partial, M, N, K, splits, accum, s);
     } else {
         const sera_stage_layout L = sera_mmq_stage_layout((size_t)sera_mmq_padded_rows(M), (size_t)K);
-        e = launch_skinny<1>(w, (const int8_t *)(base + L.qs), base + L.ds, y, partial, M, N, K, splits, s);
+        e = launch_skinny<1>(w, (const int8_t *)(base + L.qs), base + L.ds, y, partial, M, N, K, splits, accum, s);
     }
     if (e != hipSuccess || splits <= 1) return e;
-    return sera_launch_splitk_reduce(partial, y, (size_t)M * N, splits, s);
+    return sera_launch_splitk_reduce_acc(partial, y, (size_t)M * N, splits, accum, s);
 }

@@ -103,7 +103,7 @@ template <int TT, int WPE>
 __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
         const uint8_t *__restrict__ W, uint64_t wbytes, const _Float16 *__restrict__ xh,
         const float *__restrict__ d8t, float *__restrict__ y, float *__restrict__ partial, int M, int Mpad,
-        int N, int K, int kb_per_split) {
+        int N, int K, int kb_per_split, int accum) {
     constexpr int BM = 32 * TT;
     constexpr int WINST = Q6M_BN * Q6M_WCH * 16 / 1024;   /* load-to-LDS instructions per weight tile */
     __shared__ __attribute__((aligned(16))) Q6MmqSmem<BM> sm;
@@ -327,13 +327,16 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m < M) out[(size_t)m * N + col] = acc[t][r];
+                if (m < M) {
+                    float *dst = out + (size_t)m * N + col;
+                    *dst = !partial && accum ? *dst + acc[t][r] : acc[t][r];
+                }
             }
     }
 }
 
-extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits,
-                                                hipStream_t s);
+extern "C" hipError_t sera_launch_splitk_reduce_acc(const float *partial, float *y, size_t n, int splits, int accum,
+                                                    hipStream_t s);
 
 
 /* K splits: double while the grid holds fewer than 1024 (tile, split)
@@ -350,23 +353,25 @@ extern "C" int sera_q6k_mmq_splits(int M, int N, int K) {
 
 template <int TT, int WPE>
 static hipError_t launch_q6k_mmq(const uint8_t *W, uint64_t wbytes, const _Float16 *xh, const float *d8t, float *y,
-                                 float *partial, int M, int Mpad, int N, int K, int splits, hipStream_t s) {
+                                 float *partial, int M, int Mpad, int N, int K, int splits, int accum,
+                                 hipStream_t s) {
     constexpr int BM = 32 * TT;
     const int tiles = (Mpad / BM) * ((N + Q6M_BN - 1) / Q6M_BN);
     const int nkb = K / Q4K_QK;
     const int per = (nkb + splits - 1) / splits;
     splits = (nkb + per - 1) / per;
     hipLaunchKernelGGL((sera_q6k_mmq_kernel<TT, WPE>), dim3(tiles, splits), dim3(256), 0, s, W, wbytes, xh, d8t, y,
-                       splits > 1 ? partial : nullptr, M, Mpad, N, K, per);
+                       splits > 1 ? partial : nullptr, M, Mpad, N, K, per, accum);
     if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
     if (splits == 1) return hipSuccess;
-    return sera_launch_splitk_reduce(partial, y, (size_t)M * N, splits, s);
+    return sera_launch_splitk_reduce_acc(partial, y, (size_t)M * N, splits, accum, s);
 }
 
 /* stage: the Q6_K MMQ stage for Mpad = sera_q6k_mmq_padded_rows(M) rows;
- * partial: splits*M*N floats when splits > 1 (M*N % 4 == 0). */
-extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
-                                          int K, int splits, hipStream_t s) {
+ * partial: splits*M*N floats when splits > 1 (M*N % 4 == 0); accum != 0
+ * adds the product to y. */
+extern "C" hipError_t sera_launch_q6k_mmq_acc(const void *W, const void *stage, float *y, float *partial, int M,
+                                              int N, int K, int splits, int accum, hipStream_t s) {
     const int Mpad = sera_q6k_mmq_padded_rows(M);
     const sera_stage_layout L = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K);
     const char *base = (const char *)stage;
@@ -375,5 +380,10 @@ extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, floa
     const uint8_t *w = (const uint8_t *)W;
     const uint64_t wbytes = (uint64_t)N * (uint64_t)(K / Q4K_QK) * Q6K_BLOCK_BYTES;
     if (splits < 1) splits = 1;
-    return launch_q6k_mmq<1, 2>(w, wbytes, xh, d8t, y, partial, M, Mpad, N, K, splits, s);
+    return launch_q6k_mmq<1, 2>(w, wbytes, xh, d8t, y, partial, M, Mpad, N, K, splits, accum, s);
+}
+
+extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
+                                          int K, int splits, hipStream_t s) {
+    return sera_launch_q6k_mmq_acc(W, stage, y, partial, M, N, K, splits, 0, s);
 }

@@ -81,7 +81,7 @@ __device__ __forceinline__ uint32_t lds_read16(const uint8_t *lds, uint32_t a) {
 template <int M, int R>
 __global__ __launch_bounds__(256) void sera_q6k_mmvq_kernel(
         const uint8_t *__restrict__ W, uint64_t wbytes, const int8_t *__restrict__ xq,
-        const uint32_t *__restrict__ xds, float *__restrict__ y, int N, int K) {
+        const uint32_t *__restrict__ xds, float *__restrict__ y, int N, int K, int accum) {
     using S = Q6Shape<R>;
     __shared__ __attribute__((aligned(16))) uint8_t s_buf[4][2][S::BUF];
     const int lane = threadIdx.x & 63;
@@ -257,16 +257,19 @@ __global__ __launch_bounds__(256) void sera_q6k_mmvq_kernel(
         }
     if (lane < R * M) {
         const int r = lane / M, t = lane - (lane / M) * M;
-        if (row0 + r < N) y[(size_t)t * N + row0 + r] = mine;
+        if (row0 + r < N) {
+            float *dst = y + (size_t)t * N + row0 + r;
+            *dst = accum ? *dst + mine : mine;
+        }
     }
 }
 
 template <int M, int R>
 static hipError_t launch_q6k_mmvq(const uint8_t *W, uint64_t wbytes, const int8_t *xq, const uint32_t *xds,
-                                  float *y, int N, int K, hipStream_t s) {
+                                  float *y, int N, int K, int accum, hipStream_t s) {
     const int waves = (N + R - 1) / R;
     hipLaunchKernelGGL((sera_q6k_mmvq_kernel<M, R>), dim3((waves + 3) / 4), dim3(256), 0, s, W, wbytes, xq, xds,
-                       y, N, K);
+                       y, N, K, accum);
     return hipGetLastError();
 }
 
@@ -280,17 +283,26 @@ extern "C" int sera_q6k_mmvq_rows(int N, int M) {
 
 template <int M>
 static hipError_t dispatch_q6k_r(int r, const uint8_t *W, uint64_t wbytes, const int8_t *xq,
-                                 const uint32_t *xds, float *y, int N, int K, hipStream_t s) {
+                                 const uint32_t *xds, float *y, int N, int K, int accum, hipStream_t s) {
     switch (r) {
-        case 4: if constexpr (M <= 4) return launch_q6k_mmvq<M, 4>(W, wbytes, xq, xds, y, N, K, s);
+        case 4: if constexpr (M <= 4) return launch_q6k_mmvq<M, 4>(W, wbytes, xq, xds, y, N, K, accum, s);
                 [[fallthrough]];
-        case 2: return launch_q6k_mmvq<M, 2>(W, wbytes, xq, xds, y, N, K, s);
-        default: return launch_q6k_mmvq<M, 1>(W, wbytes, xq, xds, y, N, K, s);
+        case 2: return launch_q6k_mmvq<M, 2>(W, wbytes, xq, xds, y, N, K, accum, s);
+        default: return launch_q6k_mmvq<M, 1>(W, wbytes, xq, xds, y, N, K, accum, s);
     }
 }
 
+extern "C" hipError_t sera_launch_q6k_mmvq_acc(const void *W, const void *stage, float *y, int M, int N, int K,
+                                               int rows, int accum, hipStream_t s);
+
 extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K,
                                            int rows, hipStream_t s) {
+    return sera_launch_q6k_mmvq_acc(W, stage, y, M, N, K, rows, 0, s);
+}
+
+/* accum != 0 adds the product to y. */
+extern "C" hipError_t sera_launch_q6k_mmvq_acc(const void *W, const void *stage, float *y, int M, int N, int K,
+                                               int rows, int accum, hipStream_t s) {
     const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
     const char *base = (const char *)stage;
     const int8_t *xq = (const int8_t *)(base + L.qs);
@@ -299,14 +311,14 @@ extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, flo
     const uint64_t wbytes = (uint64_t)N * (uint64_t)(K / Q4K_QK) * Q6K_BLOCK_BYTES;
     if (rows <= 0) rows = sera_q6k_mmvq_rows(N, M);
     switch (M) {
-        case 1: return dispatch_q6k_r<1>(rows, w, wbytes, xq, xds, y, N, K, s);
-        case 2: return dispatch_q6k_r<2>(rows, w, wbytes, xq, xds, y, N, K, s);
-        case 3: return dispatch_q6k_r<3>(rows, w, wbytes, xq, xds, y, N, K, s);
-        case 4: return dispatch_q6k_r<4>(rows, w, wbytes, xq, xds, y, N, K, s);
-        case 5: return dispatch_q6k_r<5>(rows, w, wbytes, xq, xds, y, N, K, s);
-        case 6: return dispatch_q6k_r<6>(rows, w, wbytes, xq, xds, y, N, K, s);
-        case 7: return dispatch_q6k_r<7>(rows, w, wbytes, xq, xds, y, N, K, s);
-        case 8: return dispatch_q6k_r<8>(rows, w, wbytes, xq, xds, y, N, K, s);
+        case 1: return dispatch_q6k_r<1>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
+        case 2: return dispatch_q6k_r<2>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
+        case 3: return dispatch_q6k_r<3>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
+        case 4: return dispatch_q6k_r<4>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
+        case 5: return dispatch_q6k_r<5>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
+        case 6: return dispatch_q6k_r<6>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
+        case 7: return dispatch_q6k_r<7>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
+        case 8: return dispatch_q6k_r<8>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -19,6 +19,18 @@
  *     This library stores 16 * quant as fp16 (exact) for the fp16-MFMA
  *     Q6_K kernel and d transposed per 256-wide K step (see q4k_common.h).
  *
+ * Producers (sera_producer): each quantizer can compute its input row on the
+ * fly instead of reading a materialized one, fusing the reference's
+ * rms_norm_batched_kernel (src/q3_forward.cu:117-146) or silu_mul_kernel
+ * (:154-161) into the quantize that follows it. RMSNorm: every workgroup of
+ * a row first reduces the row's sum of squares in a fixed order (thread t
+ * adds x[t + 256i]^2 in i order, the square exact in double and each sum
+ * rounded to fp32 as the reference's float += double does; then an xor
+ * butterfly over the wave and the four wave sums left to right), then
+ * inv = 1 / sqrt(sum / K + eps) with IEEE division and square root (the
+ * reference's rsqrtf is an approximation), x = (x * inv) * gamma. SiLU:
+ * (g / (1 + expf(-g))) * u with the device expf.
+ *
  * Division is IEEE correctly rounded (hipcc default), roundf rounds half
  * away from zero, fp16 conversion rounds to nearest even. The float sums are
  * pure additions in a fixed pairing, so they cannot be contracted or
@@ -26,15 +38,66 @@
  */
 #include "q4k_common.h"
 
+/* 1 / sqrt(mean(x^2) + eps) of one row, computed by all 256 threads of the
+ * workgroup (every thread returns the same value). */
+__device__ __forceinline__ float q8_row_inv_rms(const float *__restrict__ xr, int K, float eps) {
+    __shared__ float s_red[4];
+    float s = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const double v = (double)xr[k];
+        s = (float)((double)s + v * v);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o, 64));
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float tot = __fadd_rn(__fadd_rn(__fadd_rn(s_red[0], s_red[1]), s_red[2]), s_red[3]);
+    /* sqrtf is correctly rounded with hipcc defaults (__fsqrt_rn is not on gfx950) */
+    return __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)K), eps)));
+}
+
+__device__ __forceinline__ float q8_silu_mul(float g, float u) {
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+}
+
+/* The producer's value at (row, k) given the row's inv_rms. */
+template <int PK>
+__device__ __forceinline__ float q8_produce(const float *__restrict__ x, const sera_producer &p, size_t idx, int k,
+                                            float inv) {
+    const float v = x[idx];
+    if (PK == 1) return __fmul_rn(__fmul_rn(v, inv), p.gamma[k]);
+    if (PK == 2) return q8_silu_mul(v, p.x2[idx]);
+    return v;
+}
+
+template <int PK>
+__device__ __forceinline__ float4 q8_produce4(const float *__restrict__ x, const sera_producer &p, size_t idx, int k,
+                                              float inv) {
+    const float4 v = *(const float4 *)(x + idx);
+    if (PK == 1) {
+        const float4 g = *(const float4 *)(p.gamma + k);
+        return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x), __fmul_rn(__fmul_rn(v.y, inv), g.y),
+                           __fmul_rn(__fmul_rn(v.z, inv), g.z), __fmul_rn(__fmul_rn(v.w, inv), g.w));
+    }
+    if (PK == 2) {
+        const float4 u = *(const float4 *)(p.x2 + idx);
+        return make_float4(q8_silu_mul(v.x, u.x), q8_silu_mul(v.y, u.y), q8_silu_mul(v.z, u.z),
+                           q8_silu_mul(v.w, u.w));
+    }
+    return v;
+}
+
 /* One wave-64 handles two consecutive Q8_1 blocks (lanes 0-31 and 32-63);
  * a 256-thread workgroup covers 256 values of one activation row.
  * grid = (K/256, M). Writes qs, ds and the MMVQ helper dsf. */
+template <int PK>
 __global__ __launch_bounds__(256) void sera_q8_1_row_kernel(
-        const float *__restrict__ x, int K, int8_t *__restrict__ qs,
+        const float *__restrict__ x, sera_producer prod, int K, int8_t *__restrict__ qs,
         uint32_t *__restrict__ ds, float4 *__restrict__ dsf) {
     const int row = blockIdx.y;
     const int k = blockIdx.x * 256 + threadIdx.x;
-    const float xi = x[(size_t)row * K + k];
+    const float inv = PK == 1 ? q8_row_inv_rms(x + (size_t)row * K, K, prod.eps) : 0.0f;
+    const float xi = q8_produce<PK>(x, prod, (size_t)row * K + k, k, inv);
 
     float amax = fabsf(xi);
     float sum = xi;
@@ -72,14 +135,16 @@ __global__ __launch_bounds__(256) void sera_q8_1_row_kernel(
 /* DS4 quantizer. Each thread holds 4 consecutive values (one float4); a
  * 256-thread workgroup covers 1024 values of one row. grid = (ceil(K/1024),
  * Mpad). Rows >= M (padding up to the MMQ tile) are written as zeros. */
+template <int PK>
 __global__ __launch_bounds__(256) void sera_q8_1_mmq_kernel(
-        const float *__restrict__ x, int M, int K, int8_t *__restrict__ qs,
+        const float *__restrict__ x, sera_producer prod, int M, int K, int8_t *__restrict__ qs,
         uint32_t *__restrict__ ds) {
     const int row = blockIdx.y;
     const int k = (blockIdx.x * 256 + threadIdx.x) * 4;
+    const float inv = PK == 1 && row < M ? q8_row_inv_rms(x + (size_t)row * K, K, prod.eps) : 0.0f;
     if (k >= K) return;
     float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (row < M) v = *(const float4 *)(x + (size_t)row * K + k);
+    if (row < M) v = q8_produce4<PK>(x, prod, (size_t)row * K + k, k, inv);
 
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     float sum = ((v.x + v.y) + v.z) + v.w;
@@ -113,15 +178,16 @@ __global__ __launch_bounds__(256) void sera_q8_1_mmq_kernel(
  * ROW = true: the row quantizer's values (MMVQ arithmetic, the same as
  *   sera_q8_1_row_kernel): d = amax/127, q = roundf(x/d), and the scale
  *   kept as fp32(fp16(d)), the d8 the MMVQ formula multiplies by. */
-template <bool ROW>
+template <bool ROW, int PK>
 __global__ __launch_bounds__(256) void sera_q8_1_q6k_stage_kernel(
-        const float *__restrict__ x, int M, int Mpad, int K, _Float16 *__restrict__ xh,
+        const float *__restrict__ x, sera_producer prod, int M, int Mpad, int K, _Float16 *__restrict__ xh,
         float *__restrict__ d8t) {
     const int row = blockIdx.y;
     const int k = (blockIdx.x * 256 + threadIdx.x) * 4;
+    const float inv = PK == 1 && row < M ? q8_row_inv_rms(x + (size_t)row * K, K, prod.eps) : 0.0f;
     if (k >= K) return;
     float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (row < M) v = *(const float4 *)(x + (size_t)row * K + k);
+    if (row < M) v = q8_produce4<PK>(x, prod, (size_t)row * K + k, k, inv);
 
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 #pragma unroll
@@ -152,38 +218,64 @@ __global__ __launch_bounds__(256) void sera_q8_1_q6k_stage_kernel(
         d8t[((size_t)(k >> 8) * 8 + ((k >> 5) & 7)) * Mpad + row] = d;
 }
 
+#define Q8_DISPATCH_PK(KIND, ...)                                                                         \
+    switch (KIND) {                                                                                        \
+        case 1: { constexpr int PK = 1; __VA_ARGS__; } break;                                              \
+        case 2: { constexpr int PK = 2; __VA_ARGS__; } break;                                              \
+        default: { constexpr int PK = 0; __VA_ARGS__; } break;                                             \
+    }
+
 /* row_formula = 0: D4 (MMQ) values, 1: row-quantizer (MMVQ) values. */
-extern "C" hipError_t sera_launch_q8_1_q6k_stage(const float *x, int M, int Mpad, int K, int row_formula,
-                                                 void *stage, hipStream_t stream) {
+extern "C" hipError_t sera_launch_q8_1_q6k_stage_p(const float *x, const sera_producer *prod, int M, int Mpad, int K,
+                                                   int row_formula, void *stage, hipStream_t stream) {
     const sera_stage_layout L = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K);
     char *base = (char *)stage;
+    const sera_producer p = prod ? *prod : sera_producer{0, nullptr, nullptr, 0.0f};
     dim3 grid((K + 1023) / 1024, Mpad);
-    if (row_formula)
-        hipLaunchKernelGGL(sera_q8_1_q6k_stage_kernel<true>, grid, dim3(256), 0, stream, x, M, Mpad, K,
-                           (_Float16 *)(base + L.qs), (float *)(base + L.ds));
-    else
-        hipLaunchKernelGGL(sera_q8_1_q6k_stage_kernel<false>, grid, dim3(256), 0, stream, x, M, Mpad, K,
-                           (_Float16 *)(base + L.qs), (float *)(base + L.ds));
+    Q8_DISPATCH_PK(p.kind,
+        if (row_formula)
+            hipLaunchKernelGGL((sera_q8_1_q6k_stage_kernel<true, PK>), grid, dim3(256), 0, stream, x, p, M, Mpad, K,
+                               (_Float16 *)(base + L.qs), (float *)(base + L.ds));
+        else
+            hipLaunchKernelGGL((sera_q8_1_q6k_stage_kernel<false, PK>), grid, dim3(256), 0, stream, x, p, M, Mpad,
+                               K, (_Float16 *)(base + L.qs), (float *)(base + L.ds)))
     return hipGetLastError();
 }
 
-extern "C" hipError_t sera_launch_q8_1_row(const float *x, int M, int K, void *stage,
-                                           hipStream_t stream) {
+extern "C" hipError_t sera_launch_q8_1_row_p(const float *x, const sera_producer *prod, int M, int K, void *stage,
+                                             hipStream_t stream) {
     const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
     char *base = (char *)stage;
+    const sera_producer p = prod ? *prod : sera_producer{0, nullptr, nullptr, 0.0f};
     dim3 grid(K / 256, M);
-    hipLaunchKernelGGL(sera_q8_1_row_kernel, grid, dim3(256), 0, stream, x, K,
-                       (int8_t *)(base + L.qs), (uint32_t *)(base + L.ds),
-                       (float4 *)(base + L.dsf));
+    Q8_DISPATCH_PK(p.kind,
+        hipLaunchKernelGGL((sera_q8_1_row_kernel<PK>), grid, dim3(256), 0, stream, x, p, K,
+                           (int8_t *)(base + L.qs), (uint32_t *)(base + L.ds), (float4 *)(base + L.dsf)))
     return hipGetLastError();
+}
+
+extern "C" hipError_t sera_launch_q8_1_mmq_p(const float *x, const sera_producer *prod, int M, int Mpad, int K,
+                                             void *stage, hipStream_t stream) {
+    const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
+    char *base = (char *)stage;
+    const sera_producer p = prod ? *prod : sera_producer{0, nullptr, nullptr, 0.0f};
+    dim3 grid((K + 1023) / 1024, Mpad);
+    Q8_DISPATCH_PK(p.kind,
+        hipLaunchKernelGGL((sera_q8_1_mmq_kernel<PK>), grid, dim3(256), 0, stream, x, p, M, K,
+                           (int8_t *)(base + L.qs), (uint32_t *)(base + L.ds)))
+    return hipGetLastError();
+}
+
+extern "C" hipError_t sera_launch_q8_1_q6k_stage(const float *x, int M, int Mpad, int K, int row_formula,
+                                                 void *stage, hipStream_t stream) {
+    return sera_launch_q8_1_q6k_stage_p(x, nullptr, M, Mpad, K, row_formula, stage, stream);
+}
+
+extern "C" hipError_t sera_launch_q8_1_row(const float *x, int M, int K, void *stage, hipStream_t stream) {
+    return sera_launch_q8_1_row_p(x, nullptr, M, K, stage, stream);
 }
 
 extern "C" hipError_t sera_launch_q8_1_mmq(const float *x, int M, int Mpad, int K, void *stage,
                                            hipStream_t stream) {
-    const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
-    char *base = (char *)stage;
-    dim3 grid((K + 1023) / 1024, Mpad);
-    hipLaunchKernelGGL(sera_q8_1_mmq_kernel, grid, dim3(256), 0, stream, x, M, K,
-                       (int8_t *)(base + L.qs), (uint32_t *)(base + L.ds));
-    return hipGetLastError();
+    return sera_launch_q8_1_mmq_p(x, nullptr, M, Mpad, K, stage, stream);
 }

@@ -9,6 +9,7 @@
  * stream, and timings are read only after the caller has synchronized.
  */
 #include "q4k_common.h"
+#include "../../include/q3_q4_linear.h"
 #include "../../include/sera_q4k.h"
 
 #include <stdarg.h>
@@ -31,6 +32,27 @@ extern "C" hipError_t sera_launch_q8_1_q6k_stage(const float *x, int M, int Mpad
 extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
                                           int K, int splits, hipStream_t s);
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
+extern "C" hipError_t sera_launch_q8_1_row_p(const float *x, const sera_producer *prod, int M, int K, void *stage,
+                                             hipStream_t s);
+extern "C" hipError_t sera_launch_q8_1_mmq_p(const float *x, const sera_producer *prod, int M, int Mpad, int K,
+                                             void *stage, hipStream_t s);
+extern "C" hipError_t sera_launch_q8_1_q6k_stage_p(const float *x, const sera_producer *prod, int M, int Mpad, int K,
+                                                   int row_formula, void *stage, hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W, float *const *y, const int *N,
+                                                 const void *stage, int M, int K, int rows, int accum,
+                                                 hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_skinny_acc(int form, const void *W, const void *stage, float *y,
+                                                 float *partial, int M, int N, int K, int splits, int accum,
+                                                 hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, float *y, float *partial,
+                                              int M, int N, int K, int splits, int accum, hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots,
+                                                      int *counters, int M, int N, int K, int P, int accum,
+                                                      hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmvq_acc(const void *W, const void *stage, float *y, int M, int N, int K,
+                                               int rows, int accum, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmq_acc(const void *W, const void *stage, float *y, float *partial, int M,
+                                              int N, int K, int splits, int accum, hipStream_t s);
 extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
                                                    const uint32_t *ids, int branches, int per_branch,
                                                    float *logits, hipStream_t s);
@@ -559,6 +581,116 @@ extern "C" int sera_embedding(int qtype, const void *W, int N, int K, const uint
     if (((uintptr_t)hidden & 15u) != 0) return fail(-1, "sera_embedding: hidden must be 16-byte aligned");
     return sera_launch_embedding(qtype, W, N, K, ids, tokens, hidden, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_embedding: launch failed");
+}
+
+/* ---- fused linear group ----------------------------------------------- */
+
+extern "C" int sera_linear_group(int count, const void *const *geometries, const void *const *weights,
+                                 float *const *outputs, const float *X, const float *X2, const float *gamma, float eps,
+                                 size_t M_, unsigned flags, void *stream) {
+    const char *tag = "sera_linear_group";
+    if (count < 1 || count > SERA_LINEAR_GROUP_MAX || !geometries || !weights || !outputs || !X)
+        return fail(-1, "%s: bad arguments (count=%d)", tag, count);
+    if (!g_arena) return fail(-1, "%s: no arena attached", tag);
+    if (M_ == 0 || M_ > 0x7fffffff) return fail(-1, "%s: bad token count", tag);
+    if (flags & ~(SERA_LIN_ACCUMULATE | SERA_LIN_RMSNORM | SERA_LIN_SILU_MUL))
+        return fail(-1, "%s: unknown flags 0x%x", tag, flags);
+    if ((flags & SERA_LIN_RMSNORM) && (flags & SERA_LIN_SILU_MUL))
+        return fail(-1, "%s: RMSNORM and SILU_MUL are exclusive", tag);
+    if ((flags & SERA_LIN_RMSNORM) && (!gamma || ((uintptr_t)gamma & 15u)))
+        return fail(-1, "%s: RMSNORM needs a 16-byte aligned gamma", tag);
+    if ((flags & SERA_LIN_SILU_MUL) && (!X2 || ((uintptr_t)X2 & 15u)))
+        return fail(-1, "%s: SILU_MUL needs a 16-byte aligned X2", tag);
+    const int M = (int)M_;
+    const q3_q4_linear_geometry *g0 = (const q3_q4_linear_geometry *)geometries[0];
+    if (!g0) return fail(-1, "%s: null geometry", tag);
+    const int K = g0->K;
+    const uint32_t qt = g0->qtype;
+    int N[SERA_LINEAR_GROUP_MAX];
+    size_t maxMN = 0;
+    for (int i = 0; i < count; i++) {
+        const q3_q4_linear_geometry *g = (const q3_q4_linear_geometry *)geometries[i];
+        if (!g || g->K != K || g->qtype != qt || g->N <= 0)
+            return fail(-1, "%s: geometry %d differs in K/qtype or is unresolved", tag, i);
+        if (!check_shape(tag, weights[i], X, outputs[i], M, g->N, K)) return -1;
+        N[i] = g->N;
+        if ((size_t)M * N[i] > maxMN) maxMN = (size_t)M * N[i];
+    }
+    if (qt != 12 && qt != 14) return fail(-1, "%s: qtype %u is not Q4_K/Q6_K", tag, qt);
+    if (qt == 14 && !q6k_shape_ok(tag, N[0], K)) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    const int accum = (flags & SERA_LIN_ACCUMULATE) ? 1 : 0;
+    sera_producer prod = {0, X2, gamma, eps};
+    if (flags & SERA_LIN_RMSNORM) prod.kind = 1;
+    if (flags & SERA_LIN_SILU_MUL) prod.kind = 2;
+
+    /* stage, then per-matrix split-K partials or stream-K slots */
+    size_t stage_bytes;
+    int Mpad = M;
+    if (qt == 12) {
+        if (M <= SERA_Q4K_MMVQ_MAX_BATCH) {
+            stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
+        } else {
+            Mpad = sera_mmq_padded_rows(M);
+            stage_bytes = sera_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
+        }
+    } else if (M < SERA_Q6K_VEC_MFMA_MIN_BATCH) {
+        stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
+    } else {
+        Mpad = sera_q6k_mmq_padded_rows(M);
+        stage_bytes = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
+    }
+    if (stage_bytes > g_arena_bytes) return fail(-1, "%s: arena too small for the stage", tag);
+    float *partial = (float *)(g_arena + stage_bytes);
+    const size_t partial_cap = (g_arena_bytes - stage_bytes) / sizeof(float);
+    (void)maxMN;
+
+    /* quantize once */
+    hipError_t qe;
+    if (qt == 12)
+        qe = M <= SERA_Q4K_MMVQ_MAX_BATCH ? sera_launch_q8_1_row_p(X, &prod, M, K, g_arena, s)
+                                          : sera_launch_q8_1_mmq_p(X, &prod, M, Mpad, K, g_arena, s);
+    else
+        qe = M < SERA_Q6K_VEC_MFMA_MIN_BATCH
+                 ? sera_launch_q8_1_row_p(X, &prod, M, K, g_arena, s)
+                 : sera_launch_q8_1_q6k_stage_p(X, &prod, M, Mpad, K, M <= SERA_Q4K_MMVQ_MAX_BATCH ? 1 : 0,
+                                                g_arena, s);
+    if (qe != hipSuccess) return fail(-2, "%s: quantize launch failed", tag);
+
+    /* the products */
+    if (qt == 12 && M < SERA_Q4K_VEC_MFMA_MIN_BATCH) {
+        if (sera_launch_q4k_mmvq_group(count, weights, outputs, N, g_arena, M, K, 0, accum, s) != hipSuccess)
+            return fail(-3, "%s: grouped mmvq launch failed", tag);
+        return 0;
+    }
+    for (int i = 0; i < count; i++) {
+        hipError_t e;
+        const int n = N[i];
+        const bool mn4 = ((size_t)M * n) % 4 == 0;
+        if (qt == 12 && M <= SERA_Q4K_MMVQ_MAX_BATCH) {
+            int sp = mn4 ? sera_skinny_splits(M, n, K) : 1;
+            if ((size_t)sp * M * n > partial_cap) sp = 1;
+            e = sera_launch_q4k_skinny_acc(0, weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
+        } else if (qt == 12) {
+            const size_t slot_floats = (size_t)2 * streamk_wgs(M) * sera_mmq_slot_floats(M);
+            if (use_streamk(M, n, K) && slot_floats <= partial_cap) {
+                e = sera_launch_q4k_mmq_streamk_acc(weights[i], g_arena, outputs[i], partial, g_counters, M, n, K,
+                                                    streamk_wgs(M), accum, s);
+            } else {
+                int sp = mn4 ? sera_mmq_splits(M, n, K) : 1;
+                if ((size_t)sp * M * n > partial_cap) sp = 1;
+                e = sera_launch_q4k_mmq_acc(weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
+            }
+        } else if (M < SERA_Q6K_VEC_MFMA_MIN_BATCH) {
+            e = sera_launch_q6k_mmvq_acc(weights[i], g_arena, outputs[i], M, n, K, 0, accum, s);
+        } else {
+            int sp = mn4 ? sera_q6k_mmq_splits(M, n, K) : 1;
+            if ((size_t)sp * M * n > partial_cap) sp = 1;
+            e = sera_launch_q6k_mmq_acc(weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
+        }
+        if (e != hipSuccess) return fail(-3, "%s: product %d launch failed", tag, i);
+    }
+    return 0;
 }
 
 extern "C" void sera_q4k_read_timings(double *quant_ms, double *kernel_ms, double *total_ms) {

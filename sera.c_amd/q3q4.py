@@ -124,6 +124,7 @@ def load():
         "sera_q6k_mmq": ([P, P, P, P, I, I, I, I, P], I),
         "sera_q6k_mmq_splits_for": ([I, I, I], I),
         "sera_candidate_logits": ([I, P, I, I, P, I, P, I, P, P], I),
+        "sera_linear_group": ([I, P, P, P, P, P, P, ctypes.c_float, SZ, ctypes.c_uint, P], I),
         "sera_embedding": ([I, P, I, I, P, I, P, P], I),
         "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_stream": ([P, P, P, P, P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),
@@ -346,3 +347,22 @@ def candidate_logits(qtype, W, N, K, hidden, ids, per_branch, logits, stream=Non
 def embedding(qtype, W, N, K, ids, hidden, stream=None):
     _check(load().sera_embedding(qtype, _ptr(W), N, K, _ptr(ids), ids.numel(), _ptr(hidden), _stream(stream)),
            "sera_embedding")
+
+
+# ---------------------------------------------------------------------------
+# Fused linear group
+# ---------------------------------------------------------------------------
+
+LIN_ACCUMULATE = 1
+LIN_RMSNORM = 2
+LIN_SILU_MUL = 4
+
+
+def linear_group(geometries, weights, outputs, x, x2=None, gamma=None, eps=0.0, flags=0, stream=None):
+    """outputs[i] (+)= op(x) . W_i^T for the geometries/weights given (1..4)."""
+    n = len(weights)
+    G = (ctypes.c_void_p * n)(*[ctypes.addressof(g) for g in geometries])
+    Wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in weights])
+    Yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in outputs])
+    _check(load().sera_linear_group(n, G, Wp, Yp, _ptr(x), _ptr(x2), _ptr(gamma), float(eps), x.shape[0], flags,
+                                    _stream(stream)), "sera_linear_group")

@@ -553,3 +553,30 @@ def test_reference_q6_value_dev_disagrees_with_its_own_dequant(golden_dir):
     same = np.array([all(q6_value_dev(i, e) == ref_rows[i, e] for i in range(nblk)) for e in range(256)])
     assert same[:16].all()                       # weights 0..15: both maps read ql[l], qh[l], sc[0]
     assert same.sum() <= 32 and not same[16:64].any()
+
+
+# ---------------------------------------------------------------------------
+# Producers fused into the quantize
+# ---------------------------------------------------------------------------
+
+def test_rmsnorm_fused_order_matches_exact_math():
+    """Against the float64 formula x / sqrt(mean(x^2) + eps) * gamma: the
+    fixed fp32 order is within a few ulp; and a constant row is exact."""
+    H = (RNG.standard_normal((3, 5120)) * np.array([[0.01], [1.0], [300.0]])).astype(np.float32)
+    g = RNG.uniform(0.5, 1.5, 5120).astype(np.float32)
+    x = oracle.rmsnorm_fused_order(H, g, 1e-6)
+    Hd = H.astype(np.float64)
+    ref = Hd / np.sqrt((Hd ** 2).mean(axis=1, keepdims=True) + 1e-6) * g
+    assert np.max(np.abs(x - ref) / np.abs(ref).max(axis=1, keepdims=True)) < 3e-7
+    c = np.full((1, 512), 2.0, np.float32)
+    assert np.all(oracle.rmsnorm_fused_order(c, np.ones(512, np.float32), 0.0) == 1.0)
+
+
+def test_silu_mul_matches_exact_math():
+    G = (RNG.standard_normal((4, 1000)) * 6).astype(np.float32)
+    U = RNG.standard_normal((4, 1000)).astype(np.float32)
+    s = oracle.silu_mul(G, U)
+    Gd = G.astype(np.float64)
+    ref = Gd / (1 + np.exp(-Gd)) * U
+    assert np.max(np.abs(s - ref) / (np.abs(ref) + 1e-30)) < 4e-7
+    assert oracle.silu_mul(np.float32([0.0]), np.float32([5.0]))[0] == 0.0
