@@ -449,9 +449,46 @@ def decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr):
         out.update({f"{label}ms_per_token": round(t, 3),
                     f"{label}sustained_GBps": round(total_w / (t * 1e-3) / 1e9, 1),
                     f"{label}frac_hbm": round(total_w / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    # the same weights through the fused linear group: per layer q/k/v with the
+    # input RMSNorm in one quantize + one grouped MMVQ, o with the residual add
+    # in its store, gate/up with the MLP RMSNorm likewise grouped, down with
+    # SiLU*up in its quantize and the residual add in its store; then the
+    # final-norm LM head: 8 launches per layer instead of 14 plus 3 elementwise
+    hid = torch.randn((1, 5120), device=dev)
+    attn = torch.randn((1, 8192), device=dev)
+    gam = [torch.rand(5120, device=dev) + 0.5 for _ in range(3)]
+    bufs = {n: torch.empty((1, SHAPES[n][0]), dtype=torch.float32, device=dev)
+            for n in ("q", "k", "v", "gate", "up", "lm_head")}
+    G = q3q4
+    fcalls = []
+    for layer in range(64):
+        w = {name: keep[layer * 7 + order.index(name)] for name in order}
+        fcalls.append(G.group_call([geos["q"], geos["k"], geos["v"]], [w["q"], w["k"], w["v"]],
+                                   [bufs["q"], bufs["k"], bufs["v"]], hid, gamma=gam[0], eps=1e-6,
+                                   flags=G.LIN_RMSNORM))
+        fcalls.append(G.group_call([geos["o"]], [w["o"]], [hid], attn, flags=G.LIN_ACCUMULATE))
+        fcalls.append(G.group_call([geos["gate"], geos["up"]], [w["gate"], w["up"]], [bufs["gate"], bufs["up"]],
+                                   hid, gamma=gam[1], eps=1e-6, flags=G.LIN_RMSNORM))
+        fcalls.append(G.group_call([geos["down"]], [w["down"]], [hid], bufs["gate"], x2=bufs["up"],
+                                   flags=G.LIN_SILU_MUL | G.LIN_ACCUMULATE))
+    fcalls.append(G.group_call([geos["lm_head"]], [lm], [bufs["lm_head"]], hid, gamma=gam[2], eps=1e-6,
+                               flags=G.LIN_RMSNORM))
+    carr = (G.GroupCall * len(fcalls))(*fcalls)
+    for label, use_graph, strm in (("fused_", 0, sptr), ("fused_graph_", 1, ctypes.c_void_p(side.cuda_stream))):
+        ms = ctypes.c_double()
+        rc = L.sera_q4k_bench_group_stream(carr, len(fcalls), strm, 2, 10, use_graph, ctypes.byref(ms))
+        if rc != 0:
+            raise RuntimeError(f"bench_group_stream rc={rc}: {L.sera_q4k_last_error().decode()}")
+        torch.cuda.synchronize()
+        t = ms.value
+        out.update({f"{label}ms_per_token": round(t, 3),
+                    f"{label}sustained_GBps": round(total_w / (t * 1e-3) / 1e9, 1),
+                    f"{label}frac_hbm": round(total_w / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
     del keep, lm
     out["note"] = ("449 q3_cuda_q4k_linear calls (Q8_1 quantize + MMVQ each) per token, issued from C; "
-                   "graph_*: the same pass captured once into a HIP graph and replayed; 10 timed tokens")
+                   "graph_*: the same pass captured once into a HIP graph and replayed; fused_*: the layer as "
+                   "4 sera_linear_group calls (input/MLP RMSNorm, SiLU*up and both residual adds fused; q/k/v "
+                   "and gate/up grouped) plus the final-norm LM head, 514 launches per token; 10 timed tokens")
     return out
 
 

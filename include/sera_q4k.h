@@ -239,6 +239,20 @@ int sera_linear_group(int count, const void *const *geometries, const void *cons
                       const float *X, const float *X2, const float *gamma, float eps, size_t M, unsigned flags,
                       void *stream);
 
+/* One sera_linear_group call, for sera_q4k_bench_group_stream. */
+typedef struct {
+    int count;
+    const void *geometries[SERA_LINEAR_GROUP_MAX];
+    const void *weights[SERA_LINEAR_GROUP_MAX];
+    float *outputs[SERA_LINEAR_GROUP_MAX];
+    const float *X;
+    const float *X2;
+    const float *gamma;
+    float eps;
+    size_t M;
+    unsigned flags;
+} sera_linear_group_call;
+
 /* ---- gathered rows of a Q4_K (12) / Q6_K (14) matrix ------------------
  * fp32 dequant with the expression order of src/q3_quant.c:57-103 (Q4_K
  * (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32)) and the GGUF Q6_K byte mapping of
@@ -294,6 +308,11 @@ int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, co
 int sera_q4k_bench_stream(const void *const *geometries, const void *const *weights,
                           const float *const *xs, const size_t *Ms, float *const *ys, int ncalls,
                           void *stream, int warmup, int reps, int use_graph, double *ms_per_rep);
+
+/* sera_q4k_bench_stream for a sequence of sera_linear_group calls (the
+ * fused decode stream). */
+int sera_q4k_bench_group_stream(const sera_linear_group_call *calls, int ncalls, void *stream, int warmup, int reps,
+                                int use_graph, double *ms_per_rep);
 
 #ifdef __cplusplus
 }

@@ -116,6 +116,63 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
  * projections and the LM head without a host language in the loop. With
  * use_graph != 0 the sequence is captured once into a HIP graph (stream
  * must not be the null stream) and the graph is replayed instead. */
+namespace {
+/* Time `reps` passes of `pass` (after `warmup`), optionally captured once
+ * into a HIP graph and replayed. */
+template <class Pass>
+int time_passes(Pass pass, hipStream_t s, int warmup, int reps, int use_graph, double *ms_per_rep) {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (use_graph) {
+        if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return -1;
+        const bool ok = pass();
+        if (hipStreamEndCapture(s, &graph) != hipSuccess || !ok) return -3;
+        if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            return -3;
+        }
+    }
+    auto run = [&]() -> bool { return use_graph ? hipGraphLaunch(exec, s) == hipSuccess : pass(); };
+    int rc = 0;
+    for (int i = 0; i < warmup && rc == 0; i++)
+        if (!run()) rc = -3;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (rc == 0 && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)) rc = -1;
+    if (rc == 0) {
+        (void)hipEventRecord(a, s);
+        for (int i = 0; i < reps && rc == 0; i++)
+            if (!run()) rc = -3;
+        (void)hipEventRecord(b, s);
+        (void)hipEventSynchronize(b);
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, a, b);
+        *ms_per_rep = (double)ms / reps;
+    }
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+}
+}  // namespace
+
+extern "C" int sera_q4k_bench_group_stream(const sera_linear_group_call *calls, int ncalls, void *stream, int warmup,
+                                           int reps, int use_graph, double *ms_per_rep) {
+    if (!calls || ncalls <= 0 || reps <= 0 || !ms_per_rep) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    if (use_graph && !s) return -1;
+    auto pass = [&]() -> bool {
+        for (int i = 0; i < ncalls; i++) {
+            const sera_linear_group_call &c = calls[i];
+            if (sera_linear_group(c.count, c.geometries, c.weights, c.outputs, c.X, c.X2, c.gamma, c.eps, c.M,
+                                  c.flags, stream) != 0)
+                return false;
+        }
+        return true;
+    };
+    return time_passes(pass, s, warmup, reps, use_graph, ms_per_rep);
+}
+
 extern "C" int sera_q4k_bench_stream(const void *const *geometries, const void *const *weights,
                                      const float *const *xs, const size_t *Ms, float *const *ys, int ncalls,
                                      void *stream, int warmup, int reps, int use_graph, double *ms_per_rep) {

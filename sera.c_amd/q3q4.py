@@ -125,6 +125,7 @@ def load():
         "sera_q6k_mmq_splits_for": ([I, I, I], I),
         "sera_candidate_logits": ([I, P, I, I, P, I, P, I, P, P], I),
         "sera_linear_group": ([I, P, P, P, P, P, P, ctypes.c_float, SZ, ctypes.c_uint, P], I),
+        "sera_q4k_bench_group_stream": ([P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_embedding": ([I, P, I, I, P, I, P, P], I),
         "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_stream": ([P, P, P, P, P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),
@@ -356,6 +357,33 @@ def embedding(qtype, W, N, K, ids, hidden, stream=None):
 LIN_ACCUMULATE = 1
 LIN_RMSNORM = 2
 LIN_SILU_MUL = 4
+GROUP_MAX = 4
+
+
+class GroupCall(ctypes.Structure):
+    """sera_linear_group_call (include/sera_q4k.h)."""
+    _fields_ = [("count", ctypes.c_int),
+                ("geometries", ctypes.c_void_p * GROUP_MAX),
+                ("weights", ctypes.c_void_p * GROUP_MAX),
+                ("outputs", ctypes.c_void_p * GROUP_MAX),
+                ("X", ctypes.c_void_p), ("X2", ctypes.c_void_p), ("gamma", ctypes.c_void_p),
+                ("eps", ctypes.c_float), ("M", ctypes.c_size_t), ("flags", ctypes.c_uint)]
+
+
+def group_call(geometries, weights, outputs, x, x2=None, gamma=None, eps=0.0, flags=0):
+    c = GroupCall()
+    c.count = len(weights)
+    for i, (g, w, y) in enumerate(zip(geometries, weights, outputs)):
+        c.geometries[i] = ctypes.addressof(g)
+        c.weights[i] = w.data_ptr()
+        c.outputs[i] = y.data_ptr()
+    c.X = x.data_ptr()
+    c.X2 = x2.data_ptr() if x2 is not None else None
+    c.gamma = gamma.data_ptr() if gamma is not None else None
+    c.eps = eps
+    c.M = x.shape[0]
+    c.flags = flags
+    return c
 
 
 def linear_group(geometries, weights, outputs, x, x2=None, gamma=None, eps=0.0, flags=0, stream=None):
