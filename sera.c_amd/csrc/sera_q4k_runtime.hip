@@ -391,12 +391,11 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
 namespace {
 /* Q6_K rows are K/256 * 210 bytes; the kernels address a row's bytes with
  * 32-bit offsets from the start of a group of rows. */
-bool q6k_shape_ok(const char *tag, int N, int K) {
+bool q6k_shape_ok(const char *tag, int K) {
     if ((uint64_t)(K / Q4K_QK) * 210u * 256u >= (1ull << 31)) {
         fail(-1, "%s: K=%d too long for 32-bit row offsets", tag, K);
         return false;
     }
-    (void)N;
     return true;
 }
 }  // namespace
@@ -415,7 +414,7 @@ extern "C" int sera_q6k_mmvq(const void *W, const void *row_stage, float *Y, int
         return fail(-1, "sera_q6k_mmvq: rows_per_wave=%d not in {0,1,2,4}", rows_per_wave);
     if (rows_per_wave == 4 && M > 4) return fail(-1, "sera_q6k_mmvq: rows_per_wave=4 needs M <= 4");
     if (((uintptr_t)W & 15u) != 0) return fail(-1, "sera_q6k_mmvq: W must be 16-byte aligned");
-    if (!q6k_shape_ok("sera_q6k_mmvq", N, K)) return -1;
+    if (!q6k_shape_ok("sera_q6k_mmvq", K)) return -1;
     return sera_launch_q6k_mmvq(W, row_stage, Y, M, N, K, rows_per_wave, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q6k_mmvq: launch failed");
 }
@@ -432,7 +431,7 @@ extern "C" int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M
     if (!check_shape("sera_q6k_dense_vec", W, X, Y, M, N, K)) return -1;
     if (M > SERA_Q4K_MMVQ_MAX_BATCH)
         return fail(-1, "sera_q6k_dense_vec: batch M=%d exceeds MMVQ cap %d", M, SERA_Q4K_MMVQ_MAX_BATCH);
-    if (!q6k_shape_ok("sera_q6k_dense_vec", N, K)) return -1;
+    if (!q6k_shape_ok("sera_q6k_dense_vec", K)) return -1;
     if (!g_arena) return fail(-1, "sera_q6k_dense_vec: no arena attached");
     hipStream_t s = (hipStream_t)stream;
     const bool mfma = M >= SERA_Q6K_VEC_MFMA_MIN_BATCH;
@@ -515,7 +514,7 @@ extern "C" int sera_q6k_mmq(const void *W, const void *q6k_mmq_stage, float *Y, 
     if (!W || !q6k_mmq_stage || !Y) return fail(-1, "sera_q6k_mmq: null pointer");
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q6k_mmq: bad shape M=%d N=%d K=%d", M, N, K);
     if (((uintptr_t)W & 15u) != 0) return fail(-1, "sera_q6k_mmq: W must be 16-byte aligned");
-    if (!q6k_shape_ok("sera_q6k_mmq", N, K)) return -1;
+    if (!q6k_shape_ok("sera_q6k_mmq", K)) return -1;
     if (splits == 0) splits = q6k_splits(M, N, K);
     if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q6k_mmq: splits=%d outside 1..K/256", splits);
     if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
@@ -527,7 +526,7 @@ extern "C" int sera_q6k_mmq(const void *W, const void *q6k_mmq_stage, float *Y, 
 extern "C" int sera_q6k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
                               int timed) {
     if (!check_shape("sera_q6k_dense", W, X, Y, M, N, K)) return -1;
-    if (!q6k_shape_ok("sera_q6k_dense", N, K)) return -1;
+    if (!q6k_shape_ok("sera_q6k_dense", K)) return -1;
     if (!g_arena) return fail(-1, "sera_q6k_dense: no arena attached");
     hipStream_t s = (hipStream_t)stream;
     const int Mpad = sera_q6k_mmq_padded_rows(M);
@@ -607,17 +606,15 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
     const int K = g0->K;
     const uint32_t qt = g0->qtype;
     int N[SERA_LINEAR_GROUP_MAX];
-    size_t maxMN = 0;
     for (int i = 0; i < count; i++) {
         const q3_q4_linear_geometry *g = (const q3_q4_linear_geometry *)geometries[i];
         if (!g || g->K != K || g->qtype != qt || g->N <= 0)
             return fail(-1, "%s: geometry %d differs in K/qtype or is unresolved", tag, i);
         if (!check_shape(tag, weights[i], X, outputs[i], M, g->N, K)) return -1;
         N[i] = g->N;
-        if ((size_t)M * N[i] > maxMN) maxMN = (size_t)M * N[i];
     }
     if (qt != 12 && qt != 14) return fail(-1, "%s: qtype %u is not Q4_K/Q6_K", tag, qt);
-    if (qt == 14 && !q6k_shape_ok(tag, N[0], K)) return -1;
+    if (qt == 14 && !q6k_shape_ok(tag, K)) return -1;
     hipStream_t s = (hipStream_t)stream;
     const int accum = (flags & SERA_LIN_ACCUMULATE) ? 1 : 0;
     sera_producer prod = {0, X2, gamma, eps};
@@ -643,7 +640,6 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
     if (stage_bytes > g_arena_bytes) return fail(-1, "%s: arena too small for the stage", tag);
     float *partial = (float *)(g_arena + stage_bytes);
     const size_t partial_cap = (g_arena_bytes - stage_bytes) / sizeof(float);
-    (void)maxMN;
 
     /* quantize once */
     hipError_t qe;
