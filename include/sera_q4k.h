@@ -156,7 +156,18 @@ const char *sera_q4k_last_error(void);
  * 16-wide groups, fp16 d (cuda/mmq/ggml-common.h:348-357, src/q3_quant.c:78-103).
  * Rows are 2-byte aligned only; W itself must be 16-byte aligned and
  * readable up to the next 16-byte boundary past its last byte (any hipMalloc
- * allocation is). */
+ * allocation is).
+ *
+ * Every Q6_K entry point takes the qtype of its weight bytes: 14 for the
+ * GGUF bytes, or SERA_QTYPE_Q6K_SPLIT for the split device layout that
+ * sera_weight_upload / sera_weight_to_device_layout produce (no reference
+ * counterpart; the reference keeps GGUF bytes on the device,
+ * cuda/q3_model_loader_cuda.cu:290-342): the N*K/256 blocks in row order,
+ * block b's ql, qh, sc (208 bytes) at 208*b, then all d as fp16 at
+ * 208*N*K/256 + 2*b. Same byte count as GGUF; each block's 208 bytes are
+ * 16-byte aligned, which the kernels load directly. Values and results are
+ * those of the GGUF bytes. A q3_q4_linear geometry may carry this qtype. */
+#define SERA_QTYPE_Q6K_SPLIT 270u
 
 /* Y = X . W^T through the MMVQ path (MMVQ arithmetic), 1 <= M <= 8: the
  * reference quantizes Q6_K decode activations with the same
@@ -164,7 +175,7 @@ const char *sera_q4k_last_error(void);
  * on the row stage, from 5 the fp16-MFMA tile kernel on a row-formula Q6_K
  * stage. Replaces q3_mmq_q6_K_dense_vec (cuda/q3_mmq.cu:515-519 over
  * q3_mmq_dense_vec_impl, :408-506). */
-int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
+int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
 
 /* Same contract through the MMQ path, any M >= 1 (the ABI uses it for
@@ -172,7 +183,7 @@ int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M, int N, in
  * q3_mmq_dense_impl, :258-379). Activations go through the D4 MMQ quantizer
  * (fp32 scale per 32 values, cuda/mmq/quantize.cu:271-367,
  * mmq.cuh:64-103). */
-int sera_q6k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
+int sera_q6k_dense(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
                    void *stream, int timed);
 
 /* Kernel launches one sera_q6k_dense / sera_q6k_dense_vec call makes. */
@@ -181,10 +192,11 @@ int sera_q6k_kernel_launches(int M, int N, int K);
 /* MMVQ kernel on a row stage (mul_mat_vec_q<Q6_K>, cuda/mmq/mmvq.cu:907-911,
  * with vec_dot_q6_K_q8_1, cuda/mmq/vecdotq.cuh:624-643,956-980):
  * y = sum_blk d * sum_g d8[g/2] * (I_g * sc_g), I_g the exact int dot of a
- * 16-wide group. rows_per_wave in {1, 2, 4} (4 only for M <= 4), or 0 for
- * the built-in choice (sera_q6k_mmvq_rows_per_wave). */
-int sera_q6k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
-                  int rows_per_wave, void *stream);
+ * 16-wide group. GGUF bytes: rows = rows per wave in {1, 2, 4} (4 only for
+ * M <= 4); split layout: rows per workgroup in {2, 4}; 0 = the built-in
+ * choice (sera_q6k_mmvq_rows_per_wave for GGUF bytes). */
+int sera_q6k_mmvq(uint32_t qtype, const void *W, const void *row_stage, float *Y, int M, int N, int K,
+                  int rows, void *stream);
 int sera_q6k_mmvq_rows_per_wave(int M, int N);
 
 /* Q6_K MMQ activation stage (D4 quantizer of cuda/mmq/quantize.cu:271-367
@@ -206,9 +218,35 @@ int sera_q8_1_quantize_row_q6k(const float *X, int M, int K, void *stage, void *
  * y = sum_blk d * sum_b d8_b * (sc_2b*I_2b + sc_2b+1*I_2b+1). splits > 1
  * splits K (partial: splits*M*N floats, M*N % 4 == 0); 0 = built-in choice
  * (sera_q6k_mmq_splits_for). */
-int sera_q6k_mmq(const void *W, const void *q6k_mmq_stage, float *Y, float *partial, int M, int N, int K,
-                 int splits, void *stream);
+int sera_q6k_mmq(uint32_t qtype, const void *W, const void *q6k_mmq_stage, float *Y, float *partial, int M, int N,
+                 int K, int splits, void *stream);
 int sera_q6k_mmq_splits_for(int M, int N, int K);
+
+/* ---- weight upload into the device layout -------------------------------
+ * Replaces the verbatim tensor copy of the reference's resident loader
+ * (q3_loader_load, cuda/q3_model_loader_cuda.cu:171-373; pinned staging +
+ * H2D + D2D at :290-342) for the weights of this path. qtype names the
+ * device layout: 12 and 14 keep the GGUF bytes (a plain copy), and
+ * SERA_QTYPE_Q6K_SPLIT repacks GGUF Q6_K bytes into the split layout on the
+ * device. The source is always the tensor's GGUF bytes (N rows of K/256
+ * blocks). */
+
+/* Bytes of the weight matrix in any of these layouts (= the GGUF size);
+ * 0 for a bad qtype or shape. */
+size_t sera_weight_bytes(uint32_t qtype, int N, int K);
+
+/* GGUF bytes already on the device -> dst in the layout of qtype (enqueue
+ * only). Split: gguf 2-byte aligned, dst 16-byte aligned, no overlap. */
+int sera_weight_to_device_layout(uint32_t qtype, int N, int K, const void *gguf, void *dst, void *stream);
+
+/* Host GGUF bytes -> dst in the layout of qtype, on `stream` (enqueue
+ * only; host_gguf must stay valid until the stream reaches the copies, as
+ * for hipMemcpyAsync; pinned memory makes the copies asynchronous). The
+ * split layout streams the bytes through the caller's device staging
+ * buffer (>= 210 bytes, 16-byte aligned; whole blocks per pass) and repacks
+ * each pass into dst; GGUF layouts copy straight to dst (staging unused). */
+int sera_weight_upload(uint32_t qtype, int N, int K, const void *host_gguf, void *dst, void *staging,
+                       size_t staging_bytes, void *stream);
 
 /* ---- fused linear group (the path's edges) -----------------------------
  * No single reference counterpart: one call replaces the sequence the
@@ -253,7 +291,7 @@ typedef struct {
     unsigned flags;
 } sera_linear_group_call;
 
-/* ---- gathered rows of a Q4_K (12) / Q6_K (14) matrix ------------------
+/* ---- gathered rows of a Q4_K (12) / Q6_K (14, SERA_QTYPE_Q6K_SPLIT) matrix ---
  * fp32 dequant with the expression order of src/q3_quant.c:57-103 (Q4_K
  * (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32)) and the GGUF Q6_K byte mapping of
  * q3_quant.c. The reference's device twin q6_value_dev

@@ -244,6 +244,26 @@ def q6k_weights(rng, N, K, **kw):
     return q6k_blocks(rng, N * (K // 256), **kw).reshape(N, K // 256 * Q6K_BYTES)
 
 
+def q6k_split(W, N, K):
+    """GGUF Q6_K bytes [N][K/256][210] -> the split device layout as one flat
+    uint8 array: every block's first 208 bytes (ql, qh, sc) in block order,
+    then every block's 2-byte d in block order. A byte permutation, nothing
+    more (the block fields are those of src/q3_quant.c:78-103)."""
+    B = np.ascontiguousarray(W, dtype=np.uint8).reshape(N * (K // 256), Q6K_BYTES)
+    return np.concatenate([B[:, :208].reshape(-1), B[:, 208:].reshape(-1)])
+
+
+def q6k_unsplit(S, N, K):
+    """Inverse of q6k_split: split layout -> GGUF bytes [N][K/256*210]."""
+    nblk = N * (K // 256)
+    S = np.ascontiguousarray(S, dtype=np.uint8).reshape(-1)
+    assert S.size == nblk * Q6K_BYTES
+    B = np.empty((nblk, Q6K_BYTES), np.uint8)
+    B[:, :208] = S[:nblk * 208].reshape(nblk, 208)
+    B[:, 208:] = S[nblk * 208:].reshape(nblk, 2)
+    return B.reshape(N, (K // 256) * Q6K_BYTES)
+
+
 def q6k_unpack(block):
     """(q - 32 as int8 [256], int8 scales [16], d as float32) of one block."""
     block = np.ascontiguousarray(block, dtype=np.uint8)

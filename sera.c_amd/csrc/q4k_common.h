@@ -84,6 +84,18 @@ static inline sera_stage_layout sera_q6k_mmq_stage_layout(size_t rows_padded, si
 
 static inline int sera_q6k_mmq_padded_rows(int M) { return (M + 31) / 32 * 32; }
 
+/* Q6_K device layouts of a weight matrix of nblk = N * K/256 blocks:
+ *   GGUF  (qtype 14):  block b at 210*b: ql[128], qh[64], sc[16], fp16 d;
+ *                      rows and blocks are only 2-byte aligned.
+ *   split (qtype SERA_QTYPE_Q6K_SPLIT): block b's ql, qh, sc (208 bytes,
+ *                      16-byte aligned) at 208*b; its fp16 d at
+ *                      208*nblk + 2*b. The same byte count as GGUF. */
+#define Q6K_GGUF_BYTES 210
+#define Q6K_SPLIT_QBYTES 208
+#ifndef SERA_QTYPE_Q6K_SPLIT
+#define SERA_QTYPE_Q6K_SPLIT 270u
+#endif
+
 #ifdef __HIPCC__
 typedef _Float16 f16;
 typedef int v4i __attribute__((ext_vector_type(4)));

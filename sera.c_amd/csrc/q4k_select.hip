@@ -18,11 +18,16 @@
  * of 2*(l/32) + (l%32)/16, so it agrees with q3_quant.c only on some
  * weights of each block.
  *
+ * Q6_K rows come as GGUF bytes (qtype 14) or in the split device layout
+ * (SERA_QTYPE_Q6K_SPLIT: 208-byte aligned ql/qh/sc blocks and a separate
+ * fp16 d array); both give the same values.
+ *
  * gfx950 mapping: one wave per output row; lane l takes weights 4l..4l+3 of
  * each 256-weight block (one sub-block, one group scale), reads its bytes as
- * aligned dwords through a buffer resource (Q6_K blocks are 2-byte aligned:
- * funnel shifts put the bytes in place) and its activations as one float4;
- * partial sums are reduced over the wave with xor shuffles in a fixed order.
+ * aligned dwords through a buffer resource (GGUF Q6_K blocks are 2-byte
+ * aligned: funnel shifts put the bytes in place) and its activations as one
+ * float4; partial sums are reduced over the wave with xor shuffles in a fixed
+ * order.
  */
 #include "q4k_common.h"
 
@@ -45,10 +50,19 @@ __device__ __forceinline__ uint32_t sel_load4(__amdgpu_buffer_rsrc_t r, uint32_t
     return __builtin_amdgcn_alignbit(hi, lo, (off & 3u) * 8u);
 }
 
-/* Weights e0..e0+3 (e0 % 4 == 0) of block `blk` of the row starting at byte
- * `row` (relative to the resource). */
+/* Block bytes of a row in each layout: Q4_K 144, Q6_K GGUF 210, Q6_K split
+ * 208 (ql, qh, sc; d in the separate array). */
 template <int QT>
-__device__ __forceinline__ void sel_dequant4(__amdgpu_buffer_rsrc_t r, uint32_t row, int blk, int e0, float w[4]) {
+__host__ __device__ constexpr uint32_t sel_block_bytes() {
+    return QT == 12 ? Q4K_BLOCK_BYTES : QT == 14 ? Q6K_GGUF_BYTES : Q6K_SPLIT_QBYTES;
+}
+
+/* Weights e0..e0+3 (e0 % 4 == 0) of block `blk` of the row starting at byte
+ * `row` (relative to the resource); dsplit = the block's fp16 d bits for the
+ * split layout. */
+template <int QT>
+__device__ __forceinline__ void sel_dequant4(__amdgpu_buffer_rsrc_t r, uint32_t row, int blk, int e0, uint32_t dsplit,
+                                             float w[4]) {
     if (QT == 12) {
         const uint32_t b = row + (uint32_t)blk * Q4K_BLOCK_BYTES;
         const uint32_t h0 = __builtin_amdgcn_raw_buffer_load_b32(r, b, 0, 0);
@@ -66,12 +80,21 @@ __device__ __forceinline__ void sel_dequant4(__amdgpu_buffer_rsrc_t r, uint32_t 
 #pragma unroll
         for (int i = 0; i < 4; i++) w[i] = __fsub_rn(__fmul_rn(d1, (float)((nib >> (8 * i)) & 15u)), m1);
     } else {
-        const uint32_t b = row + (uint32_t)blk * 210u;
+        const uint32_t b = row + (uint32_t)blk * sel_block_bytes<QT>();
         const int jh = e0 >> 7, k = (e0 & 127) >> 5, l = e0 & 31;
-        const uint32_t ql = sel_load4(r, b + 64 * jh + 32 * (k & 1) + l);
-        const uint32_t qh = sel_load4(r, b + 128 + 32 * jh + l);
-        const uint32_t sd = sel_load4(r, b + 192 + 8 * jh + 2 * k + (l >> 4));   /* byte 0 = the group scale */
-        const uint32_t dd = sel_load4(r, b + 208);                                  /* low half = d */
+        uint32_t ql, qh, sd, dd;
+        if (QT == 14) {
+            ql = sel_load4(r, b + 64 * jh + 32 * (k & 1) + l);
+            qh = sel_load4(r, b + 128 + 32 * jh + l);
+            sd = sel_load4(r, b + 192 + 8 * jh + 2 * k + (l >> 4));   /* byte 0 = the group scale */
+            dd = sel_load4(r, b + 208);                                  /* low half = d */
+        } else {   /* split: b is 16-byte aligned, l % 4 == 0 */
+            ql = __builtin_amdgcn_raw_buffer_load_b32(r, b + 64 * jh + 32 * (k & 1) + l, 0, 0);
+            qh = __builtin_amdgcn_raw_buffer_load_b32(r, b + 128 + 32 * jh + l, 0, 0);
+            const uint32_t so = b + 192 + 8 * jh + 2 * k + (l >> 4);
+            sd = __builtin_amdgcn_raw_buffer_load_b32(r, so & ~3u, 0, 0) >> (8 * (so & 3u));
+            dd = dsplit;
+        }
         const int sc = (int)(sd << 24) >> 24;
         const float dsc = __fmul_rn(h2f_bits(dd & 0xffffu), (float)sc);
         const uint32_t nib = (k >= 2) ? (ql >> 4) : ql;
@@ -86,11 +109,12 @@ __device__ __forceinline__ void sel_dequant4(__amdgpu_buffer_rsrc_t r, uint32_t 
 }  // namespace
 
 /* One wave per (branch, candidate); 4 per workgroup. Invalid ids (>= N)
- * give NaN. */
+ * give NaN. Wd: the split layout's d array (unused otherwise). */
 template <int QT>
 __global__ __launch_bounds__(256) void sera_candidate_logits_kernel(
-        const uint8_t *__restrict__ W, uint64_t wbytes, int N, int K, const float *__restrict__ hidden,
-        const uint32_t *__restrict__ ids, int per_branch, int total, float *__restrict__ logits) {
+        const uint8_t *__restrict__ W, const uint16_t *__restrict__ Wd, uint64_t wbytes, int N, int K,
+        const float *__restrict__ hidden, const uint32_t *__restrict__ ids, int per_branch, int total,
+        float *__restrict__ logits) {
     const int lane = threadIdx.x & 63;
     const int index = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (index >= total) return;
@@ -100,15 +124,16 @@ __global__ __launch_bounds__(256) void sera_candidate_logits_kernel(
         return;
     }
     const int nb = K / Q4K_QK;
-    const uint64_t rb = (uint64_t)nb * (QT == 12 ? Q4K_BLOCK_BYTES : 210u);
+    const uint64_t rb = (uint64_t)nb * sel_block_bytes<QT>();
     const uint64_t base = ((uint64_t)id * rb) & ~(uint64_t)15;
     const __amdgpu_buffer_rsrc_t r = sel_rsrc(W + base, wbytes - base);
     const uint32_t row = (uint32_t)((uint64_t)id * rb - base);
     const float *x = hidden + (size_t)(index / per_branch) * K;
+    const uint16_t *drow = QT == SERA_QTYPE_Q6K_SPLIT ? Wd + (size_t)id * nb : nullptr;
     float acc = 0.0f;
     for (int blk = 0; blk < nb; blk++) {
         float w[4];
-        sel_dequant4<QT>(r, row, blk, 4 * lane, w);
+        sel_dequant4<QT>(r, row, blk, 4 * lane, QT == SERA_QTYPE_Q6K_SPLIT ? drow[blk] : 0u, w);
         const float4 xv = *(const float4 *)(x + blk * Q4K_QK + 4 * lane);
         acc = fmaf(w[0], xv.x, acc);
         acc = fmaf(w[1], xv.y, acc);
@@ -124,8 +149,8 @@ __global__ __launch_bounds__(256) void sera_candidate_logits_kernel(
  * Tokens with ids >= N are left untouched, as in the reference. */
 template <int QT>
 __global__ __launch_bounds__(256) void sera_embedding_kernel(
-        const uint8_t *__restrict__ W, uint64_t wbytes, int N, int K, const uint32_t *__restrict__ ids, int tokens,
-        float *__restrict__ hidden) {
+        const uint8_t *__restrict__ W, const uint16_t *__restrict__ Wd, uint64_t wbytes, int N, int K,
+        const uint32_t *__restrict__ ids, int tokens, float *__restrict__ hidden) {
     const int lane = threadIdx.x & 63;
     const int nb = K / Q4K_QK;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -133,39 +158,57 @@ __global__ __launch_bounds__(256) void sera_embedding_kernel(
     const int t = (int)(unit / nb), blk = (int)(unit - (int64_t)t * nb);
     const uint32_t id = ids[t];
     if (id >= (uint32_t)N) return;
-    const uint64_t rb = (uint64_t)nb * (QT == 12 ? Q4K_BLOCK_BYTES : 210u);
+    const uint64_t rb = (uint64_t)nb * sel_block_bytes<QT>();
     const uint64_t base = ((uint64_t)id * rb) & ~(uint64_t)15;
     const __amdgpu_buffer_rsrc_t r = sel_rsrc(W + base, wbytes - base);
     float w[4];
-    sel_dequant4<QT>(r, (uint32_t)((uint64_t)id * rb - base), blk, 4 * lane, w);
+    sel_dequant4<QT>(r, (uint32_t)((uint64_t)id * rb - base), blk, 4 * lane,
+                     QT == SERA_QTYPE_Q6K_SPLIT ? Wd[(size_t)id * nb + blk] : 0u, w);
     *(float4 *)(hidden + (size_t)t * K + (size_t)blk * Q4K_QK + 4 * lane) = make_float4(w[0], w[1], w[2], w[3]);
 }
 
+namespace {
+/* bytes the kernels address through the resource, and the d array */
+uint64_t sel_qbytes(int qtype, int N, int K) {
+    const uint64_t nblk = (uint64_t)N * (uint64_t)(K / Q4K_QK);
+    return nblk * (qtype == 12 ? Q4K_BLOCK_BYTES : qtype == 14 ? Q6K_GGUF_BYTES : Q6K_SPLIT_QBYTES);
+}
+}  // namespace
+
+/* qtype 12 (Q4_K), 14 (Q6_K GGUF bytes) or SERA_QTYPE_Q6K_SPLIT. */
 extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
                                                    const uint32_t *ids, int branches, int per_branch,
                                                    float *logits, hipStream_t s) {
     const int total = branches * per_branch;
-    const uint64_t wbytes = (uint64_t)N * (uint64_t)(K / Q4K_QK) * (qtype == 12 ? Q4K_BLOCK_BYTES : 210u);
+    const uint64_t qb = sel_qbytes(qtype, N, K);
+    const uint8_t *w = (const uint8_t *)W;
+    const uint16_t *wd = (const uint16_t *)(w + qb);
     const dim3 grid((total + 3) / 4);
     if (qtype == 12)
-        hipLaunchKernelGGL(sera_candidate_logits_kernel<12>, grid, dim3(256), 0, s, (const uint8_t *)W, wbytes, N,
-                           K, hidden, ids, per_branch, total, logits);
+        hipLaunchKernelGGL(sera_candidate_logits_kernel<12>, grid, dim3(256), 0, s, w, wd, qb, N, K, hidden, ids,
+                           per_branch, total, logits);
+    else if (qtype == 14)
+        hipLaunchKernelGGL(sera_candidate_logits_kernel<14>, grid, dim3(256), 0, s, w, wd, qb, N, K, hidden, ids,
+                           per_branch, total, logits);
     else
-        hipLaunchKernelGGL(sera_candidate_logits_kernel<14>, grid, dim3(256), 0, s, (const uint8_t *)W, wbytes, N,
-                           K, hidden, ids, per_branch, total, logits);
+        hipLaunchKernelGGL(sera_candidate_logits_kernel<(int)SERA_QTYPE_Q6K_SPLIT>, grid, dim3(256), 0, s, w, wd, qb,
+                           N, K, hidden, ids, per_branch, total, logits);
     return hipGetLastError();
 }
 
 extern "C" hipError_t sera_launch_embedding(int qtype, const void *W, int N, int K, const uint32_t *ids, int tokens,
                                             float *hidden, hipStream_t s) {
-    const uint64_t wbytes = (uint64_t)N * (uint64_t)(K / Q4K_QK) * (qtype == 12 ? Q4K_BLOCK_BYTES : 210u);
+    const uint64_t qb = sel_qbytes(qtype, N, K);
+    const uint8_t *w = (const uint8_t *)W;
+    const uint16_t *wd = (const uint16_t *)(w + qb);
     const int64_t units = (int64_t)tokens * (K / Q4K_QK);
     const dim3 grid((unsigned)((units + 3) / 4));
     if (qtype == 12)
-        hipLaunchKernelGGL(sera_embedding_kernel<12>, grid, dim3(256), 0, s, (const uint8_t *)W, wbytes, N, K, ids,
-                           tokens, hidden);
+        hipLaunchKernelGGL(sera_embedding_kernel<12>, grid, dim3(256), 0, s, w, wd, qb, N, K, ids, tokens, hidden);
+    else if (qtype == 14)
+        hipLaunchKernelGGL(sera_embedding_kernel<14>, grid, dim3(256), 0, s, w, wd, qb, N, K, ids, tokens, hidden);
     else
-        hipLaunchKernelGGL(sera_embedding_kernel<14>, grid, dim3(256), 0, s, (const uint8_t *)W, wbytes, N, K, ids,
-                           tokens, hidden);
+        hipLaunchKernelGGL(sera_embedding_kernel<(int)SERA_QTYPE_Q6K_SPLIT>, grid, dim3(256), 0, s, w, wd, qb, N, K,
+                           ids, tokens, hidden);
     return hipGetLastError();
 }

@@ -99,9 +99,9 @@ __device__ __forceinline__ int q6m_sext8(uint32_t w, int sh) { return (int)(w <<
 }  // namespace
 
 /* Grid (tiles, K splits); splits > 1 write fp32 partials per split. */
-template <int TT, int WPE>
+template <int TT, int WPE, bool SPLIT>
 __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
-        const uint8_t *__restrict__ W, uint64_t wbytes, const _Float16 *__restrict__ xh,
+        const uint8_t *__restrict__ W, const uint16_t *__restrict__ Wd, uint64_t wbytes, const _Float16 *__restrict__ xh,
         const float *__restrict__ d8t, float *__restrict__ y, float *__restrict__ partial, int M, int Mpad,
         int N, int K, int kb_per_split, int accum) {
     constexpr int BM = 32 * TT;
@@ -114,7 +114,10 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
     const int n0 = (tile / ntt) * Q6M_BN, m0 = (tile % ntt) * BM;
     const int nb = K / Q4K_QK;
     const int kb0 = blockIdx.y * kb_per_split, kb1 = min(nb, kb0 + kb_per_split);
-    const uint32_t rb = (uint32_t)nb * Q6K_BLOCK_BYTES;
+    /* GGUF: 210-byte blocks at any 2-byte phase; split: 208-byte aligned
+     * blocks (ql, qh, sc) and d from the separate array Wd */
+    constexpr uint32_t BB = SPLIT ? Q6K_SPLIT_QBYTES : Q6K_BLOCK_BYTES;
+    const uint32_t rb = (uint32_t)nb * BB;
 
     /* weights: resource from the tile's first row (16-byte aligned down) to
      * the end of the matrix rounded up to 16 bytes (a chunk that straddles the
@@ -133,8 +136,8 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             if (inst < WINST) {
                 const int f = inst * 64 + lane;
                 const int r = f / Q6M_WCH, c = f - r * Q6M_WCH;
-                const uint32_t g = (uint32_t)((uint64_t)min(n0 + r, N - 1) * rb - gbase) + (uint32_t)kb * Q6K_BLOCK_BYTES;
-                const uint32_t vo = c < 14 ? (g & ~15u) + 16u * (uint32_t)c : 0x80000000u;
+                const uint32_t g = (uint32_t)((uint64_t)min(n0 + r, N - 1) * rb - gbase) + (uint32_t)kb * BB;
+                const uint32_t vo = c < (SPLIT ? 13 : 14) ? (g & ~15u) + 16u * (uint32_t)c : 0x80000000u;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, vo, 0, 0, 0);
             }
         }
@@ -161,6 +164,10 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
     /* this lane's weight row (B column) and its phase in the LDS window */
     const int wr = 32 * wave + l32;
     const uint32_t rowg = (uint32_t)((uint64_t)min(n0 + wr, N - 1) * rb - gbase);
+    /* split layout: this lane's d for the next K step, loaded a step ahead */
+    const uint16_t *drow = SPLIT ? Wd + (size_t)min(n0 + wr, N - 1) * nb : nullptr;
+    uint32_t dnext = 0;
+    if (SPLIT && kb0 < kb1) dnext = drow[kb0];
 
     v16f acc[TT], tmp[TT];
 #pragma unroll
@@ -182,11 +189,17 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
         const int buf = (kb - kb0) & 1;
         /* the lane's runs of this block from LDS: ql[64j + 32p + 16h + 0..15],
          * qh[32j + 16h + 0..15], bytes 192..207 (scales) and d */
-        const uint32_t base = (uint32_t)wr * (Q6M_WCH * 16) + (((rowg + (uint32_t)kb * Q6K_BLOCK_BYTES)) & 15u);
+        const uint32_t base = (uint32_t)wr * (Q6M_WCH * 16) + (SPLIT ? 0u : ((rowg + (uint32_t)kb * BB) & 15u));
         const uint32_t sh = (base & 2u) * 8u;
         q6v4u QL[4], QH[2], SC;
-        uint32_t dword;
-        {
+        uint32_t dword = 0;
+        if constexpr (SPLIT) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) QL[i] = *(const q6v4u *)&sm.w[base + 32u * i + 16u * h];
+#pragma unroll
+            for (int i = 0; i < 2; i++) QH[i] = *(const q6v4u *)&sm.w[base + 128u + 32u * i + 16u * h];
+            SC = *(const q6v4u *)&sm.w[base + 192u];
+        } else {
             const uint32_t X[6] = {16u * h, 32u + 16u * h, 64u + 16u * h, 96u + 16u * h, 128u + 16u * h,
                                    160u + 16u * h};
 #pragma unroll
@@ -201,11 +214,12 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             SC = q6m_align16(v, sh);
             dword = v[4];
         }
-        const float d = h2f_bits((dword >> sh) & 0xffffu);
+        const float d = SPLIT ? h2f_bits(dnext) : h2f_bits((dword >> sh) & 0xffffu);
         __syncthreads();   /* every wave has its runs: the weight buffer is free */
         if (kb + 1 < kb1) {
             issue_w(kb + 1);
             issue_x(kb + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
+            if (SPLIT) dnext = drow[kb + 1];
         }
 
         /* The lane's group scales sc = 16*sh + sl of sub-blocks b = 2m, 2m+1
@@ -351,17 +365,17 @@ extern "C" int sera_q6k_mmq_splits(int M, int N, int K) {
     return s;
 }
 
-template <int TT, int WPE>
-static hipError_t launch_q6k_mmq(const uint8_t *W, uint64_t wbytes, const _Float16 *xh, const float *d8t, float *y,
-                                 float *partial, int M, int Mpad, int N, int K, int splits, int accum,
-                                 hipStream_t s) {
+template <int TT, int WPE, bool SPLIT>
+static hipError_t launch_q6k_mmq(const uint8_t *W, const uint16_t *Wd, uint64_t wbytes, const _Float16 *xh,
+                                 const float *d8t, float *y, float *partial, int M, int Mpad, int N, int K, int splits,
+                                 int accum, hipStream_t s) {
     constexpr int BM = 32 * TT;
     const int tiles = (Mpad / BM) * ((N + Q6M_BN - 1) / Q6M_BN);
     const int nkb = K / Q4K_QK;
     const int per = (nkb + splits - 1) / splits;
     splits = (nkb + per - 1) / per;
-    hipLaunchKernelGGL((sera_q6k_mmq_kernel<TT, WPE>), dim3(tiles, splits), dim3(256), 0, s, W, wbytes, xh, d8t, y,
-                       splits > 1 ? partial : nullptr, M, Mpad, N, K, per, accum);
+    hipLaunchKernelGGL((sera_q6k_mmq_kernel<TT, WPE, SPLIT>), dim3(tiles, splits), dim3(256), 0, s, W, Wd, wbytes,
+                       xh, d8t, y, splits > 1 ? partial : nullptr, M, Mpad, N, K, per, accum);
     if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
     if (splits == 1) return hipSuccess;
     return sera_launch_splitk_reduce_acc(partial, y, (size_t)M * N, splits, accum, s);
@@ -369,21 +383,28 @@ static hipError_t launch_q6k_mmq(const uint8_t *W, uint64_t wbytes, const _Float
 
 /* stage: the Q6_K MMQ stage for Mpad = sera_q6k_mmq_padded_rows(M) rows;
  * partial: splits*M*N floats when splits > 1 (M*N % 4 == 0); accum != 0
- * adds the product to y. */
-extern "C" hipError_t sera_launch_q6k_mmq_acc(const void *W, const void *stage, float *y, float *partial, int M,
-                                              int N, int K, int splits, int accum, hipStream_t s) {
+ * adds the product to y. qtype 14: W is GGUF bytes; SERA_QTYPE_Q6K_SPLIT:
+ * W is the split layout. */
+extern "C" hipError_t sera_launch_q6k_mmq_acc(uint32_t qtype, const void *W, const void *stage, float *y,
+                                              float *partial, int M, int N, int K, int splits, int accum,
+                                              hipStream_t s) {
     const int Mpad = sera_q6k_mmq_padded_rows(M);
     const sera_stage_layout L = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K);
     const char *base = (const char *)stage;
     const _Float16 *xh = (const _Float16 *)(base + L.qs);
     const float *d8t = (const float *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
-    const uint64_t wbytes = (uint64_t)N * (uint64_t)(K / Q4K_QK) * Q6K_BLOCK_BYTES;
+    const uint64_t nblk = (uint64_t)N * (uint64_t)(K / Q4K_QK);
     if (splits < 1) splits = 1;
-    return launch_q6k_mmq<1, 2>(w, wbytes, xh, d8t, y, partial, M, Mpad, N, K, splits, accum, s);
+    if (qtype == SERA_QTYPE_Q6K_SPLIT)
+        return launch_q6k_mmq<1, 2, true>(w, (const uint16_t *)(w + nblk * Q6K_SPLIT_QBYTES),
+                                          nblk * Q6K_SPLIT_QBYTES, xh, d8t, y, partial, M, Mpad, N, K, splits, accum,
+                                          s);
+    return launch_q6k_mmq<1, 2, false>(w, nullptr, nblk * Q6K_BLOCK_BYTES, xh, d8t, y, partial, M, Mpad, N, K,
+                                       splits, accum, s);
 }
 
-extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
-                                          int K, int splits, hipStream_t s) {
-    return sera_launch_q6k_mmq_acc(W, stage, y, partial, M, N, K, splits, 0, s);
+extern "C" hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial,
+                                          int M, int N, int K, int splits, hipStream_t s) {
+    return sera_launch_q6k_mmq_acc(qtype, W, stage, y, partial, M, N, K, splits, 0, s);
 }

@@ -37,6 +37,7 @@
 #include "q4k_common.h"
 
 typedef __attribute__((address_space(3))) void q6_lds_void;
+typedef unsigned q6_v4u __attribute__((ext_vector_type(4)));
 
 #define Q6K_BLOCK_BYTES 210
 #define Q6K_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
@@ -264,6 +265,194 @@ __global__ __launch_bounds__(256) void sera_q6k_mmvq_kernel(
     }
 }
 
+/* ---- split device layout --------------------------------------------------
+ * The same product on the split layout (block b's ql, qh, sc at 208*b,
+ * 16-byte aligned; d in a separate fp16 array). Every lane field is now an
+ * aligned 16-byte load, so the kernel streams straight from HBM into
+ * registers, as the Q4_K MMVQ kernel does:
+ *   - a quad of lanes takes one block; lane q = (half j = q/2, l-half
+ *     lh = q%2) takes weights 128j + 32k + 16lh + [0, 16), k = 0..3: ql
+ *     bytes 64j + 16lh + [0, 16) (k = 0, 2) and 64j + 32 + 16lh + [0, 16)
+ *     (k = 1, 3), qh bytes 128 + 32j + 16lh + [0, 16), scale bytes
+ *     192 + 8j + [0, 8) (its group scales sc[8j + 2k + lh]) and d.
+ *   - a wave-load covers 8 consecutive blocks of 2 rows (lanes 32-63 take
+ *     the odd row); each lane walks R/2 row pairs with one activation slice
+ *     per token (4 x 16 quants, the 4 fp16 d8 of its Q8_1 blocks).
+ *   - NW waves split the row's groups of 8 blocks; partial sums meet in LDS
+ *     and are added in wave order (deterministic).
+ * Arithmetic as above: I_g exact (dot4 of the raw quants minus 32 * the
+ * group's activation quant sum), y = sum_blk d * sum_g d8 * (I_g * sc_g).
+ * Bounds: rows come from a buffer resource over this tile's rows; the
+ * last tile is shifted back to end at row N, and R = 4 needs N >= 4 (the
+ * launcher falls back to R = 2, whose odd row sits in the vector offset
+ * and reads zeros past N). */
+template <int M, int R, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(M == 1 ? 8 : 1))) void sera_q6s_mmvq_kernel(
+        const uint8_t *__restrict__ Wq, const uint16_t *__restrict__ Wd, const int8_t *__restrict__ xq,
+        const uint32_t *__restrict__ xds, float *__restrict__ y, int N, int K, int accum) {
+    constexpr int HR = R / 2;
+    static_assert(HR == 1 || HR == 2, "rows per workgroup 2 or 4");
+    __shared__ float s_part[NW][R][M];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane & 3, g = (lane >> 2) & 7, rs = lane >> 5;
+    const int j = q >> 1, lh = q & 1;
+    const int tile0 = blockIdx.x * R;
+    const int row0 = tile0 + R > N && N >= R ? N - R : tile0;
+    const int nb = K / Q4K_QK;
+    const int ngroups = (nb + 7) >> 3;
+    const int rowbytes = nb * Q6K_SPLIT_QBYTES;
+    const int nrows = min(R, N - row0);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(Wq + (size_t)row0 * rowbytes), (short)0, nrows * rowbytes, Q6K_RSRC_FLAGS);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(Wd + (size_t)row0 * nb), (short)0, (nrows * nb * 2 + 3) & ~3, Q6K_RSRC_FLAGS);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t *>(xq), (short)0, M * K, Q6K_RSRC_FLAGS);
+    const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t *>(xds), (short)0, M * (K / 32) * 4, Q6K_RSRC_FLAGS);
+    const int vo_w = rs * rowbytes + g * Q6K_SPLIT_QBYTES;
+    const int vo_la = vo_w + 64 * j + 16 * lh, vo_lb = vo_la + 32;
+    const int vo_qh = vo_w + 128 + 32 * j + 16 * lh, vo_sc = vo_w + 192 + 8 * j;
+    const int vo_d = (rs * nb + g) * 2;
+    const int vo_x = Q4K_QK * g + 128 * j + 16 * lh;
+    const int vo_ds = (8 * g + 4 * j) * 4;
+
+    float acc[HR][M];
+#pragma unroll
+    for (int r = 0; r < HR; r++)
+#pragma unroll
+        for (int t = 0; t < M; t++) acc[r][t] = 0.0f;
+
+    for (int bg = wave; bg < ngroups; bg += NW) {
+        if (bg * 8 + g >= nb) continue;
+        v4i x[M][4];
+        q6_v4u ds[M];
+#pragma unroll
+        for (int t = 0; t < M; t++) {
+            const int so = t * K + bg * 8 * Q4K_QK;
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                x[t][k] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x + 32 * k, so, 0));
+            ds[t] = __builtin_amdgcn_raw_buffer_load_b128(rf, vo_ds, (t * (K / 32) + bg * 64) * 4, 0);
+        }
+        q6_v4u la[HR], lb[HR], qh[HR];
+        uint32_t sc0[HR], sc1[HR], dd[HR];
+#pragma unroll
+        for (int r = 0; r < HR; r++) {
+            const int so = 2 * r * rowbytes + bg * 8 * Q6K_SPLIT_QBYTES;
+            la[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_la, so, 0);
+            lb[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_lb, so, 0);
+            qh[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qh, so, 0);
+            const uint2 sv = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, vo_sc, so, 0));
+            sc0[r] = sv.x;
+            sc1[r] = sv.y;
+            dd[r] = __builtin_amdgcn_raw_buffer_load_b16(rd, vo_d, (2 * r * nb + bg * 8) * 2, 0);
+        }
+        /* -32 * (sum of each group's 16 activation quants), shared by the rows */
+        int corr[M][4];
+#pragma unroll
+        for (int t = 0; t < M; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int m32 = (int)0xE0E0E0E0u;   /* four int8 -32 */
+                int c = __builtin_amdgcn_sdot4(x[t][k].x, m32, 0, false);
+                c = __builtin_amdgcn_sdot4(x[t][k].y, m32, c, false);
+                c = __builtin_amdgcn_sdot4(x[t][k].z, m32, c, false);
+                corr[t][k] = __builtin_amdgcn_sdot4(x[t][k].w, m32, c, false);
+            }
+#pragma unroll
+        for (int r = 0; r < HR; r++) {
+            const uint32_t A[4] = {la[r].x, la[r].y, la[r].z, la[r].w};
+            const uint32_t B[4] = {lb[r].x, lb[r].y, lb[r].z, lb[r].w};
+            const uint32_t H[4] = {qh[r].x, qh[r].y, qh[r].z, qh[r].w};
+            /* raw 6-bit quants of quarter k, four per dword (src/q3_quant.c:88-95) */
+            uint32_t v[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[0][i] = (A[i] & 0x0F0F0F0Fu) | ((H[i] << 4) & 0x30303030u);
+                v[1][i] = (B[i] & 0x0F0F0F0Fu) | ((H[i] << 2) & 0x30303030u);
+                v[2][i] = ((A[i] >> 4) & 0x0F0F0F0Fu) | (H[i] & 0x30303030u);
+                v[3][i] = ((B[i] >> 4) & 0x0F0F0F0Fu) | ((H[i] >> 2) & 0x30303030u);
+            }
+            const int scq[4] = {sext8(sc0[r], 8 * lh), sext8(sc0[r], 16 + 8 * lh), sext8(sc1[r], 8 * lh),
+                                sext8(sc1[r], 16 + 8 * lh)};
+            const float d = h2f_bits(dd[r] & 0xffffu);
+#pragma unroll
+            for (int t = 0; t < M; t++) {
+                float part = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    int I = __builtin_amdgcn_sdot4((int)v[k][0], x[t][k].x, corr[t][k], false);
+                    I = __builtin_amdgcn_sdot4((int)v[k][1], x[t][k].y, I, false);
+                    I = __builtin_amdgcn_sdot4((int)v[k][2], x[t][k].z, I, false);
+                    I = __builtin_amdgcn_sdot4((int)v[k][3], x[t][k].w, I, false);
+                    const uint32_t dw = k == 0 ? ds[t].x : k == 1 ? ds[t].y : k == 2 ? ds[t].z : ds[t].w;
+                    /* |I| <= 16 * 32 * 127 and |sc| <= 128: a 24-bit multiply is exact */
+                    part = fmaf(h2f_bits(dw & 0xffffu), (float)__mul24(I, scq[k]), part);
+                }
+                acc[r][t] = fmaf(d, part, acc[r][t]);
+            }
+        }
+    }
+
+    /* rows of a lane: row pair r, parity rs. HR = 2: one halving step
+     * (lanes with bit 16 keep row pair 1), then xor 8..1; HR = 1: xor 16..1. */
+#pragma unroll
+    for (int t = 0; t < M; t++) {
+        float s;
+        int row;
+        if constexpr (HR == 2) {
+            const bool up = (lane & 16) != 0;
+            const float send = up ? acc[0][t] : acc[1][t];
+            s = (up ? acc[1][t] : acc[0][t]) + __shfl_xor(send, 16, 64);
+            row = 2 * (up ? 1 : 0) + rs;
+        } else {
+            s = acc[0][t] + __shfl_xor(acc[0][t], 16, 64);
+            row = rs;
+        }
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+        if ((lane & 15) == 0 && (HR == 2 || (lane & 16) == 0)) s_part[wave][row][t] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < R * M) {
+        const int r = threadIdx.x / M, t = threadIdx.x % M;
+        float v = s_part[0][r][t];
+#pragma unroll
+        for (int w = 1; w < NW; w++) v += s_part[w][r][t];
+        if (row0 + r >= tile0 && row0 + r < N) {
+            float *dst = y + (size_t)t * N + row0 + r;
+            *dst = accum ? *dst + v : v;
+        }
+    }
+}
+
+template <int M, int R>
+static hipError_t launch_q6s_mmvq(const uint8_t *Wq, const uint16_t *Wd, const int8_t *xq, const uint32_t *xds,
+                                  float *y, int N, int K, int accum, hipStream_t s) {
+    const int ngroups = (K / Q4K_QK + 7) / 8;
+    const dim3 grid((N + R - 1) / R);
+    switch (ngroups >= 4 ? 4 : ngroups) {
+        case 1: hipLaunchKernelGGL((sera_q6s_mmvq_kernel<M, R, 1>), grid, dim3(64), 0, s, Wq, Wd, xq, xds, y, N, K,
+                                   accum); break;
+        case 2: hipLaunchKernelGGL((sera_q6s_mmvq_kernel<M, R, 2>), grid, dim3(128), 0, s, Wq, Wd, xq, xds, y, N,
+                                   K, accum); break;
+        case 3: hipLaunchKernelGGL((sera_q6s_mmvq_kernel<M, R, 3>), grid, dim3(192), 0, s, Wq, Wd, xq, xds, y, N,
+                                   K, accum); break;
+        default: hipLaunchKernelGGL((sera_q6s_mmvq_kernel<M, R, 4>), grid, dim3(256), 0, s, Wq, Wd, xq, xds, y, N,
+                                    K, accum); break;
+    }
+    return hipGetLastError();
+}
+
+template <int M>
+static hipError_t dispatch_q6s_r(int r, const uint8_t *Wq, const uint16_t *Wd, const int8_t *xq,
+                                 const uint32_t *xds, float *y, int N, int K, int accum, hipStream_t s) {
+    if (r == 4 && N >= 4) return launch_q6s_mmvq<M, 4>(Wq, Wd, xq, xds, y, N, K, accum, s);
+    return launch_q6s_mmvq<M, 2>(Wq, Wd, xq, xds, y, N, K, accum, s);
+}
+
 template <int M, int R>
 static hipError_t launch_q6k_mmvq(const uint8_t *W, uint64_t wbytes, const int8_t *xq, const uint32_t *xds,
                                   float *y, int N, int K, int accum, hipStream_t s) {
@@ -292,23 +481,42 @@ static hipError_t dispatch_q6k_r(int r, const uint8_t *W, uint64_t wbytes, const
     }
 }
 
-extern "C" hipError_t sera_launch_q6k_mmvq_acc(const void *W, const void *stage, float *y, int M, int N, int K,
-                                               int rows, int accum, hipStream_t s);
-
-extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K,
-                                           int rows, hipStream_t s) {
-    return sera_launch_q6k_mmvq_acc(W, stage, y, M, N, K, rows, 0, s);
+/* Rows per workgroup of the split-layout kernel (2 or 4): 2 measured
+ * fastest on MI355X at one token on down (5120 x 25600), the LM head
+ * (151936 x 5120) and v (1024 x 5120). */
+extern "C" int sera_q6s_mmvq_rows(int N, int M) {
+    (void)N;
+    (void)M;
+    return 2;
 }
 
-/* accum != 0 adds the product to y. */
-extern "C" hipError_t sera_launch_q6k_mmvq_acc(const void *W, const void *stage, float *y, int M, int N, int K,
-                                               int rows, int accum, hipStream_t s) {
+/* qtype 14: W is GGUF bytes, rows = rows per wave (1, 2, 4; 0 = built-in).
+ * qtype SERA_QTYPE_Q6K_SPLIT: W is the split layout, rows = rows per
+ * workgroup (2, 4; 0 = built-in). accum != 0 adds the product to y. */
+extern "C" hipError_t sera_launch_q6k_mmvq_acc(uint32_t qtype, const void *W, const void *stage, float *y, int M,
+                                               int N, int K, int rows, int accum, hipStream_t s) {
     const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
     const char *base = (const char *)stage;
     const int8_t *xq = (const int8_t *)(base + L.qs);
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
-    const uint64_t wbytes = (uint64_t)N * (uint64_t)(K / Q4K_QK) * Q6K_BLOCK_BYTES;
+    const uint64_t nblk = (uint64_t)N * (uint64_t)(K / Q4K_QK);
+    if (qtype == SERA_QTYPE_Q6K_SPLIT) {
+        const uint16_t *wd = (const uint16_t *)(w + nblk * Q6K_SPLIT_QBYTES);
+        if (rows <= 0) rows = sera_q6s_mmvq_rows(N, M);
+        switch (M) {
+            case 1: return dispatch_q6s_r<1>(rows, w, wd, xq, xds, y, N, K, accum, s);
+            case 2: return dispatch_q6s_r<2>(rows, w, wd, xq, xds, y, N, K, accum, s);
+            case 3: return dispatch_q6s_r<3>(rows, w, wd, xq, xds, y, N, K, accum, s);
+            case 4: return dispatch_q6s_r<4>(rows, w, wd, xq, xds, y, N, K, accum, s);
+            case 5: return dispatch_q6s_r<5>(rows, w, wd, xq, xds, y, N, K, accum, s);
+            case 6: return dispatch_q6s_r<6>(rows, w, wd, xq, xds, y, N, K, accum, s);
+            case 7: return dispatch_q6s_r<7>(rows, w, wd, xq, xds, y, N, K, accum, s);
+            case 8: return dispatch_q6s_r<8>(rows, w, wd, xq, xds, y, N, K, accum, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    const uint64_t wbytes = nblk * Q6K_BLOCK_BYTES;
     if (rows <= 0) rows = sera_q6k_mmvq_rows(N, M);
     switch (M) {
         case 1: return dispatch_q6k_r<1>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
@@ -321,4 +529,9 @@ extern "C" hipError_t sera_launch_q6k_mmvq_acc(const void *W, const void *stage,
         case 8: return dispatch_q6k_r<8>(rows, w, wbytes, xq, xds, y, N, K, accum, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+extern "C" hipError_t sera_launch_q6k_mmvq(uint32_t qtype, const void *W, const void *stage, float *y, int M, int N,
+                                           int K, int rows, hipStream_t s) {
+    return sera_launch_q6k_mmvq_acc(qtype, W, stage, y, M, N, K, rows, 0, s);
 }

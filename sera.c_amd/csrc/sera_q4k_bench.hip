@@ -21,10 +21,10 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *sta
 extern "C" int sera_mmq_slot_floats(int M);
 extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
                                              int M, int N, int K, int splits, hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K,
-                                           int rows, hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
-                                          int K, int splits, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmvq(uint32_t qtype, const void *W, const void *stage, float *y, int M, int N,
+                                           int K, int rows, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial,
+                                          int M, int N, int K, int splits, hipStream_t s);
 extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
                                                    const uint32_t *ids, int branches, int per_branch,
                                                    float *logits, hipStream_t s);
@@ -61,7 +61,8 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
  * the zeroed tile counters), 5 = Q6_K MMVQ (param = rows per wave), 6 = Q6_K
  * MMQ (param = splits), 7 / 8 = selected-row LM head on Q6_K / Q4_K rows
  * (stage = fp32 hidden [M][K], partial = the M*param candidate ids,
- * param = candidates per branch, y = logits).
+ * param = candidates per branch, y = logits), 9 / 10 / 11 = paths 5 / 6 / 7
+ * on Q6_K weights in the split layout (path 9: param = rows per workgroup).
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
  * elapsed time over iters (each launch's duration plus the dispatch gap to
@@ -77,11 +78,17 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
         switch (path) {
             case 0: return sera_launch_q4k_mmvq(w, stage, y, M, N, K, param, s);
             case 1: return sera_launch_q4k_mmq(w, stage, y, partial, M, N, K, param, s);
-            case 5: return sera_launch_q6k_mmvq(w, stage, y, M, N, K, param, s);
-            case 6: return sera_launch_q6k_mmq(w, stage, y, partial, M, N, K, param, s);
+            case 5:
+            case 9: return sera_launch_q6k_mmvq(path == 5 ? 14u : SERA_QTYPE_Q6K_SPLIT, w, stage, y, M, N, K, param,
+                                                s);
+            case 6:
+            case 10: return sera_launch_q6k_mmq(path == 6 ? 14u : SERA_QTYPE_Q6K_SPLIT, w, stage, y, partial, M, N, K,
+                                                param, s);
             case 7:
-            case 8: return sera_launch_candidate_logits(path == 7 ? 14 : 12, w, N, K, (const float *)stage,
-                                                        (const uint32_t *)partial, M, param, y, s);
+            case 8:
+            case 11: return sera_launch_candidate_logits(path == 7 ? 14 : path == 8 ? 12 : (int)SERA_QTYPE_Q6K_SPLIT,
+                                                         w, N, K, (const float *)stage, (const uint32_t *)partial, M,
+                                                         param, y, s);
             case 4: return sera_launch_q4k_mmq_streamk(
                         w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),
                         M, N, K, param, s);

@@ -24,13 +24,16 @@ extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, flo
 extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
                                           int M, int N, int K, int splits, hipStream_t s);
 extern "C" int sera_mmvq_rows_per_wave(int N, int M);
-extern "C" hipError_t sera_launch_q6k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K,
-                                           int rows, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmvq(uint32_t qtype, const void *W, const void *stage, float *y, int M, int N,
+                                           int K, int rows, hipStream_t s);
+extern "C" int sera_q6s_mmvq_rows(int N, int M);
+extern "C" hipError_t sera_launch_q6k_split(const void *src, void *dst, uint64_t first, uint64_t count,
+                                            uint64_t total, hipStream_t s);
 extern "C" int sera_q6k_mmvq_rows(int N, int M);
 extern "C" hipError_t sera_launch_q8_1_q6k_stage(const float *x, int M, int Mpad, int K, int row_formula,
                                                  void *stage, hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N,
-                                          int K, int splits, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial,
+                                          int M, int N, int K, int splits, hipStream_t s);
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
 extern "C" hipError_t sera_launch_q8_1_row_p(const float *x, const sera_producer *prod, int M, int K, void *stage,
                                              hipStream_t s);
@@ -49,10 +52,11 @@ extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, 
 extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots,
                                                       int *counters, int M, int N, int K, int P, int accum,
                                                       hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmvq_acc(const void *W, const void *stage, float *y, int M, int N, int K,
-                                               int rows, int accum, hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmq_acc(const void *W, const void *stage, float *y, float *partial, int M,
-                                              int N, int K, int splits, int accum, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmvq_acc(uint32_t qtype, const void *W, const void *stage, float *y, int M,
+                                               int N, int K, int rows, int accum, hipStream_t s);
+extern "C" hipError_t sera_launch_q6k_mmq_acc(uint32_t qtype, const void *W, const void *stage, float *y,
+                                              float *partial, int M, int N, int K, int splits, int accum,
+                                              hipStream_t s);
 extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
                                                    const uint32_t *ids, int branches, int per_branch,
                                                    float *logits, hipStream_t s);
@@ -390,8 +394,13 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
 
 namespace {
 /* Q6_K rows are K/256 * 210 bytes; the kernels address a row's bytes with
- * 32-bit offsets from the start of a group of rows. */
-bool q6k_shape_ok(const char *tag, int K) {
+ * 32-bit offsets from the start of a group of rows. qtype: 14 (GGUF bytes)
+ * or SERA_QTYPE_Q6K_SPLIT. */
+bool q6k_shape_ok(const char *tag, uint32_t qtype, int K) {
+    if (qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) {
+        fail(-1, "%s: qtype %u is not Q6_K (14) or Q6_K split (%u)", tag, qtype, SERA_QTYPE_Q6K_SPLIT);
+        return false;
+    }
     if ((uint64_t)(K / Q4K_QK) * 210u * 256u >= (1ull << 31)) {
         fail(-1, "%s: K=%d too long for 32-bit row offsets", tag, K);
         return false;
@@ -405,17 +414,22 @@ extern "C" int sera_q6k_mmvq_rows_per_wave(int M, int N) {
     return sera_q6k_mmvq_rows(N, M);
 }
 
-extern "C" int sera_q6k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
-                             int rows_per_wave, void *stream) {
+extern "C" int sera_q6k_mmvq(uint32_t qtype, const void *W, const void *row_stage, float *Y, int M, int N, int K,
+                             int rows, void *stream) {
     if (!W || !row_stage || !Y) return fail(-1, "sera_q6k_mmvq: null pointer");
     if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q6k_mmvq: batch M=%d outside 1..8", M);
     if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q6k_mmvq: bad shape N=%d K=%d", N, K);
-    if (rows_per_wave != 0 && rows_per_wave != 1 && rows_per_wave != 2 && rows_per_wave != 4)
-        return fail(-1, "sera_q6k_mmvq: rows_per_wave=%d not in {0,1,2,4}", rows_per_wave);
-    if (rows_per_wave == 4 && M > 4) return fail(-1, "sera_q6k_mmvq: rows_per_wave=4 needs M <= 4");
+    if (!q6k_shape_ok("sera_q6k_mmvq", qtype, K)) return -1;
+    if (qtype == SERA_QTYPE_Q6K_SPLIT) {
+        if (rows != 0 && rows != 2 && rows != 4)
+            return fail(-1, "sera_q6k_mmvq: rows=%d not in {0,2,4} for the split layout", rows);
+    } else {
+        if (rows != 0 && rows != 1 && rows != 2 && rows != 4)
+            return fail(-1, "sera_q6k_mmvq: rows_per_wave=%d not in {0,1,2,4}", rows);
+        if (rows == 4 && M > 4) return fail(-1, "sera_q6k_mmvq: rows_per_wave=4 needs M <= 4");
+    }
     if (((uintptr_t)W & 15u) != 0) return fail(-1, "sera_q6k_mmvq: W must be 16-byte aligned");
-    if (!q6k_shape_ok("sera_q6k_mmvq", K)) return -1;
-    return sera_launch_q6k_mmvq(W, row_stage, Y, M, N, K, rows_per_wave, (hipStream_t)stream) == hipSuccess
+    return sera_launch_q6k_mmvq(qtype, W, row_stage, Y, M, N, K, rows, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q6k_mmvq: launch failed");
 }
 
@@ -426,12 +440,12 @@ extern "C" int sera_q6k_mmvq(const void *W, const void *row_stage, float *Y, int
 
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
 
-extern "C" int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
-                                  int timed) {
+extern "C" int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
+                                  void *stream, int timed) {
     if (!check_shape("sera_q6k_dense_vec", W, X, Y, M, N, K)) return -1;
     if (M > SERA_Q4K_MMVQ_MAX_BATCH)
         return fail(-1, "sera_q6k_dense_vec: batch M=%d exceeds MMVQ cap %d", M, SERA_Q4K_MMVQ_MAX_BATCH);
-    if (!q6k_shape_ok("sera_q6k_dense_vec", K)) return -1;
+    if (!q6k_shape_ok("sera_q6k_dense_vec", qtype, K)) return -1;
     if (!g_arena) return fail(-1, "sera_q6k_dense_vec: no arena attached");
     hipStream_t s = (hipStream_t)stream;
     const bool mfma = M >= SERA_Q6K_VEC_MFMA_MIN_BATCH;
@@ -451,9 +465,9 @@ extern "C" int sera_q6k_dense_vec(const void *W, const float *X, float *Y, int M
     if (timed) record(g_ev.kernel_begin, s);
     if (mfma) {
         float *partial = partial_bytes ? (float *)(g_arena + stage_bytes) : nullptr;
-        if (sera_launch_q6k_mmq(W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
+        if (sera_launch_q6k_mmq(qtype, W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
             return fail(-3, "sera_q6k_dense_vec: tile kernel launch failed");
-    } else if (sera_launch_q6k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
+    } else if (sera_launch_q6k_mmvq(qtype, W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
         return fail(-3, "sera_q6k_dense_vec: mmvq launch failed");
     }
     if (timed) record(g_ev.kernel_end, s);
@@ -509,24 +523,25 @@ extern "C" int sera_q6k_mmq_splits_for(int M, int N, int K) {
     return q6k_splits(M, N, K);
 }
 
-extern "C" int sera_q6k_mmq(const void *W, const void *q6k_mmq_stage, float *Y, float *partial, int M, int N, int K,
-                            int splits, void *stream) {
+extern "C" int sera_q6k_mmq(uint32_t qtype, const void *W, const void *q6k_mmq_stage, float *Y, float *partial,
+                            int M, int N, int K, int splits, void *stream) {
     if (!W || !q6k_mmq_stage || !Y) return fail(-1, "sera_q6k_mmq: null pointer");
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q6k_mmq: bad shape M=%d N=%d K=%d", M, N, K);
     if (((uintptr_t)W & 15u) != 0) return fail(-1, "sera_q6k_mmq: W must be 16-byte aligned");
-    if (!q6k_shape_ok("sera_q6k_mmq", K)) return -1;
+    if (!q6k_shape_ok("sera_q6k_mmq", qtype, K)) return -1;
     if (splits == 0) splits = q6k_splits(M, N, K);
     if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q6k_mmq: splits=%d outside 1..K/256", splits);
     if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
         return fail(-1, "sera_q6k_mmq: split-K needs a partial buffer and M*N %% 4 == 0");
-    return sera_launch_q6k_mmq(W, q6k_mmq_stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
+    return sera_launch_q6k_mmq(qtype, W, q6k_mmq_stage, Y, partial, M, N, K, splits, (hipStream_t)stream) ==
+                   hipSuccess
                ? 0 : fail(-3, "sera_q6k_mmq: launch failed");
 }
 
-extern "C" int sera_q6k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
-                              int timed) {
+extern "C" int sera_q6k_dense(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
+                              void *stream, int timed) {
     if (!check_shape("sera_q6k_dense", W, X, Y, M, N, K)) return -1;
-    if (!q6k_shape_ok("sera_q6k_dense", K)) return -1;
+    if (!q6k_shape_ok("sera_q6k_dense", qtype, K)) return -1;
     if (!g_arena) return fail(-1, "sera_q6k_dense: no arena attached");
     hipStream_t s = (hipStream_t)stream;
     const int Mpad = sera_q6k_mmq_padded_rows(M);
@@ -542,9 +557,80 @@ extern "C" int sera_q6k_dense(const void *W, const float *X, float *Y, int M, in
         return fail(-2, "sera_q6k_dense: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    if (sera_launch_q6k_mmq(W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
+    if (sera_launch_q6k_mmq(qtype, W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
         return fail(-3, "sera_q6k_dense: mmq launch failed");
     if (timed) record(g_ev.kernel_end, s);
+    return 0;
+}
+
+/* ---- device layouts at upload ------------------------------------------ */
+
+namespace {
+bool layout_args_ok(const char *tag, uint32_t qtype, int N, int K) {
+    if (qtype != 12u && qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) {
+        fail(-1, "%s: qtype %u is not Q4_K (12), Q6_K (14) or Q6_K split (%u)", tag, qtype, SERA_QTYPE_Q6K_SPLIT);
+        return false;
+    }
+    if (N <= 0 || K <= 0 || K % Q4K_QK) {
+        fail(-1, "%s: bad shape N=%d K=%d", tag, N, K);
+        return false;
+    }
+    return true;
+}
+}  // namespace
+
+extern "C" size_t sera_weight_bytes(uint32_t qtype, int N, int K) {
+    if ((qtype != 12u && qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
+    return (size_t)N * (size_t)(K / Q4K_QK) * (qtype == 12u ? Q4K_BLOCK_BYTES : Q6K_GGUF_BYTES);
+}
+
+extern "C" int sera_weight_to_device_layout(uint32_t qtype, int N, int K, const void *gguf, void *dst, void *stream) {
+    const char *tag = "sera_weight_to_device_layout";
+    if (!gguf || !dst) return fail(-1, "%s: null pointer", tag);
+    if (!layout_args_ok(tag, qtype, N, K)) return -1;
+    const size_t bytes = sera_weight_bytes(qtype, N, K);
+    hipStream_t s = (hipStream_t)stream;
+    if (qtype != SERA_QTYPE_Q6K_SPLIT) {
+        if (gguf == dst) return 0;
+        return hipMemcpyAsync(dst, gguf, bytes, hipMemcpyDeviceToDevice, s) == hipSuccess
+                   ? 0 : fail(-3, "%s: copy failed", tag);
+    }
+    const char *a = (const char *)gguf, *b = (const char *)dst;
+    if (a < b + bytes && b < a + bytes) return fail(-1, "%s: source and destination overlap", tag);
+    if (((uintptr_t)gguf & 1u) || ((uintptr_t)dst & 15u))
+        return fail(-1, "%s: GGUF bytes must be 2-byte and dst 16-byte aligned", tag);
+    const uint64_t total = (uint64_t)N * (uint64_t)(K / Q4K_QK);
+    return sera_launch_q6k_split(gguf, dst, 0, total, total, s) == hipSuccess ? 0 : fail(-3, "%s: launch failed", tag);
+}
+
+extern "C" int sera_weight_upload(uint32_t qtype, int N, int K, const void *host_gguf, void *dst, void *staging,
+                                  size_t staging_bytes, void *stream) {
+    const char *tag = "sera_weight_upload";
+    if (!host_gguf || !dst) return fail(-1, "%s: null pointer", tag);
+    if (!layout_args_ok(tag, qtype, N, K)) return -1;
+    const size_t bytes = sera_weight_bytes(qtype, N, K);
+    hipStream_t s = (hipStream_t)stream;
+    if (qtype != SERA_QTYPE_Q6K_SPLIT)
+        return hipMemcpyAsync(dst, host_gguf, bytes, hipMemcpyHostToDevice, s) == hipSuccess
+                   ? 0 : fail(-3, "%s: host-to-device copy failed", tag);
+    if (!staging || staging_bytes < Q6K_GGUF_BYTES)
+        return fail(-1, "%s: the split layout needs a device staging buffer of at least %d bytes", tag,
+                    Q6K_GGUF_BYTES);
+    if (((uintptr_t)staging & 15u) || ((uintptr_t)dst & 15u))
+        return fail(-1, "%s: staging and dst must be 16-byte aligned", tag);
+    const uint64_t total = (uint64_t)N * (uint64_t)(K / Q4K_QK);
+    const uint64_t per = staging_bytes / Q6K_GGUF_BYTES;
+    const char *src = (const char *)host_gguf;
+    /* one stream: the copy into the staging buffer waits for the repack that
+     * last read it */
+    for (uint64_t first = 0; first < total; first += per) {
+        const uint64_t count = total - first < per ? total - first : per;
+        if (hipMemcpyAsync(staging, src + first * Q6K_GGUF_BYTES, count * Q6K_GGUF_BYTES, hipMemcpyHostToDevice,
+                           s) != hipSuccess)
+            return fail(-3, "%s: host-to-device copy failed", tag);
+        if (sera_launch_q6k_split(staging, dst, first, count, total, s) != hipSuccess)
+            return fail(-3, "%s: repack launch failed", tag);
+    }
     return 0;
 }
 
@@ -553,7 +639,10 @@ extern "C" int sera_q6k_dense(const void *W, const float *X, float *Y, int M, in
 namespace {
 bool rows_shape_ok(const char *tag, int qtype, const void *W, int N, int K) {
     if (!W) { fail(-1, "%s: null weight pointer", tag); return false; }
-    if (qtype != 12 && qtype != 14) { fail(-1, "%s: qtype %d is not Q4_K (12) or Q6_K (14)", tag, qtype); return false; }
+    if (qtype != 12 && qtype != 14 && qtype != (int)SERA_QTYPE_Q6K_SPLIT) {
+        fail(-1, "%s: qtype %d is not Q4_K (12), Q6_K (14) or Q6_K split (%u)", tag, qtype, SERA_QTYPE_Q6K_SPLIT);
+        return false;
+    }
     if (N <= 0 || K <= 0 || K % Q4K_QK) { fail(-1, "%s: bad shape N=%d K=%d", tag, N, K); return false; }
     if (((uintptr_t)W & 15u) != 0) { fail(-1, "%s: W must be 16-byte aligned", tag); return false; }
     if ((uint64_t)(K / Q4K_QK) * 210u >= (1ull << 30)) { fail(-1, "%s: K=%d too long", tag, K); return false; }
@@ -613,8 +702,8 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         if (!check_shape(tag, weights[i], X, outputs[i], M, g->N, K)) return -1;
         N[i] = g->N;
     }
-    if (qt != 12 && qt != 14) return fail(-1, "%s: qtype %u is not Q4_K/Q6_K", tag, qt);
-    if (qt == 14 && !q6k_shape_ok(tag, K)) return -1;
+    if (qt != 12 && qt != 14 && qt != SERA_QTYPE_Q6K_SPLIT) return fail(-1, "%s: qtype %u is not Q4_K/Q6_K", tag, qt);
+    if (qt != 12 && !q6k_shape_ok(tag, qt, K)) return -1;
     hipStream_t s = (hipStream_t)stream;
     const int accum = (flags & SERA_LIN_ACCUMULATE) ? 1 : 0;
     sera_producer prod = {0, X2, gamma, eps};
@@ -678,11 +767,11 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
                 e = sera_launch_q4k_mmq_acc(weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
             }
         } else if (M < SERA_Q6K_VEC_MFMA_MIN_BATCH) {
-            e = sera_launch_q6k_mmvq_acc(weights[i], g_arena, outputs[i], M, n, K, 0, accum, s);
+            e = sera_launch_q6k_mmvq_acc(qt, weights[i], g_arena, outputs[i], M, n, K, 0, accum, s);
         } else {
             int sp = mn4 ? sera_q6k_mmq_splits(M, n, K) : 1;
             if ((size_t)sp * M * n > partial_cap) sp = 1;
-            e = sera_launch_q6k_mmq_acc(weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
+            e = sera_launch_q6k_mmq_acc(qt, weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
         }
         if (e != hipSuccess) return fail(-3, "%s: product %d launch failed", tag, i);
     }

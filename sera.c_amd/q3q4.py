@@ -69,6 +69,7 @@ def load():
     P, I, I64, SZ, B = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t,
                         ctypes.c_bool)
     CP = ctypes.c_char_p
+    U32 = ctypes.c_uint32
     sigs = {
         # q3_q4_linear.h
         "q3_q4_linear_bind_geometry": ([ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
@@ -111,17 +112,20 @@ def load():
         "sera_q4k_subblock_dots": ([P, P, P, I, I, I, P], I),
         "sera_q4k_quantize": ([P, I64, I64, P, P], I),
         "sera_q4k_last_error": ([], CP),
-        "sera_q6k_dense": ([P, P, P, I, I, I, P, I], I),
-        "sera_q6k_dense_vec": ([P, P, P, I, I, I, P, I], I),
+        "sera_q6k_dense": ([U32, P, P, P, I, I, I, P, I], I),
+        "sera_q6k_dense_vec": ([U32, P, P, P, I, I, I, P, I], I),
         "sera_q6k_kernel_launches": ([I, I, I], I),
-        "sera_q6k_mmvq": ([P, P, P, I, I, I, I, P], I),
+        "sera_q6k_mmvq": ([U32, P, P, P, I, I, I, I, P], I),
         "sera_q6k_mmvq_rows_per_wave": ([I, I], I),
         "sera_q8_1_q6k_mmq_padded_rows": ([I], I),
         "sera_q8_1_q6k_mmq_stage_bytes": ([I, I], SZ),
         "sera_q8_1_q6k_mmq_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ)], None),
         "sera_q8_1_quantize_mmq_d4": ([P, I, I, P, P], I),
         "sera_q8_1_quantize_row_q6k": ([P, I, I, P, P], I),
-        "sera_q6k_mmq": ([P, P, P, P, I, I, I, I, P], I),
+        "sera_q6k_mmq": ([U32, P, P, P, P, I, I, I, I, P], I),
+        "sera_weight_bytes": ([U32, I, I], SZ),
+        "sera_weight_to_device_layout": ([U32, I, I, P, P, P], I),
+        "sera_weight_upload": ([U32, I, I, P, P, P, SZ, P], I),
         "sera_q6k_mmq_splits_for": ([I, I, I], I),
         "sera_candidate_logits": ([I, P, I, I, P, I, P, I, P, P], I),
         "sera_linear_group": ([I, P, P, P, P, P, P, ctypes.c_float, SZ, ctypes.c_uint, P], I),
@@ -320,14 +324,38 @@ def quantize_row_q6k(x, stage, stream=None):
            "sera_q8_1_quantize_row_q6k")
 
 
-def q6k_mmvq(W, stage, out, M, N, K, rows_per_wave=0, stream=None):
-    _check(load().sera_q6k_mmvq(_ptr(W), _ptr(stage), _ptr(out), M, N, K, rows_per_wave,
+QTYPE_Q6K_SPLIT = 270   # SERA_QTYPE_Q6K_SPLIT: Q6_K in the split device layout
+
+
+def q6k_mmvq(W, stage, out, M, N, K, rows_per_wave=0, stream=None, qtype=14):
+    """qtype 14: W is GGUF bytes (rows_per_wave in {0,1,2,4}); QTYPE_Q6K_SPLIT:
+    W is the split layout (rows per workgroup in {0,2,4})."""
+    _check(load().sera_q6k_mmvq(qtype, _ptr(W), _ptr(stage), _ptr(out), M, N, K, rows_per_wave,
                                 _stream(stream)), "sera_q6k_mmvq")
 
 
-def q6k_mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None):
-    _check(load().sera_q6k_mmq(_ptr(W), _ptr(stage), _ptr(out), _ptr(partial), M, N, K, splits,
+def q6k_mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None, qtype=14):
+    _check(load().sera_q6k_mmq(qtype, _ptr(W), _ptr(stage), _ptr(out), _ptr(partial), M, N, K, splits,
                                _stream(stream)), "sera_q6k_mmq")
+
+
+def weight_bytes(qtype, N, K):
+    return load().sera_weight_bytes(qtype, N, K)
+
+
+def weight_to_device_layout(qtype, N, K, gguf, dst, stream=None):
+    """GGUF bytes on the device -> dst in the layout of qtype."""
+    _check(load().sera_weight_to_device_layout(qtype, N, K, _ptr(gguf), _ptr(dst), _stream(stream)),
+           "sera_weight_to_device_layout")
+
+
+def weight_upload(qtype, N, K, host_gguf, dst, staging=None, stream=None):
+    """host_gguf: a C-contiguous numpy uint8 array of GGUF bytes (kept alive
+    until the stream has run the copies); staging: a device uint8 tensor
+    (needed for the split layout)."""
+    sb = staging.numel() if staging is not None else 0
+    _check(load().sera_weight_upload(qtype, N, K, ctypes.c_void_p(host_gguf.ctypes.data), _ptr(dst),
+                                     _ptr(staging), sb, _stream(stream)), "sera_weight_upload")
 
 
 def q6k_mmq_splits(M, N, K):

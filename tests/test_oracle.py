@@ -580,3 +580,34 @@ def test_silu_mul_matches_exact_math():
     ref = Gd / (1 + np.exp(-Gd)) * U
     assert np.max(np.abs(s - ref) / (np.abs(ref) + 1e-30)) < 4e-7
     assert oracle.silu_mul(np.float32([0.0]), np.float32([5.0]))[0] == 0.0
+
+
+# ---------------------------------------------------------------------------
+# Q6_K split device layout (a byte permutation of the GGUF blocks)
+# ---------------------------------------------------------------------------
+
+def test_q6k_split_places_fields_by_hand():
+    """Two blocks of one row: block b's ql[0], qh[0], sc[0] land at 208*b,
+    208*b + 128, 208*b + 192 and its d at 208*2 + 2*b."""
+    W = np.zeros((1, 2 * 210), np.uint8)
+    for b, (ql0, qh0, sc0, d) in enumerate([(0x11, 0x22, 0x33, 1.5), (0x44, 0x55, 0x66, -2.0)]):
+        W[0, 210 * b + 0], W[0, 210 * b + 128], W[0, 210 * b + 192] = ql0, qh0, sc0
+        W[0, 210 * b + 208:210 * b + 210] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    S = oracle.q6k_split(W, 1, 512)
+    assert S.size == 420
+    assert (S[0], S[128], S[192]) == (0x11, 0x22, 0x33)
+    assert (S[208], S[208 + 128], S[208 + 192]) == (0x44, 0x55, 0x66)
+    assert S[416:418].view(np.float16)[0] == 1.5 and S[418:420].view(np.float16)[0] == -2.0
+
+
+def test_q6k_split_round_trip_and_dequant():
+    N, K = 7, 768
+    W = oracle.q6k_weights(RNG, N, K)
+    S = oracle.q6k_split(W, N, K)
+    assert S.size == W.size
+    assert np.array_equal(oracle.q6k_unsplit(S, N, K), W)
+    # a planted mistake (d of the neighbouring block) changes the values
+    bad = S.copy()
+    nblk = N * K // 256
+    bad[nblk * 208:] = np.roll(bad[nblk * 208:].reshape(nblk, 2), 1, axis=0).reshape(-1)
+    assert not np.array_equal(oracle.dequant_q6k(oracle.q6k_unsplit(bad, N, K), N, K), oracle.dequant_q6k(W, N, K))
