@@ -225,7 +225,7 @@ def main():
 
     if not args.quick:
         results["selected_row_lm_head"] = lm_head_rows(torch, dev, bench_kernel)
-        results["q6k_down"] = q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel,
+        results["q6k"] = q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel,
                                         args)
 
     if args.full:
@@ -303,50 +303,90 @@ def lm_head_rows(torch, dev, bench_kernel):
 def q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel, args):
     """Q6_K weights (random ql/qh/scale bytes, fp16 d ~2e-5: the reference
     repo has no Q6_K quantizer) on the down shape 25600 -> 5120, 4 copies
-    (430 MB) round robin: the whole q3_cuda_q4k_linear call and the kernel
-    alone (MMVQ kernel up to 4 tokens, the fp16-MFMA tile kernel from 5)."""
-    N, K, copies = 5120, 25600, 4
-    ws = []
-    for i in range(copies):
-        gen = torch.Generator(device=dev).manual_seed(700 + i)
-        w = torch.randint(0, 256, (N, K // 256, 210), generator=gen, device=dev, dtype=torch.uint8)
-        d = (torch.rand((N, K // 256), generator=gen, device=dev) + 0.5) * 2e-5
-        w[:, :, 208:210] = d.to(torch.float16).view(torch.uint8).view(N, K // 256, 2)
-        ws.append(w.view(N, -1))
-    arr = (ctypes.c_void_p * copies)(*[w.data_ptr() for w in ws])
-    geo = q3q4.bind_geometry(q3q4.QTYPE_Q6_K, K, N)
-    rows = []
-    iters = max(20, args.steps // 5)
-    for M in (1, 4, 8, 512):
-        x = activations(M, K, 40 + M)
-        y = torch.empty((M, N), dtype=torch.float32, device=dev)
-        step_ms = bench_linear(geo, arr, copies, x, y, 5, iters if M < 512 else 10)
-        tile = M >= 5
-        if tile:
-            stage = torch.empty(q3q4.q6k_mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
-            (q3q4.quantize_row_q6k if M <= 8 else q3q4.quantize_mmq_d4)(x, stage)
-            sp = q3q4.q6k_mmq_splits(M, N, K)
-            part = torch.empty(sp * M * N, dtype=torch.float32, device=dev) if sp > 1 else None
-            kavg, _ = bench_kernel(6, arr, copies, stage, y, part, M, N, K, sp, 5, iters if M < 512 else 10)
-            kname = "sera_q6k_mmq_kernel<1, 2>"
-        else:
-            stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
-            q3q4.quantize_row(x, stage)
-            rpw = L.sera_q6k_mmvq_rows_per_wave(M, N)
-            kavg, _ = bench_kernel(5, arr, copies, stage, y, None, M, N, K, rpw, 5, iters)
-            kname = f"sera_q6k_mmvq_kernel<{M}, {rpw}>"
+    (430 MB) round robin, in both device layouts (GGUF bytes, qtype 14, and
+    the split layout, qtype 270): the whole q3_cuda_q4k_linear call and the
+    kernel alone (MMVQ kernel up to 4 tokens, the fp16-MFMA tile kernel from
+    5). Then the full-vocabulary LM head (151936 x 5120) at one token on
+    both layouts, 2 copies (1.28 GB)."""
+    def q6k_copies(N, K, copies, seed):
+        ws, ss = [], []
+        for i in range(copies):
+            gen = torch.Generator(device=dev).manual_seed(seed + i)
+            w = torch.randint(0, 256, (N, K // 256, 210), generator=gen, device=dev, dtype=torch.uint8)
+            d = (torch.rand((N, K // 256), generator=gen, device=dev) + 0.5) * 2e-5
+            w[:, :, 208:210] = d.to(torch.float16).view(torch.uint8).view(N, K // 256, 2)
+            sp = torch.empty(w.numel(), dtype=torch.uint8, device=dev)
+            q3q4.weight_to_device_layout(q3q4.QTYPE_Q6K_SPLIT, N, K, w, sp)
+            ws.append(w.view(N, -1))
+            ss.append(sp)
+        torch.cuda.synchronize()
+        return ws, ss
+
+    def row_of(layout, M, N, K, kname, step_ms, kavg):
         b = alg_bytes(M, N, K, 210)
         ops = 2.0 * M * N * K
-        row = {"M": M, "N": N, "K": K, "kernel": kname,
-               "step_us": round(step_ms * 1e3, 2), "kernel_us": round(kavg * 1e3, 2),
+        row = {"layout": layout, "M": M, "N": N, "K": K, "kernel": kname,
+               "step_us": round(step_ms * 1e3, 2) if step_ms is not None else None,
+               "kernel_us": round(kavg * 1e3, 2),
                "kernel_GBps": round(b / (kavg * 1e-3) / 1e9, 1),
                "kernel_frac_hbm": round(b / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "kernel_TOPS": round(ops / (kavg * 1e-3) / 1e12, 1),
                "kernel_frac_int8": round(ops / (kavg * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
-        log(f"[bench] q6k down M={M}: step {row['step_us']} us, kernel {row['kernel_us']} us "
+        log(f"[bench] q6k {layout} N={N} K={K} M={M}: step {row['step_us']} us, kernel {row['kernel_us']} us "
             f"({row['kernel_GBps']} GB/s, {row['kernel_TOPS']} TOPS)")
-        rows.append(row)
-    del ws
+        return row
+
+    N, K, copies = 5120, 25600, 4
+    ws, ss = q6k_copies(N, K, copies, 700)
+    rows = []
+    iters = max(20, args.steps // 5)
+    for layout, qt, bufs in (("gguf", q3q4.QTYPE_Q6_K, ws), ("split", q3q4.QTYPE_Q6K_SPLIT, ss)):
+        arr = (ctypes.c_void_p * copies)(*[w.data_ptr() for w in bufs])
+        geo = q3q4.bind_geometry(qt, K, N)
+        split = qt == q3q4.QTYPE_Q6K_SPLIT
+        for M in (1, 2, 4, 8, 512):
+            x = activations(M, K, 40 + M)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            step_ms = bench_linear(geo, arr, copies, x, y, 5, iters if M < 512 else 10)
+            if M >= 5:
+                stage = torch.empty(q3q4.q6k_mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
+                (q3q4.quantize_row_q6k if M <= 8 else q3q4.quantize_mmq_d4)(x, stage)
+                sp = q3q4.q6k_mmq_splits(M, N, K)
+                part = torch.empty(sp * M * N, dtype=torch.float32, device=dev) if sp > 1 else None
+                kavg, _ = bench_kernel(10 if split else 6, arr, copies, stage, y, part, M, N, K, sp, 5,
+                                       iters if M < 512 else 10)
+                rows.append(row_of(layout, M, N, K, f"sera_q6k_mmq_kernel<1, 2, {str(split).lower()}>",
+                                   step_ms, kavg))
+                continue
+            stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
+            q3q4.quantize_row(x, stage)
+            if split:
+                # the built-in 4 rows per workgroup (the step above), then 2 for comparison
+                for r in (4, 2):
+                    kavg, _ = bench_kernel(9, arr, copies, stage, y, None, M, N, K, r, 5, iters)
+                    rows.append(row_of(layout, M, N, K, f"sera_q6s_mmvq_kernel<{M}, {r}, 4>",
+                                       step_ms if r == 4 else None, kavg))
+            else:
+                rpw = L.sera_q6k_mmvq_rows_per_wave(M, N)
+                kavg, _ = bench_kernel(5, arr, copies, stage, y, None, M, N, K, rpw, 5, iters)
+                rows.append(row_of(layout, M, N, K, f"sera_q6k_mmvq_kernel<{M}, {rpw}>", step_ms, kavg))
+    del ws, ss
+    torch.cuda.empty_cache()
+
+    N, K, copies = 151936, 5120, 2
+    ws, ss = q6k_copies(N, K, copies, 800)
+    x = activations(1, K, 41)
+    y = torch.empty((1, N), dtype=torch.float32, device=dev)
+    stage = torch.empty(q3q4.row_stage_layout(1, K)["total"], dtype=torch.uint8, device=dev)
+    q3q4.quantize_row(x, stage)
+    for layout, path, bufs, kname in (("gguf", 5, ws, "sera_q6k_mmvq_kernel<1, 4>"),
+                                      ("split", 9, ss, "sera_q6s_mmvq_kernel<1, 4, 3>")):
+        arr = (ctypes.c_void_p * copies)(*[w.data_ptr() for w in bufs])
+        geo = q3q4.bind_geometry(q3q4.QTYPE_Q6_K if path == 5 else q3q4.QTYPE_Q6K_SPLIT, K, N)
+        step_ms = bench_linear(geo, arr, copies, x, y, 3, 20)
+        kavg, _ = bench_kernel(path, arr, copies, stage, y, None, 1, N, K, 0, 3, 20)
+        rows.append(row_of(layout, 1, N, K, kname, step_ms, kavg))
+    del ws, ss
     torch.cuda.empty_cache()
     return rows
 

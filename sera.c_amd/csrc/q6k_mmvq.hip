@@ -38,6 +38,9 @@
 
 typedef __attribute__((address_space(3))) void q6_lds_void;
 typedef unsigned q6_v4u __attribute__((ext_vector_type(4)));
+#ifndef SERA_Q6S_ISSUE_ALL_MAX_M
+#define SERA_Q6S_ISSUE_ALL_MAX_M 4
+#endif
 
 #define Q6K_BLOCK_BYTES 210
 #define Q6K_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(256) void sera_q6k_mmvq_kernel(
  * launcher falls back to R = 2, whose odd row sits in the vector offset
  * and reads zeros past N). */
 template <int M, int R, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(M == 1 ? 8 : 1))) void sera_q6s_mmvq_kernel(
+__global__ __launch_bounds__(NW * 64) void sera_q6s_mmvq_kernel(
         const uint8_t *__restrict__ Wq, const uint16_t *__restrict__ Wd, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, float *__restrict__ y, int N, int K, int accum) {
     constexpr int HR = R / 2;
@@ -349,6 +352,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(M == 1 
             sc1[r] = sv.y;
             dd[r] = __builtin_amdgcn_raw_buffer_load_b16(rd, vo_d, (2 * r * nb + bg * 8) * 2, 0);
         }
+        /* up to 4 tokens every load of the group is in flight before any
+         * compute: without this fence the scheduler trades the later loads
+         * for registers and the wave waits on HBM several times per group
+         * (measured 20-25% slower at 1-4 tokens on down and the LM head) */
+        if constexpr (M <= SERA_Q6S_ISSUE_ALL_MAX_M) __builtin_amdgcn_sched_barrier(0);
         /* -32 * (sum of each group's 16 activation quants), shared by the rows */
         int corr[M][4];
 #pragma unroll
@@ -383,10 +391,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(M == 1 
                 float part = 0.0f;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    int I = __builtin_amdgcn_sdot4((int)v[k][0], x[t][k].x, corr[t][k], false);
+                    int I = __builtin_amdgcn_sdot4((int)v[k][0], x[t][k].x, 0, false);
                     I = __builtin_amdgcn_sdot4((int)v[k][1], x[t][k].y, I, false);
                     I = __builtin_amdgcn_sdot4((int)v[k][2], x[t][k].z, I, false);
                     I = __builtin_amdgcn_sdot4((int)v[k][3], x[t][k].w, I, false);
+                    I += corr[t][k];
                     const uint32_t dw = k == 0 ? ds[t].x : k == 1 ? ds[t].y : k == 2 ? ds[t].z : ds[t].w;
                     /* |I| <= 16 * 32 * 127 and |sc| <= 128: a 24-bit multiply is exact */
                     part = fmaf(h2f_bits(dw & 0xffffu), (float)__mul24(I, scq[k]), part);
@@ -481,13 +490,14 @@ static hipError_t dispatch_q6k_r(int r, const uint8_t *W, uint64_t wbytes, const
     }
 }
 
-/* Rows per workgroup of the split-layout kernel (2 or 4): 2 measured
- * fastest on MI355X at one token on down (5120 x 25600), the LM head
- * (151936 x 5120) and v (1024 x 5120). */
+/* Rows per workgroup of the split-layout kernel (2 or 4): 4 measured
+ * fastest on MI355X for 1..4 tokens on down (5120 x 25600) and the LM head
+ * (151936 x 5120), and equal on v (1024 x 5120); the launcher drops to 2
+ * when N < 4. */
 extern "C" int sera_q6s_mmvq_rows(int N, int M) {
     (void)N;
     (void)M;
-    return 2;
+    return 4;
 }
 
 /* qtype 14: W is GGUF bytes, rows = rows per wave (1, 2, 4; 0 = built-in).
