@@ -40,7 +40,7 @@ sys.path.insert(0, os.path.join(ROOT, "sera.c_amd"))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
-VEC_MFMA_MIN_BATCH = 5   # MMVQ-path batches from here run the few-token MFMA kernel
+VEC_MFMA_MIN_BATCH = 4   # MMVQ-path batches from here run the few-token MFMA kernel
 METRIC = "MMVQ HBM GB/s @M=1; MMQ int8 TOPS @M=512; % of MI355X roofline"
 SHAPES = {  # name: (N, K) as (output features, input features)
     "q": (8192, 5120), "k": (1024, 5120), "v": (1024, 5120), "o": (5120, 8192),
@@ -160,10 +160,12 @@ def main():
             q3q4.quantize_row(x, stage)
             rpw = L.sera_q4k_mmvq_rows_per_tile(M, N, K)
             if M >= VEC_MFMA_MIN_BATCH:
-                # the MMVQ path's few-token MFMA kernel (MMVQ arithmetic)
-                sp = q3q4.skinny_splits(M, N, K)
-                part = torch.empty(sp * M * N, dtype=torch.float32, device=dev) if sp > 1 else None
-                kavg, _ = bench_kernel(2, arr, args.copies, stage, y, part, M, N, K, sp,
+                # the MMVQ path's few-token MFMA kernel (MMVQ arithmetic): split
+                # slots, then the zeroed row-group counters
+                sp = q3q4.fewtok_splits(M, N, K)
+                part = torch.zeros(sp * M * N + q3q4.fewtok_groups(M, N, K), dtype=torch.float32,
+                                   device=dev)
+                kavg, _ = bench_kernel(12, arr, args.copies, stage, y, part, M, N, K, 0,
                                        args.warmup, args.steps)
                 rpw = None
             else:
@@ -171,7 +173,8 @@ def main():
                                        args.warmup, args.steps)
             b = alg_bytes(M, N, K)
             row = {"proj": name, "M": M, "N": N, "K": K,
-                   "kernel": "sera_q4k_skinny_kernel<0, 1, 4>" if rpw is None else
+                   "kernel": (f"sera_q4k_fewtok_kernel<{8 if N >= 16384 or K >= 16384 else 4}> "
+                              f"(splits {q3q4.fewtok_splits(M, N, K)})") if rpw is None else
                              f"sera_q4k_mmvq_kernel<{M}, {rpw}, {min(4, (K // 256 + 7) // 8)}>",
                    "step_us": round(step_ms * 1e3, 3),
                    "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),

@@ -44,9 +44,6 @@ extern "C" hipError_t sera_launch_q8_1_q6k_stage_p(const float *x, const sera_pr
 extern "C" hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W, float *const *y, const int *N,
                                                  const void *stage, int M, int K, int rows, int accum,
                                                  hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_skinny_acc(int form, const void *W, const void *stage, float *y,
-                                                 float *partial, int M, int N, int K, int splits, int accum,
-                                                 hipStream_t s);
 extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, float *y, float *partial,
                                               int M, int N, int K, int splits, int accum, hipStream_t s);
 extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots,
@@ -62,6 +59,11 @@ extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int
                                                    float *logits, hipStream_t s);
 extern "C" hipError_t sera_launch_embedding(int qtype, const void *W, int N, int K, const uint32_t *ids, int tokens,
                                             float *hidden, hipStream_t s);
+extern "C" hipError_t sera_launch_q4k_fewtok_acc(const void *W, const void *stage, float *y, float *slots,
+                                                 int *counters, int M, int N, int K, int chunk, int accum,
+                                                 hipStream_t s);
+extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk);
+extern "C" int sera_fewtok_groups(int M, int N, int K);
 extern "C" int sera_mmq_splits(int M, int N, int K);
 extern "C" int sera_skinny_splits(int M, int N, int K);
 extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
@@ -103,10 +105,13 @@ unsigned char *g_arena = nullptr; /* stage and partial sums (after the counter r
 int *g_counters = nullptr;        /* stream-K tile counters, zero between calls */
 size_t g_arena_bytes = 0;
 
-/* The arena starts with the stream-K tile counters (zeroed when the arena
- * is attached; each call leaves them zero again). */
+/* The arena starts with the counters of the stream-K MMQ tiles (first
+ * half) and of the few-token kernel's row groups (second half), zeroed when
+ * the arena is attached; each call leaves them zero again. */
 constexpr size_t kCounterBytes = (size_t)256 << 10;
 constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(int));
+constexpr int kFewtokCounterBase = kMaxCounters / 2;
+constexpr int kFewtokMaxCounters = kMaxCounters - kFewtokCounterBase;
 
 /* Workgroups the stream-K MMQ schedule runs for M tokens: the resident
  * count, a multiple of 8. */
@@ -196,7 +201,14 @@ extern "C" size_t sera_q4k_arena_bytes(size_t max_tokens, int64_t max_features, 
     const size_t q6 = sera_q6k_mmq_stage_layout((size_t)sera_q6k_mmq_padded_rows(mt), (size_t)max_k).total;
     size_t stage = row > mmq ? row : mmq;
     if (q6 > stage) stage = q6;
-    const size_t partial = sera_align256(partial_floats_bound(max_tokens, max_features) * sizeof(float));
+    size_t partial_floats = partial_floats_bound(max_tokens, max_features);
+    /* the few-token kernel's split partials: at most 16 splits, or one per
+     * 20 super-blocks of a longer K */
+    const size_t few_splits = (size_t)((max_k / Q4K_QK + 19) / 20 > 16 ? (max_k / Q4K_QK + 19) / 20 : 16);
+    const size_t few = few_splits * (size_t)(mt < SERA_Q4K_MMVQ_MAX_BATCH ? mt : SERA_Q4K_MMVQ_MAX_BATCH) *
+                       (size_t)(max_features > 0 ? max_features : 0);
+    if (few > partial_floats) partial_floats = few;
+    const size_t partial = sera_align256(partial_floats * sizeof(float));
     return kCounterBytes + stage + partial;
 }
 
@@ -259,6 +271,31 @@ extern "C" int sera_q4k_skinny(int form, const void *W, const void *stage, float
                ? 0 : fail(-3, "sera_q4k_skinny: launch failed");
 }
 
+extern "C" int sera_q4k_fewtok_splits(int M, int N, int K, int chunk) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK || chunk < 0) return 0;
+    return sera_fewtok_splits(M, N, K, chunk);
+}
+
+extern "C" int sera_q4k_fewtok_groups(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
+    return sera_fewtok_groups(M, N, K);
+}
+
+extern "C" int sera_q4k_fewtok(const void *W, const void *row_stage, float *Y, float *slots, int *counters, int M,
+                               int N, int K, int chunk, int accum, void *stream) {
+    if (!W || !row_stage || !Y) return fail(-1, "sera_q4k_fewtok: null pointer");
+    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q4k_fewtok: batch M=%d outside 1..8", M);
+    if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_fewtok: bad shape N=%d K=%d", N, K);
+    if (((uintptr_t)W & 15u) || ((uintptr_t)row_stage & 15u))
+        return fail(-1, "sera_q4k_fewtok: W and the stage must be 16-byte aligned");
+    if (chunk < 0 || chunk > 20) return fail(-1, "sera_q4k_fewtok: chunk=%d outside 0..20", chunk);
+    if (sera_fewtok_splits(M, N, K, chunk) > 1 && (!slots || !counters))
+        return fail(-1, "sera_q4k_fewtok: a split K needs slots and counters");
+    return sera_launch_q4k_fewtok_acc(W, row_stage, Y, slots, counters, M, N, K, chunk, accum ? 1 : 0,
+                                      (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "sera_q4k_fewtok: launch failed");
+}
+
 extern "C" int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, float *partial, int M, int N,
                             int K, int splits, void *stream) {
     if (!W || !mmq_stage || !Y) return fail(-1, "sera_q4k_mmq: null pointer");
@@ -282,7 +319,7 @@ bool streamk_rule(int M, int N, int K) {
     const int P = streamk_wgs(M);
     if (P < 8 || M <= 32) return false;
     const int tiles = sera_mmq_tiles(M, N);
-    return tiles >= 64 && tiles < 4 * P && tiles <= kMaxCounters && (int64_t)tiles * (K / Q4K_QK) >= P;
+    return tiles >= 64 && tiles < 4 * P && tiles <= kFewtokCounterBase && (int64_t)tiles * (K / Q4K_QK) >= P;
 }
 bool use_streamk(int M, int N, int K) { return g_counters && streamk_rule(M, N, K); }
 }  // namespace
@@ -342,21 +379,35 @@ extern "C" int sera_q4k_mmq_tiles(int M, int N) { return M > 0 && N > 0 ? sera_m
 extern "C" int sera_q4k_mmq_slot_floats(int M) { return M > 0 ? sera_mmq_slot_floats(M) : 0; }
 
 /* Batches from this size up to the MMVQ cap run the few-token MFMA kernel
- * (MMVQ formula) instead of the dot4 MMVQ kernel: on MI355X it is about
- * twice as fast at 8 tokens, while dot4 wins up to 4 tokens. */
-#define SERA_Q4K_VEC_MFMA_MIN_BATCH 5
+ * (MMVQ formula) instead of the dot4 MMVQ kernel. Measured on MI355X with
+ * the weights streamed from HBM, gate/up 5120 -> 25600: the MFMA kernel
+ * takes 21 us at 4 or 8 tokens, dot4 24 us at 4 and 32 us at 8; at 3
+ * tokens they tie and below dot4 wins (its cost grows with every token,
+ * the MFMA kernel's does not). */
+#define SERA_Q4K_VEC_MFMA_MIN_BATCH 4
 
 namespace {
-int vec_splits(int M, int N, int K) {
-    if (M < SERA_Q4K_VEC_MFMA_MIN_BATCH) return 1;
-    const int sp = sera_skinny_splits(M, N, K);
-    return ((size_t)M * N) % 4 == 0 ? sp : 1;
+/* The few-token kernel on the row stage at the start of the arena: split
+ * partials go to `slots` (cap floats), counters to the second half of the
+ * counter region. */
+int fewtok_launch(const char *tag, const void *W, float *Y, float *slots, size_t cap, int M, int N, int K,
+                  int accum, hipStream_t s) {
+    const int splits = sera_fewtok_splits(M, N, K, 0);
+    if (splits > 1) {
+        if ((size_t)splits * M * N > cap)
+            return fail(-1, "%s: arena too small for %d split partials of %dx%d", tag, splits, M, N);
+        if (sera_fewtok_groups(M, N, K) > kFewtokMaxCounters)
+            return fail(-1, "%s: N=%d needs more row-group counters than the arena holds", tag, N);
+    }
+    return sera_launch_q4k_fewtok_acc(W, g_arena, Y, slots, g_counters + kFewtokCounterBase, M, N, K, 0, accum, s) ==
+                   hipSuccess
+               ? 0 : fail(-3, "%s: few-token kernel launch failed", tag);
 }
 }  // namespace
 
 extern "C" int sera_q4k_kernel_launches(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
-    if (M <= SERA_Q4K_MMVQ_MAX_BATCH) return vec_splits(M, N, K) > 1 ? 3 : 2;
+    if (M <= SERA_Q4K_MMVQ_MAX_BATCH) return 2;
     if (use_streamk(M, N, K)) return 2;
     return sera_mmq_splits(M, N, K) > 1 && ((size_t)M * N) % 4 == 0 ? 3 : 2;
 }
@@ -369,20 +420,17 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
     if (!g_arena) return fail(-1, "sera_q4k_dense_vec: no arena attached");
     hipStream_t s = (hipStream_t)stream;
     const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
-    const int splits = vec_splits(M, N, K);
-    const size_t partial_bytes = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
-    if (stage_bytes + partial_bytes > g_arena_bytes)
-        return fail(-1, "sera_q4k_dense_vec: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
-                    g_arena_bytes);
+    if (stage_bytes > g_arena_bytes)
+        return fail(-1, "sera_q4k_dense_vec: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
     if (timed) record(g_ev.quant_begin, s);
     if (sera_launch_q8_1_row(X, M, K, g_arena, s) != hipSuccess)
         return fail(-2, "sera_q4k_dense_vec: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
     if (M >= SERA_Q4K_VEC_MFMA_MIN_BATCH) {
-        float *partial = splits > 1 ? (float *)(g_arena + stage_bytes) : nullptr;
-        if (sera_launch_q4k_skinny(0, W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
-            return fail(-3, "sera_q4k_dense_vec: few-token kernel launch failed");
+        const int rc = fewtok_launch("sera_q4k_dense_vec", W, Y, (float *)(g_arena + stage_bytes),
+                                     (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s);
+        if (rc) return rc;
     } else if (sera_launch_q4k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
         return fail(-3, "sera_q4k_dense_vec: mmvq launch failed");
     }
@@ -753,9 +801,9 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         const int n = N[i];
         const bool mn4 = ((size_t)M * n) % 4 == 0;
         if (qt == 12 && M <= SERA_Q4K_MMVQ_MAX_BATCH) {
-            int sp = mn4 ? sera_skinny_splits(M, n, K) : 1;
-            if ((size_t)sp * M * n > partial_cap) sp = 1;
-            e = sera_launch_q4k_skinny_acc(0, weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
+            const int rc = fewtok_launch(tag, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
+            if (rc) return rc;
+            continue;
         } else if (qt == 12) {
             const size_t slot_floats = (size_t)2 * streamk_wgs(M) * sera_mmq_slot_floats(M);
             if (use_streamk(M, n, K) && slot_floats <= partial_cap) {

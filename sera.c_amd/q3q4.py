@@ -102,6 +102,9 @@ def load():
         "sera_q4k_mmq_splits": ([I, I, I], I),
         "sera_q4k_skinny": ([I, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_skinny_splits": ([I, I, I], I),
+        "sera_q4k_fewtok": ([P, P, P, P, P, I, I, I, I, I, P], I),
+        "sera_q4k_fewtok_splits": ([I, I, I, I], I),
+        "sera_q4k_fewtok_groups": ([I, I, I], I),
         "sera_q4k_kernel_launches": ([I, I, I], I),
         "sera_q4k_mmq_streamk": ([P, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_streamk_wgs": ([I], I),
@@ -281,6 +284,22 @@ def skinny(form, W, stage, out, M, N, K, splits=0, partial=None, stream=None):
 
 def skinny_splits(M, N, K):
     return load().sera_q4k_skinny_splits(M, N, K)
+
+
+def fewtok(W, stage, out, M, N, K, chunk=0, slots=None, counters=None, accum=False, stream=None):
+    """Few-token kernel of the MMVQ path on a row stage (MMVQ formula),
+    1 <= M <= 8; a split K needs slots (splits*M*N float32) and counters
+    (fewtok_groups int32, zero before and after)."""
+    _check(load().sera_q4k_fewtok(_ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N, K, chunk,
+                                  1 if accum else 0, _stream(stream)), "sera_q4k_fewtok")
+
+
+def fewtok_splits(M, N, K, chunk=0):
+    return load().sera_q4k_fewtok_splits(M, N, K, chunk)
+
+
+def fewtok_groups(M, N, K):
+    return load().sera_q4k_fewtok_groups(M, N, K)
 
 
 def dequantize(W, nblocks, out, stream=None):

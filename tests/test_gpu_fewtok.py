@@ -1,0 +1,161 @@
+"""The MMVQ path's few-token kernel (q4k_fewtok.hip) through the C ABI.
+
+Bars: fp32 outputs within max |y - y_oracle| <= 1e-3 * rms(y_oracle) of the
+MMVQ-formula oracle (vecdotq.cuh:505-527, the arithmetic the reference's
+mul_mat_vec_q<Q4_K> uses for 1-8 tokens); split-K results repeat bit for
+bit and leave the row-group counters at zero; accumulate adds exactly the
+product; the boundary (q3_cuda_q4k_linear) runs this kernel from 4 tokens.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import q3q4
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _t
+    if not _t.cuda.is_available():
+        pytest.fail("gpu test without a visible HIP device")
+    q3q4.load()
+    return _t
+
+
+@pytest.fixture(scope="module")
+def linear(torch):
+    return q3q4.Linear(device=0, max_tokens=2048, max_features=151936, max_k=25600)
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def outlier_activations(rng, M, K, frac=0.01, gain=20.0):
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    ch = rng.choice(K, max(1, int(np.ceil(frac * K))), replace=False)
+    x[:, ch] *= gain
+    return x
+
+
+def rand_weights(rng, N, K, scale=0.02):
+    return oracle.quantize_q4k((rng.standard_normal((N, K)) * scale).astype(np.float32))
+
+
+def check_close(y, ref, what):
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    err = float(np.max(np.abs(y.astype(np.float64) - ref)))
+    say(f"  {what}: max|err| = {err:.3e}, rms = {rms:.3e}, ratio = {err / max(rms, 1e-30):.2e}")
+    assert np.all(np.isfinite(y)), what
+    assert err <= TOL * rms, what
+
+
+def run_fewtok(torch, Wd, stage, M, N, K, chunk, y=None, accum=False):
+    s = q3q4.fewtok_splits(M, N, K, chunk)
+    slots = torch.empty(s * M * N, dtype=torch.float32, device="cuda") if s > 1 else None
+    counters = (torch.zeros(q3q4.fewtok_groups(M, N, K), dtype=torch.int32, device="cuda")
+                if s > 1 else None)
+    if y is None:
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    q3q4.fewtok(Wd, stage, y, M, N, K, chunk=chunk, slots=slots, counters=counters, accum=accum)
+    torch.cuda.synchronize()
+    if counters is not None:
+        assert int(counters.abs().sum()) == 0, "row-group counters not reset"
+    return y, s
+
+
+# (N, K): ragged N (not a multiple of 64 or 128 rows), one super-block, K
+# below and above the 20-super-block chunk limit, the wide-N plan (8 waves)
+FEWTOK_SHAPES = [(16, 256), (1000, 512), (300, 5120), (64, 25600), (203, 2304), (16500, 1024)]
+
+
+@pytest.mark.parametrize("N,K", FEWTOK_SHAPES)
+def test_fewtok_parity(torch, N, K):
+    """Every batch 1..8 and several K chunkings against the MMVQ-formula oracle."""
+    rng = np.random.default_rng(11 * N + K)
+    W = rand_weights(rng, N, K)
+    Wd = dev(torch, W)
+    nkb = K // 256
+    for M in range(1, 9):
+        x = outlier_activations(rng, M, K)
+        stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+        q3q4.quantize_row(dev(torch, x), stage)
+        xq, xd, _ = oracle.q8_1_row(x)
+        ref = oracle.gemm_mmvq(W, xq, xd, N, K)
+        for chunk in sorted({0, 1, 3, 7, min(20, nkb)}):
+            if chunk > nkb:
+                continue
+            say(f"case fewtok M={M} N={N} K={K} chunk={chunk} "
+                f"splits={q3q4.fewtok_splits(M, N, K, chunk)}")
+            y, _ = run_fewtok(torch, Wd, stage, M, N, K, chunk)
+            check_close(y.cpu().numpy(), ref, f"fewtok M={M} N={N} K={K} chunk={chunk}")
+
+
+def test_fewtok_split_repeats_and_accumulates(torch):
+    """Split-K sums in split order: two runs agree bit for bit; accumulate
+    adds exactly the product to what Y held."""
+    rng = np.random.default_rng(5)
+    M, N, K = 8, 1000, 5120
+    W = rand_weights(rng, N, K)
+    Wd = dev(torch, W)
+    x = outlier_activations(rng, M, K)
+    stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+    q3q4.quantize_row(dev(torch, x), stage)
+    for chunk in (3, 0):
+        say(f"case fewtok repeat M={M} N={N} K={K} chunk={chunk}")
+        a, s = run_fewtok(torch, Wd, stage, M, N, K, chunk)
+        b, _ = run_fewtok(torch, Wd, stage, M, N, K, chunk)
+        assert s > 1 or chunk == 0
+        assert torch.equal(a, b)
+        base = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
+        acc = base.clone()
+        run_fewtok(torch, Wd, stage, M, N, K, chunk, y=acc, accum=True)
+        assert torch.equal(acc, base + a), "accumulate is not y + product"
+
+
+def test_fewtok_matches_dot4_mmvq(torch):
+    """The two MMVQ-path kernels agree within the tolerance at every batch
+    they share (1-8 tokens) on a Qwen3-32B-width matrix."""
+    rng = np.random.default_rng(9)
+    N, K = 2048, 5120
+    Wd = dev(torch, rand_weights(rng, N, K))
+    for M in range(1, 9):
+        x = dev(torch, outlier_activations(rng, M, K))
+        stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+        q3q4.quantize_row(x, stage)
+        say(f"case fewtok vs mmvq M={M} N={N} K={K}")
+        y_mmvq = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        q3q4.mmvq(Wd, stage, y_mmvq, M, N, K)
+        y, _ = run_fewtok(torch, Wd, stage, M, N, K, 0)
+        torch.cuda.synchronize()
+        check_close(y.cpu().numpy(), y_mmvq.cpu().numpy().astype(np.float64), f"fewtok vs mmvq M={M}")
+
+
+def test_boundary_uses_fewtok_from_four_tokens(torch, linear):
+    """q3_cuda_q4k_linear at 4-8 tokens gives the few-token kernel's result
+    bit for bit (the dispatch runs it, with its planned chunk)."""
+    rng = np.random.default_rng(21)
+    N, K = 5120, 25600
+    W = rand_weights(rng, N, K)
+    Wd = dev(torch, W)
+    geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+    for M in (4, 5, 8):
+        x = dev(torch, outlier_activations(rng, M, K))
+        say(f"case boundary fewtok M={M} N={N} K={K}")
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        linear(geo, Wd, x, y)
+        stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+        q3q4.quantize_row(x, stage)
+        ref, _ = run_fewtok(torch, Wd, stage, M, N, K, 0)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref)
