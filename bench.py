@@ -190,6 +190,8 @@ def main():
     results["mmvq_sweep"] = sweep
 
     # ---------------- config 3 (gate/up only unless --full): MMQ M=512 -----
+    FEWTOK_MMQ_MAX_BATCH = 12   # the MMQ path runs the few-token kernel (MMQ formula) up to here
+
     def mmq_case(label, N, K, M, arr, ncopies, iters):
         x = activations(M, K, 7)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -199,7 +201,13 @@ def main():
         q3q4.quantize_mmq(x, stage)
         wgs = L.sera_q4k_mmq_streamk_wgs(M)
         tiles = L.sera_q4k_mmq_tiles(M, N)
-        if L.sera_q4k_mmq_schedule(M, N, K) == 1:
+        if M <= FEWTOK_MMQ_MAX_BATCH:
+            # few-token kernel, MMQ formula: split slots, then the zeroed counters
+            splits = -q3q4.fewtok_splits(M, N, K)
+            partial = torch.zeros(-splits * M * N + q3q4.fewtok_groups(M, N, K), dtype=torch.float32,
+                                  device=dev)
+            kavg, _ = bench_kernel(13, arr, ncopies, stage, y, partial, M, N, K, 0, 3, iters)
+        elif L.sera_q4k_mmq_schedule(M, N, K) == 1:
             # stream-K schedule: slots, then the zeroed tile counters
             splits = 0
             nslot = 2 * wgs * L.sera_q4k_mmq_slot_floats(M)
@@ -212,7 +220,8 @@ def main():
             kavg, _ = bench_kernel(1, arr, ncopies, stage, y, partial, M, N, K, splits, 3, iters)
         ops = 2.0 * M * N * K
         row = {"case": label, "M": M, "N": N, "K": K,
-               "schedule": "stream-K" if splits == 0 else f"split-K x{splits}",
+               "schedule": ("stream-K" if splits == 0 else f"split-K x{splits}" if splits > 0
+                            else f"few-token kernel, {-splits} K split(s) summed in-kernel"),
                "step_us": round(step_ms * 1e3, 2), "kernel_us": round(kavg * 1e3, 2),
                "kernel_TOPS": round(ops / (kavg * 1e-3) / 1e12, 1),
                "step_TOPS": round(ops / (step_ms * 1e-3) / 1e12, 1),
@@ -241,6 +250,10 @@ def main():
         results["config4_m2048"] = [mmq_case("gate_up", gN, gK, 2048, garr, args.copies, 5),
                                     mmq_case("down", 5120, 25600, 2048, sets["down"][2][1],
                                              args.copies, 5)]
+        # 9-12 tokens (a few speculative branches): the few-token kernel, MMQ formula
+        results["mmq_few_tokens"] = [mmq_case("gate_up", gN, gK, 9, garr, args.copies, 20),
+                                     mmq_case("gate_up", gN, gK, 12, garr, args.copies, 20),
+                                     mmq_case("down", 5120, 25600, 12, sets["down"][2][1], args.copies, 20)]
         lmw, lmarr = weight_set(151936, 5120, 500, 1)
         results["config4_lm_head_m16"] = mmq_case("lm_head", 151936, 5120, 16, lmarr, 1, 20)
         del lmw

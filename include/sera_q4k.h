@@ -135,18 +135,20 @@ int sera_q4k_skinny(int form, const void *W, const void *stage, float *Y, float 
                     int K, int splits, void *stream);
 int sera_q4k_skinny_splits(int M, int N, int K);
 
-/* Few-token kernel of the MMVQ path (1 <= M <= 8; sera_q4k_dense_vec runs it
- * from 4 tokens): Y (+)= X . W^T on a row stage with the MMVQ formula (as
- * sera_q4k_mmvq, vec_dot_q4_K_q8_1, cuda/mmq/vecdotq.cuh:505-527). Same role
- * as mul_mat_vec_q<Q4_K, ncols> (cuda/mmq/mmvq.cu:393-587) for ncols 4-8;
- * this build's tiling is two sub-blocks per v_mfma_i32_16x16x64_i8.
- * chunk: super-blocks of K per workgroup, 1..20, 0 = the built-in choice.
- * When the chunk splits K (sera_q4k_fewtok_splits > 1), slots holds
- * splits*M*N floats and counters sera_q4k_fewtok_groups(M, N, K) ints that
- * must be zero and are zero again after the kernel; the last split of each
- * row group sums the partials in split order, so results repeat bit for bit.
- * W and row_stage 16-byte aligned; accum != 0 adds the product to Y. */
-int sera_q4k_fewtok(const void *W, const void *row_stage, float *Y, float *slots, int *counters, int M, int N,
+/* Few-token kernel (1 <= M <= 16): Y (+)= X . W^T with two sub-blocks per
+ * v_mfma_i32_16x16x64_i8. form 0 takes a row stage and computes the MMVQ
+ * formula (as sera_q4k_mmvq, vec_dot_q4_K_q8_1, cuda/mmq/vecdotq.cuh:505-527),
+ * M <= 8: it plays the role of mul_mat_vec_q<Q4_K, ncols> (cuda/mmq/mmvq.cu:
+ * 393-587) for 4-8 tokens. form 1 takes an MMQ stage and computes the MMQ
+ * formula (as sera_q4k_mmq, cuda/mmq/mmq.cuh:2269-2283,1440-1472).
+ * chunk: super-blocks of K per workgroup, 1..20 for M <= 8 and 1..10 above,
+ * 0 = the built-in choice. When the chunk splits K (sera_q4k_fewtok_splits >
+ * 1), slots holds splits*M*N floats and counters sera_q4k_fewtok_groups(M,
+ * N, K) ints that must be zero and are zero again after the kernel; the
+ * last split of each row group sums the partials in split order, so results
+ * repeat bit for bit. W and the stage 16-byte aligned; accum != 0 adds the
+ * product to Y. */
+int sera_q4k_fewtok(int form, const void *W, const void *stage, float *Y, float *slots, int *counters, int M, int N,
                     int K, int chunk, int accum, void *stream);
 int sera_q4k_fewtok_splits(int M, int N, int K, int chunk);
 int sera_q4k_fewtok_groups(int M, int N, int K);

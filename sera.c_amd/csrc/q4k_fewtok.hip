@@ -1,11 +1,17 @@
 /*
- * q4k_fewtok.hip - Q4_K x Q8_1 for 1..8 tokens on int8 MFMA, the MMVQ path's
- * kernel from 4 tokens up.
+ * q4k_fewtok.hip - Q4_K x Q8_1 for 1..16 tokens on int8 MFMA: the MMVQ
+ * path's kernel from 4 tokens up (MMVQ formula on the row stage) and the
+ * MMQ path's kernel up to 16 tokens (MMQ formula on the MMQ stage).
  *
- * Arithmetic of the reference MMVQ (cuda/mmq/vecdotq.cuh:505-527,864-908):
- *   y[t][n] = sum_b (d*sc_b) * d8_b * I_b  -  sum_b (dmin*m_b) * (d8_b*S_b)
- * with I_b the exact int32 dot of sub-block b, d*sc_b and dmin*m_b exact in
- * fp32, d8_b and d8_b*S_b from the row stage (dsf).
+ * Arithmetic, per output and 32-wide sub-block b with I_b the exact int32
+ * dot of the sub-block:
+ *   MMVQ (cuda/mmq/vecdotq.cuh:505-527,864-908):
+ *     y = sum_b (d*sc_b) * d8_b * I_b  -  sum_b (dmin*m_b) * (d8_b*S_b)
+ *     with d*sc_b and dmin*m_b exact in fp32, d8_b and d8_b*S_b from the row
+ *     stage (dsf);
+ *   MMQ (cuda/mmq/mmq.cuh:2269-2283,1440-1472):
+ *     y = sum_b fp16(d*sc_b) * d8_b * I_b  +  fp16(-dmin*m_b) * s8_b
+ *     with d8_b and s8_b (the fp16 sum of x) from the MMQ stage (ds).
  *
  * gfx950 mapping:
  *   - One v_mfma_i32_16x16x64_i8 computes the int32 dots of TWO sub-blocks
@@ -14,23 +20,23 @@
  *     sb. A rows 0-7 are the tokens on sa (zero in groups 2-3), rows 8-15
  *     the tokens on sb (zero in groups 0-1), so result rows 0-7 are I_sa and
  *     rows 8-15 are I_sb: every lane's four results are real dots, and the
- *     fp32 epilogue runs on no padding.
+ *     fp32 epilogue runs on no padding. 9-16 tokens are two groups of 8
+ *     sharing the weight registers.
  *   - Weights are B. Lane (n = lane & 15, g = lane >> 4) owns weight row n
  *     and loads, per super-block, the 16-byte header and the 16-byte pieces
  *     at 16 + 64 j + 16 g (j = 0, 1): nibble bytes of pair 2j + (g >> 1),
  *     half g & 1. Across the wave one load instruction reads 64 contiguous
- *     bytes of each of 16 rows, which streams from HBM as fast as a plain
- *     copy (32-byte pieces per row measured 30% slower). The low nibbles
- *     feed the MFMA of sub-blocks (4j, 4j+2), the high nibbles (4j+1, 4j+3).
+ *     bytes of each of 16 rows. The low nibbles feed the MFMA of sub-blocks
+ *     (4j, 4j+2), the high nibbles (4j+1, 4j+3).
  *   - The min term is a rank-8 fp32 product, two v_mfma_f32_16x16x4_f32 per
- *     super-block into the same accumulator (A = d8*S of tokens 0-7, zero
- *     rows 8-15; B = -dmin*m of the row).
- *   - Workgroup: NW waves, one 16-row tile each, over one chunk of K (at
- *     most SERA_FEWTOK_MAX_CHUNK super-blocks). The chunk's activations
- *     (quants with 16-byte columns XOR-swizzled by token, d8 and d8*S
- *     transposed to [super-block][sub-block][token]) are staged in LDS once;
- *     after that one barrier each wave runs on its own, with its next
- *     super-block's weights in flight while it computes the current one.
+ *     super-block and token group into the same accumulator (A = the tokens'
+ *     d8*S or s8, zero rows 8-15; B = the row's -dmin*m product).
+ *   - Workgroup: NW waves, one 16-row tile each, over one chunk of K. The
+ *     chunk's activations (quants with 16-byte columns XOR-swizzled by
+ *     token, the two scale factors transposed to [super-block][sub-block]
+ *     [token]) are staged in LDS once; after that one barrier each wave runs
+ *     on its own, with its next super-block's weights in flight while it
+ *     computes the current one.
  *   - gridDim.y > 1 splits K. Each split stores its partial tile with
  *     device-scope (write-through) stores, waits for them and bumps the row
  *     group's counter; the split that completes the count sums all partials
@@ -45,15 +51,13 @@ typedef float ft_v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void ft_lds_void;
 typedef __attribute__((address_space(1))) const void ft_global_cvoid;
 
-#define SERA_FEWTOK_MAX_TOKENS 8
-#define SERA_FEWTOK_MAX_CHUNK 20                      /* super-blocks per workgroup: 51 KB of LDS */
-#define SERA_FEWTOK_QS_BYTES (SERA_FEWTOK_MAX_TOKENS * Q4K_QK)   /* quants of one super-block */
-#define SERA_FEWTOK_SC_FLOATS (8 * SERA_FEWTOK_MAX_TOKENS)       /* [sub-block][token] */
+#define SERA_FEWTOK_MAX_TOKENS 16
+#define SERA_FEWTOK_LDS_CHUNK_TOKENS 160   /* chunk x staged tokens: 20 super-blocks of 8, 10 of 16 */
 
-/* LDS bytes of a workgroup for `chunk` super-blocks: quants, d8, d8*S, and
- * a 16-byte zero operand. */
-static inline size_t fewtok_lds_bytes(int chunk) {
-    return (size_t)chunk * (SERA_FEWTOK_QS_BYTES + 2 * SERA_FEWTOK_SC_FLOATS * sizeof(float)) + 16;
+/* LDS bytes of a workgroup for `chunk` super-blocks of `tok` staged tokens:
+ * quants, d8, the min-term activation factor, and a 16-byte zero operand. */
+static inline size_t fewtok_lds_bytes(int chunk, int tok) {
+    return (size_t)chunk * tok * (Q4K_QK + 2 * 8 * sizeof(float)) + 16;
 }
 
 struct FewtokW {
@@ -61,11 +65,16 @@ struct FewtokW {
     ft_v4u q[2];    /* nibble bytes at 16 + 64 j + 16 g */
 };
 
-template <int NW>
+/* TG token groups of 8 (M <= 8 TG), FORM 0: MMVQ formula on a row stage
+ * (dsf: d8, d8*S as fp32); FORM 1: MMQ formula on an MMQ stage (ds: fp16
+ * d8, fp16 sum of x), cuda/mmq/mmq.cuh:2269-2283,1440-1472:
+ *   y = sum_b fp16(d*sc_b) * d8_b * I_b + fp16(-dmin*m_b) * s8_b */
+template <int NW, int TG, int FORM>
 __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
-        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq, const float4 *__restrict__ dsf,
+        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq, const void *__restrict__ xsc,
         float *__restrict__ y, float *__restrict__ slots, int *__restrict__ counters, int M, int N, int K,
         int chunk, int accum) {
+    constexpr int TOK = 8 * TG;                          /* staged tokens */
     extern __shared__ __attribute__((aligned(16))) uint8_t ft_smem[];
     __shared__ int s_last;
     const int tid = threadIdx.x;
@@ -77,10 +86,11 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     const int nkb = K / Q4K_QK;
     const int kb0 = blockIdx.y * chunk;
     const int C = min(nkb - kb0, chunk);
+    /* LDS: quants [u][t][256] | d8 [u][b][t] | min factor [u][b][t] | zero */
     int8_t *xs = (int8_t *)ft_smem;
-    float *d8s = (float *)(ft_smem + (size_t)chunk * SERA_FEWTOK_QS_BYTES);
-    float *dSs = d8s + (size_t)chunk * SERA_FEWTOK_SC_FLOATS;
-    uint8_t *zero = (uint8_t *)(dSs + (size_t)chunk * SERA_FEWTOK_SC_FLOATS);
+    float *d8s = (float *)(ft_smem + (size_t)chunk * TOK * Q4K_QK);
+    float *mns = d8s + (size_t)chunk * 8 * TOK;
+    uint8_t *zero = (uint8_t *)(mns + (size_t)chunk * 8 * TOK);
 
     constexpr int RW = 16 * NW;       /* weight rows per workgroup */
     int row = blockIdx.x * RW + 16 * wave + n;
@@ -104,33 +114,53 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     {
         /* quants: 16-byte piece (u, token t, column c) at LDS column c ^ t;
          * one wave-instruction writes 1 KB; tokens past M copy the last */
-        const int pieces = C * (SERA_FEWTOK_QS_BYTES / 16);
+        const int pieces = C * TOK * 16;
         for (int base = wave * 64; base < pieces; base += NW * 64) {
             const int q = min(base + lane, pieces - 1);
-            const int u = q >> 7, t = (q >> 4) & 7, col = q & 15;
+            const int u = q / (TOK * 16), t = (q >> 4) % TOK, col = q & 15;
             const int8_t *src = xq + (size_t)min(t, M - 1) * K + (size_t)(kb0 + u) * Q4K_QK + 16 * (col ^ t);
             __builtin_amdgcn_global_load_lds((ft_global_cvoid *)src, (ft_lds_void *)(xs + (size_t)base * 16), 16, 0, 0);
         }
-        /* d8 and d8*S: float4 (d_2p, d_2p+1, dS_2p, dS_2p+1) per token and
-         * sub-block pair, all loads first, then the transposed LDS writes */
-        constexpr int SCR = (SERA_FEWTOK_MAX_CHUNK * 32 + NW * 64 - 1) / (NW * 64);
-        float4 f[SCR];
+        /* scales, transposed to [u][sub-block][token]: all loads first, then
+         * the LDS writes. FORM 0: float4 (d_2p, d_2p+1, dS_2p, dS_2p+1) per
+         * token and sub-block pair; FORM 1: four half2 (d8, s8) per token
+         * and sub-block quad */
+        constexpr int ITEMS = (SERA_FEWTOK_LDS_CHUNK_TOKENS / TOK) * TOK * (FORM == 0 ? 4 : 2);
+        constexpr int SCR = (ITEMS + NW * 64 - 1) / (NW * 64);
+        const int items = C * TOK * (FORM == 0 ? 4 : 2);
+        ft_v4u f[SCR];
 #pragma unroll
         for (int r = 0; r < SCR; r++) {
-            const int i = min(tid + r * NW * 64, C * 32 - 1);
-            const int u = i >> 5, t = (i >> 2) & 7, p = i & 3;
-            f[r] = dsf[(size_t)min(t, M - 1) * (K / 64) + (size_t)(kb0 + u) * 4 + p];
+            const int i = min(tid + r * NW * 64, items - 1);
+            if (FORM == 0) {
+                const int u = i / (TOK * 4), t = (i >> 2) % TOK, p = i & 3;
+                f[r] = ((const ft_v4u *)xsc)[(size_t)min(t, M - 1) * (K / 64) + (size_t)(kb0 + u) * 4 + p];
+            } else {
+                const int u = i / (TOK * 2), t = (i >> 1) % TOK, p = i & 1;
+                f[r] = ((const ft_v4u *)xsc)[(size_t)min(t, M - 1) * (K / 128) + (size_t)(kb0 + u) * 2 + p];
+            }
         }
 #pragma unroll
         for (int r = 0; r < SCR; r++) {
             const int i = tid + r * NW * 64;
-            if (i < C * 32) {
-                const int u = i >> 5, t = (i >> 2) & 7, p = i & 3;
-                float *d8u = d8s + u * SERA_FEWTOK_SC_FLOATS, *dSu = dSs + u * SERA_FEWTOK_SC_FLOATS;
-                d8u[(2 * p) * 8 + t] = f[r].x;
-                d8u[(2 * p + 1) * 8 + t] = f[r].y;
-                dSu[(2 * p) * 8 + t] = f[r].z;
-                dSu[(2 * p + 1) * 8 + t] = f[r].w;
+            if (i < items) {
+                if (FORM == 0) {
+                    const int u = i / (TOK * 4), t = (i >> 2) % TOK, p = i & 3;
+                    float *d8u = d8s + u * 8 * TOK, *mnu = mns + u * 8 * TOK;
+                    d8u[(2 * p) * TOK + t] = __uint_as_float(f[r].x);
+                    d8u[(2 * p + 1) * TOK + t] = __uint_as_float(f[r].y);
+                    mnu[(2 * p) * TOK + t] = __uint_as_float(f[r].z);
+                    mnu[(2 * p + 1) * TOK + t] = __uint_as_float(f[r].w);
+                } else {
+                    const int u = i / (TOK * 2), t = (i >> 1) % TOK, p = i & 1;
+                    float *d8u = d8s + u * 8 * TOK, *mnu = mns + u * 8 * TOK;
+                    const uint32_t ds[4] = {f[r].x, f[r].y, f[r].z, f[r].w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        d8u[(4 * p + e) * TOK + t] = h2f_bits(ds[e] & 0xffffu);
+                        mnu[(4 * p + e) * TOK + t] = h2f_bits(ds[e] >> 16);
+                    }
+                }
             }
         }
         if (tid == 0) *(ft_v4u *)zero = (ft_v4u){0u, 0u, 0u, 0u};
@@ -139,62 +169,80 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     __syncthreads();
 
     /* A operand offsets: lane (row i = n, group g) is real when (i < 8) ==
-     * (g < 2): token i & 7 on sub-block 4j + 2 (i >> 3) + h, 16 bytes at
-     * k-half hq; other lanes read the zero operand */
-    const int ti = n & 7;
-    const bool a_real = ((n < 8) == (g < 2)) && ti < M;
-    int aoff[4];
+     * (g < 2): token 8 tg + (i & 7) on sub-block 4j + 2 (i >> 3) + h, 16
+     * bytes at k-half hq; other lanes read the zero operand */
+    int aoff[TG][4];
+    bool m_real[TG];
 #pragma unroll
-    for (int jh = 0; jh < 4; jh++) {
-        const int sbk = 4 * (jh >> 1) + 2 * (n >> 3) + (jh & 1);
-        aoff[jh] = a_real ? ti * Q4K_QK + 16 * ((2 * sbk + hq) ^ ti) : -1;
+    for (int tg = 0; tg < TG; tg++) {
+        const int t = 8 * tg + (n & 7);
+        const bool a_real = ((n < 8) == (g < 2)) && t < M;
+#pragma unroll
+        for (int jh = 0; jh < 4; jh++) {
+            const int sbk = 4 * (jh >> 1) + 2 * (n >> 3) + (jh & 1);
+            aoff[tg][jh] = a_real ? t * Q4K_QK + 16 * ((2 * sbk + hq) ^ t) : -1;
+        }
+        m_real[tg] = n < 8 && 8 * tg + n < M;
     }
     const int sg = g >> 1;            /* result sub-block: 4j + 2 sg + h */
-    const int tq = 4 * hq;            /* result tokens tq .. tq + 3 */
-    const bool m_real = n < 8 && n < M;
-    ft_v4f acc = {0.f, 0.f, 0.f, 0.f};
+    const int tq = 4 * hq;            /* result tokens 8 tg + tq .. + 3 */
+    ft_v4f acc[TG];
+#pragma unroll
+    for (int tg = 0; tg < TG; tg++) acc[tg] = (ft_v4f){0.f, 0.f, 0.f, 0.f};
 
     auto compute = [&](int u, const FewtokW &w) {
         const float live = u < C ? 1.0f : 0.0f;
         const int uu = min(u, C - 1);
-        const int8_t *xu = xs + (size_t)uu * SERA_FEWTOK_QS_BYTES;
-        const float *d8u = d8s + uu * SERA_FEWTOK_SC_FLOATS, *dSu = dSs + uu * SERA_FEWTOK_SC_FLOATS;
-        v4i A[4];
-        ft_v4f D8[4];
-#pragma unroll
-        for (int jh = 0; jh < 4; jh++) {
-            A[jh] = *(const v4i *)(aoff[jh] >= 0 ? (const void *)(xu + aoff[jh]) : (const void *)zero);
-            D8[jh] = *(const ft_v4f *)&d8u[(4 * (jh >> 1) + 2 * sg + (jh & 1)) * 8 + tq];
-        }
-        const float am0 = m_real ? dSu[g * 8 + n] : 0.0f;
-        const float am1 = m_real ? dSu[(4 + g) * 8 + n] : 0.0f;
+        const int8_t *xu = xs + (size_t)uu * TOK * Q4K_QK;
+        const float *d8u = d8s + uu * 8 * TOK, *mnu = mns + uu * 8 * TOK;
         /* (scale, min) bytes of sub-blocks 0-3 and 4-7 (src/q3_quant.c:44-55) */
         const ft_v4u hd = w.hd;
         const uint32_t sc03 = hd.y & 0x3F3F3F3Fu;
         const uint32_t m03 = hd.z & 0x3F3F3F3Fu;
         const uint32_t sc47 = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
         const uint32_t m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-        const float d = live * h2f_bits(hd.x & 0xffffu);
-        const float ndmin = -live * h2f_bits(hd.x >> 16);
+        /* sub-block scale and min products: FORM 0 exact in fp32 (d*sc,
+         * -dmin*m); FORM 1 one fp16 rounding each, as the reference's half2
+         * store (d, dmin) * (1, -1) * (sc, m) */
+        auto scale = [&](uint32_t v) -> float {
+            if (FORM == 0) return h2f_bits(hd.x & 0xffffu) * (float)v;
+            return (float)((_Float16)v * (_Float16)h2f_bits(hd.x & 0xffffu));
+        };
+        auto minp = [&](uint32_t v) -> float {
+            if (FORM == 0) return -h2f_bits(hd.x >> 16) * (float)v;
+            return (float)((_Float16)v * (_Float16)(-h2f_bits(hd.x >> 16)));
+        };
         /* min term: lane (n, g) gives A[n][g] and B[g][n] for sub-blocks g
-         * and 4 + g */
-        const float bm0 = ndmin * (float)((m03 >> (8 * g)) & 0xffu);
-        const float bm1 = ndmin * (float)((m47 >> (8 * g)) & 0xffu);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(am0, bm0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(am1, bm1, acc, 0, 0, 0);
+         * and 4 + g (A: FORM 0 d8*S, FORM 1 the fp16 sum of x) */
+        const float bm0 = live * minp((m03 >> (8 * g)) & 0xffu);
+        const float bm1 = live * minp((m47 >> (8 * g)) & 0xffu);
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) {
+            const float am0 = m_real[tg] ? mnu[g * TOK + 8 * tg + n] : 0.0f;
+            const float am1 = m_real[tg] ? mnu[(4 + g) * TOK + 8 * tg + n] : 0.0f;
+            acc[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(am0, bm0, acc[tg], 0, 0, 0);
+            acc[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(am1, bm1, acc[tg], 0, 0, 0);
+        }
 #pragma unroll
         for (int jh = 0; jh < 4; jh++) {
             const int j = jh >> 1, h = jh & 1;
-            const float swb = d * (float)(((j ? sc47 : sc03) >> (8 * (2 * sg + h))) & 0xffu);
+            const int sbl = 4 * j + 2 * sg + h;
+            const float swb = live * scale(((j ? sc47 : sc03) >> (8 * (2 * sg + h))) & 0xffu);
             const ft_v4u q = w.q[j];
             v4i B;
             B.x = (int)((q.x >> (4 * h)) & 0x0F0F0F0Fu);
             B.y = (int)((q.y >> (4 * h)) & 0x0F0F0F0Fu);
             B.z = (int)((q.z >> (4 * h)) & 0x0F0F0F0Fu);
             B.w = (int)((q.w >> (4 * h)) & 0x0F0F0F0Fu);
-            const v4i I = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[jh], B, (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[r] = fmaf((float)I[r], D8[jh][r] * swb, acc[r]);
+            for (int tg = 0; tg < TG; tg++) {
+                const v4i A = *(const v4i *)(aoff[tg][jh] >= 0 ? (const void *)(xu + aoff[tg][jh])
+                                                               : (const void *)zero);
+                const ft_v4f D8 = *(const ft_v4f *)&d8u[sbl * TOK + 8 * tg + tq];
+                const v4i I = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[tg][r] = fmaf((float)I[r], D8[r] * swb, acc[tg][r]);
+            }
         }
     };
     for (int u0 = 0; u0 < C; u0 += 2) {
@@ -205,7 +253,9 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     }
     /* lanes g and g ^ 2 hold the two sub-block halves of the same outputs */
 #pragma unroll
-    for (int r = 0; r < 4; r++) acc[r] += __shfl_xor(acc[r], 32, 64);
+    for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[tg][r] += __shfl_xor(acc[tg][r], 32, 64);
     const bool owner = g < 2 && row_ok;
 
     if (gridDim.y > 1) {
@@ -215,10 +265,14 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         if (owner) {
             float *mine = slots + (size_t)blockIdx.y * M * N;
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                if (tq + r < M)
-                    __hip_atomic_store(&mine[(size_t)(tq + r) * N + row], acc[r], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+            for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = 8 * tg + tq + r;
+                    if (t < M)
+                        __hip_atomic_store(&mine[(size_t)t * N + row], acc[tg][r], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -230,63 +284,65 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         if (tid == 0) __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (owner) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                if (tq + r >= M) continue;
-                const size_t at = (size_t)(tq + r) * N + row;
-                float v = __hip_atomic_load(&slots[at], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                for (int k = 1; k < S; k++)
-                    v += __hip_atomic_load(&slots[(size_t)k * M * N + at], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                acc[r] = v;
-            }
+            for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = 8 * tg + tq + r;
+                    if (t >= M) continue;
+                    const size_t at = (size_t)t * N + row;
+                    float v = __hip_atomic_load(&slots[at], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    for (int k = 1; k < S; k++)
+                        v += __hip_atomic_load(&slots[(size_t)k * M * N + at], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    acc[tg][r] = v;
+                }
         }
     }
     if (owner) {
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-            if (tq + r < M) {
-                float *dst = y + (size_t)(tq + r) * N + row;
-                *dst = accum ? *dst + acc[r] : acc[r];
+        for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = 8 * tg + tq + r;
+                if (t < M) {
+                    float *dst = y + (size_t)t * N + row;
+                    *dst = accum ? *dst + acc[tg][r] : acc[tg][r];
+                }
             }
     }
 }
 
 /* Workgroup shape and K chunk for M tokens of an N x K matrix, from sweeps
- * on MI355X over the Qwen3-32B projections: 8 waves (128 rows) for the
- * large matrices, 4 otherwise, and enough K splits to give the chip about
- * 192 (8 waves) or 256 (4 waves) workgroups. */
+ * on MI355X over the Qwen3-32B projections (weights streamed from HBM): 8
+ * waves (128 rows) for the large matrices, 4 otherwise, and enough K splits
+ * to give the chip about 192 (8 waves) or 256 (4 waves) workgroups, with
+ * chunks of at least 5 super-blocks (below that the LDS staging dominates).
+ * A chunk holds at most 160 / staged tokens super-blocks (20 for 8 tokens,
+ * 10 for 16), which keeps the LDS at 51 KB. */
 extern "C" void sera_fewtok_plan(int M, int N, int K, int *nwave, int *chunk) {
-    (void)M;
     const int nw = (N >= 16384 || K >= 16384) ? 8 : 4;
     const int groups = (N + 16 * nw - 1) / (16 * nw);
     const int nkb = K / Q4K_QK;
+    const int maxc = SERA_FEWTOK_LDS_CHUNK_TOKENS / (M > 8 ? 16 : 8);
     const int target = nw == 8 ? 192 : 256;
     int s = (target + groups - 1) / groups;
     if (s > 16) s = 16;
-    if (s > nkb) s = nkb;
+    if (s > nkb / 5) s = nkb / 5;   /* chunks of at least 5 super-blocks: staging amortised */
     if (s < 1) s = 1;
     int c = (nkb + s - 1) / s;
-    if (c > SERA_FEWTOK_MAX_CHUNK) c = SERA_FEWTOK_MAX_CHUNK;   /* more splits when K is long */
+    if (c > maxc) c = maxc;   /* more splits when K is long */
     *nwave = nw;
     *chunk = c;
 }
+
+/* Largest chunk for M tokens. */
+extern "C" int sera_fewtok_max_chunk(int M) { return SERA_FEWTOK_LDS_CHUNK_TOKENS / (M > 8 ? 16 : 8); }
 
 /* Row groups (counters needed when K is split) of the planned launch. */
 extern "C" int sera_fewtok_groups(int M, int N, int K) {
     int nw, c;
     sera_fewtok_plan(M, N, K, &nw, &c);
     return (N + 16 * nw - 1) / (16 * nw);
-}
-
-template <int NW>
-static hipError_t launch_fewtok(const uint8_t *W, const int8_t *xq, const float4 *dsf, float *y, float *slots,
-                                int *counters, int M, int N, int K, int chunk, int accum, hipStream_t s) {
-    const int nkb = K / Q4K_QK;
-    const int splits = (nkb + chunk - 1) / chunk;
-    dim3 grid((N + 16 * NW - 1) / (16 * NW), splits);
-    hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW>), grid, dim3(NW * 64), fewtok_lds_bytes(chunk), s, W, xq, dsf, y,
-                       slots, counters, M, N, K, chunk, accum);
-    return hipGetLastError();
 }
 
 /* Splits of K (grid rows) for a chunk (0 = planned). */
@@ -298,21 +354,49 @@ extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk) {
     return (nkb + c - 1) / c;
 }
 
-/* y (+)= X . W^T for 1 <= M <= 8 on a row stage. chunk: super-blocks per
- * workgroup (1..SERA_FEWTOK_MAX_CHUNK, 0 = planned); when it splits K,
- * slots holds splits*M*N floats and counters sera_fewtok_groups() ints,
- * zero on entry and zero again after the kernel. */
-extern "C" hipError_t sera_launch_q4k_fewtok_acc(const void *W, const void *stage, float *y, float *slots,
+extern "C" int sera_mmq_padded_rows(int M);
+
+template <int NW, int TG, int FORM>
+static hipError_t launch_fewtok(const uint8_t *W, const int8_t *xq, const void *xsc, float *y, float *slots,
+                                int *counters, int M, int N, int K, int chunk, int accum, hipStream_t s) {
+    const int nkb = K / Q4K_QK;
+    const int splits = (nkb + chunk - 1) / chunk;
+    dim3 grid((N + 16 * NW - 1) / (16 * NW), splits);
+    hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM>), grid, dim3(NW * 64), fewtok_lds_bytes(chunk, 8 * TG),
+                       s, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum);
+    return hipGetLastError();
+}
+
+template <int TG, int FORM>
+static hipError_t launch_fewtok_nw(int nw, const uint8_t *W, const int8_t *xq, const void *xsc, float *y,
+                                   float *slots, int *counters, int M, int N, int K, int chunk, int accum,
+                                   hipStream_t s) {
+    if (nw == 8) return launch_fewtok<8, TG, FORM>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, s);
+    return launch_fewtok<4, TG, FORM>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, s);
+}
+
+/* y (+)= X . W^T for 1 <= M <= 16. form 0: row stage, MMVQ formula (M <= 8);
+ * form 1: MMQ stage, MMQ formula. chunk: super-blocks per workgroup
+ * (1..sera_fewtok_max_chunk(M), 0 = planned); when it splits K, slots holds
+ * splits*M*N floats and counters sera_fewtok_groups() ints, zero on entry
+ * and zero again after the kernel. */
+extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
                                                  int *counters, int M, int N, int K, int chunk, int accum,
                                                  hipStream_t s) {
     int nw, c;
     sera_fewtok_plan(M, N, K, &nw, &c);
     if (chunk > 0) c = chunk;
-    const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
     const char *base = (const char *)stage;
-    const int8_t *xq = (const int8_t *)(base + L.qs);
-    const float4 *dsf = (const float4 *)(base + L.dsf);
     const uint8_t *w = (const uint8_t *)W;
-    if (nw == 8) return launch_fewtok<8>(w, xq, dsf, y, slots, counters, M, N, K, c, accum, s);
-    return launch_fewtok<4>(w, xq, dsf, y, slots, counters, M, N, K, c, accum, s);
+    if (form == 0) {
+        const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
+        return launch_fewtok_nw<1, 0>(nw, w, (const int8_t *)(base + L.qs), base + L.dsf, y, slots, counters, M, N,
+                                      K, c, accum, s);
+    }
+    const sera_stage_layout L = sera_mmq_stage_layout((size_t)sera_mmq_padded_rows(M), (size_t)K);
+    if (M > 8)
+        return launch_fewtok_nw<2, 1>(nw, w, (const int8_t *)(base + L.qs), base + L.ds, y, slots, counters, M, N, K,
+                                      c, accum, s);
+    return launch_fewtok_nw<1, 1>(nw, w, (const int8_t *)(base + L.qs), base + L.ds, y, slots, counters, M, N, K, c,
+                                  accum, s);
 }

@@ -21,7 +21,7 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *sta
 extern "C" int sera_mmq_slot_floats(int M);
 extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
                                              int M, int N, int K, int splits, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_fewtok_acc(const void *W, const void *stage, float *y, float *slots,
+extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
                                                  int *counters, int M, int N, int K, int chunk, int accum,
                                                  hipStream_t s);
 extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk);
@@ -67,8 +67,9 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
  * (stage = fp32 hidden [M][K], partial = the M*param candidate ids,
  * param = candidates per branch, y = logits), 9 / 10 / 11 = paths 5 / 6 / 7
  * on Q6_K weights in the split layout (path 9: param = rows per workgroup),
- * 12 = few-token kernel of the MMVQ path (param = chunk, 0 = planned;
- * partial = split slots followed by the zeroed row-group counters).
+ * 12 / 13 = few-token kernel on a row stage (MMVQ formula) / an MMQ stage
+ * (MMQ formula) (param = chunk, 0 = planned; partial = split slots followed
+ * by the zeroed row-group counters).
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
  * elapsed time over iters (each launch's duration plus the dispatch gap to
@@ -95,9 +96,10 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
             case 11: return sera_launch_candidate_logits(path == 7 ? 14 : path == 8 ? 12 : (int)SERA_QTYPE_Q6K_SPLIT,
                                                          w, N, K, (const float *)stage, (const uint32_t *)partial, M,
                                                          param, y, s);
-            case 12: return sera_launch_q4k_fewtok_acc(
-                         w, stage, y, partial, (int *)(partial + (size_t)sera_fewtok_splits(M, N, K, param) * M * N),
-                         M, N, K, param, 0, s);
+            case 12:
+            case 13: return sera_launch_q4k_fewtok_acc(
+                         path - 12, w, stage, y, partial,
+                         (int *)(partial + (size_t)sera_fewtok_splits(M, N, K, param) * M * N), M, N, K, param, 0, s);
             case 4: return sera_launch_q4k_mmq_streamk(
                         w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),
                         M, N, K, param, s);

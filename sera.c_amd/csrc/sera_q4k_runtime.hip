@@ -59,10 +59,11 @@ extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int
                                                    float *logits, hipStream_t s);
 extern "C" hipError_t sera_launch_embedding(int qtype, const void *W, int N, int K, const uint32_t *ids, int tokens,
                                             float *hidden, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_fewtok_acc(const void *W, const void *stage, float *y, float *slots,
+extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
                                                  int *counters, int M, int N, int K, int chunk, int accum,
                                                  hipStream_t s);
 extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk);
+extern "C" int sera_fewtok_max_chunk(int M);
 extern "C" int sera_fewtok_groups(int M, int N, int K);
 extern "C" int sera_mmq_splits(int M, int N, int K);
 extern "C" int sera_skinny_splits(int M, int N, int K);
@@ -112,6 +113,20 @@ constexpr size_t kCounterBytes = (size_t)256 << 10;
 constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(int));
 constexpr int kFewtokCounterBase = kMaxCounters / 2;
 constexpr int kFewtokMaxCounters = kMaxCounters - kFewtokCounterBase;
+
+/* Batches from this size up to the MMVQ cap run the few-token MFMA kernel
+ * (MMVQ formula) instead of the dot4 MMVQ kernel. Measured on MI355X with
+ * the weights streamed from HBM, gate/up 5120 -> 25600: the MFMA kernel
+ * takes 21 us at 4 or 8 tokens, dot4 24 us at 4 and 32 us at 8; at 3
+ * tokens they tie and below dot4 wins (its cost grows with every token,
+ * the MFMA kernel's does not). */
+#define SERA_Q4K_VEC_MFMA_MIN_BATCH 4
+
+/* The MMQ path up to this batch runs the same kernel with the MMQ formula
+ * on the MMQ stage: at 9 tokens it beats the 32-token MMQ tiles by 10-20%
+ * (gate/up 31 against 35 us, down 40 against 47), at 12 by up to 8%, and at
+ * 16 they tie (both are bound by the fp32 epilogue there). */
+#define SERA_Q4K_FEWTOK_MMQ_MAX_BATCH 12
 
 /* Workgroups the stream-K MMQ schedule runs for M tokens: the resident
  * count, a multiple of 8. */
@@ -203,9 +218,9 @@ extern "C" size_t sera_q4k_arena_bytes(size_t max_tokens, int64_t max_features, 
     if (q6 > stage) stage = q6;
     size_t partial_floats = partial_floats_bound(max_tokens, max_features);
     /* the few-token kernel's split partials: at most 16 splits, or one per
-     * 20 super-blocks of a longer K */
-    const size_t few_splits = (size_t)((max_k / Q4K_QK + 19) / 20 > 16 ? (max_k / Q4K_QK + 19) / 20 : 16);
-    const size_t few = few_splits * (size_t)(mt < SERA_Q4K_MMVQ_MAX_BATCH ? mt : SERA_Q4K_MMVQ_MAX_BATCH) *
+     * 10 super-blocks of a longer K */
+    const size_t few_splits = (size_t)((max_k / Q4K_QK + 9) / 10 > 16 ? (max_k / Q4K_QK + 9) / 10 : 16);
+    const size_t few = few_splits * (size_t)(mt < SERA_Q4K_FEWTOK_MMQ_MAX_BATCH ? mt : SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) *
                        (size_t)(max_features > 0 ? max_features : 0);
     if (few > partial_floats) partial_floats = few;
     const size_t partial = sera_align256(partial_floats * sizeof(float));
@@ -281,17 +296,20 @@ extern "C" int sera_q4k_fewtok_groups(int M, int N, int K) {
     return sera_fewtok_groups(M, N, K);
 }
 
-extern "C" int sera_q4k_fewtok(const void *W, const void *row_stage, float *Y, float *slots, int *counters, int M,
-                               int N, int K, int chunk, int accum, void *stream) {
-    if (!W || !row_stage || !Y) return fail(-1, "sera_q4k_fewtok: null pointer");
-    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q4k_fewtok: batch M=%d outside 1..8", M);
+extern "C" int sera_q4k_fewtok(int form, const void *W, const void *stage, float *Y, float *slots, int *counters,
+                               int M, int N, int K, int chunk, int accum, void *stream) {
+    if (!W || !stage || !Y) return fail(-1, "sera_q4k_fewtok: null pointer");
+    if (form != 0 && form != 1) return fail(-1, "sera_q4k_fewtok: form=%d not 0 (row stage) or 1 (MMQ stage)", form);
+    const int mmax = form == 0 ? SERA_Q4K_MMVQ_MAX_BATCH : SERA_Q4K_SKINNY_MAX_BATCH;
+    if (M < 1 || M > mmax) return fail(-1, "sera_q4k_fewtok: batch M=%d outside 1..%d", M, mmax);
     if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_fewtok: bad shape N=%d K=%d", N, K);
-    if (((uintptr_t)W & 15u) || ((uintptr_t)row_stage & 15u))
+    if (((uintptr_t)W & 15u) || ((uintptr_t)stage & 15u))
         return fail(-1, "sera_q4k_fewtok: W and the stage must be 16-byte aligned");
-    if (chunk < 0 || chunk > 20) return fail(-1, "sera_q4k_fewtok: chunk=%d outside 0..20", chunk);
+    if (chunk < 0 || chunk > sera_fewtok_max_chunk(M))
+        return fail(-1, "sera_q4k_fewtok: chunk=%d outside 0..%d", chunk, sera_fewtok_max_chunk(M));
     if (sera_fewtok_splits(M, N, K, chunk) > 1 && (!slots || !counters))
         return fail(-1, "sera_q4k_fewtok: a split K needs slots and counters");
-    return sera_launch_q4k_fewtok_acc(W, row_stage, Y, slots, counters, M, N, K, chunk, accum ? 1 : 0,
+    return sera_launch_q4k_fewtok_acc(form, W, stage, Y, slots, counters, M, N, K, chunk, accum ? 1 : 0,
                                       (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q4k_fewtok: launch failed");
 }
@@ -324,6 +342,26 @@ bool streamk_rule(int M, int N, int K) {
 bool use_streamk(int M, int N, int K) { return g_counters && streamk_rule(M, N, K); }
 }  // namespace
 
+
+namespace {
+/* The few-token kernel on the stage at the start of the arena (form 0: row
+ * stage, 1: MMQ stage): split partials go to `slots` (cap floats), counters
+ * to the second half of the counter region. */
+int fewtok_launch(const char *tag, int form, const void *W, float *Y, float *slots, size_t cap, int M, int N, int K,
+                  int accum, hipStream_t s) {
+    const int splits = sera_fewtok_splits(M, N, K, 0);
+    if (splits > 1) {
+        if ((size_t)splits * M * N > cap)
+            return fail(-1, "%s: arena too small for %d split partials of %dx%d", tag, splits, M, N);
+        if (sera_fewtok_groups(M, N, K) > kFewtokMaxCounters)
+            return fail(-1, "%s: N=%d needs more row-group counters than the arena holds", tag, N);
+    }
+    return sera_launch_q4k_fewtok_acc(form, W, g_arena, Y, slots, g_counters + kFewtokCounterBase, M, N, K, 0, accum,
+                                      s) == hipSuccess
+               ? 0 : fail(-3, "%s: few-token kernel launch failed", tag);
+}
+}  // namespace
+
 extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
                               int timed) {
     if (!check_shape("sera_q4k_dense", W, X, Y, M, N, K)) return -1;
@@ -346,6 +384,13 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
         return fail(-2, "sera_q4k_dense: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
+    if (M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) {
+        const int rc = fewtok_launch("sera_q4k_dense", 1, W, Y, (float *)(g_arena + stage_bytes),
+                                     (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s);
+        if (rc) return rc;
+        if (timed) record(g_ev.kernel_end, s);
+        return 0;
+    }
     const hipError_t e = sk ? sera_launch_q4k_mmq_streamk(W, stage, Y, partial, g_counters, M, N, K, streamk_wgs(M), s)
                             : sera_launch_q4k_mmq(W, stage, Y, partial, M, N, K, splits, s);
     if (e != hipSuccess) return fail(-3, "sera_q4k_dense: mmq launch failed");
@@ -378,36 +423,9 @@ extern "C" int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float 
 extern "C" int sera_q4k_mmq_tiles(int M, int N) { return M > 0 && N > 0 ? sera_mmq_tiles(M, N) : 0; }
 extern "C" int sera_q4k_mmq_slot_floats(int M) { return M > 0 ? sera_mmq_slot_floats(M) : 0; }
 
-/* Batches from this size up to the MMVQ cap run the few-token MFMA kernel
- * (MMVQ formula) instead of the dot4 MMVQ kernel. Measured on MI355X with
- * the weights streamed from HBM, gate/up 5120 -> 25600: the MFMA kernel
- * takes 21 us at 4 or 8 tokens, dot4 24 us at 4 and 32 us at 8; at 3
- * tokens they tie and below dot4 wins (its cost grows with every token,
- * the MFMA kernel's does not). */
-#define SERA_Q4K_VEC_MFMA_MIN_BATCH 4
-
-namespace {
-/* The few-token kernel on the row stage at the start of the arena: split
- * partials go to `slots` (cap floats), counters to the second half of the
- * counter region. */
-int fewtok_launch(const char *tag, const void *W, float *Y, float *slots, size_t cap, int M, int N, int K,
-                  int accum, hipStream_t s) {
-    const int splits = sera_fewtok_splits(M, N, K, 0);
-    if (splits > 1) {
-        if ((size_t)splits * M * N > cap)
-            return fail(-1, "%s: arena too small for %d split partials of %dx%d", tag, splits, M, N);
-        if (sera_fewtok_groups(M, N, K) > kFewtokMaxCounters)
-            return fail(-1, "%s: N=%d needs more row-group counters than the arena holds", tag, N);
-    }
-    return sera_launch_q4k_fewtok_acc(W, g_arena, Y, slots, g_counters + kFewtokCounterBase, M, N, K, 0, accum, s) ==
-                   hipSuccess
-               ? 0 : fail(-3, "%s: few-token kernel launch failed", tag);
-}
-}  // namespace
-
 extern "C" int sera_q4k_kernel_launches(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
-    if (M <= SERA_Q4K_MMVQ_MAX_BATCH) return 2;
+    if (M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) return 2;   /* the few-token kernel sums split K inside */
     if (use_streamk(M, N, K)) return 2;
     return sera_mmq_splits(M, N, K) > 1 && ((size_t)M * N) % 4 == 0 ? 3 : 2;
 }
@@ -428,7 +446,7 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
     if (M >= SERA_Q4K_VEC_MFMA_MIN_BATCH) {
-        const int rc = fewtok_launch("sera_q4k_dense_vec", W, Y, (float *)(g_arena + stage_bytes),
+        const int rc = fewtok_launch("sera_q4k_dense_vec", 0, W, Y, (float *)(g_arena + stage_bytes),
                                      (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s);
         if (rc) return rc;
     } else if (sera_launch_q4k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
@@ -801,7 +819,11 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         const int n = N[i];
         const bool mn4 = ((size_t)M * n) % 4 == 0;
         if (qt == 12 && M <= SERA_Q4K_MMVQ_MAX_BATCH) {
-            const int rc = fewtok_launch(tag, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
+            const int rc = fewtok_launch(tag, 0, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
+            if (rc) return rc;
+            continue;
+        } else if (qt == 12 && M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) {
+            const int rc = fewtok_launch(tag, 1, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
             if (rc) return rc;
             continue;
         } else if (qt == 12) {

@@ -102,7 +102,7 @@ def load():
         "sera_q4k_mmq_splits": ([I, I, I], I),
         "sera_q4k_skinny": ([I, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_skinny_splits": ([I, I, I], I),
-        "sera_q4k_fewtok": ([P, P, P, P, P, I, I, I, I, I, P], I),
+        "sera_q4k_fewtok": ([I, P, P, P, P, P, I, I, I, I, I, P], I),
         "sera_q4k_fewtok_splits": ([I, I, I, I], I),
         "sera_q4k_fewtok_groups": ([I, I, I], I),
         "sera_q4k_kernel_launches": ([I, I, I], I),
@@ -286,12 +286,13 @@ def skinny_splits(M, N, K):
     return load().sera_q4k_skinny_splits(M, N, K)
 
 
-def fewtok(W, stage, out, M, N, K, chunk=0, slots=None, counters=None, accum=False, stream=None):
-    """Few-token kernel of the MMVQ path on a row stage (MMVQ formula),
-    1 <= M <= 8; a split K needs slots (splits*M*N float32) and counters
-    (fewtok_groups int32, zero before and after)."""
-    _check(load().sera_q4k_fewtok(_ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N, K, chunk,
-                                  1 if accum else 0, _stream(stream)), "sera_q4k_fewtok")
+def fewtok(W, stage, out, M, N, K, chunk=0, slots=None, counters=None, accum=False, form=0, stream=None):
+    """Few-token MFMA kernel: form 0 on a row stage (MMVQ formula, M <= 8),
+    form 1 on an MMQ stage (MMQ formula, M <= 16); a split K needs slots
+    (splits*M*N float32) and counters (fewtok_groups int32, zero before and
+    after)."""
+    _check(load().sera_q4k_fewtok(form, _ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N, K,
+                                  chunk, 1 if accum else 0, _stream(stream)), "sera_q4k_fewtok")
 
 
 def fewtok_splits(M, N, K, chunk=0):

@@ -1,10 +1,14 @@
-"""The MMVQ path's few-token kernel (q4k_fewtok.hip) through the C ABI.
+"""The few-token kernel (q4k_fewtok.hip) through the C ABI.
 
 Bars: fp32 outputs within max |y - y_oracle| <= 1e-3 * rms(y_oracle) of the
-MMVQ-formula oracle (vecdotq.cuh:505-527, the arithmetic the reference's
-mul_mat_vec_q<Q4_K> uses for 1-8 tokens); split-K results repeat bit for
-bit and leave the row-group counters at zero; accumulate adds exactly the
-product; the boundary (q3_cuda_q4k_linear) runs this kernel from 4 tokens.
+path-faithful oracle: the MMVQ formula (vecdotq.cuh:505-527) on a row stage
+for 1-8 tokens, the MMQ formula (mmq.cuh:2269-2283,1440-1472) on an MMQ
+stage for 1-16 tokens. The kernel sums the same fp32 terms as the oracle in
+another order, so it also sits within 2e-5 * rms, far inside the gap between
+the two formulas (the fp16 rounding of d*sc alone moves y by ~1e-4 * rms):
+that pins which formula runs. Split-K results repeat bit for bit and leave
+the row-group counters at zero; accumulate adds exactly the product; the
+boundary (q3_cuda_q4k_linear) runs this kernel from 4 tokens.
 """
 import sys
 
@@ -16,6 +20,7 @@ from oracle import oracle
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
+TIGHT = 2e-5
 
 
 def say(*a):
@@ -52,22 +57,22 @@ def rand_weights(rng, N, K, scale=0.02):
     return oracle.quantize_q4k((rng.standard_normal((N, K)) * scale).astype(np.float32))
 
 
-def check_close(y, ref, what):
+def check_close(y, ref, what, tol=TOL):
     rms = float(np.sqrt(np.mean(ref * ref)))
     err = float(np.max(np.abs(y.astype(np.float64) - ref)))
     say(f"  {what}: max|err| = {err:.3e}, rms = {rms:.3e}, ratio = {err / max(rms, 1e-30):.2e}")
     assert np.all(np.isfinite(y)), what
-    assert err <= TOL * rms, what
+    assert err <= tol * rms, what
 
 
-def run_fewtok(torch, Wd, stage, M, N, K, chunk, y=None, accum=False):
+def run_fewtok(torch, Wd, stage, M, N, K, chunk, y=None, accum=False, form=0):
     s = q3q4.fewtok_splits(M, N, K, chunk)
     slots = torch.empty(s * M * N, dtype=torch.float32, device="cuda") if s > 1 else None
     counters = (torch.zeros(q3q4.fewtok_groups(M, N, K), dtype=torch.int32, device="cuda")
                 if s > 1 else None)
     if y is None:
         y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-    q3q4.fewtok(Wd, stage, y, M, N, K, chunk=chunk, slots=slots, counters=counters, accum=accum)
+    q3q4.fewtok(Wd, stage, y, M, N, K, chunk=chunk, slots=slots, counters=counters, accum=accum, form=form)
     torch.cuda.synchronize()
     if counters is not None:
         assert int(counters.abs().sum()) == 0, "row-group counters not reset"
@@ -98,7 +103,29 @@ def test_fewtok_parity(torch, N, K):
             say(f"case fewtok M={M} N={N} K={K} chunk={chunk} "
                 f"splits={q3q4.fewtok_splits(M, N, K, chunk)}")
             y, _ = run_fewtok(torch, Wd, stage, M, N, K, chunk)
-            check_close(y.cpu().numpy(), ref, f"fewtok M={M} N={N} K={K} chunk={chunk}")
+            check_close(y.cpu().numpy(), ref, f"fewtok M={M} N={N} K={K} chunk={chunk}", TIGHT)
+
+
+@pytest.mark.parametrize("N,K", FEWTOK_SHAPES)
+def test_fewtok_mmq_formula_parity(torch, N, K):
+    """form 1 (MMQ stage) for 1-16 tokens against the MMQ-formula oracle."""
+    rng = np.random.default_rng(13 * N + K)
+    W = rand_weights(rng, N, K)
+    Wd = dev(torch, W)
+    nkb = K // 256
+    for M in (1, 4, 8, 9, 13, 16):
+        x = outlier_activations(rng, M, K)
+        stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+        q3q4.quantize_mmq(dev(torch, x), stage)
+        xq, xd, xs = oracle.q8_1_mmq(x)
+        ref = oracle.gemm_mmq(W, xq, xd, xs, N, K)
+        for chunk in sorted({0, 1, 3, min(10 if M > 8 else 20, nkb)}):
+            if chunk > nkb:
+                continue
+            say(f"case fewtok form=1 M={M} N={N} K={K} chunk={chunk} "
+                f"splits={q3q4.fewtok_splits(M, N, K, chunk)}")
+            y, _ = run_fewtok(torch, Wd, stage, M, N, K, chunk, form=1)
+            check_close(y.cpu().numpy(), ref, f"fewtok form 1 M={M} N={N} K={K} chunk={chunk}", TIGHT)
 
 
 def test_fewtok_split_repeats_and_accumulates(torch):
@@ -159,3 +186,26 @@ def test_boundary_uses_fewtok_from_four_tokens(torch, linear):
         ref, _ = run_fewtok(torch, Wd, stage, M, N, K, 0)
         torch.cuda.synchronize()
         assert torch.equal(y, ref)
+
+
+def test_boundary_uses_fewtok_mmq_formula_to_twelve_tokens(torch, linear):
+    """q3_cuda_q4k_linear at 9-12 tokens gives the few-token kernel's MMQ-formula
+    result bit for bit, and stays within the tolerance of the MMQ oracle."""
+    rng = np.random.default_rng(23)
+    N, K = 1000, 25600
+    W = rand_weights(rng, N, K)
+    Wd = dev(torch, W)
+    geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+    for M in (9, 12):
+        xh = outlier_activations(rng, M, K)
+        x = dev(torch, xh)
+        say(f"case boundary fewtok form=1 M={M} N={N} K={K}")
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        linear(geo, Wd, x, y)
+        stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+        q3q4.quantize_mmq(x, stage)
+        ref, _ = run_fewtok(torch, Wd, stage, M, N, K, 0, form=1)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref)
+        xq, xd, xs = oracle.q8_1_mmq(xh)
+        check_close(y.cpu().numpy(), oracle.gemm_mmq(W, xq, xd, xs, N, K), f"boundary M={M}", TIGHT)
