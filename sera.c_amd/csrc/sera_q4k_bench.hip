@@ -205,36 +205,5 @@ extern "C" int sera_q4k_bench_stream(const void *const *geometries, const void *
                 return false;
         return true;
     };
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-    if (use_graph) {
-        if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return -1;
-        const bool ok = pass();
-        if (hipStreamEndCapture(s, &graph) != hipSuccess || !ok) return -3;
-        if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
-            (void)hipGraphDestroy(graph);
-            return -3;
-        }
-    }
-    auto run = [&]() -> bool { return use_graph ? hipGraphLaunch(exec, s) == hipSuccess : pass(); };
-    int rc = 0;
-    for (int i = 0; i < warmup && rc == 0; i++)
-        if (!run()) rc = -3;
-    hipEvent_t a = nullptr, b = nullptr;
-    if (rc == 0 && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)) rc = -1;
-    if (rc == 0) {
-        (void)hipEventRecord(a, s);
-        for (int i = 0; i < reps && rc == 0; i++)
-            if (!run()) rc = -3;
-        (void)hipEventRecord(b, s);
-        (void)hipEventSynchronize(b);
-        float ms = 0.0f;
-        (void)hipEventElapsedTime(&ms, a, b);
-        *ms_per_rep = (double)ms / reps;
-    }
-    if (a) (void)hipEventDestroy(a);
-    if (b) (void)hipEventDestroy(b);
-    if (exec) (void)hipGraphExecDestroy(exec);
-    if (graph) (void)hipGraphDestroy(graph);
-    return rc;
+    return time_passes(pass, s, warmup, reps, use_graph, ms_per_rep);
 }
