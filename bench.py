@@ -41,6 +41,14 @@ sys.path.insert(0, os.path.join(ROOT, "sera.c_amd"))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 VEC_MFMA_MIN_BATCH = 4   # MMVQ-path batches from here run the few-token MFMA kernel
+
+
+def mmvq_waves(M, K):
+    """Waves per workgroup of the dot4 MMVQ kernel (dispatch_nw in q4k_mmvq.hip)."""
+    groups = (K // 256 + 7) // 8
+    if M == 1 and groups >= 8:
+        return 8
+    return 4 if groups >= 4 or (M == 1 and groups == 3) else groups
 METRIC = "MMVQ HBM GB/s @M=1; MMQ int8 TOPS @M=512; % of MI355X roofline"
 SHAPES = {  # name: (N, K) as (output features, input features)
     "q": (8192, 5120), "k": (1024, 5120), "v": (1024, 5120), "o": (5120, 8192),
@@ -175,7 +183,7 @@ def main():
             row = {"proj": name, "M": M, "N": N, "K": K,
                    "kernel": (f"sera_q4k_fewtok_kernel<{8 if N >= 16384 or K >= 16384 else 4}> "
                               f"(splits {q3q4.fewtok_splits(M, N, K)})") if rpw is None else
-                             f"sera_q4k_mmvq_kernel<{M}, {rpw}, {min(4, (K // 256 + 7) // 8)}>",
+                             f"sera_q4k_mmvq_kernel<{M}, {rpw}, {mmvq_waves(M, K)}>",
                    "step_us": round(step_ms * 1e3, 3),
                    "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),
                    "kernel_us": round(kavg * 1e3, 3),

@@ -261,13 +261,24 @@ extern "C" int sera_mmvq_rows_per_wave(int N, int M) {
     return N >= 16384 ? 4 : 2;
 }
 
+/* Waves per workgroup: one per group of 8 blocks, at most 4. One token
+ * (measured on MI355X, weights streamed from HBM): with 3 groups (K = 5120)
+ * a fourth, idle wave is 1-2% faster, since a 4-wave workgroup puts one
+ * wave on each SIMD of the CU; from 8 groups (K = 25600: 13) 8 waves are
+ * 3-4% faster than 4, with more of the row's groups in flight at once.
+ * Neither helps at 2-3 tokens, whose waves hold more registers. */
 template <int NCOLS, int R>
 static hipError_t dispatch_nw(int K, const MmvqGroup &grp, const int8_t *xq, const float4 *dsf, hipStream_t s) {
     const int ngroups = (K / Q4K_QK + 7) / 8;
-    switch (ngroups >= 4 ? 4 : ngroups) {
+    int nw = ngroups >= 4 ? 4 : ngroups;
+    if (NCOLS == 1 && ngroups == 3) nw = 4;
+    if (NCOLS == 1 && ngroups >= 8) nw = 8;
+    switch (nw) {
         case 1: return launch_mmvq<NCOLS, R, 1>(grp, xq, dsf, K, s);
         case 2: return launch_mmvq<NCOLS, R, 2>(grp, xq, dsf, K, s);
         case 3: return launch_mmvq<NCOLS, R, 3>(grp, xq, dsf, K, s);
+        case 8: if constexpr (NCOLS == 1) return launch_mmvq<NCOLS, R, 8>(grp, xq, dsf, K, s);
+                [[fallthrough]];
         default: return launch_mmvq<NCOLS, R, 4>(grp, xq, dsf, K, s);
     }
 }
