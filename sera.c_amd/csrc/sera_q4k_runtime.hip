@@ -369,6 +369,21 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
     hipStream_t s = (hipStream_t)stream;
     const int Mpad = sera_mmq_padded_rows(M);
     const size_t stage_bytes = sera_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
+    if (M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) {
+        /* few tokens: the few-token kernel with the MMQ formula on the MMQ stage */
+        if (stage_bytes > g_arena_bytes)
+            return fail(-1, "sera_q4k_dense: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
+        if (timed) record(g_ev.quant_begin, s);
+        if (sera_launch_q8_1_mmq(X, M, Mpad, K, g_arena, s) != hipSuccess)
+            return fail(-2, "sera_q4k_dense: quantize launch failed");
+        if (timed) record(g_ev.quant_end, s);
+        if (timed) record(g_ev.kernel_begin, s);
+        const int rc = fewtok_launch("sera_q4k_dense", 1, W, Y, (float *)(g_arena + stage_bytes),
+                                     (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s);
+        if (rc) return rc;
+        if (timed) record(g_ev.kernel_end, s);
+        return 0;
+    }
     const size_t slot_bytes = (size_t)2 * streamk_wgs(M) * sera_mmq_slot_floats(M) * sizeof(float);
     const bool sk = use_streamk(M, N, K) && stage_bytes + slot_bytes <= g_arena_bytes;
     int splits = sk ? 1 : sera_mmq_splits(M, N, K);
@@ -384,13 +399,6 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
         return fail(-2, "sera_q4k_dense: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    if (M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) {
-        const int rc = fewtok_launch("sera_q4k_dense", 1, W, Y, (float *)(g_arena + stage_bytes),
-                                     (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s);
-        if (rc) return rc;
-        if (timed) record(g_ev.kernel_end, s);
-        return 0;
-    }
     const hipError_t e = sk ? sera_launch_q4k_mmq_streamk(W, stage, Y, partial, g_counters, M, N, K, streamk_wgs(M), s)
                             : sera_launch_q4k_mmq(W, stage, Y, partial, M, N, K, splits, s);
     if (e != hipSuccess) return fail(-3, "sera_q4k_dense: mmq launch failed");
