@@ -31,7 +31,7 @@ extern "C" {
 #endif
 
 #define SERA_Q4K_MMVQ_MAX_BATCH 8    /* cuda/q3_mmq.h:77 Q3_MMVQ_MAX_BATCH */
-#define SERA_Q4K_SKINNY_MAX_BATCH 16 /* token tile of the few-token MFMA kernel */
+#define SERA_Q4K_FEWTOK_MAX_BATCH 16 /* largest batch of the few-token MFMA kernel */
 
 /* ---- set-up (cuda/q3_mmq.h:35-38, 84-94) ------------------------------ */
 
@@ -122,18 +122,6 @@ int sera_q4k_mmq_streamk_wgs(int M);   /* resident workgroups for M tokens (afte
 int sera_q4k_mmq_schedule(int M, int N, int K);
 int sera_q4k_mmq_tiles(int M, int N);
 int sera_q4k_mmq_slot_floats(int M);
-
-/* Few-token kernel (1 <= M <= 16) on 16x16 int8 MFMA tiles. form 0 takes a
- * row stage and computes the MMVQ formula (the same arithmetic as
- * sera_q4k_mmvq, vec_dot_q4_K_q8_1, cuda/mmq/vecdotq.cuh:505-527); form 1
- * takes an MMQ stage and computes the MMQ formula (as sera_q4k_mmq,
- * cuda/mmq/mmq.cuh:2269-2283,1440-1472). No reference counterpart as a
- * kernel: it is this build's tiling for the reference's small-batch cases.
- * splits > 1 splits K; partial then holds splits*M*N floats (M*N % 4 == 0);
- * 0 picks the built-in choice (sera_q4k_skinny_splits). */
-int sera_q4k_skinny(int form, const void *W, const void *stage, float *Y, float *partial, int M, int N,
-                    int K, int splits, void *stream);
-int sera_q4k_skinny_splits(int M, int N, int K);
 
 /* Few-token kernel (1 <= M <= 16): Y (+)= X . W^T with two sub-blocks per
  * v_mfma_i32_16x16x64_i8. form 0 takes a row stage and computes the MMVQ

@@ -19,8 +19,6 @@ extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, floa
 extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots,
                                                   int *counters, int M, int N, int K, int P, hipStream_t s);
 extern "C" int sera_mmq_slot_floats(int M);
-extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
-                                             int M, int N, int K, int splits, hipStream_t s);
 extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
                                                  int *counters, int M, int N, int K, int chunk, int accum,
                                                  hipStream_t s);
@@ -60,8 +58,7 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
     return 0;
 }
 
-/* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ, 2 / 3 = few-token
- * kernel with the MMVQ / MMQ formula, 4 = stream-K MMQ (partial = slots, then
+/* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ, 4 = stream-K MMQ (partial = slots, then
  * the zeroed tile counters), 5 = Q6_K MMVQ (param = rows per wave), 6 = Q6_K
  * MMQ (param = splits), 7 / 8 = selected-row LM head on Q6_K / Q4_K rows
  * (stage = fp32 hidden [M][K], partial = the M*param candidate ids,
@@ -103,7 +100,7 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
             case 4: return sera_launch_q4k_mmq_streamk(
                         w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),
                         M, N, K, param, s);
-            default: return sera_launch_q4k_skinny(path - 2, w, stage, y, partial, M, N, K, param, s);
+            default: return hipErrorInvalidValue;
         }
     };
     for (int i = 0; i < warmup; i++)

@@ -66,9 +66,6 @@ extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk);
 extern "C" int sera_fewtok_max_chunk(int M);
 extern "C" int sera_fewtok_groups(int M, int N, int K);
 extern "C" int sera_mmq_splits(int M, int N, int K);
-extern "C" int sera_skinny_splits(int M, int N, int K);
-extern "C" hipError_t sera_launch_q4k_skinny(int form, const void *W, const void *stage, float *y, float *partial,
-                                             int M, int N, int K, int splits, hipStream_t s);
 extern "C" int sera_mmq_padded_rows(int M);
 extern "C" int sera_mmq_tiles(int M, int N);
 extern "C" int sera_mmq_slot_floats(int M);
@@ -270,22 +267,6 @@ extern "C" int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int
 
 extern "C" int sera_q4k_mmq_splits(int M, int N, int K) { return sera_mmq_splits(M, N, K); }
 
-extern "C" int sera_q4k_skinny_splits(int M, int N, int K) { return sera_skinny_splits(M, N, K); }
-
-extern "C" int sera_q4k_skinny(int form, const void *W, const void *stage, float *Y, float *partial, int M,
-                               int N, int K, int splits, void *stream) {
-    if (!W || !stage || !Y) return fail(-1, "sera_q4k_skinny: null pointer");
-    if (form != 0 && form != 1) return fail(-1, "sera_q4k_skinny: form=%d not 0 (row stage) or 1 (MMQ stage)", form);
-    if (M < 1 || M > SERA_Q4K_SKINNY_MAX_BATCH) return fail(-1, "sera_q4k_skinny: batch M=%d outside 1..16", M);
-    if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_skinny: bad shape N=%d K=%d", N, K);
-    if (splits == 0) splits = sera_skinny_splits(M, N, K);
-    if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q4k_skinny: splits=%d outside 1..K/256", splits);
-    if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
-        return fail(-1, "sera_q4k_skinny: split-K needs a partial buffer and M*N %% 4 == 0");
-    return sera_launch_q4k_skinny(form, W, stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
-               ? 0 : fail(-3, "sera_q4k_skinny: launch failed");
-}
-
 extern "C" int sera_q4k_fewtok_splits(int M, int N, int K, int chunk) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK || chunk < 0) return 0;
     return sera_fewtok_splits(M, N, K, chunk);
@@ -300,7 +281,7 @@ extern "C" int sera_q4k_fewtok(int form, const void *W, const void *stage, float
                                int M, int N, int K, int chunk, int accum, void *stream) {
     if (!W || !stage || !Y) return fail(-1, "sera_q4k_fewtok: null pointer");
     if (form != 0 && form != 1) return fail(-1, "sera_q4k_fewtok: form=%d not 0 (row stage) or 1 (MMQ stage)", form);
-    const int mmax = form == 0 ? SERA_Q4K_MMVQ_MAX_BATCH : SERA_Q4K_SKINNY_MAX_BATCH;
+    const int mmax = form == 0 ? SERA_Q4K_MMVQ_MAX_BATCH : SERA_Q4K_FEWTOK_MAX_BATCH;
     if (M < 1 || M > mmax) return fail(-1, "sera_q4k_fewtok: batch M=%d outside 1..%d", M, mmax);
     if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_fewtok: bad shape N=%d K=%d", N, K);
     if (((uintptr_t)W & 15u) || ((uintptr_t)stage & 15u))

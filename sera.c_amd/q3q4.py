@@ -100,8 +100,6 @@ def load():
         "sera_q4k_mmvq_rows_per_tile": ([I, I, I], I),
         "sera_q4k_mmq": ([P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_splits": ([I, I, I], I),
-        "sera_q4k_skinny": ([I, P, P, P, P, I, I, I, I, P], I),
-        "sera_q4k_skinny_splits": ([I, I, I], I),
         "sera_q4k_fewtok": ([I, P, P, P, P, P, I, I, I, I, I, P], I),
         "sera_q4k_fewtok_splits": ([I, I, I, I], I),
         "sera_q4k_fewtok_groups": ([I, I, I], I),
@@ -273,17 +271,6 @@ def mmq_streamk(W, stage, out, M, N, K, slots, counters, wgs=0, stream=None):
     must be zero and are zero again afterwards."""
     _check(load().sera_q4k_mmq_streamk(_ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N, K,
                                        wgs, _stream(stream)), "sera_q4k_mmq_streamk")
-
-
-def skinny(form, W, stage, out, M, N, K, splits=0, partial=None, stream=None):
-    """Few-token MFMA kernel: form 0 on a row stage (MMVQ formula), form 1 on
-    an MMQ stage (MMQ formula); 1 <= M <= 16."""
-    _check(load().sera_q4k_skinny(form, _ptr(W), _ptr(stage), _ptr(out), _ptr(partial), M, N, K, splits,
-                                  _stream(stream)), "sera_q4k_skinny")
-
-
-def skinny_splits(M, N, K):
-    return load().sera_q4k_skinny_splits(M, N, K)
 
 
 def fewtok(W, stage, out, M, N, K, chunk=0, slots=None, counters=None, accum=False, form=0, stream=None):

@@ -107,13 +107,6 @@ def test_kernel_entry_points_validate_on_host(L):
     assert L.sera_q4k_mmq(d, d, d, None, 64, 128, 1024, 2, None) == -1
     assert b"partial" in L.sera_q4k_last_error()
     assert L.sera_q4k_set_arena(ctypes.c_void_p(100), 1024) == -1
-    assert L.sera_q4k_skinny(0, d, d, d, None, 17, 128, 256, 1, None) == -1
-    assert b"outside 1..16" in L.sera_q4k_last_error()
-    assert L.sera_q4k_skinny(2, d, d, d, None, 4, 128, 256, 1, None) == -1
-    assert L.sera_q4k_skinny(1, d, d, d, None, 4, 128, 512, 3, None) == -1
-    assert b"splits" in L.sera_q4k_last_error()
-    assert L.sera_q4k_skinny(1, d, d, d, None, 4, 128, 512, 2, None) == -1
-    assert b"partial" in L.sera_q4k_last_error()
     assert L.sera_q4k_fewtok(0, d, d, d, None, None, 9, 128, 256, 0, 0, None) == -1
     assert b"outside 1..8" in L.sera_q4k_last_error()
     assert L.sera_q4k_fewtok(1, d, d, d, None, None, 17, 128, 256, 0, 0, None) == -1

@@ -283,57 +283,6 @@ def test_mmq_streamk_parity(torch, M, N, K, wgs):
     assert np.array_equal(outs[0], outs[1])
 
 
-SKINNY_SHAPES = [(16, 256), (1000, 512), (300, 5120), (64, 25600), (203, 2304)]
-
-
-@pytest.mark.parametrize("N,K", SKINNY_SHAPES)
-def test_skinny_mmvq_formula_parity(torch, N, K):
-    """Few-token MFMA kernel on a row stage against the MMVQ-formula oracle."""
-    rng = np.random.default_rng(7 * N + K)
-    W = rand_weights(rng, N, K)
-    Wd = dev(torch, W)
-    nkb = K // 256
-    for M in (1, 2, 3, 5, 8, 11, 16):
-        x = outlier_activations(rng, M, K)
-        stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
-        q3q4.quantize_row(dev(torch, x), stage)
-        xq, xd, _ = oracle.q8_1_row(x)
-        ref = oracle.gemm_mmvq(W, xq, xd, N, K)
-        for s in sorted({1, min(2, nkb), min(3, nkb), q3q4.skinny_splits(M, N, K)}):
-            if s > 1 and (M * N) % 4:
-                continue
-            say(f"case skinny form=0 M={M} N={N} K={K} splits={s}")
-            y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-            part = torch.empty(s * M * N, dtype=torch.float32, device="cuda") if s > 1 else None
-            q3q4.skinny(0, Wd, stage, y, M, N, K, splits=s, partial=part)
-            torch.cuda.synchronize()
-            check_close(y.cpu().numpy(), ref, f"skinny form 0 M={M} N={N} K={K} splits={s}")
-
-
-@pytest.mark.parametrize("N,K", SKINNY_SHAPES)
-def test_skinny_mmq_formula_parity(torch, N, K):
-    """Few-token MFMA kernel on an MMQ stage against the MMQ-formula oracle."""
-    rng = np.random.default_rng(11 * N + K)
-    W = rand_weights(rng, N, K)
-    Wd = dev(torch, W)
-    nkb = K // 256
-    for M in (1, 4, 9, 13, 16):
-        x = outlier_activations(rng, M, K)
-        stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
-        q3q4.quantize_mmq(dev(torch, x), stage)
-        xq, xd, xs = oracle.q8_1_mmq(x)
-        ref = oracle.gemm_mmq(W, xq, xd, xs, N, K)
-        for s in sorted({1, min(2, nkb), q3q4.skinny_splits(M, N, K)}):
-            if s > 1 and (M * N) % 4:
-                continue
-            say(f"case skinny form=1 M={M} N={N} K={K} splits={s}")
-            y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-            part = torch.empty(s * M * N, dtype=torch.float32, device="cuda") if s > 1 else None
-            q3q4.skinny(1, Wd, stage, y, M, N, K, splits=s, partial=part)
-            torch.cuda.synchronize()
-            check_close(y.cpu().numpy(), ref, f"skinny form 1 M={M} N={N} K={K} splits={s}")
-
-
 # ---------------------------------------------------------------------------
 # The q3_q4_linear boundary end to end
 # ---------------------------------------------------------------------------
