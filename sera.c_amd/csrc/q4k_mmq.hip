@@ -161,7 +161,9 @@ __device__ __forceinline__ void mmq_segment(
             const int inst = wave + 4 * i;        /* wave-instruction index: 64 pieces each */
             const int c = inst * 64 + lane;       /* LDS piece: token c/16, column c%16 */
             const int tok = c >> 4, col = c & 15;
-            const int8_t *src = xq + (size_t)(m0 + tok) * K + (size_t)kb * Q4K_QK + 16 * (col ^ (tok & 15));
+            /* 32-bit offset (Mpad*K < 2^31): the stream-K loop would otherwise
+             * keep four 64-bit per-lane bases live across segments and spill */
+            const int8_t *src = xq + (uint32_t)((m0 + tok) * K + kb * Q4K_QK + 16 * (col ^ (tok & 15)));
             __builtin_amdgcn_global_load_lds((global_cvoid_t *)src, (lds_void_t *)&sm.xs[buf][0][inst * 1024], 16, 0, 0);
         }
     };
@@ -467,8 +469,11 @@ extern "C" int sera_mmq_bm(int M) { return M <= 32 ? 32 : 64; }
 
 static int mmq_bn(int bm) { (void)bm; return 256; }
 
-/* Workgroups of the MMQ kernel one CU keeps resident. */
-extern "C" int sera_mmq_wgs_per_cu(int M) { return sera_mmq_bm(M) == 32 ? 3 : 2; }
+/* Workgroups of the stream-K MMQ kernel one CU keeps resident: two for
+ * either tile. The 32-token stream-K kernel is built for 2 waves per SIMD:
+ * cut to 3 (168 VGPRs) it spills inside the K loop and measured 20-33%
+ * slower. */
+extern "C" int sera_mmq_wgs_per_cu(int M) { (void)M; return 2; }
 
 /* Split-K factor: enough workgroups to give every CU at least two, but
  * never fewer than 2 super-blocks per split. */
@@ -570,6 +575,6 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void 
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
     if (sera_mmq_bm(M) == 32)
-        return launch_mmq_streamk_cfg<1, 1, 4, 3>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
+        return launch_mmq_streamk_cfg<1, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
     return launch_mmq_streamk_cfg<2, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
 }
