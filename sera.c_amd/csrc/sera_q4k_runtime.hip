@@ -311,13 +311,15 @@ namespace {
 /* The schedule rule, from MI355X measurements over the Qwen3-32B shapes:
  * stream-K for 64-token tiles when there are at least 64 tiles and fewer
  * than four rounds of resident workgroups (beyond that the last round's idle
- * share is small and plain tiles are faster); split-K (or plain tiles) for
- * 32-token tiles and for grids of a few dozen tiles, where each tile would
- * be cut into many short pieces. */
+ * share is small and plain tiles are faster). 32-token tiles (M <= 32) take
+ * stream-K only from one full round of tiles on (the 151936-row LM head:
+ * 152 against 157 us); below that split-K wins by 10-90%, since each tile
+ * would be cut into many short pieces. */
 bool streamk_rule(int M, int N, int K) {
     const int P = streamk_wgs(M);
-    if (P < 8 || M <= 32) return false;
+    if (P < 8) return false;
     const int tiles = sera_mmq_tiles(M, N);
+    if (M <= 32 && tiles < P) return false;
     return tiles >= 64 && tiles < 4 * P && tiles <= kFewtokCounterBase && (int64_t)tiles * (K / Q4K_QK) >= P;
 }
 bool use_streamk(int M, int N, int K) { return g_counters && streamk_rule(M, N, K); }

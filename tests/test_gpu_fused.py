@@ -95,11 +95,16 @@ def test_group_products_and_accumulate(torch, linear, qtype, M):
         assert np.array_equal(ya[i].view(np.uint32), (y0[i] + ys[i]).astype(np.float32).view(np.uint32)), i
 
 
-@pytest.mark.parametrize("M,N,K", [(9, 256, 2048), (64, 16384, 1024), (100, 4096, 5120)])
-def test_accumulate_on_split_and_streamk_schedules(torch, linear, M, N, K):
+@pytest.mark.parametrize("M,N,K,streamk", [(9, 256, 2048, 0), (64, 16384, 2048, 1), (100, 4096, 5120, 0),
+                                            (20, 131328, 256, 1), (20, 4096, 1024, 0)])
+def test_accumulate_on_split_and_streamk_schedules(torch, linear, M, N, K, streamk):
     """Q4_K MMQ under split-K (few tiles) and stream-K (64+ tiles of 64
-    tokens): the accumulating store stays bit-identical to product + add."""
-    say(f"case accumulate schedules M={M} N={N} K={K}")
+    tokens; a full round or more of 32-token tiles): the accumulating store
+    stays bit-identical to product + add."""
+    sched = q3q4.load().sera_q4k_mmq_schedule(M, N, K)
+    say(f"case accumulate schedules M={M} N={N} K={K} stream-K={sched}")
+    if streamk is not None:
+        assert sched == streamk
     rng = np.random.default_rng(M + N)
     W = weights(rng, 12, N, K)
     x = rng.standard_normal((M, K)).astype(np.float32)
