@@ -1,0 +1,107 @@
+"""q3_cuda_q4k_linear under HIP graph capture.
+
+The reference's contract for the call (src/q3_q4_linear.h:99-106) is
+enqueue-only: no host synchronisation, no allocation, no copies. Capture in
+global mode fails on any of those, so a clean capture checks the contract.
+Replays must give the eager result bit for bit, several times in a row with
+eager work (including other calls through the same arena) between them: the
+split-K and stream-K counters are reset by the kernels themselves, so a
+replay finds them at zero as an eager call does. Stats are NULL, as a
+captured caller passes them (event records are for eager timing only).
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import q3q4
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _t
+    if not _t.cuda.is_available():
+        pytest.fail("gpu test without a visible HIP device")
+    q3q4.load()
+    return _t
+
+
+@pytest.fixture(scope="module")
+def linear(torch):
+    return q3q4.Linear(device=0, max_tokens=2048, max_features=151936, max_k=25600)
+
+
+def weights(rng, qtype, N, K):
+    if qtype == q3q4.QTYPE_Q4_K:
+        return oracle.quantize_q4k((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    return oracle.q6k_weights(rng, N, K)
+
+
+def call(torch, geo, W, x, y):
+    """One q3_cuda_q4k_linear on torch's current stream, stats NULL."""
+    L = q3q4.load()
+    err = ctypes.create_string_buffer(512)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ok = L.q3_cuda_q4k_linear(ctypes.byref(geo), ctypes.c_void_p(W.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                              x.shape[0], ctypes.c_void_p(y.data_ptr()), stream, None, err, 512)
+    assert ok, err.value.decode()
+
+
+# (qtype, M, N, K): MMVQ, the few-token kernel with in-kernel split-K (both
+# formulas), stream-K, split-K + reduce; Q6_K MMVQ and its tile kernel
+CASES = [
+    (12, 1, 4096, 5120),
+    (12, 6, 2048, 5120),
+    (12, 10, 1000, 2560),
+    (12, 64, 16384, 2048),
+    (12, 100, 4096, 5120),
+    (14, 1, 2048, 5120),
+    (14, 8, 2048, 5120),
+]
+
+
+@pytest.mark.parametrize("qtype,M,N,K", CASES)
+def test_graph_replay_matches_eager(torch, linear, qtype, M, N, K):
+    say(f"case graph qtype={qtype} M={M} N={N} K={K} path={q3q4.load().q3_cuda_q4k_linear_path_for_batch(M)}")
+    rng = np.random.default_rng(1000 * M + qtype)
+    Wd = torch.from_numpy(weights(rng, qtype, N, K)).cuda()
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    x_other = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    geo = q3q4.bind_geometry(qtype, K, N)
+    y_ref = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    call(torch, geo, Wd, x, y_ref)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y_ref).all())
+
+    y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    y_other = torch.empty_like(y)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(torch, geo, Wd, x, y)          # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        call(torch, geo, Wd, x, y)
+    for rep in range(3):
+        y.fill_(float("nan"))
+        call(torch, geo, Wd, x_other, y_other)  # eager call through the same arena
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        say(f"  replay {rep}: equal={bool(torch.equal(y, y_ref))}")
+        assert torch.equal(y, y_ref), f"replay {rep} differs from the eager result"
+    del graph
+    torch.cuda.synchronize()
