@@ -77,6 +77,9 @@ def main():
                     help="headline only (gate/up M=1): for counter-collection runs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes 20 times (counter scale)")
+    ap.add_argument("--linear-case", default="", metavar="M,N,K",
+                    help="only time q3_cuda_q4k_linear on one Q4_K shape, one weight copy, "
+                         "--steps calls (for counter-collection runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -142,6 +145,18 @@ def main():
         if rc != 0:
             raise RuntimeError(f"bench_kernel rc={rc}: {L.sera_q4k_last_error().decode()}")
         return avg.value, tot.value / iters
+
+    if args.linear_case:
+        M, N, K = (int(v) for v in args.linear_case.split(","))
+        w = quantized(N, K, 7)
+        arr = (ctypes.c_void_p * 1)(w.data_ptr())
+        geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+        x = activations(M, K, 3)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        ms = bench_linear(geo, arr, 1, x, y, 2, args.steps)
+        log(f"[bench] linear case M={M} N={N} K={K} ({L.q3_cuda_q4k_linear_path_for_batch(M).decode()}, "
+            f"{L.sera_q4k_kernel_launches(M, N, K)} launches): {ms * 1e3:.2f} us per call over {args.steps} calls")
+        return
 
     results = {}
 
