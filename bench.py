@@ -213,7 +213,7 @@ def main():
     results["mmvq_sweep"] = sweep
 
     # ---------------- config 3 (gate/up only unless --full): MMQ M=512 -----
-    FEWTOK_MMQ_MAX_BATCH = 12   # the MMQ path runs the few-token kernel (MMQ formula) up to here
+    FEWTOK_MMQ_MAX_BATCH = 9    # the MMQ path runs the few-token kernel (MMQ formula) up to here
 
     def mmq_case(label, N, K, M, arr, ncopies, iters):
         x = activations(M, K, 7)
@@ -273,10 +273,13 @@ def main():
         results["config4_m2048"] = [mmq_case("gate_up", gN, gK, 2048, garr, args.copies, 5),
                                     mmq_case("down", 5120, 25600, 2048, sets["down"][2][1],
                                              args.copies, 5)]
-        # 9-12 tokens (a few speculative branches): the few-token kernel, MMQ formula
+        # 9-16 tokens (a few speculative branches): the few-token kernel (MMQ
+        # formula) at 9, the paired 16-token MMQ tile above
         results["mmq_few_tokens"] = [mmq_case("gate_up", gN, gK, 9, garr, args.copies, 20),
                                      mmq_case("gate_up", gN, gK, 12, garr, args.copies, 20),
-                                     mmq_case("down", 5120, 25600, 12, sets["down"][2][1], args.copies, 20)]
+                                     mmq_case("gate_up", gN, gK, 16, garr, args.copies, 20),
+                                     mmq_case("down", 5120, 25600, 12, sets["down"][2][1], args.copies, 20),
+                                     mmq_case("down", 5120, 25600, 16, sets["down"][2][1], args.copies, 20)]
         lmw, lmarr = weight_set(151936, 5120, 500, 1)
         results["config4_lm_head_m16"] = mmq_case("lm_head", 151936, 5120, 16, lmarr, 1, 20)
         del lmw

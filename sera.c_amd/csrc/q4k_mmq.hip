@@ -113,9 +113,13 @@ __device__ __forceinline__ void q4k_scales_f16(v4u hd, h2 sw[4], h2 mw[4]) {
     }
 }
 
-template <int TT, int WGT, int WGN>
+/* PR = 1 is the paired 16-token tile (TT = WGT = 1): the 32 MFMA rows are
+ * the 16 tokens twice, rows 0-15 on sub-block 2p and rows 16-31 on
+ * sub-block 2p + 1, so the fp32 epilogue runs on no padding rows. */
+template <int TT, int WGT, int WGN, int PR = 0>
 struct MmqShape {
-    static constexpr int BMW = 32 * TT;     /* tokens per wave */
+    static_assert(PR == 0 || (TT == 1 && WGT == 1), "the paired tile is one 32-row MFMA tile per wave");
+    static constexpr int BMW = PR ? 16 : 32 * TT;  /* tokens per wave */
     static constexpr int BM = BMW * WGT;    /* tokens per workgroup */
     static constexpr int BN = 64 * WGN;     /* weight rows per workgroup */
     static constexpr int NACC = TT * 2 * 16; /* accumulator floats per lane */
@@ -124,13 +128,24 @@ struct MmqShape {
 /* One output tile (tokens m0.., weight rows n0..) over super-blocks
  * [kb_begin, kb_end): TT token tiles (of 32) per wave, WGT x WGN waves
  * (along tokens x rows), two 32-row weight tiles per wave. Starts and ends
- * with all threads past a barrier, so consecutive calls may restage. */
-template <int TT, int WGT, int WGN>
+ * with all threads past a barrier, so consecutive calls may restage.
+ *
+ * Paired tile (PR = 1, 16 tokens): for sub-blocks sa = 2p, sb = 2p + 1 two
+ * MFMAs accumulate in int32. Lane (l32, h) holds the 16 nibble bytes
+ * [16h, 16h + 16) of pair p of weight row l32. The first MFMA takes its
+ * nibble plane h (k-half h of the B operand: sa's k 0-15 for h = 0, sb's
+ * k 16-31 for h = 1), the second the other plane (sb's k 0-15, sa's k
+ * 16-31). A row l32 (token l32 & 15 on sub-block 2p + (l32 >> 4)) is real
+ * in k-half h exactly when its slice matches: in the first MFMA when
+ * h == l32 >> 4, in the second otherwise, always reading the token's bytes
+ * [16h, 16h + 16) of its sub-block; the other half is zero. Result rows
+ * 0-15 are I_sa, rows 16-31 I_sb. */
+template <int TT, int WGT, int WGN, int PR = 0>
 __device__ __forceinline__ void mmq_segment(
-        MmqSmem<MmqShape<TT, WGT, WGN>::BM> &sm, const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
+        MmqSmem<MmqShape<TT, WGT, WGN, PR>::BM> &sm, const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, int N, int K, int m0, int n0, int kb_begin, int kb_end,
         v16f (&acc)[TT][2]) {
-    using S = MmqShape<TT, WGT, WGN>;
+    using S = MmqShape<TT, WGT, WGN, PR>;
     constexpr int BMW = S::BMW, BM = S::BM;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -242,8 +257,42 @@ __device__ __forceinline__ void mmq_segment(
             }
         }
 
+        if constexpr (PR) {
+            const int sh = l32 >> 4;            /* this A row's sub-block of the pair */
+            const int t = l32 & 15;             /* this A row's token */
 #pragma unroll
-        for (int b = 0; b < 8; b++) {
+            for (int p = 0; p < 4; p++) {
+                v4i B0[2], B1[2];
+                float swa[2], swbb[2];
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++) {
+                    B0[nt] = unpack_nib(qw[nt][p], h);
+                    B1[nt] = unpack_nib(qw[nt][p], 1 - h);
+                    swa[nt] = (float)sw[nt][p].x;
+                    swbb[nt] = (float)sw[nt][p].y;
+                }
+                const void *real = &sm.xs[buf][t][16 * ((4 * p + 2 * sh + h) ^ t)];
+                const v4i A0 = *(const v4i *)(h == sh ? real : (const void *)&sm.zero8[0]);
+                const v4i A1 = *(const v4i *)(h != sh ? real : (const void *)&sm.zero8[0]);
+                float d8v[16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const v4f f4 = *(const v4f *)&sm.d8[buf][2 * p + (q >> 1)][8 * (q & 1) + 4 * h];
+                    d8v[4 * q] = f4.x; d8v[4 * q + 1] = f4.y; d8v[4 * q + 2] = f4.z; d8v[4 * q + 3] = f4.w;
+                }
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++) {
+                    const v16i zero = {};
+                    v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0[nt], zero, 0, 0, 0);
+                    I = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1[nt], I, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        acc[0][nt][r] = fmaf((float)I[r], d8v[r] * (r < 8 ? swa[nt] : swbb[nt]), acc[0][nt][r]);
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < (PR ? 0 : 8); b++) {
             v4i Bw[2];
             float swb[2];
 #pragma unroll
@@ -274,8 +323,10 @@ __device__ __forceinline__ void mmq_segment(
         /* min term of this super-block */
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-            const int tok = BMW * wt + 32 * t + l32;
-            const v8h as8 = *(const v8h *)(h ? (const void *)&sm.zero8[0] : (const void *)&sm.s8[buf][tok][0]);
+            /* paired tile: the min term goes to rows 0-15 only (each token once) */
+            const int tok = PR ? (l32 & 15) : BMW * wt + 32 * t + l32;
+            const bool none = h || (PR && l32 >= 16);
+            const v8h as8 = *(const v8h *)(none ? (const void *)&sm.zero8[0] : (const void *)&sm.s8[buf][tok][0]);
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
                 acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as8, bmin[nt], acc[t][nt], 0, 0, 0);
@@ -290,11 +341,12 @@ __device__ __forceinline__ void mmq_segment(
 }
 
 /* Store an output tile: lane holds weight row n0+64*wn+32*nt+l32 for tokens
- * m0+BMW*wt+32*t + 8*(r/4) + 4*h + r%4. */
-template <int TT, int WGT, int WGN>
+ * m0+BMW*wt+32*t + 8*(r/4) + 4*h + r%4 (paired tile: r < 8, the sum of the
+ * even and odd sub-block rows r and r + 8). */
+template <int TT, int WGT, int WGN, int PR = 0>
 __device__ __forceinline__ void mmq_store(float *__restrict__ out, int M, int N, int m0, int n0,
                                           const v16f (&acc)[TT][2], int accum) {
-    constexpr int BMW = MmqShape<TT, WGT, WGN>::BMW;
+    constexpr int BMW = MmqShape<TT, WGT, WGN, PR>::BMW;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l32 = lane & 31, h = lane >> 5;
     const int wt = wave % WGT, wn = wave / WGT;
@@ -305,11 +357,12 @@ __device__ __forceinline__ void mmq_store(float *__restrict__ out, int M, int N,
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
+            for (int r = 0; r < (PR ? 8 : 16); r++) {
                 const int m = m0 + BMW * wt + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                const float v = PR ? acc[t][nt][r] + acc[t][nt][r + 8] : acc[t][nt][r];
                 if (m < M) {
                     float *dst = out + (size_t)m * N + n;
-                    *dst = accum ? *dst + acc[t][nt][r] : acc[t][nt][r];
+                    *dst = accum ? *dst + v : v;
                 }
             }
     }
@@ -317,13 +370,13 @@ __device__ __forceinline__ void mmq_store(float *__restrict__ out, int M, int N,
 
 /* Grid over (tile, K split); splits > 1 write fp32 partials per split.
  * WPE: waves per SIMD the register budget is cut for. */
-template <int TT, int WGT, int WGN, int WPE = 2>
+template <int TT, int WGT, int WGN, int WPE = 2, int PR = 0>
 __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ partial,
         int M, int N, int K, int kb_per_split, int accum) {
     static_assert(WGT * WGN == 4, "4 waves per workgroup");
-    using S = MmqShape<TT, WGT, WGN>;
+    using S = MmqShape<TT, WGT, WGN, PR>;
     __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
     const int ntt = (M + S::BM - 1) / S::BM;
     const int nrt = (N + S::BN - 1) / S::BN;
@@ -334,9 +387,9 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
     const int kb_begin = blockIdx.y * kb_per_split;
     const int kb_end = min(nkb_total, kb_begin + kb_per_split);
     v16f acc[TT][2];
-    mmq_segment<TT, WGT, WGN>(sm, W, xq, xds, N, K, m0, n0, kb_begin, kb_end, acc);
+    mmq_segment<TT, WGT, WGN, PR>(sm, W, xq, xds, N, K, m0, n0, kb_begin, kb_end, acc);
     float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
-    mmq_store<TT, WGT, WGN>(out, M, N, m0, n0, acc, partial ? 0 : accum);
+    mmq_store<TT, WGT, WGN, PR>(out, M, N, m0, n0, acc, partial ? 0 : accum);
 }
 
 /* Stream-K schedule: P persistent workgroups split the ntiles x nkb
@@ -353,13 +406,13 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
 __device__ __forceinline__ int64_t sk_u0(int w, int64_t U, int P) { return (int64_t)w * U / P; }
 __device__ __forceinline__ int sk_owner(int64_t u, int64_t U, int P) { return (int)(((u + 1) * P - 1) / U); }
 
-template <int TT, int WGT, int WGN, int WPE = 2>
+template <int TT, int WGT, int WGN, int WPE = 2, int PR = 0>
 __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ slots,
         int *__restrict__ counters, int M, int N, int K, int accum) {
     static_assert(WGT * WGN == 4, "4 waves per workgroup");
-    using S = MmqShape<TT, WGT, WGN>;
+    using S = MmqShape<TT, WGT, WGN, PR>;
     __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
     __shared__ int s_last;
     const int tid = threadIdx.x;
@@ -377,9 +430,9 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         const int kb1 = (int)min<int64_t>(nkb, kb0 + (myu1 - u));
         const int m0 = (t % ntt) * S::BM, n0 = (t / ntt) * S::BN;
         v16f acc[TT][2];
-        mmq_segment<TT, WGT, WGN>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc);
+        mmq_segment<TT, WGT, WGN, PR>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc);
         if (kb0 == 0 && kb1 == nkb) {
-            mmq_store<TT, WGT, WGN>(y, M, N, m0, n0, acc, accum);
+            mmq_store<TT, WGT, WGN, PR>(y, M, N, m0, n0, acc, accum);
         } else {
             /* slot rule: 2c for a contributor c whose range starts inside the
              * tile, 2c + 1 for one that started before it (then the tile is
@@ -420,7 +473,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
                                 acc[tt][nt][r] = c == c0 ? v : acc[tt][nt][r] + v;
                             }
                 }
-                mmq_store<TT, WGT, WGN>(y, M, N, m0, n0, acc, accum);
+                mmq_store<TT, WGT, WGN, PR>(y, M, N, m0, n0, acc, accum);
             }
         }
         u += kb1 - kb0;
@@ -459,13 +512,13 @@ extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, 
     return sera_launch_splitk_reduce_acc(partial, y, n, splits, 0, s);
 }
 
-/* Token-tile width of the workgroup for M tokens: 32 (one token tile per
- * wave, 4 waves along weight rows, registers cut for 3 waves per SIMD) or
- * 64 (two per wave, 2 waves per SIMD); both tiles span 256 weight rows.
- * Measured on MI355X against 128 x 128 tiles: the 64 x 256 tile under the
- * stream-K schedule is the fastest at 512 tokens for both the 5120 -> 25600
- * and the 25600 -> 5120 shapes. */
-extern "C" int sera_mmq_bm(int M) { return M <= 32 ? 32 : 64; }
+/* Token-tile width of the workgroup for M tokens: 16 (the paired tile, one
+ * per wave), 32 (one token tile per wave, 4 waves along weight rows,
+ * registers cut for 3 waves per SIMD) or 64 (two per wave, 2 waves per
+ * SIMD); all tiles span 256 weight rows. Measured on MI355X against 128 x
+ * 128 tiles: the 64 x 256 tile under the stream-K schedule is the fastest at
+ * 512 tokens for both the 5120 -> 25600 and the 25600 -> 5120 shapes. */
+extern "C" int sera_mmq_bm(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : 64; }
 
 static int mmq_bn(int bm) { (void)bm; return 256; }
 
@@ -493,15 +546,15 @@ extern "C" int sera_mmq_padded_rows(int M) {
     return (M + bm - 1) / bm * bm;
 }
 
-template <int TT, int WGT, int WGN, int WPE>
+template <int TT, int WGT, int WGN, int WPE, int PR = 0>
 static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
                                  float *partial, int M, int N, int K, int splits, int accum, hipStream_t s) {
-    constexpr int BM = 32 * TT * WGT, BN = 64 * WGN;
+    constexpr int BM = MmqShape<TT, WGT, WGN, PR>::BM, BN = MmqShape<TT, WGT, WGN, PR>::BN;
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     const int nkb = K / Q4K_QK;
     const int per = (nkb + splits - 1) / splits;
     dim3 grid(tiles, splits);
-    hipLaunchKernelGGL((sera_q4k_mmq_kernel<TT, WGT, WGN, WPE>), grid, dim3(256), 0, s, W, xq, xds, y,
+    hipLaunchKernelGGL((sera_q4k_mmq_kernel<TT, WGT, WGN, WPE, PR>), grid, dim3(256), 0, s, W, xq, xds, y,
                        splits > 1 ? partial : nullptr, M, N, K, per, accum);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
@@ -526,6 +579,8 @@ extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, 
     const int8_t *xq = (const int8_t *)(base + L.qs);
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
+    if (sera_mmq_bm(M) == 16)
+        return launch_mmq_cfg<1, 1, 4, 2, 1>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
     if (sera_mmq_bm(M) == 32)
         return launch_mmq_cfg<1, 1, 4, 3>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
     return launch_mmq_cfg<2, 1, 4, 2>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
@@ -540,14 +595,18 @@ extern "C" int sera_mmq_tiles(int M, int N) {
     return ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
 }
 
-/* Floats of one stream-K partial slot (a whole tile's accumulators). */
-extern "C" int sera_mmq_slot_floats(int M) { return sera_mmq_bm(M) * mmq_bn(sera_mmq_bm(M)); }
+/* Floats of one stream-K partial slot (a whole tile's accumulators; the
+ * paired 16-token tile keeps its 32 MFMA rows). */
+extern "C" int sera_mmq_slot_floats(int M) {
+    const int bm = sera_mmq_bm(M);
+    return (bm < 32 ? 32 : bm) * mmq_bn(bm);
+}
 
-template <int TT, int WGT, int WGN, int WPE>
+template <int TT, int WGT, int WGN, int WPE, int PR = 0>
 static hipError_t launch_mmq_streamk_cfg(const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
                                          float *slots, int *counters, int M, int N, int K, int P, int accum,
                                          hipStream_t s) {
-    hipLaunchKernelGGL((sera_q4k_mmq_streamk_kernel<TT, WGT, WGN, WPE>), dim3(P), dim3(256), 0, s, W, xq, xds, y,
+    hipLaunchKernelGGL((sera_q4k_mmq_streamk_kernel<TT, WGT, WGN, WPE, PR>), dim3(P), dim3(256), 0, s, W, xq, xds, y,
                        slots, counters, M, N, K, accum);
     return hipGetLastError();
 }
@@ -574,6 +633,8 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void 
     const int8_t *xq = (const int8_t *)(base + L.qs);
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
+    if (sera_mmq_bm(M) == 16)
+        return launch_mmq_streamk_cfg<1, 1, 4, 2, 1>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
     if (sera_mmq_bm(M) == 32)
         return launch_mmq_streamk_cfg<1, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
     return launch_mmq_streamk_cfg<2, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);

@@ -120,10 +120,12 @@ constexpr int kFewtokMaxCounters = kMaxCounters - kFewtokCounterBase;
 #define SERA_Q4K_VEC_MFMA_MIN_BATCH 4
 
 /* The MMQ path up to this batch runs the same kernel with the MMQ formula
- * on the MMQ stage: at 9 tokens it beats the 32-token MMQ tiles by 10-20%
- * (gate/up 31 against 35 us, down 40 against 47), at 12 by up to 8%, and at
- * 16 they tie (both are bound by the fp32 epilogue there). */
-#define SERA_Q4K_FEWTOK_MMQ_MAX_BATCH 12
+ * on the MMQ stage. Against the paired 16-token MMQ tile, measured on the
+ * Qwen3-32B projections: at 9 tokens it is faster on gate/up, down, q and
+ * k by 0.4-1 us (a layer of seven projections 163 against 167 us); from 10
+ * tokens the paired tile is faster or equal on all but gate/up (down 41
+ * against 42-47 us, o 18.5 against 19-21, LM head 138 against 147-153). */
+#define SERA_Q4K_FEWTOK_MMQ_MAX_BATCH 9
 
 /* Workgroups the stream-K MMQ schedule runs for M tokens: the resident
  * count, a multiple of 8. */

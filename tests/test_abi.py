@@ -161,9 +161,9 @@ def test_stage_layouts_and_workspace_sizing():
             need = q3q4.mmq_stage_layout(M, K)["total"] + (s * M * N * 4 if s > 1 else 0)
             assert need <= L.sera_q4k_arena_bytes(2048, 151936, 25600), (M, N, K, s)
     # and every few-token split, for arenas sized down to the batch (row
-    # stage up to 8 tokens, MMQ stage from 9 to 12)
-    for mt in (1, 4, 8, 12, 2048):
-        for M in range(1, min(mt, 12) + 1):
+    # stage up to 8 tokens, MMQ stage at 9)
+    for mt in (1, 4, 8, 9, 12, 2048):
+        for M in range(1, min(mt, 9) + 1):
             for N, K in ((1024, 5120), (5120, 25600), (25600, 5120), (151936, 5120), (100, 128 * 1024)):
                 s = L.sera_q4k_fewtok_splits(M, N, K, 0)
                 stage = q3q4.row_stage_layout(M, K) if M <= 8 else q3q4.mmq_stage_layout(M, K)
@@ -176,7 +176,8 @@ def test_kernel_launch_counts(L):
     assert L.sera_q4k_kernel_launches(1, 25600, 5120) == 2          # dot4 MMVQ
     for N, K in ((25600, 5120), (5120, 25600)):                     # few-token kernel,
         assert L.sera_q4k_kernel_launches(8, N, K) == 2             # split K summed inside
-    assert L.sera_q4k_kernel_launches(12, 5120, 25600) == 2         # few-token kernel, MMQ formula
+    assert L.sera_q4k_kernel_launches(9, 5120, 25600) == 2          # few-token kernel, MMQ formula
+    assert L.sera_q4k_kernel_launches(10, 25600, 5120) == 3         # paired MMQ tile, split K
     assert L.sera_q4k_kernel_launches(512, 25600, 5120) == 2        # MMQ, enough tiles
     assert L.sera_q4k_kernel_launches(16, 5120, 25600) == 3         # MMQ, split K
     assert L.sera_q4k_kernel_launches(0, 5120, 25600) == 0

@@ -8,7 +8,7 @@ another order, so it also sits within 2e-5 * rms, far inside the gap between
 the two formulas (the fp16 rounding of d*sc alone moves y by ~1e-4 * rms):
 that pins which formula runs. Split-K results repeat bit for bit and leave
 the row-group counters at zero; accumulate adds exactly the product; the
-boundary (q3_cuda_q4k_linear) runs this kernel from 4 tokens.
+boundary (q3_cuda_q4k_linear) runs this kernel from 4 to 9 tokens.
 """
 import sys
 
@@ -188,23 +188,30 @@ def test_boundary_uses_fewtok_from_four_tokens(torch, linear):
         assert torch.equal(y, ref)
 
 
-def test_boundary_uses_fewtok_mmq_formula_to_twelve_tokens(torch, linear):
-    """q3_cuda_q4k_linear at 9-12 tokens gives the few-token kernel's MMQ-formula
-    result bit for bit, and stays within the tolerance of the MMQ oracle."""
+def test_boundary_uses_fewtok_mmq_formula_at_nine_tokens(torch, linear):
+    """q3_cuda_q4k_linear at 9 tokens gives the few-token kernel's MMQ-formula
+    result bit for bit, and stays within the tolerance of the MMQ oracle; from
+    10 tokens it gives the paired MMQ tile's result."""
     rng = np.random.default_rng(23)
     N, K = 1000, 25600
     W = rand_weights(rng, N, K)
     Wd = dev(torch, W)
     geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
-    for M in (9, 12):
+    for M in (9, 10, 16):
         xh = outlier_activations(rng, M, K)
         x = dev(torch, xh)
-        say(f"case boundary fewtok form=1 M={M} N={N} K={K}")
+        say(f"case boundary MMQ formula M={M} N={N} K={K}")
         y = torch.empty((M, N), dtype=torch.float32, device="cuda")
         linear(geo, Wd, x, y)
         stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
         q3q4.quantize_mmq(x, stage)
-        ref, _ = run_fewtok(torch, Wd, stage, M, N, K, 0, form=1)
+        if M == 9:
+            ref, _ = run_fewtok(torch, Wd, stage, M, N, K, 0, form=1)
+        else:
+            s = q3q4.mmq_splits(M, N, K)
+            ref = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            partial = torch.empty(s * M * N, dtype=torch.float32, device="cuda") if s > 1 else None
+            q3q4.mmq(Wd, stage, ref, M, N, K, splits=s, partial=partial)
         torch.cuda.synchronize()
         assert torch.equal(y, ref)
         xq, xd, xs = oracle.q8_1_mmq(xh)
