@@ -140,7 +140,7 @@ struct MmqShape {
  * h == l32 >> 4, in the second otherwise, always reading the token's bytes
  * [16h, 16h + 16) of its sub-block; the other half is zero. Result rows
  * 0-15 are I_sa, rows 16-31 I_sb. */
-template <int TT, int WGT, int WGN, int PR = 0>
+template <int TT, int WGT, int WGN, int PR = 0, bool AHEAD = false>
 __device__ __forceinline__ void mmq_segment(
         MmqSmem<MmqShape<TT, WGT, WGN, PR>::BM> &sm, const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, int N, int K, int m0, int n0, int kb_begin, int kb_end,
@@ -221,6 +221,12 @@ __device__ __forceinline__ void mmq_segment(
 
     v4u dr = {};
     v4u hdr[2] = {}, qw[2][4];
+    /* AHEAD (one token tile per wave at 2 waves per SIMD leaves registers for
+     * a second weight set): the next step's weights are issued before this
+     * step's compute, so their latency hides behind it instead of behind the
+     * step's barrier. */
+    constexpr bool kWeightsAhead = AHEAD;
+    v4u hdrn[2] = {}, qwn[2][4];
 
     /* zero8 is the min-term A operand of the lanes (h = 1) whose k
      * positions carry no sub-block */
@@ -240,6 +246,7 @@ __device__ __forceinline__ void mmq_segment(
         if (more) {
             issue_x(kb_begin + it + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
             load_x(kb_begin + it + 1, dr);
+            if constexpr (kWeightsAhead) load_w(kb_begin + it + 1, hdrn, qwn);
         }
 
         /* per weight tile: fp16(d*sc_b) as fp32 for the epilogue and the
@@ -332,11 +339,19 @@ __device__ __forceinline__ void mmq_segment(
                 acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as8, bmin[nt], acc[t][nt], 0, 0, 0);
         }
         if (more) {
-            load_w(kb_begin + it + 1, hdr, qw);
+            if constexpr (!kWeightsAhead) load_w(kb_begin + it + 1, hdr, qw);
             store_x(buf ^ 1, dr);
         }
         __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads to LDS have landed */
         __syncthreads();
+        if constexpr (kWeightsAhead) {
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                hdr[nt] = hdrn[nt];
+#pragma unroll
+                for (int j2 = 0; j2 < 4; j2++) qw[nt][j2] = qwn[nt][j2];
+            }
+        }
     }
 }
 
@@ -387,7 +402,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
     const int kb_begin = blockIdx.y * kb_per_split;
     const int kb_end = min(nkb_total, kb_begin + kb_per_split);
     v16f acc[TT][2];
-    mmq_segment<TT, WGT, WGN, PR>(sm, W, xq, xds, N, K, m0, n0, kb_begin, kb_end, acc);
+    mmq_segment<TT, WGT, WGN, PR, TT == 1 && WPE <= 2>(sm, W, xq, xds, N, K, m0, n0, kb_begin, kb_end, acc);
     float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
     mmq_store<TT, WGT, WGN, PR>(out, M, N, m0, n0, acc, partial ? 0 : accum);
 }
@@ -430,7 +445,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         const int kb1 = (int)min<int64_t>(nkb, kb0 + (myu1 - u));
         const int m0 = (t % ntt) * S::BM, n0 = (t / ntt) * S::BN;
         v16f acc[TT][2];
-        mmq_segment<TT, WGT, WGN, PR>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc);
+        mmq_segment<TT, WGT, WGN, PR, TT == 1 && WPE <= 2>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc);
         if (kb0 == 0 && kb1 == nkb) {
             mmq_store<TT, WGT, WGN, PR>(y, M, N, m0, n0, acc, accum);
         } else {
