@@ -96,11 +96,12 @@ def test_group_products_and_accumulate(torch, linear, qtype, M):
 
 
 @pytest.mark.parametrize("M,N,K,streamk", [(9, 256, 2048, 0), (64, 16384, 2048, 1), (100, 4096, 5120, 0),
-                                            (20, 131328, 256, 1), (20, 4096, 1024, 0)])
+                                            (20, 131328, 256, 1), (20, 4096, 1024, 0),
+                                            (13, 1000, 2304, 0), (16, 131328, 256, 1)])
 def test_accumulate_on_split_and_streamk_schedules(torch, linear, M, N, K, streamk):
     """Q4_K MMQ under split-K (few tiles) and stream-K (64+ tiles of 64
-    tokens; a full round or more of 32-token tiles): the accumulating store
-    stays bit-identical to product + add."""
+    tokens; a full round or more of 32- or paired 16-token tiles): the
+    accumulating store stays bit-identical to product + add."""
     sched = q3q4.load().sera_q4k_mmq_schedule(M, N, K)
     say(f"case accumulate schedules M={M} N={N} K={K} stream-K={sched}")
     if streamk is not None:
