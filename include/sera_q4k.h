@@ -83,7 +83,8 @@ void sera_q8_1_row_stage_offsets(int M, int K, size_t *qs, size_t *ds, size_t *d
 int sera_q8_1_quantize_row(const float *X, int M, int K, void *stage, void *stream);
 
 /* MMQ-layout Q8_1 stage: qs int8 [Mpad][K], ds half2 [Mpad][K/32], rows
- * M..Mpad-1 zero. Quantizer of cuda/mmq/quantize.cu:271-367
+ * M..Mpad-1 zero; Mpad is M rounded up to the MMQ token tile (16 up to 16
+ * tokens, 32 up to 32, else 64). Quantizer of cuda/mmq/quantize.cu:271-367
  * (quantize_mmq_q8_1<DS4>, launcher :385-413). */
 int sera_q8_1_mmq_padded_rows(int M);
 size_t sera_q8_1_mmq_stage_bytes(int M, int K);
