@@ -160,6 +160,20 @@ def test_stage_layouts_and_workspace_sizing():
             s = q3q4.mmq_splits(M, N, K)
             need = q3q4.mmq_stage_layout(M, K)["total"] + (s * M * N * 4 if s > 1 else 0)
             assert need <= L.sera_q4k_arena_bytes(2048, 151936, 25600), (M, N, K, s)
+    # arenas sized down to 16 or 32 tokens hold every split-K choice of the
+    # 16- and 32-token tiles, and the stream-K slots of the LM head at 16
+    # tokens (P = 2 x 256 CUs on MI355X), so the boundary takes the planned
+    # schedule there instead of falling back
+    for mt in (16, 32):
+        room = L.sera_q4k_arena_bytes(mt, 151936, 25600) - (256 << 10)
+        for M in sorted({10, 13, 16, mt}):
+            for N, K in ((1024, 5120), (5120, 25600), (25600, 5120), (151936, 5120), (8192, 5120)):
+                s = q3q4.mmq_splits(M, N, K)
+                need = q3q4.mmq_stage_layout(M, K)["total"] + (s * M * N * 4 if s > 1 else 0)
+                assert need <= room, (mt, M, N, K, s)
+        slots = 2 * 512 * L.sera_q4k_mmq_slot_floats(16) * 4
+        assert L.sera_q4k_mmq_slot_floats(16) == 32 * 256   # the paired tile keeps 32 MFMA rows
+        assert q3q4.mmq_stage_layout(16, 5120)["total"] + slots <= room, mt
     # and every few-token split, for arenas sized down to the batch (row
     # stage up to 8 tokens, MMQ stage at 9)
     for mt in (1, 4, 8, 9, 12, 2048):
