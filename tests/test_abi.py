@@ -196,3 +196,14 @@ def test_kernel_launch_counts(L):
     assert L.sera_q4k_kernel_launches(16, 5120, 25600) == 3         # MMQ, split K
     assert L.sera_q4k_kernel_launches(0, 5120, 25600) == 0
     assert L.sera_q4k_kernel_launches(4, 5120, 300) == 0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits non-zero with a message
+    (before anything touches a GPU)."""
+    import sys as _sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([_sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
