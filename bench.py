@@ -40,7 +40,6 @@ sys.path.insert(0, os.path.join(ROOT, "sera.c_amd"))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
-VEC_MFMA_MIN_BATCH = 4   # MMVQ-path batches from here run the few-token MFMA kernel
 
 
 def mmvq_waves(M, K):
@@ -78,8 +77,8 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes 20 times (counter scale)")
     ap.add_argument("--linear-case", default="", metavar="M,N,K",
-                    help="only time q3_cuda_q4k_linear on one Q4_K shape, one weight copy, "
-                         "--steps calls (for counter-collection runs)")
+                    help="only time q3_cuda_q4k_linear on one Q4_K shape over --copies weight copies, "
+                         "--steps calls (for counter-collection runs and batch sweeps)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -148,14 +147,14 @@ def main():
 
     if args.linear_case:
         M, N, K = (int(v) for v in args.linear_case.split(","))
-        w = quantized(N, K, 7)
-        arr = (ctypes.c_void_p * 1)(w.data_ptr())
+        ws, arr = weight_set(N, K, 7, args.copies)
         geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
         x = activations(M, K, 3)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
-        ms = bench_linear(geo, arr, 1, x, y, 2, args.steps)
+        ms = bench_linear(geo, arr, args.copies, x, y, 2, args.steps)
         log(f"[bench] linear case M={M} N={N} K={K} ({L.q3_cuda_q4k_linear_path_for_batch(M).decode()}, "
-            f"{L.sera_q4k_kernel_launches(M, N, K)} launches): {ms * 1e3:.2f} us per call over {args.steps} calls")
+            f"{L.sera_q4k_kernel_launches(M, N, K)} launches, {args.copies} weight copies): "
+            f"{ms * 1e3:.2f} us per call over {args.steps} calls")
         return
 
     results = {}
@@ -182,7 +181,7 @@ def main():
             stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
             q3q4.quantize_row(x, stage)
             rpw = L.sera_q4k_mmvq_rows_per_tile(M, N, K)
-            if M >= VEC_MFMA_MIN_BATCH:
+            if L.sera_q4k_vec_uses_fewtok(M, N, K):
                 # the MMVQ path's few-token MFMA kernel (MMVQ arithmetic): split
                 # slots, then the zeroed row-group counters
                 sp = q3q4.fewtok_splits(M, N, K)

@@ -59,14 +59,21 @@ int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
                    void *stream, int timed);
 
 /* Same contract through the MMVQ path (MMVQ arithmetic), 1 <= M <= 8:
- * the dot4 MMVQ kernel up to 4 tokens, the few-token MFMA kernel (form 0)
- * from 5. Replaces q3_mmq_q4_K_dense_vec (cuda/q3_mmq.cu:408-506). */
+ * the dot4 MMVQ kernel or the few-token MFMA kernel (form 0), as
+ * sera_q4k_vec_uses_fewtok chooses. Replaces q3_mmq_q4_K_dense_vec
+ * (cuda/q3_mmq.cu:408-506). */
 int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
 
 /* Kernel launches (quantize + matmul + split-K reduce if any) one dense or
  * dense_vec call makes for this shape; 0 for an invalid shape. */
 int sera_q4k_kernel_launches(int M, int N, int K);
+
+/* 1 if the MMVQ path (1 <= M <= 8) runs the few-token MFMA kernel for an
+ * N x K matrix (tall matrices from 3 tokens, 4096-16383 rows from 5, never
+ * below 4096 rows), 0 if it runs the dot4 MMVQ kernel. No counterpart in
+ * the reference (cuda/mmq/mmvq.cu has one kernel); a dispatch query. */
+int sera_q4k_vec_uses_fewtok(int M, int N, int K);
 
 /* Event timings of the last timed dense call, valid after the caller
  * synchronized its stream (q3_mmq_read_timings, cuda/q3_mmq.h:48-50). */

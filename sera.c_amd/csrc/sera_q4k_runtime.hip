@@ -111,13 +111,23 @@ constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(int));
 constexpr int kFewtokCounterBase = kMaxCounters / 2;
 constexpr int kFewtokMaxCounters = kMaxCounters - kFewtokCounterBase;
 
-/* Batches from this size up to the MMVQ cap run the few-token MFMA kernel
- * (MMVQ formula) instead of the dot4 MMVQ kernel. Measured on MI355X with
- * the weights streamed from HBM, gate/up 5120 -> 25600: the MFMA kernel
- * takes 21 us at 4 or 8 tokens, dot4 24 us at 4 and 32 us at 8; at 3
- * tokens they tie and below dot4 wins (its cost grows with every token,
- * the MFMA kernel's does not). */
-#define SERA_Q4K_VEC_MFMA_MIN_BATCH 4
+/* The MMVQ path (M <= 8) runs the few-token MFMA kernel (MMVQ formula)
+ * instead of the dot4 MMVQ kernel where that is faster. Measured on MI355X
+ * per Qwen3-32B shape with the weights streamed from HBM (kernel us, dot4 /
+ * few-token): the few-token kernel's time is flat in M, dot4's grows with
+ * every token and jumps at 5 (fewer rows per wave).
+ *   gate/up 25600 rows: 3 tokens 21.7 / 19.7, 4: 24.8 / 20.1;
+ *   LM head 151936 rows: 3: 106.6 / 96.3;
+ *   q 8192, o and down 5120 rows: 4: 9.9 / 11.2, 10.5 / 15.2, 26.6 / 27.0;
+ *     5: 19.1 / 11.4, 17.9 / 15.4, 50.3 / 27.1;
+ *   k/v 1024 rows: 8 tokens 6.8 / 10.4 (dot4 at every batch). */
+extern "C" int sera_q4k_vec_uses_fewtok(int M, int N, int K) {
+    (void)K;
+    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH || N <= 0) return 0;
+    if (N >= 16384) return M >= 3;
+    if (N >= 4096) return M >= 5;
+    return 0;
+}
 
 /* The MMQ path up to this batch runs the same kernel with the MMQ formula
  * on the MMQ stage. Against the paired 16-token MMQ tile, measured on the
@@ -438,7 +448,7 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
         return fail(-2, "sera_q4k_dense_vec: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    if (M >= SERA_Q4K_VEC_MFMA_MIN_BATCH) {
+    if (sera_q4k_vec_uses_fewtok(M, N, K)) {
         const int rc = fewtok_launch("sera_q4k_dense_vec", 0, W, Y, (float *)(g_arena + stage_bytes),
                                      (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s);
         if (rc) return rc;
@@ -802,20 +812,35 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
     if (qe != hipSuccess) return fail(-2, "%s: quantize launch failed", tag);
 
     /* the products */
-    if (qt == 12 && M < SERA_Q4K_VEC_MFMA_MIN_BATCH) {
-        if (sera_launch_q4k_mmvq_group(count, weights, outputs, N, g_arena, M, K, 0, accum, s) != hipSuccess)
+    if (qt == 12 && M <= SERA_Q4K_MMVQ_MAX_BATCH) {
+        /* the matrices the dot4 kernel takes share one grouped launch; the
+         * few-token kernel runs the others one by one */
+        const void *gw[SERA_LINEAR_GROUP_MAX];
+        float *gy[SERA_LINEAR_GROUP_MAX];
+        int gn[SERA_LINEAR_GROUP_MAX];
+        int g = 0;
+        for (int i = 0; i < count; i++)
+            if (!sera_q4k_vec_uses_fewtok(M, N[i], K)) {
+                gw[g] = weights[i];
+                gy[g] = outputs[i];
+                gn[g] = N[i];
+                g++;
+            }
+        if (g > 0 && sera_launch_q4k_mmvq_group(g, gw, gy, gn, g_arena, M, K, 0, accum, s) != hipSuccess)
             return fail(-3, "%s: grouped mmvq launch failed", tag);
+        for (int i = 0; i < count; i++)
+            if (sera_q4k_vec_uses_fewtok(M, N[i], K)) {
+                const int rc = fewtok_launch(tag, 0, weights[i], outputs[i], partial, partial_cap, M, N[i], K,
+                                             accum, s);
+                if (rc) return rc;
+            }
         return 0;
     }
     for (int i = 0; i < count; i++) {
         hipError_t e;
         const int n = N[i];
         const bool mn4 = ((size_t)M * n) % 4 == 0;
-        if (qt == 12 && M <= SERA_Q4K_MMVQ_MAX_BATCH) {
-            const int rc = fewtok_launch(tag, 0, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
-            if (rc) return rc;
-            continue;
-        } else if (qt == 12 && M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) {
+        if (qt == 12 && M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) {
             const int rc = fewtok_launch(tag, 1, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
             if (rc) return rc;
             continue;

@@ -207,3 +207,15 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU only" in r.stderr
+
+
+def test_vec_dispatch_rule(L):
+    """The MMVQ path's kernel choice by shape: the few-token kernel on tall
+    matrices from 3 tokens, on 4096-16383 rows from 5, never below 4096 rows."""
+    f = L.sera_q4k_vec_uses_fewtok
+    assert [f(M, 25600, 5120) for M in range(1, 9)] == [0, 0, 1, 1, 1, 1, 1, 1]
+    assert [f(M, 151936, 5120) for M in range(1, 9)] == [0, 0, 1, 1, 1, 1, 1, 1]
+    for N in (5120, 8192):
+        assert [f(M, N, 25600) for M in range(1, 9)] == [0, 0, 0, 0, 1, 1, 1, 1]
+    assert [f(M, 1024, 5120) for M in range(1, 9)] == [0] * 8
+    assert f(0, 25600, 5120) == 0 and f(9, 25600, 5120) == 0

@@ -8,7 +8,8 @@ another order, so it also sits within 2e-5 * rms, far inside the gap between
 the two formulas (the fp16 rounding of d*sc alone moves y by ~1e-4 * rms):
 that pins which formula runs. Split-K results repeat bit for bit and leave
 the row-group counters at zero; accumulate adds exactly the product; the
-boundary (q3_cuda_q4k_linear) runs this kernel from 4 to 9 tokens.
+boundary (q3_cuda_q4k_linear) runs this kernel where sera_q4k_vec_uses_fewtok
+says so (2-8 tokens) and at 9 tokens.
 """
 import sys
 
@@ -168,22 +169,29 @@ def test_fewtok_matches_dot4_mmvq(torch):
         check_close(y.cpu().numpy(), y_mmvq.cpu().numpy().astype(np.float64), f"fewtok vs mmvq M={M}")
 
 
-def test_boundary_uses_fewtok_from_four_tokens(torch, linear):
-    """q3_cuda_q4k_linear at 4-8 tokens gives the few-token kernel's result
-    bit for bit (the dispatch runs it, with its planned chunk)."""
-    rng = np.random.default_rng(21)
-    N, K = 5120, 25600
+@pytest.mark.parametrize("N,K", [(25600, 5120), (5120, 25600), (1024, 5120)])
+def test_boundary_vec_dispatch(torch, linear, N, K):
+    """q3_cuda_q4k_linear at 2-8 tokens gives, bit for bit, the result of the
+    kernel sera_q4k_vec_uses_fewtok names: the few-token kernel (its planned
+    chunk) or the dot4 MMVQ kernel."""
+    rng = np.random.default_rng(21 + N)
     W = rand_weights(rng, N, K)
     Wd = dev(torch, W)
     geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
-    for M in (4, 5, 8):
+    L = q3q4.load()
+    for M in (2, 3, 4, 5, 8):
         x = dev(torch, outlier_activations(rng, M, K))
-        say(f"case boundary fewtok M={M} N={N} K={K}")
+        few = L.sera_q4k_vec_uses_fewtok(M, N, K)
+        say(f"case boundary vec M={M} N={N} K={K} fewtok={few}")
         y = torch.empty((M, N), dtype=torch.float32, device="cuda")
         linear(geo, Wd, x, y)
         stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
         q3q4.quantize_row(x, stage)
-        ref, _ = run_fewtok(torch, Wd, stage, M, N, K, 0)
+        if few:
+            ref, _ = run_fewtok(torch, Wd, stage, M, N, K, 0)
+        else:
+            ref = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            q3q4.mmvq(Wd, stage, ref, M, N, K)
         torch.cuda.synchronize()
         assert torch.equal(y, ref)
 
