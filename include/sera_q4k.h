@@ -75,6 +75,12 @@ int sera_q4k_kernel_launches(int M, int N, int K);
  * the reference (cuda/mmq/mmvq.cu has one kernel); a dispatch query. */
 int sera_q4k_vec_uses_fewtok(int M, int N, int K);
 
+/* 1 if a Q6_K call on the MMVQ path (1 <= M <= 8) runs the tile kernel on a
+ * row-formula stage for an N x K matrix (from 4 tokens at 16384 or more
+ * rows, from 6 at 4096-16383 rows, never below 4096), 0 if it runs the
+ * Q6_K MMVQ kernel. No counterpart in the reference; a dispatch query. */
+int sera_q6k_vec_uses_tile(int M, int N, int K);
+
 /* Event timings of the last timed dense call, valid after the caller
  * synchronized its stream (q3_mmq_read_timings, cuda/q3_mmq.h:48-50). */
 void sera_q4k_read_timings(double *quant_ms, double *kernel_ms, double *total_ms);

@@ -502,10 +502,21 @@ extern "C" int sera_q6k_mmvq(uint32_t qtype, const void *W, const void *row_stag
                ? 0 : fail(-3, "sera_q6k_mmvq: launch failed");
 }
 
-/* Q6_K batches from this size up to the MMVQ cap run the MFMA tile kernel
- * on a row-formula stage (the MMVQ arithmetic) instead of the dot4 MMVQ
- * kernel, which is VALU-bound there. */
-#define SERA_Q6K_VEC_MFMA_MIN_BATCH 5
+/* Q6_K batches on the MMVQ path (M <= 8) run the MFMA tile kernel on a
+ * row-formula stage (the MMVQ arithmetic) instead of the dot4 MMVQ kernel
+ * where that is faster. Measured on MI355X per shape, GGUF bytes (kernel
+ * us, MMVQ / tile): the tile kernel's time is flat in M, MMVQ's grows.
+ *   LM head 151936 rows: 4 tokens 252 / 235, 5: 287 / 217;
+ *   q 8192 and down 5120 rows: 5: 20.7 / 21.4, 52.8 / 61.1; 6: 22.4 / 21.1,
+ *     59.4 / 59.4; 8: 40.6 / 20.9, 93.3 / 58.4;
+ *   v 1024 rows: 8 tokens 8.4 / 14.7 (MMVQ at every batch). */
+extern "C" int sera_q6k_vec_uses_tile(int M, int N, int K) {
+    (void)K;
+    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH || N <= 0) return 0;
+    if (N >= 16384) return M >= 4;
+    if (N >= 4096) return M >= 6;
+    return 0;
+}
 
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
 
@@ -517,7 +528,7 @@ extern "C" int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X,
     if (!q6k_shape_ok("sera_q6k_dense_vec", qtype, K)) return -1;
     if (!g_arena) return fail(-1, "sera_q6k_dense_vec: no arena attached");
     hipStream_t s = (hipStream_t)stream;
-    const bool mfma = M >= SERA_Q6K_VEC_MFMA_MIN_BATCH;
+    const bool mfma = sera_q6k_vec_uses_tile(M, N, K) != 0;
     const int Mpad = sera_q6k_mmq_padded_rows(M);
     const size_t stage_bytes = mfma ? sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K).total
                                     : sera_row_stage_layout((size_t)M, (size_t)K).total;
@@ -551,7 +562,7 @@ int q6k_splits(int M, int N, int K) {
 
 extern "C" int sera_q6k_kernel_launches(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
-    if (M < SERA_Q6K_VEC_MFMA_MIN_BATCH) return 2;
+    if (M <= SERA_Q4K_MMVQ_MAX_BATCH && !sera_q6k_vec_uses_tile(M, N, K)) return 2;
     return q6k_splits(M, N, K) > 1 ? 3 : 2;
 }
 
@@ -779,6 +790,12 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
     if (flags & SERA_LIN_RMSNORM) prod.kind = 1;
     if (flags & SERA_LIN_SILU_MUL) prod.kind = 2;
 
+    /* Q6_K: one stage serves the whole group, so the largest matrix picks
+     * between the MMVQ kernel (row stage) and the tile kernel */
+    int n_max = 0;
+    for (int i = 0; i < count; i++) n_max = N[i] > n_max ? N[i] : n_max;
+    const bool q6_tile = M > SERA_Q4K_MMVQ_MAX_BATCH || sera_q6k_vec_uses_tile(M, n_max, K);
+
     /* stage, then per-matrix split-K partials or stream-K slots */
     size_t stage_bytes;
     int Mpad = M;
@@ -789,7 +806,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
             Mpad = sera_mmq_padded_rows(M);
             stage_bytes = sera_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
         }
-    } else if (M < SERA_Q6K_VEC_MFMA_MIN_BATCH) {
+    } else if (!q6_tile) {
         stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
     } else {
         Mpad = sera_q6k_mmq_padded_rows(M);
@@ -805,7 +822,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         qe = M <= SERA_Q4K_MMVQ_MAX_BATCH ? sera_launch_q8_1_row_p(X, &prod, M, K, g_arena, s)
                                           : sera_launch_q8_1_mmq_p(X, &prod, M, Mpad, K, g_arena, s);
     else
-        qe = M < SERA_Q6K_VEC_MFMA_MIN_BATCH
+        qe = !q6_tile
                  ? sera_launch_q8_1_row_p(X, &prod, M, K, g_arena, s)
                  : sera_launch_q8_1_q6k_stage_p(X, &prod, M, Mpad, K, M <= SERA_Q4K_MMVQ_MAX_BATCH ? 1 : 0,
                                                 g_arena, s);
@@ -854,7 +871,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
                 if ((size_t)sp * M * n > partial_cap) sp = 1;
                 e = sera_launch_q4k_mmq_acc(weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
             }
-        } else if (M < SERA_Q6K_VEC_MFMA_MIN_BATCH) {
+        } else if (!q6_tile) {
             e = sera_launch_q6k_mmvq_acc(qt, weights[i], g_arena, outputs[i], M, n, K, 0, accum, s);
         } else {
             int sp = mn4 ? sera_q6k_mmq_splits(M, n, K) : 1;

@@ -219,3 +219,15 @@ def test_vec_dispatch_rule(L):
         assert [f(M, N, 25600) for M in range(1, 9)] == [0, 0, 0, 0, 1, 1, 1, 1]
     assert [f(M, 1024, 5120) for M in range(1, 9)] == [0] * 8
     assert f(0, 25600, 5120) == 0 and f(9, 25600, 5120) == 0
+
+
+def test_q6k_vec_dispatch_rule(L):
+    """Q6_K on the MMVQ path: the tile kernel on tall matrices from 4 tokens,
+    on 4096-16383 rows from 6, never below 4096 rows; launch counts follow."""
+    f = L.sera_q6k_vec_uses_tile
+    assert [f(M, 151936, 5120) for M in range(1, 9)] == [0, 0, 0, 1, 1, 1, 1, 1]
+    for N, K in ((5120, 25600), (8192, 5120)):
+        assert [f(M, N, K) for M in range(1, 9)] == [0, 0, 0, 0, 0, 1, 1, 1]
+    assert [f(M, 1024, 5120) for M in range(1, 9)] == [0] * 8
+    assert L.sera_q6k_kernel_launches(8, 1024, 5120) == 2          # MMVQ
+    assert L.sera_q6k_kernel_launches(5, 5120, 25600) == 2         # MMVQ
