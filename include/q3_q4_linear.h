@@ -83,8 +83,11 @@ const char *q3_cuda_q4k_linear_path_for_batch(size_t token_count);
 
 /* Y[M][N] = X[M][K] . W^T with device pointers only; enqueue-only on
  * `stream` (no host sync, no allocation, no host copies). Returns false
- * with `error` filled on any failure; Q6_K weights are rejected here.
- * Replaces src/q3_q4_linear.h:99-106 (src/q3_q4_linear.cu:149-228). */
+ * with `error` filled on any failure. Q4_K (12) and Q6_K (14) geometries
+ * both run, as in the reference (src/q3_q4_linear.cu:199-209), and so does
+ * a Q6_K geometry bound to the split device layout (SERA_QTYPE_Q6K_SPLIT,
+ * include/sera_q4k.h). Replaces src/q3_q4_linear.h:99-106
+ * (src/q3_q4_linear.cu:149-228). */
 bool q3_cuda_q4k_linear(const q3_q4_linear_geometry *geometry,
                         const void *weight,
                         const float *device_input,

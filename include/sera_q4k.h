@@ -191,9 +191,10 @@ const char *sera_q4k_last_error(void);
 
 /* Y = X . W^T through the MMVQ path (MMVQ arithmetic), 1 <= M <= 8: the
  * reference quantizes Q6_K decode activations with the same
- * quantize_row_q8_1_cuda call as Q4_K. Up to 4 tokens the dot4 MMVQ kernel
- * on the row stage, from 5 the fp16-MFMA tile kernel on a row-formula Q6_K
- * stage. Replaces q3_mmq_q6_K_dense_vec (cuda/q3_mmq.cu:515-519 over
+ * quantize_row_q8_1_cuda call as Q4_K. The dot4 MMVQ kernel on the row
+ * stage, or, where sera_q6k_vec_uses_tile says so (tall matrices from 4
+ * tokens, 4096-16383 rows from 6), the fp16-MFMA tile kernel on a
+ * row-formula Q6_K stage. Replaces q3_mmq_q6_K_dense_vec (cuda/q3_mmq.cu:515-519 over
  * q3_mmq_dense_vec_impl, :408-506). */
 int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
@@ -226,7 +227,7 @@ int sera_q6k_mmvq_rows_per_wave(int M, int N);
  * multiple of 32. sera_q8_1_quantize_row_q6k fills the same layout with the
  * row quantizer's values (cuda/mmq/quantize.cu:4-48, d8 = fp32(fp16 d)):
  * the MMVQ arithmetic on the tile kernel, which sera_q6k_dense_vec uses
- * from 5 tokens. */
+ * where sera_q6k_vec_uses_tile says so. */
 int sera_q8_1_q6k_mmq_padded_rows(int M);
 size_t sera_q8_1_q6k_mmq_stage_bytes(int M, int K);
 void sera_q8_1_q6k_mmq_stage_offsets(int M, int K, size_t *qs, size_t *d);
@@ -284,8 +285,11 @@ int sera_weight_upload(uint32_t qtype, int N, int K, const void *host_gguf, void
  *       quantize (no materialized op(X)).
  * All weights share K and qtype (geometries are q3_q4_linear_geometry*);
  * the activations are quantized once for the group (q/k/v and gate/up read
- * the same normed input), and at decode (Q4_K, M <= 4) the group runs as
- * one MMVQ launch. Arithmetic per product as q3_cuda_q4k_linear (MMVQ
+ * the same normed input). At decode (Q4_K, M <= 8) the matrices the dot4
+ * MMVQ kernel takes (sera_q4k_vec_uses_fewtok == 0) share one grouped
+ * launch and the others run the few-token kernel one by one; a Q6_K group
+ * shares one stage, so its largest matrix picks the kernel
+ * (sera_q6k_vec_uses_tile). Arithmetic per product as q3_cuda_q4k_linear (MMVQ
  * formula for M <= 8, MMQ above). gamma and X2 must be 16-byte aligned.
  * Uses the arena of sera_q4k_set_arena / q3_cuda_q4k_linear_set_workspace;
  * enqueue only. */

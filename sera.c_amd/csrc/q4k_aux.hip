@@ -17,7 +17,7 @@
  * All float arithmetic in this file is uncontracted (no fused multiply-add)
  * so that it rounds exactly like the expressions it restates.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 /* numpy add.reduce over 32 values: 0 + pairwise sum with 8 accumulators. */
 template <typename T>

@@ -44,7 +44,7 @@
  *     One launch, no workgroup waits on another, and results repeat bit for
  *     bit.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 typedef uint32_t ft_v4u __attribute__((ext_vector_type(4)));
 typedef float ft_v4f __attribute__((ext_vector_type(4)));
@@ -354,7 +354,6 @@ extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk) {
     return (nkb + c - 1) / c;
 }
 
-extern "C" int sera_mmq_padded_rows(int M);
 
 template <int NW, int TG, int FORM>
 static hipError_t launch_fewtok(const uint8_t *W, const int8_t *xq, const void *xsc, float *y, float *slots,

@@ -38,7 +38,7 @@
  *     split writes fp32 partials that a second kernel sums in a fixed order
  *     (deterministic, no atomics).
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) const void global_cvoid_t;
@@ -578,9 +578,6 @@ static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint3
 
 /* partial: M*N*splits floats of scratch when splits > 1 (M*N % 4 == 0);
  * accum != 0 adds the product to y. */
-extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, float *y, float *partial,
-                                              int M, int N, int K, int splits, int accum, hipStream_t s);
-
 extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
                                           int M, int N, int K, int splits, hipStream_t s) {
     return sera_launch_q4k_mmq_acc(W, stage, y, partial, M, N, K, splits, 0, s);
@@ -630,10 +627,6 @@ static hipError_t launch_mmq_streamk_cfg(const uint8_t *W, const int8_t *xq, con
  * workgroups the device keeps resident, and ntiles*K/256 >= P).
  * slots: 2*P*sera_mmq_slot_floats(M) floats; counters: sera_mmq_tiles(M,N)
  * ints, zero on entry and zero again on exit. */
-extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots,
-                                                      int *counters, int M, int N, int K, int P, int accum,
-                                                      hipStream_t s);
-
 extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots,
                                                   int *counters, int M, int N, int K, int P, hipStream_t s) {
     return sera_launch_q4k_mmq_streamk_acc(W, stage, y, slots, counters, M, N, K, P, 0, s);

@@ -27,7 +27,7 @@
  *     lanes with xor shuffles and summed across waves through LDS in a fixed
  *     order, so results repeat bit for bit.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 #define SERA_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */

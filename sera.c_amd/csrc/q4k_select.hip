@@ -29,7 +29,7 @@
  * float4; partial sums are reduced over the wave with xor shuffles in a fixed
  * order.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 #define SEL_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
 

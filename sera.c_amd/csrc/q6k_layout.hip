@@ -15,7 +15,7 @@
  * source is 2-byte aligned) and writes it with one 16-byte store; chunk 13
  * writes d. Memory-bound, one pass.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 /* src: GGUF blocks [first, first + count) of a matrix of `total` blocks,
  * back to back; dst: the whole matrix in the split layout. */

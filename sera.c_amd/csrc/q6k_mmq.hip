@@ -38,7 +38,7 @@
  *     rows (one 32 x 32 MFMA tile each), two workgroups per CU; split-K
  *     with a fixed-order reduce when tiles are few.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 typedef __attribute__((address_space(3))) void q6m_lds_void;
 typedef __attribute__((address_space(1))) const void q6m_global_cvoid;
@@ -348,10 +348,6 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             }
     }
 }
-
-extern "C" hipError_t sera_launch_splitk_reduce_acc(const float *partial, float *y, size_t n, int splits, int accum,
-                                                    hipStream_t s);
-
 
 /* K splits: double while the grid holds fewer than 1024 (tile, split)
  * workgroups (two resident per CU, two rounds on 256 CUs) and each split

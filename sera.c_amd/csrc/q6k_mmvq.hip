@@ -34,7 +34,7 @@
  * only, and slots a stage does not need are given an offset past the range
  * (they read zeros, no traffic).
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 typedef __attribute__((address_space(3))) void q6_lds_void;
 typedef unsigned q6_v4u __attribute__((ext_vector_type(4)));

@@ -36,7 +36,7 @@
  * pure additions in a fixed pairing, so they cannot be contracted or
  * reassociated by the compiler.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 
 /* 1 / sqrt(mean(x^2) + eps) of one row, computed by all 256 threads of the
  * workgroup (every thread returns the same value). */

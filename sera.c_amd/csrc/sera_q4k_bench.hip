@@ -7,29 +7,9 @@
  * working set larger than the 256 MB last-level (MALL) cache keeps every
  * weight read an HBM read.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 #include "../../include/q3_q4_linear.h"
 #include "../../include/sera_q4k.h"
-
-
-extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y, int M, int N,
-                                           int K, int rpw, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
-                                          int M, int N, int K, int splits, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots,
-                                                  int *counters, int M, int N, int K, int P, hipStream_t s);
-extern "C" int sera_mmq_slot_floats(int M);
-extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
-                                                 int *counters, int M, int N, int K, int chunk, int accum,
-                                                 hipStream_t s);
-extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk);
-extern "C" hipError_t sera_launch_q6k_mmvq(uint32_t qtype, const void *W, const void *stage, float *y, int M, int N,
-                                           int K, int rows, hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial,
-                                          int M, int N, int K, int splits, hipStream_t s);
-extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
-                                                   const uint32_t *ids, int branches, int per_branch,
-                                                   float *logits, hipStream_t s);
 
 /* `warmup` untimed then `iters` timed calls of q3_cuda_q4k_linear; weight i
  * of the call is weights[i % nweights]. elapsed_ms: first-to-last event of

@@ -8,76 +8,13 @@
  * attached once by the caller, every launch is enqueued on the caller's
  * stream, and timings are read only after the caller has synchronized.
  */
-#include "q4k_common.h"
+#include "sera_launch.h"
 #include "../../include/q3_q4_linear.h"
 #include "../../include/sera_q4k.h"
 
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
-
-extern "C" hipError_t sera_launch_q8_1_row(const float *x, int M, int K, void *stage, hipStream_t s);
-extern "C" hipError_t sera_launch_q8_1_mmq(const float *x, int M, int Mpad, int K, void *stage,
-                                           hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y, int M, int N,
-                                           int K, int rpw, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
-                                          int M, int N, int K, int splits, hipStream_t s);
-extern "C" int sera_mmvq_rows_per_wave(int N, int M);
-extern "C" hipError_t sera_launch_q6k_mmvq(uint32_t qtype, const void *W, const void *stage, float *y, int M, int N,
-                                           int K, int rows, hipStream_t s);
-extern "C" int sera_q6s_mmvq_rows(int N, int M);
-extern "C" hipError_t sera_launch_q6k_split(const void *src, void *dst, uint64_t first, uint64_t count,
-                                            uint64_t total, hipStream_t s);
-extern "C" int sera_q6k_mmvq_rows(int N, int M);
-extern "C" hipError_t sera_launch_q8_1_q6k_stage(const float *x, int M, int Mpad, int K, int row_formula,
-                                                 void *stage, hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial,
-                                          int M, int N, int K, int splits, hipStream_t s);
-extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
-extern "C" hipError_t sera_launch_q8_1_row_p(const float *x, const sera_producer *prod, int M, int K, void *stage,
-                                             hipStream_t s);
-extern "C" hipError_t sera_launch_q8_1_mmq_p(const float *x, const sera_producer *prod, int M, int Mpad, int K,
-                                             void *stage, hipStream_t s);
-extern "C" hipError_t sera_launch_q8_1_q6k_stage_p(const float *x, const sera_producer *prod, int M, int Mpad, int K,
-                                                   int row_formula, void *stage, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W, float *const *y, const int *N,
-                                                 const void *stage, int M, int K, int rows, int accum,
-                                                 hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, float *y, float *partial,
-                                              int M, int N, int K, int splits, int accum, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots,
-                                                      int *counters, int M, int N, int K, int P, int accum,
-                                                      hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmvq_acc(uint32_t qtype, const void *W, const void *stage, float *y, int M,
-                                               int N, int K, int rows, int accum, hipStream_t s);
-extern "C" hipError_t sera_launch_q6k_mmq_acc(uint32_t qtype, const void *W, const void *stage, float *y,
-                                              float *partial, int M, int N, int K, int splits, int accum,
-                                              hipStream_t s);
-extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
-                                                   const uint32_t *ids, int branches, int per_branch,
-                                                   float *logits, hipStream_t s);
-extern "C" hipError_t sera_launch_embedding(int qtype, const void *W, int N, int K, const uint32_t *ids, int tokens,
-                                            float *hidden, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
-                                                 int *counters, int M, int N, int K, int chunk, int accum,
-                                                 hipStream_t s);
-extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk);
-extern "C" int sera_fewtok_max_chunk(int M);
-extern "C" int sera_fewtok_groups(int M, int N, int K);
-extern "C" int sera_mmq_splits(int M, int N, int K);
-extern "C" int sera_mmq_padded_rows(int M);
-extern "C" int sera_mmq_tiles(int M, int N);
-extern "C" int sera_mmq_slot_floats(int M);
-extern "C" int sera_mmq_wgs_per_cu(int M);
-extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots,
-                                                  int *counters, int M, int N, int K, int P, hipStream_t s);
-extern "C" int sera_mmq_bm(int M);
-extern "C" hipError_t sera_launch_q4k_quantize(const float *x, int64_t rows, int64_t K, void *out,
-                                               hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_dequant(const void *W, int64_t nblocks, float *out, hipStream_t s);
-extern "C" hipError_t sera_launch_q4k_subblock_dots(const void *W, const int8_t *xq, int32_t *I, int M,
-                                                    int N, int K, hipStream_t s);
 
 namespace {
 
@@ -517,8 +454,6 @@ extern "C" int sera_q6k_vec_uses_tile(int M, int N, int K) {
     if (N >= 4096) return M >= 6;
     return 0;
 }
-
-extern "C" int sera_q6k_mmq_splits(int M, int N, int K);
 
 extern "C" int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
                                   void *stream, int timed) {

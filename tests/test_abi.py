@@ -47,7 +47,7 @@ def test_struct_layouts_match_reference():
     (12, 5120, 25600, 73_728_000),     # gate/up
     (12, 25600, 5120, 73_728_000),     # down
     (12, 5120, 151936, 437_575_680),   # LM head
-    (14, 5120, 1024, 1024 * 20 * 210), # Q6_K geometry is bound (kernel path is Q4_K only)
+    (14, 5120, 1024, 1024 * 20 * 210), # Q6_K: 210-byte blocks, run by the same call
 ])
 def test_bind_geometry(qtype, dim0, dim1, wbytes):
     g = q3q4.bind_geometry(qtype, dim0, dim1)

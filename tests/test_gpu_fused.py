@@ -146,3 +146,69 @@ def test_silu_mul_producer_with_residual(torch, linear, qtype, M):
     y = run_group(torch, qtype, [W], [N], K, g, flags=q3q4.LIN_SILU_MUL | q3q4.LIN_ACCUMULATE, x2=u, y0=[y0])[0]
     ref = path_oracle(qtype, W, oracle.silu_mul(g, u), N, K)
     check_close(y - y0, ref, "silu*up product")
+
+
+@pytest.mark.parametrize("M,Ns", [(3, [16384, 1024]), (5, [4096, 1024, 256]), (8, [4096, 1024])])
+def test_q4k_group_mixes_grouped_dot4_and_fewtok(torch, linear, M, Ns):
+    """A Q4_K group at decode whose matrices split between the kernels: the
+    ones dot4 takes share one grouped launch, the tall ones run the
+    few-token kernel one by one (split K through the shared arena slots).
+    Products against the MMVQ-formula oracle, accumulate bit-identical to
+    product + add."""
+    K = 4096
+    L = q3q4.load()
+    kinds = [bool(L.sera_q4k_vec_uses_fewtok(M, n, K)) for n in Ns]
+    say(f"case mixed q4k group M={M} Ns={Ns} fewtok={kinds}")
+    assert any(kinds) and not all(kinds), "case meant to mix the two kernels"
+    assert all(q3q4.fewtok_splits(M, n, K) > 1 for n, f in zip(Ns, kinds) if f), "case meant to split K"
+    rng = np.random.default_rng(500 + M)
+    Ws = [weights(rng, 12, n, K) for n in Ns]
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    ys = run_group(torch, 12, Ws, Ns, K, x)
+    for i, n in enumerate(Ns):
+        idx = np.sort(rng.choice(n, min(n, 256), replace=False))
+        check_close(ys[i][:, idx], oracle.linear_reference(Ws[i][idx], x, len(idx), K), f"group[{i}] N={n}")
+    y0 = [rng.standard_normal((M, n)).astype(np.float32) for n in Ns]
+    ya = run_group(torch, 12, Ws, Ns, K, x, flags=q3q4.LIN_ACCUMULATE, y0=y0)
+    for i in range(len(Ns)):
+        assert np.array_equal(ya[i].view(np.uint32), (y0[i] + ys[i]).astype(np.float32).view(np.uint32)), i
+
+
+@pytest.mark.parametrize("M", [6, 8])
+def test_q6k_group_on_the_tile_branch(torch, linear, M):
+    """A Q6_K group whose largest matrix has 4096+ rows at 6-8 tokens: the
+    whole group runs the tile kernel on one row-formula stage. Products
+    against the oracle and accumulate bit-identical to product + add; the
+    RMSNorm producer bit-identical to the unfused group on the oracle's
+    norm; the SiLU*up producer within tolerance of the oracle."""
+    K = 2048
+    Ns = [4096, 1024]
+    L = q3q4.load()
+    assert L.sera_q6k_vec_uses_tile(M, max(Ns), K)
+    say(f"case q6k group tile branch M={M} Ns={Ns}")
+    rng = np.random.default_rng(600 + M)
+    Ws = [weights(rng, 14, n, K) for n in Ns]
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    ys = run_group(torch, 14, Ws, Ns, K, x)
+    for i, n in enumerate(Ns):
+        idx = np.sort(rng.choice(n, 256, replace=False))
+        check_close(ys[i][:, idx], oracle.linear_reference_q6k(np.ascontiguousarray(Ws[i][idx]), x, 256, K),
+                    f"group[{i}] N={n}")
+    y0 = [rng.standard_normal((M, n)).astype(np.float32) for n in Ns]
+    ya = run_group(torch, 14, Ws, Ns, K, x, flags=q3q4.LIN_ACCUMULATE, y0=y0)
+    for i in range(len(Ns)):
+        assert np.array_equal(ya[i].view(np.uint32), (y0[i] + ys[i]).astype(np.float32).view(np.uint32)), i
+    h = (rng.standard_normal((M, K)) * 2.5).astype(np.float32)
+    gamma = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    fused = run_group(torch, 14, Ws, Ns, K, h, flags=q3q4.LIN_RMSNORM, gamma=gamma, eps=1e-6)
+    plain = run_group(torch, 14, Ws, Ns, K, oracle.rmsnorm_fused_order(h, gamma, 1e-6))
+    for i in range(len(Ns)):
+        assert np.array_equal(fused[i].view(np.uint32), plain[i].view(np.uint32)), i
+    g = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    u = rng.standard_normal((M, K)).astype(np.float32)
+    ysil = run_group(torch, 14, Ws, Ns, K, g, flags=q3q4.LIN_SILU_MUL, x2=u)
+    xs = oracle.silu_mul(g, u)
+    for i, n in enumerate(Ns):
+        idx = np.sort(rng.choice(n, 256, replace=False))
+        check_close(ysil[i][:, idx], oracle.linear_reference_q6k(np.ascontiguousarray(Ws[i][idx]), xs, 256, K),
+                    f"silu group[{i}] N={n}")

@@ -56,22 +56,45 @@ def call(torch, geo, W, x, y):
     assert ok, err.value.decode()
 
 
-# (qtype, M, N, K): MMVQ, the few-token kernel with in-kernel split-K (both
-# formulas), stream-K, split-K + reduce; Q6_K MMVQ and its tile kernel
+def kernel_of(qtype, M, N, K):
+    """The kernel the boundary runs for this call, from the library's own
+    dispatch queries."""
+    L = q3q4.load()
+    if qtype == q3q4.QTYPE_Q4_K:
+        if M <= 8:
+            return "fewtok" if L.sera_q4k_vec_uses_fewtok(M, N, K) else "dot4"
+        if M <= 9:
+            return "fewtok-mmq"
+        return "mmq-streamk" if L.sera_q4k_mmq_schedule(M, N, K) == 1 else "mmq"
+    return "q6k-tile" if M > 8 or L.sera_q6k_vec_uses_tile(M, N, K) else "q6k-mmvq"
+
+
+# (qtype, M, N, K, kernel): dot4 MMVQ; the few-token kernel with in-kernel
+# split K on the row stage (form 0: a 4096-row matrix from 5 tokens, a tall
+# one from 3) and on the MMQ stage (form 1, 9 tokens); the paired MMQ tile
+# with split-K + reduce; stream-K; the 64-token tile with split-K + reduce;
+# Q6_K MMVQ and the Q6_K tile kernel on the row-formula stage
 CASES = [
-    (12, 1, 4096, 5120),
-    (12, 6, 2048, 5120),
-    (12, 10, 1000, 2560),
-    (12, 64, 16384, 2048),
-    (12, 100, 4096, 5120),
-    (14, 1, 2048, 5120),
-    (14, 8, 2048, 5120),
+    (12, 1, 4096, 5120, "dot4"),
+    (12, 6, 2048, 5120, "dot4"),
+    (12, 8, 4096, 5120, "fewtok"),
+    (12, 3, 16384, 5120, "fewtok"),
+    (12, 9, 1000, 25600, "fewtok-mmq"),
+    (12, 10, 1000, 2560, "mmq"),
+    (12, 64, 16384, 2048, "mmq-streamk"),
+    (12, 100, 4096, 5120, "mmq"),
+    (14, 1, 2048, 5120, "q6k-mmvq"),
+    (14, 8, 2048, 5120, "q6k-mmvq"),
+    (14, 8, 4096, 5120, "q6k-tile"),
 ]
 
 
-@pytest.mark.parametrize("qtype,M,N,K", CASES)
-def test_graph_replay_matches_eager(torch, linear, qtype, M, N, K):
-    say(f"case graph qtype={qtype} M={M} N={N} K={K} path={q3q4.load().q3_cuda_q4k_linear_path_for_batch(M)}")
+@pytest.mark.parametrize("qtype,M,N,K,kernel", CASES)
+def test_graph_replay_matches_eager(torch, linear, qtype, M, N, K, kernel):
+    say(f"case graph qtype={qtype} M={M} N={N} K={K} kernel={kernel}")
+    assert kernel_of(qtype, M, N, K) == kernel, "dispatch moved: choose a case that reaches this kernel"
+    if kernel.startswith("fewtok"):
+        assert q3q4.fewtok_splits(M, N, K) > 1, "case meant to split K inside the few-token kernel"
     rng = np.random.default_rng(1000 * M + qtype)
     Wd = torch.from_numpy(weights(rng, qtype, N, K)).cuda()
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()

@@ -270,6 +270,40 @@ def test_split_linear_boundary(torch, linear, M):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N", [(4, 16384), (6, 4096), (8, 5120), (4, 4096)])
+def test_q6k_boundary_tile_branch_of_mmvq_path(torch, linear, M, N):
+    """q3_cuda_q4k_linear on Q6_K matrices of 4096+ rows at 4-8 tokens, where
+    sera_q6k_dense_vec may run the tile kernel on a row-formula stage (stage
+    sized from the padded batch, split partials in the arena): sampled rows
+    within 1e-3 * rms of the MMVQ-formula oracle, the split layout
+    bit-identical to the GGUF bytes whenever the tile kernel runs, and the
+    launch count the stats report equal to sera_q6k_kernel_launches."""
+    L = q3q4.load()
+    K = 5120
+    tile = bool(L.sera_q6k_vec_uses_tile(M, N, K))
+    say(f"case q6k boundary M={M} N={N} K={K} tile={tile} launches={L.sera_q6k_kernel_launches(M, N, K)}")
+    if (M, N) != (4, 4096):
+        assert tile, "case meant for the tile branch"
+    rng = np.random.default_rng(70 * M + N)
+    W = oracle.q6k_weights(rng, N, K)
+    xh = outlier_activations(rng, M, K)
+    x = dev(torch, xh)
+    outs = {}
+    for qt, Wx in ((14, dev(torch, W)), (SPLIT, to_split(torch, W, N, K))):
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        st = linear(q3q4.bind_geometry(qt, K, N), Wx, x, y)
+        torch.cuda.synchronize()
+        assert st.kernel_launches == L.sera_q6k_kernel_launches(M, N, K)
+        outs[qt] = y.cpu().numpy()
+        del Wx
+    rows = np.sort(rng.choice(N, 256, replace=False))
+    ref = oracle.linear_reference_q6k(np.ascontiguousarray(W[rows]), xh, len(rows), K)
+    for qt, y in outs.items():
+        check_close(y[:, rows], ref, f"q6k boundary qtype={qt} M={M} N={N}")
+    if tile:
+        assert np.array_equal(outs[14].view(np.uint32), outs[SPLIT].view(np.uint32))
+
+
 @pytest.mark.parametrize("M", [1, 3, 6, 40])
 def test_split_linear_group_accumulate(torch, linear, M):
     K = 2048

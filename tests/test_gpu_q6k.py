@@ -123,7 +123,8 @@ def test_q8_row_q6k_stage_bit_exact(torch, M, K):
 @pytest.mark.parametrize("N,K", [(256, 256), (515, 5120), (64, 25600), (203, 2304)])
 def test_q6k_tile_kernel_mmvq_formula_parity(torch, N, K):
     """The tile kernel on a row-formula stage computes the MMVQ formula
-    (what sera_q6k_dense_vec runs for 5..8 tokens)."""
+    (what sera_q6k_dense_vec runs at 4-8 tokens where
+    sera_q6k_vec_uses_tile says so)."""
     rng = np.random.default_rng(N * 7 + K)
     W = q6k_weights_with_edges(rng, N, K)
     Wd = dev(torch, W)

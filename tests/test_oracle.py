@@ -283,6 +283,26 @@ def test_subblock_dot_extreme_is_closed_form():
     assert np.all(I[0] == 60960) and np.all(I[1] == -60960)
 
 
+def test_q8_sums_brute_force():
+    """orc_q8_sums: S[m][b] = sum of the 32 quants of block b of row m (the
+    dp4a against 0x01010101 of vecdotq.cuh:517, kept per block in the MMVQ
+    stage as d8*S). Python integer loops on a ragged-looking input, plus
+    the extremes +-32*127 and a block whose sum is zero only over the whole
+    32 (a 16-wide or shifted block would not be)."""
+    M, K = 3, 512
+    xq = RNG.integers(-127, 128, (M, K)).astype(np.int8)
+    xq[1, 0:32] = 127
+    xq[1, 32:64] = -127
+    xq[2, 64:96] = np.repeat(np.array([5, -5], np.int8), 16)
+    got = oracle.q8_sums(xq)
+    assert got.shape == (M, K // 32) and got.dtype == np.int32
+    for m in range(M):
+        for b in range(K // 32):
+            assert got[m, b] == sum(int(v) for v in xq[m, 32 * b:32 * b + 32]), (m, b)
+    assert got[1, 0] == 4064 and got[1, 1] == -4064
+    assert got[2, 2] == 0 and int(xq[2, 64:80].astype(np.int32).sum()) == 80
+
+
 def _exact_case(M, N, K, balanced_sums):
     """Weights with d = 2^-8, dmin = 2^-9 and activations x = q * 2^-5 with a
     +-127 in every 32-block: every weight, every Q8_1 value and every product
