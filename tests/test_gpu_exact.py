@@ -214,7 +214,7 @@ def test_mmq_exact_plain_and_splitk(torch, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K,wgs", [(1, 700, 5120, 8), (16, 512, 5120, 24), (20, 300, 2304, 8),
-                                       (32, 640, 1024, 16), (100, 256, 2048, 8), (200, 640, 1024, 40)])
+                                       (32, 640, 1024, 8), (100, 256, 2048, 8), (200, 640, 1024, 40)])
 def test_mmq_exact_streamk(torch, M, N, K, wgs):
     rng = np.random.default_rng(M * 11 + N + K + wgs)
     W, X = exact_inputs(rng, M, N, K)
