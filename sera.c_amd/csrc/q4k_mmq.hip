@@ -15,10 +15,15 @@
  *     columns = weight rows), so in the 32x32 result each lane owns one
  *     weight row: its sub-block scale fp16(d*sc_b) is a per-lane value the
  *     lane decodes from the block header it loaded itself, and the token
- *     scales d8 come from LDS as float4s. The fp32 epilogue per element is
- *     cvt + mul + fma on the VALU (measured faster on gfx950 than moving the
- *     scale products onto the matrix unit, which the VALU overlaps only in
- *     part).
+ *     scales d8 come from LDS as float4s.
+ *   - the fp32 epilogue is two VALU ops per element and sub-block, with no
+ *     int-to-float convert: the MFMA's int32 accumulator starts at the bit
+ *     pattern of 1.5 * 2^23, so its result, read as a float, is exactly
+ *     1.5 * 2^23 + I (|I| <= 32*15*127 < 2^22 keeps the exponent fixed);
+ *     t = fma(F, sw, -1.5 * 2^23 * sw) is then I * sw rounded once (the
+ *     offset product is exact: sw is an fp16 value), and acc = fma(t, d8,
+ *     acc). The reference rounds sw * d8 first and multiplies by I; both are
+ *     single fp32 roundings of the same exact products.
  *   - the min term is a plain matrix product over the sub-block index,
  *     [tokens x 8] fp16 s8 times [8 x rows] fp16(-dmin*m_b), done once per
  *     super-block by one v_mfma_f32_32x32x16_f16 accumulating into the same
@@ -57,6 +62,24 @@ struct alignas(16) MmqSmem {
     alignas(16) _Float16 s8[2][BM][8];       /* fp16 s8, [token][sub-block] */
     alignas(16) _Float16 zero8[8];           /* a zero min-term operand */
 };
+
+/* The int32 accumulator seed whose result reads as the float 1.5 * 2^23 + I.
+ * Built from an opaque register so that the compiler keeps one copy live for
+ * every MFMA instead of rematerializing sixteen moves per use. */
+#define SERA_MAGIC_BITS 0x4B400000
+#define SERA_MAGIC_F 12582912.0f
+__device__ __forceinline__ v16i magic_seed() {
+    int m = SERA_MAGIC_BITS;
+    __asm__ volatile("" : "+v"(m));
+    v16i v;
+#pragma unroll
+    for (int r = 0; r < 16; r++) v[r] = m;
+    return v;
+}
+
+/* I * sw rounded once, from F = 1.5 * 2^23 + I (the magic-seeded MFMA
+ * result) and nsw = -1.5 * 2^23 * sw (exact). */
+__device__ __forceinline__ float scaled_dot(int F, float sw, float nsw) { return fmaf(__int_as_float(F), sw, nsw); }
 
 /* Tile order: consecutive workgroup ids go to consecutive XCDs (8 on
  * MI355X). Give each XCD a contiguous run of tiles, token tiles fastest,
@@ -211,6 +234,15 @@ __device__ __forceinline__ void mmq_segment(
             for (int j2 = 0; j2 < 4; j2++) q[nt][j2] = *(const v4u *)(b + 16 + 32 * j2 + 16 * h);
         }
     };
+    auto load_hdr = [&](int kb, v4u *hdr) {
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) hdr[nt] = *(const v4u *)(wbase[nt] + (size_t)kb * Q4K_BLOCK_BYTES);
+    };
+    auto load_piece = [&](int kb, int j2, v4u *q) {
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+            q[nt] = *(const v4u *)(wbase[nt] + (size_t)kb * Q4K_BLOCK_BYTES + 16 + 32 * j2 + 16 * h);
+    };
 
 #pragma unroll
     for (int t = 0; t < TT; t++)
@@ -219,6 +251,7 @@ __device__ __forceinline__ void mmq_segment(
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[t][nt][r] = 0.0f;
 
+    const v16i magic = magic_seed();
     v4u dr = {};
     v4u hdr[2] = {}, qw[2][4];
     /* AHEAD (one token tile per wave at 2 waves per SIMD leaves registers for
@@ -227,6 +260,14 @@ __device__ __forceinline__ void mmq_segment(
      * step's barrier. */
     constexpr bool kWeightsAhead = AHEAD;
     v4u hdrn[2] = {}, qwn[2][4];
+    /* Otherwise (PR = 0) the next step's weights come in piece by piece as
+     * this step frees their registers: its header as soon as the scales are
+     * decoded, piece 0 into a spare set at once, piece j2 + 1 into the
+     * registers of piece j2 when sub-block 2 * j2 + 2 starts (pieces j2 feed
+     * sub-blocks 2 * j2 and 2 * j2 + 1). Every load then has at least two
+     * sub-blocks of compute to land in; the sets rotate at the step's end. */
+    constexpr bool kProgressive = !AHEAD && !PR;
+    v4u spare[2] = {};
 
     /* zero8 is the min-term A operand of the lanes (h = 1) whose k
      * positions carry no sub-block */
@@ -263,6 +304,13 @@ __device__ __forceinline__ void mmq_segment(
                 bmin[nt][2 * p + 1] = mw[p].y;
             }
         }
+        /* the next step's super-block; the last step reloads its own (in
+         * bounds, unused), which keeps the prefetch free of branches */
+        const int kb_next = more ? kb_begin + it + 1 : kb_begin + it;
+        if constexpr (kProgressive) {
+            load_hdr(kb_next, hdr);
+            load_piece(kb_next, 0, spare);
+        }
 
         if constexpr (PR) {
             const int sh = l32 >> 4;            /* this A row's sub-block of the pair */
@@ -270,13 +318,15 @@ __device__ __forceinline__ void mmq_segment(
 #pragma unroll
             for (int p = 0; p < 4; p++) {
                 v4i B0[2], B1[2];
-                float swa[2], swbb[2];
+                float swa[2], swbb[2], nswa[2], nswbb[2];
 #pragma unroll
                 for (int nt = 0; nt < 2; nt++) {
                     B0[nt] = unpack_nib(qw[nt][p], h);
                     B1[nt] = unpack_nib(qw[nt][p], 1 - h);
                     swa[nt] = (float)sw[nt][p].x;
                     swbb[nt] = (float)sw[nt][p].y;
+                    nswa[nt] = -SERA_MAGIC_F * swa[nt];
+                    nswbb[nt] = -SERA_MAGIC_F * swbb[nt];
                 }
                 const void *real = &sm.xs[buf][t][16 * ((4 * p + 2 * sh + h) ^ t)];
                 const v4i A0 = *(const v4i *)(h == sh ? real : (const void *)&sm.zero8[0]);
@@ -289,28 +339,48 @@ __device__ __forceinline__ void mmq_segment(
                 }
 #pragma unroll
                 for (int nt = 0; nt < 2; nt++) {
-                    const v16i zero = {};
-                    v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0[nt], zero, 0, 0, 0);
-                    I = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1[nt], I, 0, 0, 0);
+                    v16i F = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0[nt], magic, 0, 0, 0);
+                    F = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1[nt], F, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        acc[0][nt][r] = fmaf((float)I[r], d8v[r] * (r < 8 ? swa[nt] : swbb[nt]), acc[0][nt][r]);
+                    for (int r = 0; r < 16; r++) {
+                        const float t = r < 8 ? scaled_dot(F[r], swa[nt], nswa[nt])
+                                              : scaled_dot(F[r], swbb[nt], nswbb[nt]);
+                        acc[0][nt][r] = fmaf(t, d8v[r], acc[0][nt][r]);
+                    }
                 }
             }
         }
-#pragma unroll
-        for (int b = 0; b < (PR ? 0 : 8); b++) {
-            v4i Bw[2];
-            float swb[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                Bw[nt] = unpack_nib(qw[nt][b >> 1], b & 1);
-                swb[nt] = (float)((b & 1) ? sw[nt][b >> 1].y : sw[nt][b >> 1].x);
-            }
-#pragma unroll
-            for (int t = 0; t < TT; t++) {
+        if constexpr (!PR) {
+            /* The 16 * TT MFMAs of the step in order (sub-block b, token tile
+             * t, weight tile nt; nt fastest), software pipelined: MFMA i + 1
+             * is issued before the epilogue of MFMA i, so the matrix unit
+             * runs while the VALU consumes the previous result. */
+            constexpr int NI = 8 * TT * 2;
+            auto a_of = [&](int b, int t) -> v4i {
                 const int tok = BMW * wt + 32 * t + l32;
-                const v4i A = *(const v4i *)&sm.xs[buf][tok][16 * ((2 * b + h) ^ (tok & 15))];
+                return *(const v4i *)&sm.xs[buf][tok][16 * ((2 * b + h) ^ (tok & 15))];
+            };
+            auto mfma_of = [&](int i) -> v16i {
+                const int b = i / (2 * TT), t = (i >> 1) % TT, nt = i & 1;
+                return __builtin_amdgcn_mfma_i32_32x32x32_i8(a_of(b, t), unpack_nib(qw[nt][b >> 1], b & 1), magic, 0,
+                                                             0, 0);
+            };
+            v16i Fc = mfma_of(0);
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int b = i / (2 * TT), t = (i >> 1) % TT, nt = i & 1;
+                if constexpr (kProgressive) {
+                    if (i % (2 * TT) == 0 && b >= 2 && (b & 1) == 0) {
+                        v4u nq[2];
+                        load_piece(kb_next, b >> 1, nq);
+                        qw[0][(b >> 1) - 1] = nq[0];
+                        qw[1][(b >> 1) - 1] = nq[1];
+                    }
+                }
+                v16i Fn = {};
+                if (i + 1 < NI) Fn = mfma_of(i + 1);
+                const float swb = (float)((b & 1) ? sw[nt][b >> 1].y : sw[nt][b >> 1].x);
+                const float nswb = -SERA_MAGIC_F * swb;
                 float d8v[16];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -318,13 +388,9 @@ __device__ __forceinline__ void mmq_segment(
                     d8v[4 * q] = f4.x; d8v[4 * q + 1] = f4.y; d8v[4 * q + 2] = f4.z; d8v[4 * q + 3] = f4.w;
                 }
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    const v16i zero = {};
-                    const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bw[nt], zero, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        acc[t][nt][r] = fmaf((float)I[r], d8v[r] * swb[nt], acc[t][nt][r]);
-                }
+                for (int r = 0; r < 16; r++)
+                    acc[t][nt][r] = fmaf(scaled_dot(Fc[r], swb, nswb), d8v[r], acc[t][nt][r]);
+                Fc = Fn;
             }
         }
         /* min term of this super-block */
@@ -339,7 +405,7 @@ __device__ __forceinline__ void mmq_segment(
                 acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as8, bmin[nt], acc[t][nt], 0, 0, 0);
         }
         if (more) {
-            if constexpr (!kWeightsAhead) load_w(kb_begin + it + 1, hdr, qw);
+            if constexpr (!kWeightsAhead && !kProgressive) load_w(kb_begin + it + 1, hdr, qw);
             store_x(buf ^ 1, dr);
         }
         __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads to LDS have landed */
@@ -350,6 +416,16 @@ __device__ __forceinline__ void mmq_segment(
                 hdr[nt] = hdrn[nt];
 #pragma unroll
                 for (int j2 = 0; j2 < 4; j2++) qw[nt][j2] = qwn[nt][j2];
+            }
+        }
+        if constexpr (kProgressive) {
+            /* pieces 1-3 of the next step sit in the sets of pieces 0-2 */
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                qw[nt][3] = qw[nt][2];
+                qw[nt][2] = qw[nt][1];
+                qw[nt][1] = qw[nt][0];
+                qw[nt][0] = spare[nt];
             }
         }
     }
@@ -528,9 +604,12 @@ extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, 
 }
 
 /* Token-tile width of the workgroup for M tokens: 16 (the paired tile, one
- * per wave), 32 (one token tile per wave, 4 waves along weight rows,
- * registers cut for 3 waves per SIMD) or 64 (two per wave, 2 waves per
- * SIMD); all tiles span 256 weight rows. Measured on MI355X against 128 x
+ * per wave), 32 (one token tile per wave, 4 waves along weight rows) or 64
+ * (two per wave); all at 2 waves per SIMD, and all tiles span 256 weight
+ * rows. The 32-token tile ran at 3 waves per SIMD until the magic-seeded
+ * epilogue: its 16 seed registers made that budget spill (37 -> 52 us on
+ * gate/up at 32 tokens), while at 2 waves with the next step's weights
+ * issued ahead it measures 37 us. Measured on MI355X against 128 x
  * 128 tiles: the 64 x 256 tile under the stream-K schedule is the fastest at
  * 512 tokens for both the 5120 -> 25600 and the 25600 -> 5120 shapes. */
 extern "C" int sera_mmq_bm(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : 64; }
@@ -594,7 +673,7 @@ extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, 
     if (sera_mmq_bm(M) == 16)
         return launch_mmq_cfg<1, 1, 4, 2, 1>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
     if (sera_mmq_bm(M) == 32)
-        return launch_mmq_cfg<1, 1, 4, 3>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
+        return launch_mmq_cfg<1, 1, 4, 2>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
     return launch_mmq_cfg<2, 1, 4, 2>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
 }
 
