@@ -19,13 +19,17 @@ Also printed in the same JSON line:
   cpu_baseline  the reference's CPU path on this host: Q4_K dequant with the
                 reference's q3_quant.c (oracle/_ref, single thread) plus
                 numpy fp32 matmul, on the full gate/up matrix at M=1
-  results       MMVQ sweep M in {1,2,4,8} x {gate/up, down}; MMQ at M=512 on
-                gate/up in int8 TOPS against 5.0 POPS; Q6_K (GGUF type 14)
-                through the same ABI on the 25600 -> 5120 down shape (a Q6_K
-                tensor in stock Q4_K_M files): M in {1,4,8} and M=512; with --full also
-                configs 3-5 (all seven projections, M=2048 + LM head, the
-                64-layer decode stream)
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--full] [--no-cpu]
+  results       every BASELINE configuration, each with its kernel's fraction
+                of the bound that limits it (HBM 8 TB/s or int8 MFMA 5.0 POPS):
+                config 1 (q_proj 8192x5120, M=1), config 2 (MMVQ sweep M in
+                {1,2,4,8} x {gate/up, down}), config 3 (all seven projections
+                at M=512), config 4 (gate/up and down at M=2048, the LM head
+                151936x5120 at M=16), config 5 (the 64-layer decode stream,
+                449 calls per token, plain, graph-replayed and fused); plus
+                9-16 token MMQ-path cases, the selected-row LM head and Q6_K
+                (GGUF type 14) through the same ABI on the 25600 -> 5120 down
+                shape and the LM head
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
 import argparse
 import ctypes
@@ -70,7 +74,7 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=8)
-    ap.add_argument("--full", action="store_true")
+    ap.add_argument("--full", action="store_true", help="accepted for compatibility: every config runs by default")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true",
                     help="headline only (gate/up M=1): for counter-collection runs")
@@ -211,6 +215,31 @@ def main():
                 headline = (row, step_ms, b)
     results["mmvq_sweep"] = sweep
 
+    # ---------------- config 1: q_proj 8192 x 5120 at M=1 ------------------
+    if not args.quick:
+        N, K = SHAPES["q"]
+        ncopy = 16   # 377 MB, more than the 256 MB last-level cache
+        qws, qarr = weight_set(N, K, 200, ncopy)
+        geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+        x = activations(1, K, 11)
+        y = torch.empty((1, N), dtype=torch.float32, device=dev)
+        step_ms = bench_linear(geo, qarr, ncopy, x, y, args.warmup, args.steps)
+        stage = torch.empty(q3q4.row_stage_layout(1, K)["total"], dtype=torch.uint8, device=dev)
+        q3q4.quantize_row(x, stage)
+        kavg, _ = bench_kernel(0, qarr, ncopy, stage, y, None, 1, N, K, 0, args.warmup, args.steps)
+        b = alg_bytes(1, N, K)
+        row = {"proj": "q", "M": 1, "N": N, "K": K,
+               "kernel": f"sera_q4k_mmvq_kernel<1, {L.sera_q4k_mmvq_rows_per_tile(1, N, K)}, {mmvq_waves(1, K)}>",
+               "step_us": round(step_ms * 1e3, 3), "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),
+               "kernel_us": round(kavg * 1e3, 3), "kernel_GBps": round(b / (kavg * 1e-3) / 1e9, 1),
+               "kernel_frac_hbm": round(b / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "weight_copies": ncopy}
+        log(f"[bench] config 1 q_proj M=1: step {row['step_us']} us, kernel {row['kernel_us']} us "
+            f"({100 * row['kernel_frac_hbm']:.1f}% of HBM)")
+        results["config1_q_proj_m1"] = row
+        del qws, qarr
+        torch.cuda.empty_cache()
+
     # ---------------- config 3 (gate/up only unless --full): MMQ M=512 -----
     FEWTOK_MMQ_MAX_BATCH = 9    # the MMQ path runs the few-token kernel (MMQ formula) up to here
 
@@ -262,11 +291,14 @@ def main():
         results["q6k"] = q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel,
                                         args)
 
-    if args.full:
+    if not args.quick:
         full = []
-        for name in ("q", "k", "v", "o", "down"):
+        for name in ("q", "k", "v", "o", "gate", "up", "down"):
             N, K = SHAPES[name]
-            ws, arr = (sets["down"][2] if name == "down" else weight_set(N, K, 300, 2))
+            if name == "gate":
+                full.append(results["mmq_m512_gate"])
+                continue
+            ws, arr = (sets["down"][2] if name == "down" else weight_set(N, K, 300 + len(full), 2))
             full.append(mmq_case(name, N, K, 512, arr, len(ws), 20))
         results["config3_m512"] = full
         results["config4_m2048"] = [mmq_case("gate_up", gN, gK, 2048, garr, args.copies, 5),
@@ -280,7 +312,10 @@ def main():
                                      mmq_case("down", 5120, 25600, 12, sets["down"][2][1], args.copies, 20),
                                      mmq_case("down", 5120, 25600, 16, sets["down"][2][1], args.copies, 20)]
         lmw, lmarr = weight_set(151936, 5120, 500, 1)
-        results["config4_lm_head_m16"] = mmq_case("lm_head", 151936, 5120, 16, lmarr, 1, 20)
+        lm = mmq_case("lm_head", 151936, 5120, 16, lmarr, 1, 20)
+        # at 16 tokens the LM head is bound by its 437 MB of weights
+        lm["kernel_frac_hbm"] = round(lm["kernel_GBps"] / HBM_PEAK_GBS, 4)
+        results["config4_lm_head_m16"] = lm
         del lmw
         results["config5_decode_stream"] = decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr)
 
