@@ -65,6 +65,24 @@ int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
 int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
 
+/* The MMVQ path of sera_q4k_dense_vec, allocating nothing and needing no
+ * attached workspace. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory or attach a workspace (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).
+ * Its scratch (row-group counters, the Q8_1 row stage, the few-token
+ * kernel's split slots) is a static device array of
+ * SERA_Q4K_STATIC_SCRATCH_BYTES that every GPU the library runs on holds
+ * until the process ends; sera_q4k_init sets it up for its device, and
+ * otherwise the first call on a device does (enqueueing a small clearing
+ * kernel on `stream`). Shapes needing more scratch than that
+ * (sera_q4k_dense_vec_static_bytes) are rejected with -1 and a message.
+ * Same arithmetic, kernels and results as sera_q4k_dense_vec; enqueue only,
+ * no timings. All calls on one GPU share its scratch: calls that overlap on
+ * one GPU (concurrent streams or threads) race. */
+#define SERA_Q4K_STATIC_SCRATCH_BYTES ((size_t)8 << 20)
+int sera_q4k_dense_vec_static(const void *W, const float *X, float *Y, int M, int N, int K, void *stream);
+size_t sera_q4k_dense_vec_static_bytes(int M, int N, int K);   /* 0 for a bad shape */
+
 /* Kernel launches (quantize + matmul + split-K reduce if any) one dense or
  * dense_vec call makes for this shape; 0 for an invalid shape. */
 int sera_q4k_kernel_launches(int M, int N, int K);

@@ -108,6 +108,41 @@ void record(hipEvent_t e, hipStream_t s) {
 
 extern "C" const char *sera_q4k_last_error(void) { return g_err; }
 
+/* ---- the decode path on a library-owned static scratch ------------------
+ * sera_q4k_dense_vec_static keeps its scratch (row-regime counters, the
+ * Q8_1 row stage, the few-token kernel's split slots) in this file-scope
+ * device array instead of the caller's workspace. Every GPU the library
+ * runs on holds its own copy until the process ends; host code never uses
+ * the name `scratch` itself (on the host it is a stand-in, not a device
+ * address), only the per-device address hipGetSymbolAddress returns. */
+static __device__ __align__(256) unsigned char scratch[SERA_Q4K_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+constexpr size_t kStaticCounterBytes = (size_t)16 << 10;   /* row-group counters, zero between calls */
+unsigned char *g_scratch_ptr[kMaxDevices];                  /* device address of `scratch`, per device */
+
+__global__ void sera_zero_words_kernel(uint32_t *p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+/* Look up this device's copy of `scratch` (the device must be current) and
+ * clear its counter region with a fill kernel on `s`; once per device. */
+int static_scratch_setup(int device, hipStream_t s) {
+    if (device < 0 || device >= kMaxDevices) return fail(-1, "static scratch: device %d out of range", device);
+    if (g_scratch_ptr[device]) return 0;
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+        return fail(-1, "static scratch: hipGetSymbolAddress failed on device %d", device);
+    const int words = (int)(kStaticCounterBytes / 4);
+    hipLaunchKernelGGL(sera_zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, s, (uint32_t *)p, words);
+    if (hipGetLastError() != hipSuccess) return fail(-1, "static scratch: clearing the counters failed");
+    g_scratch_ptr[device] = (unsigned char *)p;
+    return 0;
+}
+}  // namespace
+
 extern "C" int sera_q4k_init(int device) {
     if (device < 0) return fail(-1, "sera_q4k_init: invalid device %d", device);
     if (hipSetDevice(device) != hipSuccess) return fail(-1, "sera_q4k_init: hipSetDevice(%d) failed", device);
@@ -124,6 +159,15 @@ extern "C" int sera_q4k_init(int device) {
         return fail(-1, "sera_q4k_init: cannot read the compute-unit count of device %d", device);
     g_cus = cus;
     g_device = device;
+    /* the static scratch of sera_q4k_dense_vec_static, set up while this
+     * device is current; the clearing kernel runs on the null stream, and
+     * init waits for it (a caller's non-blocking stream is not ordered after
+     * the null stream) */
+    if (!g_scratch_ptr[device]) {
+        if (static_scratch_setup(device, nullptr) != 0) return -1;
+        if (hipStreamSynchronize(nullptr) != hipSuccess)
+            return fail(-1, "sera_q4k_init: clearing the static scratch failed");
+    }
     return 0;
 }
 
@@ -276,21 +320,50 @@ bool use_streamk(int M, int N, int K) { return g_counters && streamk_rule(M, N, 
 
 
 namespace {
-/* The few-token kernel on the stage at the start of the arena (form 0: row
- * stage, 1: MMQ stage): split partials go to `slots` (cap floats), counters
- * to the second half of the counter region. */
-int fewtok_launch(const char *tag, int form, const void *W, float *Y, float *slots, size_t cap, int M, int N, int K,
-                  int accum, hipStream_t s) {
+/* The few-token kernel on `stage` (form 0: row stage, 1: MMQ stage): split
+ * partials go to `slots` (cap floats), row-group counters to `counters`
+ * (ncounters ints, zero between calls). */
+int fewtok_launch_on(const char *tag, int form, const void *W, const void *stage, float *Y, float *slots, size_t cap,
+                     int *counters, int ncounters, int M, int N, int K, int accum, hipStream_t s) {
     const int splits = sera_fewtok_splits(M, N, K, 0);
     if (splits > 1) {
         if ((size_t)splits * M * N > cap)
-            return fail(-1, "%s: arena too small for %d split partials of %dx%d", tag, splits, M, N);
-        if (sera_fewtok_groups(M, N, K) > kFewtokMaxCounters)
-            return fail(-1, "%s: N=%d needs more row-group counters than the arena holds", tag, N);
+            return fail(-1, "%s: scratch too small for %d split partials of %dx%d", tag, splits, M, N);
+        if (sera_fewtok_groups(M, N, K) > ncounters)
+            return fail(-1, "%s: N=%d needs more row-group counters than the scratch holds", tag, N);
     }
-    return sera_launch_q4k_fewtok_acc(form, W, g_arena, Y, slots, g_counters + kFewtokCounterBase, M, N, K, 0, accum,
-                                      s) == hipSuccess
+    return sera_launch_q4k_fewtok_acc(form, W, stage, Y, slots, counters, M, N, K, 0, accum, s) == hipSuccess
                ? 0 : fail(-3, "%s: few-token kernel launch failed", tag);
+}
+
+/* The same on the caller's arena: the stage at its start, the counters in
+ * the second half of the counter region. */
+int fewtok_launch(const char *tag, int form, const void *W, float *Y, float *slots, size_t cap, int M, int N, int K,
+                  int accum, hipStream_t s) {
+    return fewtok_launch_on(tag, form, W, g_arena, Y, slots, cap, g_counters + kFewtokCounterBase, kFewtokMaxCounters,
+                            M, N, K, accum, s);
+}
+
+/* The MMVQ path (quantize + dot4 MMVQ or the few-token kernel) on explicit
+ * scratch: the row stage at `stage`, split slots after it (slot_cap
+ * floats), row-group counters at `counters`. */
+int dense_vec_on(const char *tag, const void *W, const float *X, float *Y, int M, int N, int K, hipStream_t s,
+                 int timed, unsigned char *stage, size_t stage_cap, int *counters, int ncounters) {
+    const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
+    if (stage_bytes > stage_cap) return fail(-1, "%s: scratch too small (%zu > %zu)", tag, stage_bytes, stage_cap);
+    if (timed) record(g_ev.quant_begin, s);
+    if (sera_launch_q8_1_row(X, M, K, stage, s) != hipSuccess) return fail(-2, "%s: quantize launch failed", tag);
+    if (timed) record(g_ev.quant_end, s);
+    if (timed) record(g_ev.kernel_begin, s);
+    if (sera_q4k_vec_uses_fewtok(M, N, K)) {
+        const int rc = fewtok_launch_on(tag, 0, W, stage, Y, (float *)(stage + stage_bytes),
+                                        (stage_cap - stage_bytes) / sizeof(float), counters, ncounters, M, N, K, 0, s);
+        if (rc) return rc;
+    } else if (sera_launch_q4k_mmvq(W, stage, Y, M, N, K, 0, s) != hipSuccess) {
+        return fail(-3, "%s: mmvq launch failed", tag);
+    }
+    if (timed) record(g_ev.kernel_end, s);
+    return 0;
 }
 }  // namespace
 
@@ -376,24 +449,39 @@ extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M
     if (M > SERA_Q4K_MMVQ_MAX_BATCH)
         return fail(-1, "sera_q4k_dense_vec: batch M=%d exceeds MMVQ cap %d", M, SERA_Q4K_MMVQ_MAX_BATCH);
     if (!g_arena) return fail(-1, "sera_q4k_dense_vec: no arena attached");
-    hipStream_t s = (hipStream_t)stream;
-    const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
-    if (stage_bytes > g_arena_bytes)
-        return fail(-1, "sera_q4k_dense_vec: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
-    if (timed) record(g_ev.quant_begin, s);
-    if (sera_launch_q8_1_row(X, M, K, g_arena, s) != hipSuccess)
-        return fail(-2, "sera_q4k_dense_vec: quantize launch failed");
-    if (timed) record(g_ev.quant_end, s);
-    if (timed) record(g_ev.kernel_begin, s);
+    return dense_vec_on("sera_q4k_dense_vec", W, X, Y, M, N, K, (hipStream_t)stream, timed, g_arena, g_arena_bytes,
+                        g_counters + kFewtokCounterBase, kFewtokMaxCounters);
+}
+
+extern "C" size_t sera_q4k_dense_vec_static_bytes(int M, int N, int K) {
+    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
+    size_t bytes = kStaticCounterBytes + sera_row_stage_layout((size_t)M, (size_t)K).total;
     if (sera_q4k_vec_uses_fewtok(M, N, K)) {
-        const int rc = fewtok_launch("sera_q4k_dense_vec", 0, W, Y, (float *)(g_arena + stage_bytes),
-                                     (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s);
-        if (rc) return rc;
-    } else if (sera_launch_q4k_mmvq(W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
-        return fail(-3, "sera_q4k_dense_vec: mmvq launch failed");
+        const int splits = sera_fewtok_splits(M, N, K, 0);
+        if (splits > 1) bytes += (size_t)splits * M * N * sizeof(float);
     }
-    if (timed) record(g_ev.kernel_end, s);
-    return 0;
+    return bytes;
+}
+
+extern "C" int sera_q4k_dense_vec_static(const void *W, const float *X, float *Y, int M, int N, int K, void *stream) {
+    const char *tag = "sera_q4k_dense_vec_static";
+    if (!check_shape(tag, W, X, Y, M, N, K)) return -1;
+    if (M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "%s: batch M=%d exceeds MMVQ cap %d", tag, M, SERA_Q4K_MMVQ_MAX_BATCH);
+    const size_t need = sera_q4k_dense_vec_static_bytes(M, N, K);
+    if (need > SERA_Q4K_STATIC_SCRATCH_BYTES)
+        return fail(-1, "%s: M=%d N=%d K=%d needs %zu bytes of scratch, more than the static %zu", tag, M, N, K, need,
+                    (size_t)SERA_Q4K_STATIC_SCRATCH_BYTES);
+    if (sera_q4k_vec_uses_fewtok(M, N, K) && sera_fewtok_splits(M, N, K, 0) > 1 &&
+        sera_fewtok_groups(M, N, K) > (int)(kStaticCounterBytes / sizeof(int)))
+        return fail(-1, "%s: N=%d needs more row-group counters than the static scratch holds", tag, N);
+    hipStream_t s = (hipStream_t)stream;
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess) return fail(-1, "%s: hipGetDevice failed", tag);
+    if (static_scratch_setup(device, s) != 0) return -1;
+    unsigned char *base = g_scratch_ptr[device];
+    return dense_vec_on(tag, W, X, Y, M, N, K, s, 0, base + kStaticCounterBytes,
+                        SERA_Q4K_STATIC_SCRATCH_BYTES - kStaticCounterBytes, (int *)base,
+                        (int)(kStaticCounterBytes / sizeof(int)));
 }
 
 /* ---- Q6_K ---------------------------------------------------------------- */

@@ -87,6 +87,8 @@ def load():
         "sera_q4k_set_arena": ([P, SZ], I),
         "sera_q4k_dense": ([P, P, P, I, I, I, P, I], I),
         "sera_q4k_dense_vec": ([P, P, P, I, I, I, P, I], I),
+        "sera_q4k_dense_vec_static": ([P, P, P, I, I, I, P], I),
+        "sera_q4k_dense_vec_static_bytes": ([I, I, I], SZ),
         "sera_q4k_read_timings": ([ctypes.POINTER(ctypes.c_double)] * 3, None),
         "sera_q8_1_row_stage_bytes": ([I, I], SZ),
         "sera_q8_1_row_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ),
