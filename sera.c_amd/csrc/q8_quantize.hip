@@ -38,17 +38,60 @@
  */
 #include "sera_launch.h"
 
+/* The value of lane (lane ^ OFF) for the xor butterflies below, in VALU
+ * cross-lane operations instead of LDS permutes: DPP inside a 16-lane row
+ * (quad_perm for 1 and 2, row_ror:8 for 8, and for 4 two row shifts, each
+ * written only to the banks of four lanes whose partner it reaches), and for
+ * 16 and 32 the gfx950 row and half swaps (v_permlane16_swap /
+ * v_permlane32_swap: with both operands the same value, one result holds the
+ * partner where the lane's row (half) is odd, the other where it is even). */
+template <int OFF>
+__device__ __forceinline__ int xor_partner(int v) {
+    if constexpr (OFF == 1) {
+        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);     /* quad_perm [1,0,3,2] */
+    } else if constexpr (OFF == 2) {
+        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);     /* quad_perm [2,3,0,1] */
+    } else if constexpr (OFF == 4) {
+        const int p = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xF, 0x5, false);   /* row_shl:4, banks 0, 2 */
+        return __builtin_amdgcn_update_dpp(p, v, 0x114, 0xF, 0xA, false);          /* row_shr:4, banks 1, 3 */
+    } else if constexpr (OFF == 8) {
+        return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);    /* row_ror:8 */
+    } else if constexpr (OFF == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (threadIdx.x & 16) ? (int)r[0] : (int)r[1];
+    } else {
+        static_assert(OFF == 32, "xor partner offset");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (threadIdx.x & 32) ? (int)r[0] : (int)r[1];
+    }
+}
+
+template <int OFF>
+__device__ __forceinline__ float xor_partner(float v) { return __int_as_float(xor_partner<OFF>(__float_as_int(v))); }
+
 /* 1 / sqrt(mean(x^2) + eps) of one row, computed by all 256 threads of the
- * workgroup (every thread returns the same value). */
+ * workgroup (every thread returns the same value). Thread t adds x[t+256i]^2
+ * in i order; the loads go out 16 at a time (past K they read as zero, and
+ * adding 0 to the non-negative running sum changes nothing). */
 __device__ __forceinline__ float q8_row_inv_rms(const float *__restrict__ xr, int K, float eps) {
     __shared__ float s_red[4];
     float s = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) {
-        const double v = (double)xr[k];
-        s = (float)((double)s + v * v);
-    }
+    for (int k0 = threadIdx.x; k0 < K; k0 += 16 * 256) {
+        float v[16];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o, 64));
+        for (int j = 0; j < 16; j++) v[j] = k0 + 256 * j < K ? xr[k0 + 256 * j] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const double d = (double)v[j];
+            s = (float)((double)s + d * d);
+        }
+    }
+    s = __fadd_rn(s, xor_partner<32>(s));
+    s = __fadd_rn(s, xor_partner<16>(s));
+    s = __fadd_rn(s, xor_partner<8>(s));
+    s = __fadd_rn(s, xor_partner<4>(s));
+    s = __fadd_rn(s, xor_partner<2>(s));
+    s = __fadd_rn(s, xor_partner<1>(s));
     if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = s;
     __syncthreads();
     const float tot = __fadd_rn(__fadd_rn(__fadd_rn(s_red[0], s_red[1]), s_red[2]), s_red[3]);
@@ -99,13 +142,21 @@ __global__ __launch_bounds__(256) void sera_q8_1_row_kernel(
     const float inv = PK == 1 ? q8_row_inv_rms(x + (size_t)row * K, K, prod.eps) : 0.0f;
     const float xi = q8_produce<PK>(x, prod, (size_t)row * K + k, k, inv);
 
+    /* the 32-lane xor butterfly 16, 8, 4, 2, 1 of the reference (each lane
+     * adds its partner's value; addition is commutative, so own + partner is
+     * the reference's sum bit for bit) */
     float amax = fabsf(xi);
     float sum = xi;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-        sum = sum + __shfl_xor(sum, off, 64);
-    }
+    amax = fmaxf(amax, xor_partner<16>(amax));
+    sum = sum + xor_partner<16>(sum);
+    amax = fmaxf(amax, xor_partner<8>(amax));
+    sum = sum + xor_partner<8>(sum);
+    amax = fmaxf(amax, xor_partner<4>(amax));
+    sum = sum + xor_partner<4>(sum);
+    amax = fmaxf(amax, xor_partner<2>(amax));
+    sum = sum + xor_partner<2>(sum);
+    amax = fmaxf(amax, xor_partner<1>(amax));
+    sum = sum + xor_partner<1>(sum);
     const float d = amax / 127.0f;
     const float qf = amax == 0.0f ? 0.0f : roundf(xi / d);
     const int q = (int)qf;
@@ -113,8 +164,11 @@ __global__ __launch_bounds__(256) void sera_q8_1_row_kernel(
 
     /* S = sum of the 32 quants (exact integer), for the MMVQ min term. */
     int s = q;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    s += xor_partner<16>(s);
+    s += xor_partner<8>(s);
+    s += xor_partner<4>(s);
+    s += xor_partner<2>(s);
+    s += xor_partner<1>(s);
 
     const uint32_t dh = f2h_bits(d);
     const uint32_t sh = f2h_bits(sum);
@@ -125,8 +179,8 @@ __global__ __launch_bounds__(256) void sera_q8_1_row_kernel(
     /* dsf pairs block 2p (lanes 0-31) with block 2p+1 (lanes 32-63). */
     const float d8 = h2f_bits(dh);
     const float dS = d8 * (float)s;
-    const float d8_hi = __shfl(d8, 32, 64);
-    const float dS_hi = __shfl(dS, 32, 64);
+    const float d8_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(d8), 32));
+    const float dS_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dS), 32));
     if (lane == 0) {
         dsf[(size_t)row * (K / 64) + (k >> 6)] = make_float4(d8, d8_hi, dS, dS_hi);
     }
@@ -148,11 +202,12 @@ __global__ __launch_bounds__(256) void sera_q8_1_mmq_kernel(
 
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     float sum = ((v.x + v.y) + v.z) + v.w;
-#pragma unroll
-    for (int off = 4; off >= 1; off >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-        sum = sum + __shfl_xor(sum, off, 64);
-    }
+    amax = fmaxf(amax, xor_partner<4>(amax));
+    sum = sum + xor_partner<4>(sum);
+    amax = fmaxf(amax, xor_partner<2>(amax));
+    sum = sum + xor_partner<2>(sum);
+    amax = fmaxf(amax, xor_partner<1>(amax));
+    sum = sum + xor_partner<1>(sum);
     int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
     float d = 0.0f;
     if (amax != 0.0f) {
@@ -190,8 +245,9 @@ __global__ __launch_bounds__(256) void sera_q8_1_q6k_stage_kernel(
     if (row < M) v = q8_produce4<PK>(x, prod, (size_t)row * K + k, k, inv);
 
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-    for (int off = 4; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    amax = fmaxf(amax, xor_partner<4>(amax));
+    amax = fmaxf(amax, xor_partner<2>(amax));
+    amax = fmaxf(amax, xor_partner<1>(amax));
     float q0 = 0.0f, q1 = 0.0f, q2 = 0.0f, q3 = 0.0f, d = 0.0f;
     if (amax != 0.0f) {
         if (ROW) {
