@@ -240,7 +240,7 @@ def main():
         del qws, qarr
         torch.cuda.empty_cache()
 
-    # ---------------- config 3 (gate/up only unless --full): MMQ M=512 -----
+    # ---------------- config 3: MMQ M=512 (gate first, then the seven projections) -----
     FEWTOK_MMQ_MAX_BATCH = 9    # the MMQ path runs the few-token kernel (MMQ formula) up to here
 
     def mmq_case(label, N, K, M, arr, ncopies, iters):
