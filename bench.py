@@ -241,8 +241,6 @@ def main():
         torch.cuda.empty_cache()
 
     # ---------------- config 3: MMQ M=512 (gate first, then the seven projections) -----
-    FEWTOK_MMQ_MAX_BATCH = 9    # the MMQ path runs the few-token kernel (MMQ formula) up to here
-
     def mmq_case(label, N, K, M, arr, ncopies, iters):
         x = activations(M, K, 7)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -252,7 +250,7 @@ def main():
         q3q4.quantize_mmq(x, stage)
         wgs = L.sera_q4k_mmq_streamk_wgs(M)
         tiles = L.sera_q4k_mmq_tiles(M, N)
-        if M <= FEWTOK_MMQ_MAX_BATCH:
+        if L.sera_q4k_mmq_uses_fewtok(M, N, K):
             # few-token kernel, MMQ formula: split slots, then the zeroed counters
             splits = -q3q4.fewtok_splits(M, N, K)
             partial = torch.zeros(-splits * M * N + q3q4.fewtok_groups(M, N, K), dtype=torch.float32,

@@ -149,9 +149,16 @@ int sera_q4k_mmq_splits(int M, int N, int K);
 int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
                          int M, int N, int K, int wgs, void *stream);
 int sera_q4k_mmq_streamk_wgs(int M);   /* resident workgroups for M tokens (after init) */
-/* Schedule sera_q4k_dense picks for this shape (after init): 1 = stream-K,
- * 0 = plain tiles / split-K (sera_q4k_mmq_splits); -1 for a bad shape. */
+/* Schedule of the MMQ tile kernels for this shape (after init): 1 =
+ * stream-K, 0 = plain tiles / split-K (sera_q4k_mmq_splits); -1 for a bad
+ * shape. sera_q4k_dense runs it where sera_q4k_mmq_uses_fewtok is 0. */
 int sera_q4k_mmq_schedule(int M, int N, int K);
+/* 1 if sera_q4k_dense (the boundary's MMQ path) runs the few-token MFMA
+ * kernel with the MMQ formula for this shape instead of the MMQ tiles: 1-8
+ * tokens always, 9-16 tokens on matrices with N or K of 16384 or more (gate,
+ * up, down, the LM head); 0 otherwise. No counterpart in the reference
+ * (mul_mat_q has one kernel family); a dispatch query. */
+int sera_q4k_mmq_uses_fewtok(int M, int N, int K);
 int sera_q4k_mmq_tiles(int M, int N);
 int sera_q4k_mmq_slot_floats(int M);
 
@@ -161,7 +168,7 @@ int sera_q4k_mmq_slot_floats(int M);
  * M <= 8: it plays the role of mul_mat_vec_q<Q4_K, ncols> (cuda/mmq/mmvq.cu:
  * 393-587) for 4-8 tokens. form 1 takes an MMQ stage and computes the MMQ
  * formula (as sera_q4k_mmq, cuda/mmq/mmq.cuh:2269-2283,1440-1472).
- * chunk: super-blocks of K per workgroup, 1..20 for M <= 8 and 1..10 above,
+ * chunk: super-blocks of K per workgroup, 1..40 for M <= 8 and 1..20 above,
  * 0 = the built-in choice. When the chunk splits K (sera_q4k_fewtok_splits >
  * 1), slots holds splits*M*N floats and counters sera_q4k_fewtok_groups(M,
  * N, K) ints that must be zero and are zero again after the kernel; the

@@ -52,7 +52,7 @@ typedef __attribute__((address_space(3))) void ft_lds_void;
 typedef __attribute__((address_space(1))) const void ft_global_cvoid;
 
 #define SERA_FEWTOK_MAX_TOKENS 16
-#define SERA_FEWTOK_LDS_CHUNK_TOKENS 160   /* chunk x staged tokens: 20 super-blocks of 8, 10 of 16 */
+#define SERA_FEWTOK_LDS_CHUNK_TOKENS 320   /* chunk x staged tokens: 40 super-blocks of 8, 20 of 16 */
 
 /* LDS bytes of a workgroup for `chunk` super-blocks of `tok` staged tokens:
  * quants, d8, the min-term activation factor, and a 16-byte zero operand. */
@@ -316,14 +316,19 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
  * on MI355X over the Qwen3-32B projections (weights streamed from HBM): 8
  * waves (128 rows) for the large matrices, 4 otherwise, and enough K splits
  * to give the chip about 192 (8 waves) or 256 (4 waves) workgroups, with
- * chunks of at least 5 super-blocks (below that the LDS staging dominates).
- * A chunk holds at most 160 / staged tokens super-blocks (20 for 8 tokens,
- * 10 for 16), which keeps the LDS at 51 KB. */
+ * chunks of at least 5 super-blocks (below that the LDS staging dominates)
+ * and at most 20. The kernel takes chunks of up to 320 / staged tokens
+ * super-blocks (40 for 8 tokens, 20 for 16): up to 100 KB of LDS, one 8-wave
+ * workgroup per CU. The 20-block chunk at 16 tokens (one split on gate/up and
+ * the LM head) measured 23-24 and 112-120 us against 31-34 and 146-155 us
+ * with the earlier 10-block cap and its second split. */
 extern "C" void sera_fewtok_plan(int M, int N, int K, int *nwave, int *chunk) {
     const int nw = (N >= 16384 || K >= 16384) ? 8 : 4;
     const int groups = (N + 16 * nw - 1) / (16 * nw);
     const int nkb = K / Q4K_QK;
-    const int maxc = SERA_FEWTOK_LDS_CHUNK_TOKENS / (M > 8 ? 16 : 8);
+    /* planned chunks stay within 20 super-blocks, the range measured on the
+     * Qwen3-32B shapes; longer ones (up to the LDS limit) only on request */
+    const int maxc = 20;
     const int target = nw == 8 ? 192 : 256;
     int s = (target + groups - 1) / groups;
     if (s > 16) s = 16;
@@ -385,6 +390,7 @@ extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const 
     int nw, c;
     sera_fewtok_plan(M, N, K, &nw, &c);
     if (chunk > 0) c = chunk;
+    if (c > sera_fewtok_max_chunk(M)) return hipErrorInvalidValue;   /* the LDS staging is sized for this */
     const char *base = (const char *)stage;
     const uint8_t *w = (const uint8_t *)W;
     if (form == 0) {

@@ -66,13 +66,19 @@ extern "C" int sera_q4k_vec_uses_fewtok(int M, int N, int K) {
     return 0;
 }
 
-/* The MMQ path up to this batch runs the same kernel with the MMQ formula
- * on the MMQ stage. Against the paired 16-token MMQ tile, measured on the
- * Qwen3-32B projections: at 9 tokens it is faster on gate/up, down, q and
- * k by 0.4-1 us (a layer of seven projections 163 against 167 us); from 10
- * tokens the paired tile is faster or equal on all but gate/up (down 41
- * against 42-47 us, o 18.5 against 19-21, LM head 138 against 147-153). */
-#define SERA_Q4K_FEWTOK_MMQ_MAX_BATCH 9
+/* The MMQ path runs the same kernel with the MMQ formula on the MMQ stage
+ * at 1-8 tokens, and at 9-16 tokens on the matrices whose rows or K reach
+ * 16384 (its 8-wave plan). Against the paired 16-token MMQ tile, measured
+ * through the boundary on the Qwen3-32B shapes (weights streamed from HBM,
+ * 10-16 tokens, us per call): gate/up 25.5-26 against 33-34, down 34-36
+ * against 44-45, LM head 120-124 against 143; on q, o and k/v the paired
+ * tile stays ahead (15, 20, 15 against 18-19, 23-24, 17-18), and at 9
+ * tokens too (q 15.0 against 17.3). */
+#define SERA_Q4K_FEWTOK_MMQ_MAX_BATCH 16
+extern "C" int sera_q4k_mmq_uses_fewtok(int M, int N, int K) {
+    if (M < 1 || M > SERA_Q4K_FEWTOK_MMQ_MAX_BATCH || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
+    return M <= 8 || N >= 16384 || K >= 16384;
+}
 
 /* Workgroups the stream-K MMQ schedule runs for M tokens: the resident
  * count, a multiple of 8. */
@@ -374,7 +380,7 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
     hipStream_t s = (hipStream_t)stream;
     const int Mpad = sera_mmq_padded_rows(M);
     const size_t stage_bytes = sera_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
-    if (M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) {
+    if (sera_q4k_mmq_uses_fewtok(M, N, K)) {
         /* few tokens: the few-token kernel with the MMQ formula on the MMQ stage */
         if (stage_bytes > g_arena_bytes)
             return fail(-1, "sera_q4k_dense: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
@@ -438,7 +444,7 @@ extern "C" int sera_q4k_mmq_slot_floats(int M) { return M > 0 ? sera_mmq_slot_fl
 
 extern "C" int sera_q4k_kernel_launches(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
-    if (M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) return 2;   /* the few-token kernel sums split K inside */
+    if (sera_q4k_mmq_uses_fewtok(M, N, K)) return 2;   /* the few-token kernel sums split K inside */
     if (use_streamk(M, N, K)) return 2;
     return sera_mmq_splits(M, N, K) > 1 && ((size_t)M * N) % 4 == 0 ? 3 : 2;
 }
@@ -880,7 +886,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         hipError_t e;
         const int n = N[i];
         const bool mn4 = ((size_t)M * n) % 4 == 0;
-        if (qt == 12 && M <= SERA_Q4K_FEWTOK_MMQ_MAX_BATCH) {
+        if (qt == 12 && sera_q4k_mmq_uses_fewtok(M, n, K)) {
             const int rc = fewtok_launch(tag, 1, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
             if (rc) return rc;
             continue;

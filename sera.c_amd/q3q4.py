@@ -111,6 +111,7 @@ def load():
         "sera_q4k_mmq_streamk": ([P, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_streamk_wgs": ([I], I),
         "sera_q4k_mmq_schedule": ([I, I, I], I),
+        "sera_q4k_mmq_uses_fewtok": ([I, I, I], I),
         "sera_q4k_mmq_tiles": ([I, I], I),
         "sera_q4k_mmq_slot_floats": ([I], I),
         "sera_q4k_dequantize": ([P, SZ, P, P], I),

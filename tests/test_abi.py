@@ -115,26 +115,26 @@ def test_kernel_entry_points_validate_on_host(L):
     assert L.sera_q4k_fewtok(0, d, d, d, None, None, 4, 128, 300, 0, 0, None) == -1
     assert L.sera_q4k_fewtok(0, d, ctypes.c_void_p(264), d, None, None, 4, 128, 256, 0, 0, None) == -1
     assert b"16-byte aligned" in L.sera_q4k_last_error()
-    assert L.sera_q4k_fewtok(0, d, d, d, None, None, 4, 128, 5120, 21, 0, None) == -1
+    assert L.sera_q4k_fewtok(0, d, d, d, None, None, 4, 128, 5120, 41, 0, None) == -1
     assert b"chunk" in L.sera_q4k_last_error()
-    assert L.sera_q4k_fewtok(1, d, d, d, None, None, 12, 128, 5120, 11, 0, None) == -1
+    assert L.sera_q4k_fewtok(1, d, d, d, None, None, 12, 128, 5120, 21, 0, None) == -1
     assert b"chunk" in L.sera_q4k_last_error()
     assert L.sera_q4k_fewtok(0, d, d, d, None, None, 4, 128, 5120, 3, 0, None) == -1
     assert b"slots" in L.sera_q4k_last_error()
 
 
 def test_fewtok_plan(L):
-    """Chunks cover K in at most 20 super-blocks each (10 above 8 tokens);
-    row groups cover N."""
+    """Planned chunks cover K in at most 20 super-blocks each; explicit
+    chunks go up to 40 (20 above 8 tokens); row groups cover N."""
     for M in range(1, 17):
         for N, K in ((1024, 5120), (5120, 25600), (25600, 5120), (151936, 5120), (8192, 5120), (5120, 8192),
                      (16, 256), (203, 2304), (100, 128 * 1024)):
             nkb = K // 256
-            cmax = 20 if M <= 8 else 10
+            cmax = 40 if M <= 8 else 20
             s = L.sera_q4k_fewtok_splits(M, N, K, 0)
-            assert 1 <= s <= max(16, -(-nkb // cmax)), (M, N, K, s)
+            assert 1 <= s <= max(16, -(-nkb // 20)), (M, N, K, s)
             chunk = -(-nkb // s)
-            assert chunk <= cmax and -(-nkb // chunk) == s, (M, N, K, s)
+            assert chunk <= 20 and -(-nkb // chunk) == s, (M, N, K, s)
             g = L.sera_q4k_fewtok_groups(M, N, K)
             assert g in (-(-N // 64), -(-N // 128)), (N, g)     # 4 or 8 waves of 16 rows
             for c in (1, 3, cmax):
@@ -175,13 +175,16 @@ def test_stage_layouts_and_workspace_sizing():
         assert L.sera_q4k_mmq_slot_floats(16) == 32 * 256   # the paired tile keeps 32 MFMA rows
         assert q3q4.mmq_stage_layout(16, 5120)["total"] + slots <= room, mt
     # and every few-token split, for arenas sized down to the batch (row
-    # stage up to 8 tokens, MMQ stage at 9)
-    for mt in (1, 4, 8, 9, 12, 2048):
-        for M in range(1, min(mt, 9) + 1):
+    # stage on the MMVQ path up to 8 tokens, MMQ stage on the MMQ path up
+    # to 16)
+    for mt in (1, 4, 8, 9, 12, 16, 2048):
+        for M in range(1, min(mt, 16) + 1):
             for N, K in ((1024, 5120), (5120, 25600), (25600, 5120), (151936, 5120), (100, 128 * 1024)):
                 s = L.sera_q4k_fewtok_splits(M, N, K, 0)
-                stage = q3q4.row_stage_layout(M, K) if M <= 8 else q3q4.mmq_stage_layout(M, K)
-                need = stage["total"] + (s * M * N * 4 if s > 1 else 0)
+                stage = q3q4.mmq_stage_layout(M, K)["total"]
+                if M <= 8:
+                    stage = max(stage, q3q4.row_stage_layout(M, K)["total"])
+                need = stage + (s * M * N * 4 if s > 1 else 0)
                 assert need <= L.sera_q4k_arena_bytes(mt, 151936, 128 * 1024) - (256 << 10), (mt, M, N, K, s)
 
 
@@ -191,9 +194,10 @@ def test_kernel_launch_counts(L):
     for N, K in ((25600, 5120), (5120, 25600)):                     # few-token kernel,
         assert L.sera_q4k_kernel_launches(8, N, K) == 2             # split K summed inside
     assert L.sera_q4k_kernel_launches(9, 5120, 25600) == 2          # few-token kernel, MMQ formula
-    assert L.sera_q4k_kernel_launches(10, 25600, 5120) == 3         # paired MMQ tile, split K
+    assert L.sera_q4k_kernel_launches(10, 25600, 5120) == 2         # few-token kernel on a tall matrix
+    assert L.sera_q4k_kernel_launches(16, 5120, 25600) == 2         # few-token kernel on a long K
+    assert L.sera_q4k_kernel_launches(10, 8192, 5120) == 3          # paired MMQ tile, split K
     assert L.sera_q4k_kernel_launches(512, 25600, 5120) == 2        # MMQ, enough tiles
-    assert L.sera_q4k_kernel_launches(16, 5120, 25600) == 3         # MMQ, split K
     assert L.sera_q4k_kernel_launches(0, 5120, 25600) == 0
     assert L.sera_q4k_kernel_launches(4, 5120, 300) == 0
 

@@ -98,7 +98,7 @@ def test_fewtok_parity(torch, N, K):
         q3q4.quantize_row(dev(torch, x), stage)
         xq, xd, _ = oracle.q8_1_row(x)
         ref = oracle.gemm_mmvq(W, xq, xd, N, K)
-        for chunk in sorted({0, 1, 3, 7, min(20, nkb)}):
+        for chunk in sorted({0, 1, 3, 7, min(20, nkb), min(40, nkb)}):
             if chunk > nkb:
                 continue
             say(f"case fewtok M={M} N={N} K={K} chunk={chunk} "
@@ -120,7 +120,7 @@ def test_fewtok_mmq_formula_parity(torch, N, K):
         q3q4.quantize_mmq(dev(torch, x), stage)
         xq, xd, xs = oracle.q8_1_mmq(x)
         ref = oracle.gemm_mmq(W, xq, xd, xs, N, K)
-        for chunk in sorted({0, 1, 3, min(10 if M > 8 else 20, nkb)}):
+        for chunk in sorted({0, 1, 3, min(10, nkb), min(20 if M > 8 else 40, nkb)}):
             if chunk > nkb:
                 continue
             say(f"case fewtok form=1 M={M} N={N} K={K} chunk={chunk} "
@@ -196,24 +196,28 @@ def test_boundary_vec_dispatch(torch, linear, N, K):
         assert torch.equal(y, ref)
 
 
-def test_boundary_uses_fewtok_mmq_formula_at_nine_tokens(torch, linear):
-    """q3_cuda_q4k_linear at 9 tokens gives the few-token kernel's MMQ-formula
-    result bit for bit, and stays within the tolerance of the MMQ oracle; from
-    10 tokens it gives the paired MMQ tile's result."""
-    rng = np.random.default_rng(23)
-    N, K = 1000, 25600
+@pytest.mark.parametrize("N,K", [(1000, 25600), (1000, 2048)])
+def test_boundary_mmq_path_at_nine_to_sixteen_tokens(torch, linear, N, K):
+    """q3_cuda_q4k_linear at 9-16 tokens gives, bit for bit, the kernel that
+    sera_q4k_mmq_uses_fewtok names: the few-token kernel's MMQ-formula result
+    on a K >= 16384 matrix, the paired MMQ tile's on a small one; both stay
+    within the tolerance of the MMQ oracle."""
+    rng = np.random.default_rng(23 + K)
     W = rand_weights(rng, N, K)
     Wd = dev(torch, W)
     geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+    L = q3q4.load()
     for M in (9, 10, 16):
+        few = L.sera_q4k_mmq_uses_fewtok(M, N, K)
+        assert few == (K >= 16384)
         xh = outlier_activations(rng, M, K)
         x = dev(torch, xh)
-        say(f"case boundary MMQ formula M={M} N={N} K={K}")
+        say(f"case boundary MMQ formula M={M} N={N} K={K} fewtok={few}")
         y = torch.empty((M, N), dtype=torch.float32, device="cuda")
         linear(geo, Wd, x, y)
         stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
         q3q4.quantize_mmq(x, stage)
-        if M == 9:
+        if few:
             ref, _ = run_fewtok(torch, Wd, stage, M, N, K, 0, form=1)
         else:
             s = q3q4.mmq_splits(M, N, K)

@@ -95,17 +95,20 @@ def test_group_products_and_accumulate(torch, linear, qtype, M):
         assert np.array_equal(ya[i].view(np.uint32), (y0[i] + ys[i]).astype(np.float32).view(np.uint32)), i
 
 
-@pytest.mark.parametrize("M,N,K,streamk", [(9, 256, 2048, 0), (64, 16384, 2048, 1), (100, 4096, 5120, 0),
-                                            (20, 131328, 256, 1), (20, 4096, 1024, 0),
-                                            (13, 1000, 2304, 0), (16, 131328, 256, 1)])
-def test_accumulate_on_split_and_streamk_schedules(torch, linear, M, N, K, streamk):
-    """Q4_K MMQ under split-K (few tiles) and stream-K (64+ tiles of 64
-    tokens; a full round or more of 32- or paired 16-token tiles): the
-    accumulating store stays bit-identical to product + add."""
-    sched = q3q4.load().sera_q4k_mmq_schedule(M, N, K)
-    say(f"case accumulate schedules M={M} N={N} K={K} stream-K={sched}")
-    if streamk is not None:
-        assert sched == streamk
+@pytest.mark.parametrize("M,N,K,kind", [(9, 256, 2048, "split"), (64, 16384, 2048, "streamk"),
+                                          (100, 4096, 5120, "split"), (20, 131328, 256, "streamk"),
+                                          (20, 4096, 1024, "split"), (13, 1000, 2304, "split"),
+                                          (16, 131328, 256, "fewtok"), (12, 1000, 16384, "fewtok")])
+def test_accumulate_on_split_and_streamk_schedules(torch, linear, M, N, K, kind):
+    """Q4_K MMQ path under split-K (few tiles), stream-K (64+ tiles of 64
+    tokens; a full round or more of 32-token tiles) and the few-token kernel
+    it runs at 9-16 tokens on tall or long matrices: the accumulating store
+    stays bit-identical to product + add."""
+    L = q3q4.load()
+    got = ("fewtok" if L.sera_q4k_mmq_uses_fewtok(M, N, K)
+           else "streamk" if L.sera_q4k_mmq_schedule(M, N, K) == 1 else "split")
+    say(f"case accumulate schedules M={M} N={N} K={K} kernel={got}")
+    assert got == kind
     rng = np.random.default_rng(M + N)
     W = weights(rng, 12, N, K)
     x = rng.standard_normal((M, K)).astype(np.float32)

@@ -63,7 +63,7 @@ def kernel_of(qtype, M, N, K):
     if qtype == q3q4.QTYPE_Q4_K:
         if M <= 8:
             return "fewtok" if L.sera_q4k_vec_uses_fewtok(M, N, K) else "dot4"
-        if M <= 9:
+        if L.sera_q4k_mmq_uses_fewtok(M, N, K):
             return "fewtok-mmq"
         return "mmq-streamk" if L.sera_q4k_mmq_schedule(M, N, K) == 1 else "mmq"
     return "q6k-tile" if M > 8 or L.sera_q6k_vec_uses_tile(M, N, K) else "q6k-mmvq"
