@@ -19,15 +19,25 @@
  *   - each lane loads the Q8_1 slice matching its pair (64 int8 + one float4
  *     of scales) once per block group and reuses it for all weight rows the
  *     lane walks (R/2), so activation traffic per weight byte drops by R/2.
+ *     The two half-waves (rows of either parity) need the same slice: each
+ *     loads one 32-byte half of the quants and one v_permlane32_swap per
+ *     dword hands every lane both halves, halving the activation loads.
  *   - buffer loads with loop-invariant 32-bit lane offsets; the block-group
  *     and row steps live in the scalar offset, so the loop has no address
  *     arithmetic on the vector ALU.
  *   - the NW waves of a workgroup split the row's block groups (K). Partial
- *     sums are reduce-scattered across rows and
- *     lanes with xor shuffles and summed across waves through LDS in a fixed
- *     order, so results repeat bit for bit.
+ *     sums are reduce-scattered across rows and lanes with xor butterflies in
+ *     DPP / lane-swap form (no LDS permutes) and summed across waves through
+ *     LDS in a fixed order, so results repeat bit for bit.
+ *   - every kernel argument is read in one scalar-load round at entry
+ *     (otherwise the compiler sinks some into the branches that use them
+ *     and each workgroup waits on a second round before its first load).
+ *   Measured on gate/up at one token (interleaved runs, 8 weight copies):
+ *   the half-wave activation loads, the DPP butterflies and the single
+ *   argument round together took the kernel from 13.85 to 13.26 us.
  */
 #include "sera_launch.h"
+#include "sera_dpp.h"
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 #define SERA_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
@@ -42,15 +52,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, SERA_RSRC_FLAGS);
 }
 
-/* One halving step of the row reduce-scatter: lanes with bit `o` set keep
+/* One halving step of the row reduce-scatter: lanes with bit O set keep
  * the upper half of v[0..2h) and receive the partner's copy of it. */
-__device__ __forceinline__ void rs_halve(float *v, int h, int lane, int o) {
-    const bool up = (lane & o) != 0;
+template <int O>
+__device__ __forceinline__ void rs_halve(float *v, int h, int lane) {
+    const bool up = (lane & O) != 0;
 #pragma unroll
     for (int i = 0; i < h; i++) {
         const float send = up ? v[i] : v[i + h];
         const float keep = up ? v[i + h] : v[i];
-        v[i] = keep + __shfl_xor(send, o, 64);
+        v[i] = keep + xor_partner<O>(send);
     }
 }
 
@@ -75,13 +86,23 @@ struct MmvqGroup {
     int accum;
 };
 
-template <int NCOLS, int R, int NW>
+template <int NCOLS, int R, int NW, bool GROUPED>
 __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
         MmvqGroup grp, const int8_t *__restrict__ xq, const float4 *__restrict__ dsf, int K) {
+    {
+        const void *a0 = grp.W[0], *a1 = grp.y[0], *a2 = xq, *a3 = dsf;
+        const int a4 = grp.N[0], a5 = K, a6 = grp.accum;
+        __asm__ volatile("" : : "s"(a0), "s"(a1), "s"(a2), "s"(a3), "s"(a4), "s"(a5), "s"(a6));
+    }
+    /* one matrix: its pointers come straight from the kernel arguments, so
+     * the first loads issue without the dependent scalar loads of the
+     * matrix selection (measured 2-4% on one-token launches) */
     int gi = 0;
+    if constexpr (GROUPED) {
 #pragma unroll
-    for (int i = 1; i < SERA_MMVQ_GROUP; i++)
-        if (i < grp.count && (int)blockIdx.x >= grp.tile_end[i - 1]) gi = i;
+        for (int i = 1; i < SERA_MMVQ_GROUP; i++)
+            if (i < grp.count && (int)blockIdx.x >= grp.tile_end[i - 1]) gi = i;
+    }
     const uint8_t *__restrict__ W = grp.W[gi];
     float *__restrict__ y = grp.y[gi];
     const int N = grp.N[gi];
@@ -110,7 +131,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
     const int vo_w = rs * rowbytes + g * Q4K_BLOCK_BYTES;
     const int vo_hdr = vo_w + 4 * q;
     const int vo_qs = vo_w + 16 + 32 * q;
-    const int vo_x = g * Q4K_QK + 64 * q;
+    const int vo_xh = g * Q4K_QK + 64 * q + 32 * rs;
     const int vo_f = (g * 4 + q) * 16;
     const int sh = 16 * (q & 1);
     const bool hi_pair = q >= 2;
@@ -118,11 +139,10 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
     auto load = [&](int bg, MmvqRegs<NCOLS, HR> &t) {
 #pragma unroll
         for (int c = 0; c < NCOLS; c++) {
+            /* lanes of row parity rs load quant half rs of the slice */
             const int so = c * K + bg * 2048;
-            t.xa0[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x, so, 0));
-            t.xa1[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x + 16, so, 0));
-            t.xb0[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x + 32, so, 0));
-            t.xb1[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_x + 48, so, 0));
+            t.xa0[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_xh, so, 0));
+            t.xa1[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo_xh + 16, so, 0));
             t.f[c] = __builtin_amdgcn_raw_buffer_load_b128(rf, vo_f, c * (K / 4) + bg * 512, 0);
         }
 #pragma unroll
@@ -139,6 +159,46 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
     for (int r = 0; r < HR; r++)
 #pragma unroll
         for (int c = 0; c < NCOLS; c++) acc[r][c] = 0.0f;
+
+    /* the whole slice per lane, for the K loop at one token (where the
+     * half-wave loads and their swaps measured 2% slower on down) */
+    auto load_full = [&](int bg, MmvqRegs<NCOLS, HR> &t) {
+#pragma unroll
+        for (int c = 0; c < NCOLS; c++) {
+            const int so = c * K + bg * 2048;
+            const int vo = vo_xh - 32 * rs;
+            t.xa0[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, so, 0));
+            t.xa1[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo + 16, so, 0));
+            t.xb0[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo + 32, so, 0));
+            t.xb1[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, vo + 48, so, 0));
+            t.f[c] = __builtin_amdgcn_raw_buffer_load_b128(rf, vo_f, c * (K / 4) + bg * 512, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < HR; r++) {
+            const int so = 2 * r * rowbytes + bg * 8 * Q4K_BLOCK_BYTES;
+            t.hw[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vo_hdr, so, 0);
+            t.qa[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qs, so, 0);
+            t.qc[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qs + 16, so, 0);
+        }
+    };
+
+    /* after load(): the quant halves of the two half-waves, swapped, so
+     * every lane holds low half xa (sub-block 2q) and high half xb (2q+1) */
+    auto swap_halves = [&](MmvqRegs<NCOLS, HR> &t) {
+#pragma unroll
+        for (int c = 0; c < NCOLS; c++) {
+            const v4i h0 = t.xa0[c], h1 = t.xa1[c];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const auto p0 = __builtin_amdgcn_permlane32_swap(h0[e], h0[e], false, false);
+                const auto p1 = __builtin_amdgcn_permlane32_swap(h1[e], h1[e], false, false);
+                t.xa0[c][e] = (int)p0[0];
+                t.xb0[c][e] = (int)p0[1];
+                t.xa1[c][e] = (int)p1[0];
+                t.xb1[c][e] = (int)p1[1];
+            }
+        }
+    };
 
     auto compute = [&](const MmvqRegs<NCOLS, HR> &t) {
 #pragma unroll
@@ -193,12 +253,27 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
 
     /* groups of this wave: wave, wave+NW, ...; all lanes of a quad share blk.
      * One group in flight per wave keeps registers low; occupancy (several
-     * waves per SIMD) hides the HBM latency. */
-    for (int bg = wave; bg < ngroups; bg += NW) {
-        if (bg * 8 + g < nb) {
+     * waves per SIMD) hides the HBM latency. With at most one group per
+     * wave (K <= 8 * 256 * NW) the work is straight-line code. */
+    if (ngroups <= NW) {
+        if (wave < ngroups && wave * 8 + g < nb) {
             MmvqRegs<NCOLS, HR> cur;
-            load(bg, cur);
+            load(wave, cur);
+            swap_halves(cur);
             compute(cur);
+        }
+    } else {
+        for (int bg = wave; bg < ngroups; bg += NW) {
+            if (bg * 8 + g < nb) {
+                MmvqRegs<NCOLS, HR> cur;
+                if constexpr (NCOLS == 1) {
+                    load_full(bg, cur);
+                } else {
+                    load(bg, cur);
+                    swap_halves(cur);
+                }
+                compute(cur);
+            }
         }
     }
 
@@ -210,21 +285,24 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
 #pragma unroll
         for (int r = 0; r < HR; r++) v[r] = acc[r][c];
         int ri = 0;
-        if constexpr (HR >= 8) { rs_halve(v, 4, lane, 16); ri = ri * 2 + ((lane >> 4) & 1); }
+        if constexpr (HR >= 8) { rs_halve<16>(v, 4, lane); ri = ri * 2 + ((lane >> 4) & 1); }
         if constexpr (HR >= 4) {
             constexpr int o = HR >= 8 ? 8 : 16;
-            rs_halve(v, 2, lane, o);
+            rs_halve<o>(v, 2, lane);
             ri = ri * 2 + ((lane & o) ? 1 : 0);
         }
         if constexpr (HR >= 2) {
             constexpr int o = HR >= 8 ? 4 : (HR >= 4 ? 8 : 16);
-            rs_halve(v, 1, lane, o);
+            rs_halve<o>(v, 1, lane);
             ri = ri * 2 + ((lane & o) ? 1 : 0);
         }
         constexpr int ofirst = HR >= 8 ? 2 : (HR >= 4 ? 4 : (HR >= 2 ? 8 : 16));
         float s = v[0];
-#pragma unroll
-        for (int o = ofirst; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+        if constexpr (ofirst >= 16) s += xor_partner<16>(s);
+        if constexpr (ofirst >= 8) s += xor_partner<8>(s);
+        if constexpr (ofirst >= 4) s += xor_partner<4>(s);
+        if constexpr (ofirst >= 2) s += xor_partner<2>(s);
+        s += xor_partner<1>(s);
         if ((lane & (2 * ofirst - 1)) == 0) s_part[wave][2 * ri + rs][c] = s;
     }
     __syncthreads();
@@ -247,7 +325,12 @@ static hipError_t launch_mmvq(MmvqGroup grp, const int8_t *xq, const float4 *dsf
         tiles += (grp.N[i] + R - 1) / R;
         grp.tile_end[i] = tiles;
     }
-    hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW>), dim3(tiles), dim3(NW * 64), 0, s, grp, xq, dsf, K);
+    if (grp.count == 1)
+        hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW, false>), dim3(tiles), dim3(NW * 64), 0, s, grp, xq,
+                           dsf, K);
+    else
+        hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW, true>), dim3(tiles), dim3(NW * 64), 0, s, grp, xq,
+                           dsf, K);
     return hipGetLastError();
 }
 
