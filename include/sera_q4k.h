@@ -88,9 +88,10 @@ size_t sera_q4k_dense_vec_static_bytes(int M, int N, int K);   /* 0 for a bad sh
 int sera_q4k_kernel_launches(int M, int N, int K);
 
 /* 1 if the MMVQ path (1 <= M <= 8) runs the few-token MFMA kernel for an
- * N x K matrix (tall matrices from 3 tokens, 4096-16383 rows from 5, never
- * below 4096 rows), 0 if it runs the dot4 MMVQ kernel. No counterpart in
- * the reference (cuda/mmq/mmvq.cu has one kernel); a dispatch query. */
+ * N x K matrix (tall matrices from 3 tokens, 4096-16383 rows from 6, or
+ * from 5 when K >= 16384, never below 4096 rows), 0 if it runs the dot4
+ * MMVQ kernel. No counterpart in the reference (cuda/mmq/mmvq.cu has one
+ * kernel); a dispatch query. */
 int sera_q4k_vec_uses_fewtok(int M, int N, int K);
 
 /* 1 if a Q6_K call on the MMVQ path (1 <= M <= 8) runs the tile kernel on a

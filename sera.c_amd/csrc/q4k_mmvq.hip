@@ -334,14 +334,23 @@ static hipError_t launch_mmvq(MmvqGroup grp, const int8_t *xq, const float4 *dsf
     return hipGetLastError();
 }
 
-/* Rows per workgroup (even, 2..16), from a sweep on MI355X over the
- * Qwen3-32B shapes: 4 for one token; 8 for 2-4 tokens (each loaded
- * activation slice serves more rows); for 5-8 tokens the R/2 x M partial
- * sums crowd the registers, so 4 on tall matrices and 2 otherwise. */
-extern "C" int sera_mmvq_rows_per_wave(int N, int M) {
+/* Rows per workgroup (even, 2..16), from interleaved sweeps on MI355X over
+ * the Qwen3-32B shapes (weights streamed from HBM, kernel us):
+ *   one token: 4;
+ *   2-4 tokens: 8 where more rows per loaded activation slice pay for a
+ *     smaller grid - a long K (down, 25600: 19.4 / 20.7 / 23.0 at 2 / 3 /
+ *     4 tokens against 19.5 / 21.9 / 24.3 with 4) or a very tall matrix
+ *     (LM head at 2: 75.1 against 81.9) - and 4 elsewhere (gate/up 16.0
+ *     against 16.2, o 5.7 / 6.6 / 8.2 against 6.6 / 7.8 / 8.7, k/v 2.8 /
+ *     3.1 / 3.5 against 3.4 / 4.0 / 4.5);
+ *   5 tokens: 4 (k/v 3.8 against 4.1 with 2);
+ *   6-8 tokens: 2 (the R/2 x M partial sums of 4 rows cost occupancy:
+ *     k/v at 8 tokens 5.3 against 18.7). */
+extern "C" int sera_mmvq_rows_per_wave(int N, int K, int M) {
     if (M <= 1) return 4;
-    if (M <= 4) return 8;
-    return N >= 16384 ? 4 : 2;
+    if (M <= 4) return (K >= 16384 || N >= 65536) ? 8 : 4;
+    if (M == 5) return 4;
+    return 2;
 }
 
 /* Waves per workgroup: one per group of 8 blocks, at most 4. One token
@@ -402,7 +411,7 @@ extern "C" hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W
     }
     grp.count = count;
     grp.accum = accum;
-    if (rows <= 0) rows = sera_mmvq_rows_per_wave(nmin, M);
+    if (rows <= 0) rows = sera_mmvq_rows_per_wave(nmin, K, M);
     while (rows > 2 && rows > nmin) rows >>= 1;   /* the shifted last tile needs R <= N */
     switch (M) {
         case 1: return dispatch_r<1>(rows, grp, xq, dsf, K, s);

@@ -30,7 +30,7 @@ hipError_t sera_launch_q8_1_q6k_stage_p(const float *x, const sera_producer *pro
                                         int row_formula, void *stage, hipStream_t stream);
 
 /* ---- q4k_mmvq.hip: dot4 MMVQ ------------------------------------------ */
-int sera_mmvq_rows_per_wave(int N, int M);
+int sera_mmvq_rows_per_wave(int N, int K, int M);
 hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K, int rpw,
                                 hipStream_t s);
 hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W, float *const *y, const int *N,

@@ -50,19 +50,19 @@ constexpr int kFewtokMaxCounters = kMaxCounters - kFewtokCounterBase;
 
 /* The MMVQ path (M <= 8) runs the few-token MFMA kernel (MMVQ formula)
  * instead of the dot4 MMVQ kernel where that is faster. Measured on MI355X
- * per Qwen3-32B shape with the weights streamed from HBM (kernel us, dot4 /
- * few-token): the few-token kernel's time is flat in M, dot4's grows with
- * every token and jumps at 5 (fewer rows per wave).
- *   gate/up 25600 rows: 3 tokens 21.7 / 19.7, 4: 24.8 / 20.1;
- *   LM head 151936 rows: 3: 106.6 / 96.3;
- *   q 8192, o and down 5120 rows: 4: 9.9 / 11.2, 10.5 / 15.2, 26.6 / 27.0;
- *     5: 19.1 / 11.4, 17.9 / 15.4, 50.3 / 27.1;
- *   k/v 1024 rows: 8 tokens 6.8 / 10.4 (dot4 at every batch). */
+ * per Qwen3-32B shape with the weights streamed from HBM (kernel us, best
+ * dot4 / few-token, interleaved runs): the few-token kernel's time is flat
+ * in M, dot4's grows with every token and jumps at 6 (2 rows per wave).
+ *   gate/up 25600 rows: 3 tokens 19.9 / 19.9, 4: 22.6 / 19.9;
+ *   LM head 151936 rows: 3: 96.0 / 93.8;
+ *   q 8192 and o 5120 rows: 5 tokens 10.4 / 11.0, 9.2 / 14.7; 6: 16.6 /
+ *     11.2, 14.9 / 14.8;
+ *   down 5120 rows, K 25600: 5 tokens 26.9 / 25.5;
+ *   k/v 1024 rows: 8 tokens 5.3 / 10.5 (dot4 at every batch). */
 extern "C" int sera_q4k_vec_uses_fewtok(int M, int N, int K) {
-    (void)K;
     if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH || N <= 0) return 0;
     if (N >= 16384) return M >= 3;
-    if (N >= 4096) return M >= 5;
+    if (N >= 4096) return M >= (K >= 16384 ? 5 : 6);
     return 0;
 }
 
@@ -248,8 +248,7 @@ extern "C" int sera_q8_1_quantize_mmq(const float *X, int M, int K, void *stage,
 }
 
 extern "C" int sera_q4k_mmvq_rows_per_tile(int M, int N, int K) {
-    (void)K;
-    return sera_mmvq_rows_per_wave(N, M);
+    return sera_mmvq_rows_per_wave(N, K, M);
 }
 
 extern "C" int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,

@@ -215,12 +215,17 @@ def test_bench_refuses_more_than_one_gpu():
 
 def test_vec_dispatch_rule(L):
     """The MMVQ path's kernel choice by shape: the few-token kernel on tall
-    matrices from 3 tokens, on 4096-16383 rows from 5, never below 4096 rows."""
+    matrices from 3 tokens, on 4096-16383 rows from 6 (from 5 with K >=
+    16384), never below 4096 rows."""
     f = L.sera_q4k_vec_uses_fewtok
     assert [f(M, 25600, 5120) for M in range(1, 9)] == [0, 0, 1, 1, 1, 1, 1, 1]
     assert [f(M, 151936, 5120) for M in range(1, 9)] == [0, 0, 1, 1, 1, 1, 1, 1]
     for N in (5120, 8192):
         assert [f(M, N, 25600) for M in range(1, 9)] == [0, 0, 0, 0, 1, 1, 1, 1]
+        assert [f(M, N, 5120) for M in range(1, 9)] == [0, 0, 0, 0, 0, 1, 1, 1]
+    assert [L.sera_q4k_mmvq_rows_per_tile(M, 25600, 5120) for M in range(1, 9)] == [4, 4, 4, 4, 4, 2, 2, 2]
+    assert [L.sera_q4k_mmvq_rows_per_tile(M, 5120, 25600) for M in range(1, 9)] == [4, 8, 8, 8, 4, 2, 2, 2]
+    assert L.sera_q4k_mmvq_rows_per_tile(2, 151936, 5120) == 8
     assert [f(M, 1024, 5120) for M in range(1, 9)] == [0] * 8
     assert f(0, 25600, 5120) == 0 and f(9, 25600, 5120) == 0
 

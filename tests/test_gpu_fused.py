@@ -151,7 +151,7 @@ def test_silu_mul_producer_with_residual(torch, linear, qtype, M):
     check_close(y - y0, ref, "silu*up product")
 
 
-@pytest.mark.parametrize("M,Ns", [(3, [16384, 1024]), (5, [4096, 1024, 256]), (8, [4096, 1024])])
+@pytest.mark.parametrize("M,Ns", [(3, [16384, 1024]), (6, [4096, 1024, 256]), (8, [4096, 1024])])
 def test_q4k_group_mixes_grouped_dot4_and_fewtok(torch, linear, M, Ns):
     """A Q4_K group at decode whose matrices split between the kernels: the
     ones dot4 takes share one grouped launch, the tall ones run the
