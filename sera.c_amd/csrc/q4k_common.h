@@ -115,6 +115,27 @@ __device__ __forceinline__ uint32_t f2h_bits(float f) {
     return c.u;
 }
 
+/* Magic-seeded int8 MFMA epilogue. An int32 accumulator seeded with
+ * 0x4B400000 returns 0x4B400000 + I, which read as a float is exactly
+ * 1.5 * 2^23 + I for |I| < 2^22 (every per-32 dot: |I| <= 32 * 15 * 127).
+ * Then fma(F, sw, -1.5 * 2^23 * sw) is I * sw rounded once, with no
+ * integer-to-float convert; -1.5 * 2^23 * sw is exact whenever sw has at
+ * most 22 significant bits (fp16 products and d * sc with sc < 64). The
+ * seed comes from an opaque register so that the compiler keeps one copy
+ * live for every MFMA instead of rematerializing the moves per use. */
+#define SERA_MAGIC_BITS 0x4B400000
+#define SERA_MAGIC_F 12582912.0f
+template <int NR>
+__device__ __forceinline__ int __attribute__((ext_vector_type(NR))) sera_magic_seed() {
+    int m = SERA_MAGIC_BITS;
+    __asm__ volatile("" : "+v"(m));
+    int __attribute__((ext_vector_type(NR))) v;
+#pragma unroll
+    for (int r = 0; r < NR; r++) v[r] = m;
+    return v;
+}
+__device__ __forceinline__ float scaled_dot(int F, float sw, float nsw) { return fmaf(__int_as_float(F), sw, nsw); }
+
 /* 6-bit (scale, min) of sub-block j from the 12 scale bytes held as three
  * little-endian dwords s0 = bytes 0-3, s1 = bytes 4-7, s2 = bytes 8-11
  * (src/q3_quant.c:44-55). */

@@ -189,6 +189,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     ft_v4f acc[TG];
 #pragma unroll
     for (int tg = 0; tg < TG; tg++) acc[tg] = (ft_v4f){0.f, 0.f, 0.f, 0.f};
+    const v4i magic = sera_magic_seed<4>();
 
     auto compute = [&](int u, const FewtokW &w) {
         const float live = u < C ? 1.0f : 0.0f;
@@ -228,6 +229,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             const int j = jh >> 1, h = jh & 1;
             const int sbl = 4 * j + 2 * sg + h;
             const float swb = live * scale(((j ? sc47 : sc03) >> (8 * (2 * sg + h))) & 0xffu);
+            const float nswb = -SERA_MAGIC_F * swb;
             const ft_v4u q = w.q[j];
             v4i B;
             B.x = (int)((q.x >> (4 * h)) & 0x0F0F0F0Fu);
@@ -239,9 +241,10 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
                 const v4i A = *(const v4i *)(aoff[tg][jh] >= 0 ? (const void *)(xu + aoff[tg][jh])
                                                                : (const void *)zero);
                 const ft_v4f D8 = *(const ft_v4f *)&d8u[sbl * TOK + 8 * tg + tq];
-                const v4i I = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                /* magic-seeded: (I * scale) rounded once, then * d8 into acc */
+                const v4i F = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, magic, 0, 0, 0);
 #pragma unroll
-                for (int r = 0; r < 4; r++) acc[tg][r] = fmaf((float)I[r], D8[r] * swb, acc[tg][r]);
+                for (int r = 0; r < 4; r++) acc[tg][r] = fmaf(scaled_dot(F[r], swb, nswb), D8[r], acc[tg][r]);
             }
         }
     };

@@ -63,23 +63,7 @@ struct alignas(16) MmqSmem {
     alignas(16) _Float16 zero8[8];           /* a zero min-term operand */
 };
 
-/* The int32 accumulator seed whose result reads as the float 1.5 * 2^23 + I.
- * Built from an opaque register so that the compiler keeps one copy live for
- * every MFMA instead of rematerializing sixteen moves per use. */
-#define SERA_MAGIC_BITS 0x4B400000
-#define SERA_MAGIC_F 12582912.0f
-__device__ __forceinline__ v16i magic_seed() {
-    int m = SERA_MAGIC_BITS;
-    __asm__ volatile("" : "+v"(m));
-    v16i v;
-#pragma unroll
-    for (int r = 0; r < 16; r++) v[r] = m;
-    return v;
-}
-
-/* I * sw rounded once, from F = 1.5 * 2^23 + I (the magic-seeded MFMA
- * result) and nsw = -1.5 * 2^23 * sw (exact). */
-__device__ __forceinline__ float scaled_dot(int F, float sw, float nsw) { return fmaf(__int_as_float(F), sw, nsw); }
+__device__ __forceinline__ v16i magic_seed() { return sera_magic_seed<16>(); }
 
 /* Tile order: consecutive workgroup ids go to consecutive XCDs (8 on
  * MI355X). Give each XCD a contiguous run of tiles, token tiles fastest,
