@@ -19,6 +19,12 @@
  */
 #include "sera_launch.h"
 
+/* No floating-point contraction in this file: the values here must follow
+ * the reference's separately rounded multiplies and adds (hipcc fuses a * b
+ * + c into one FMA by default, and the _rn intrinsics are plain operators
+ * that do not prevent it). Explicit fmaf calls are unaffected. */
+#pragma clang fp contract(off)
+
 /* numpy add.reduce over 32 values: 0 + pairwise sum with 8 accumulators. */
 template <typename T>
 __device__ __forceinline__ T np_pairwise32(const T *a) {

@@ -31,6 +31,12 @@
  */
 #include "sera_launch.h"
 
+/* No floating-point contraction in this file: the values here must follow
+ * the reference's separately rounded multiplies and adds (hipcc fuses a * b
+ * + c into one FMA by default, and the _rn intrinsics are plain operators
+ * that do not prevent it). Explicit fmaf calls are unaffected. */
+#pragma clang fp contract(off)
+
 #define SEL_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
 
 namespace {

@@ -39,19 +39,26 @@
 #include "sera_launch.h"
 #include "sera_dpp.h"
 
+/* No floating-point contraction in this file: the values here must follow
+ * the reference's separately rounded multiplies and adds (hipcc fuses a * b
+ * + c into one FMA by default, and the _rn intrinsics are plain operators
+ * that do not prevent it). Explicit fmaf calls are unaffected. */
+#pragma clang fp contract(off)
+
 /* 1 / sqrt(mean(x^2) + eps) of one row, computed by all 256 threads of the
  * workgroup (every thread returns the same value). Thread t adds x[t+256i]^2
- * in i order; the loads go out 16 at a time (past K they read as zero, and
- * adding 0 to the non-negative running sum changes nothing). */
+ * in i order; the loads go out 32 at a time, so a row of up to 8192 values
+ * costs one memory round trip (past K they read as zero, and adding 0 to the
+ * non-negative running sum changes nothing). */
 __device__ __forceinline__ float q8_row_inv_rms(const float *__restrict__ xr, int K, float eps) {
     __shared__ float s_red[4];
     float s = 0.0f;
-    for (int k0 = threadIdx.x; k0 < K; k0 += 16 * 256) {
-        float v[16];
+    for (int k0 = threadIdx.x; k0 < K; k0 += 32 * 256) {
+        float v[32];
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = k0 + 256 * j < K ? xr[k0 + 256 * j] : 0.0f;
+        for (int j = 0; j < 32; j++) v[j] = k0 + 256 * j < K ? xr[k0 + 256 * j] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
+        for (int j = 0; j < 32; j++) {
             const double d = (double)v[j];
             s = (float)((double)s + d * d);
         }
@@ -73,31 +80,54 @@ __device__ __forceinline__ float q8_silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
 }
 
-/* The producer's value at (row, k) given the row's inv_rms. */
+/* The producer's value at (row, k). For RMSNorm the element and its gamma
+ * are loaded before the row's sum of squares (q8_produce_rms), so both
+ * travel in the same memory round trip as the reduction's loads. */
 template <int PK>
-__device__ __forceinline__ float q8_produce(const float *__restrict__ x, const sera_producer &p, size_t idx, int k,
-                                            float inv) {
+__device__ __forceinline__ float q8_produce(const float *__restrict__ x, const sera_producer &p, size_t idx) {
     const float v = x[idx];
-    if (PK == 1) return __fmul_rn(__fmul_rn(v, inv), p.gamma[k]);
     if (PK == 2) return q8_silu_mul(v, p.x2[idx]);
     return v;
 }
 
+__device__ __forceinline__ float q8_produce_rms(const float *__restrict__ x, const sera_producer &p, int row, int K,
+                                                int k) {
+    const float v = x[(size_t)row * K + k];
+    const float g = p.gamma[k];
+    const float inv = q8_row_inv_rms(x + (size_t)row * K, K, p.eps);
+    return __fmul_rn(__fmul_rn(v, inv), g);
+}
+
 template <int PK>
-__device__ __forceinline__ float4 q8_produce4(const float *__restrict__ x, const sera_producer &p, size_t idx, int k,
-                                              float inv) {
+__device__ __forceinline__ float4 q8_produce4(const float *__restrict__ x, const sera_producer &p, size_t idx) {
     const float4 v = *(const float4 *)(x + idx);
-    if (PK == 1) {
-        const float4 g = *(const float4 *)(p.gamma + k);
-        return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x), __fmul_rn(__fmul_rn(v.y, inv), g.y),
-                           __fmul_rn(__fmul_rn(v.z, inv), g.z), __fmul_rn(__fmul_rn(v.w, inv), g.w));
-    }
     if (PK == 2) {
         const float4 u = *(const float4 *)(p.x2 + idx);
         return make_float4(q8_silu_mul(v.x, u.x), q8_silu_mul(v.y, u.y), q8_silu_mul(v.z, u.z),
                            q8_silu_mul(v.w, u.w));
     }
     return v;
+}
+
+/* Four consecutive producer values (row, k..k+3) for the DS4 / Q6_K stage
+ * kernels: zeros for padding rows (row >= M) and for k >= K. Every thread
+ * of the workgroup takes part in the RMSNorm reduction, and its own values
+ * and gammas are loaded before it. */
+template <int PK>
+__device__ __forceinline__ float4 q8_produce4_row(const float *__restrict__ x, const sera_producer &p, int row, int M,
+                                                  int K, int k) {
+    const bool live = row < M && k < K;
+    if (PK == 1) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g = v;
+        if (live) {
+            v = *(const float4 *)(x + (size_t)row * K + k);
+            g = *(const float4 *)(p.gamma + k);
+        }
+        const float inv = row < M ? q8_row_inv_rms(x + (size_t)row * K, K, p.eps) : 0.0f;
+        return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x), __fmul_rn(__fmul_rn(v.y, inv), g.y),
+                           __fmul_rn(__fmul_rn(v.z, inv), g.z), __fmul_rn(__fmul_rn(v.w, inv), g.w));
+    }
+    return live ? q8_produce4<PK>(x, p, (size_t)row * K + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 /* One wave-64 handles two consecutive Q8_1 blocks (lanes 0-31 and 32-63);
@@ -109,8 +139,7 @@ __global__ __launch_bounds__(256) void sera_q8_1_row_kernel(
         uint32_t *__restrict__ ds, float4 *__restrict__ dsf) {
     const int row = blockIdx.y;
     const int k = blockIdx.x * 256 + threadIdx.x;
-    const float inv = PK == 1 ? q8_row_inv_rms(x + (size_t)row * K, K, prod.eps) : 0.0f;
-    const float xi = q8_produce<PK>(x, prod, (size_t)row * K + k, k, inv);
+    const float xi = PK == 1 ? q8_produce_rms(x, prod, row, K, k) : q8_produce<PK>(x, prod, (size_t)row * K + k);
 
     /* the 32-lane xor butterfly 16, 8, 4, 2, 1 of the reference (each lane
      * adds its partner's value; addition is commutative, so own + partner is
@@ -165,10 +194,8 @@ __global__ __launch_bounds__(256) void sera_q8_1_mmq_kernel(
         uint32_t *__restrict__ ds) {
     const int row = blockIdx.y;
     const int k = (blockIdx.x * 256 + threadIdx.x) * 4;
-    const float inv = PK == 1 && row < M ? q8_row_inv_rms(x + (size_t)row * K, K, prod.eps) : 0.0f;
+    const float4 v = q8_produce4_row<PK>(x, prod, row, M, K, k);
     if (k >= K) return;
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (row < M) v = q8_produce4<PK>(x, prod, (size_t)row * K + k, k, inv);
 
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     float sum = ((v.x + v.y) + v.z) + v.w;
@@ -209,10 +236,8 @@ __global__ __launch_bounds__(256) void sera_q8_1_q6k_stage_kernel(
         float *__restrict__ d8t) {
     const int row = blockIdx.y;
     const int k = (blockIdx.x * 256 + threadIdx.x) * 4;
-    const float inv = PK == 1 && row < M ? q8_row_inv_rms(x + (size_t)row * K, K, prod.eps) : 0.0f;
+    const float4 v = q8_produce4_row<PK>(x, prod, row, M, K, k);
     if (k >= K) return;
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (row < M) v = q8_produce4<PK>(x, prod, (size_t)row * K + k, k, inv);
 
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, xor_partner<4>(amax));

@@ -136,6 +136,29 @@ def test_rmsnorm_producer_is_bit_identical_to_unfused(torch, linear, qtype, M):
         assert np.array_equal(fused[i].view(np.uint32), plain[i].view(np.uint32)), i
 
 
+def test_rmsnorm_producer_rows_in_decode_batches(torch, linear):
+    """The RMSNorm producer on the row stage over 33 rows, in MMVQ-path
+    batches of up to 8: bit-identical to the unfused path fed with the
+    oracle's RMSNorm. Row 8 of this input is one whose block sums changed
+    when the compiler fused the producer's last multiply into the quantizer's
+    sum (the quantizer files are compiled without contraction)."""
+    K = 5120
+    Ns = [512, 256]
+    M = 33
+    rng = np.random.default_rng(7 * M + 12)
+    h = (rng.standard_normal((M, K)) * 2.5).astype(np.float32)
+    gamma = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    Ws = [weights(np.random.default_rng(99), 12, n, K) for n in Ns]
+    xn = oracle.rmsnorm_fused_order(h, gamma, 1e-6)
+    for r0 in range(0, M, 8):
+        hb, xb = h[r0:r0 + 8], xn[r0:r0 + 8]
+        say(f"case rmsnorm producer rows {r0}..{r0 + len(hb) - 1}")
+        fused = run_group(torch, 12, Ws, Ns, K, hb, flags=q3q4.LIN_RMSNORM, gamma=gamma, eps=1e-6)
+        plain = run_group(torch, 12, Ws, Ns, K, xb)
+        for i in range(len(Ns)):
+            assert np.array_equal(fused[i].view(np.uint32), plain[i].view(np.uint32)), (r0, i)
+
+
 @pytest.mark.parametrize("qtype,M", [(12, 1), (12, 8), (12, 40), (14, 1), (14, 6), (14, 64)])
 def test_silu_mul_producer_with_residual(torch, linear, qtype, M):
     """The down projection step: y += (silu(g) * u) . W^T."""
