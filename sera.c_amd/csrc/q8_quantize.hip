@@ -48,15 +48,20 @@
 /* 1 / sqrt(mean(x^2) + eps) of one row, computed by all 256 threads of the
  * workgroup (every thread returns the same value). Thread t adds x[t+256i]^2
  * in i order; the loads go out 32 at a time, so a row of up to 8192 values
- * costs one memory round trip (past K they read as zero, and adding 0 to the
- * non-negative running sum changes nothing). */
+ * costs one memory round trip. Past K a load reads the last element (a
+ * valid address, no branch) and its value is replaced by zero, which the
+ * non-negative running sum absorbs unchanged; a branch around each load
+ * made the compiler wait for every load on its own. */
 __device__ __forceinline__ float q8_row_inv_rms(const float *__restrict__ xr, int K, float eps) {
     __shared__ float s_red[4];
     float s = 0.0f;
     for (int k0 = threadIdx.x; k0 < K; k0 += 32 * 256) {
         float v[32];
 #pragma unroll
-        for (int j = 0; j < 32; j++) v[j] = k0 + 256 * j < K ? xr[k0 + 256 * j] : 0.0f;
+        for (int j = 0; j < 32; j++) {
+            const float t = xr[min(k0 + 256 * j, K - 1)];
+            v[j] = k0 + 256 * j < K ? t : 0.0f;
+        }
 #pragma unroll
         for (int j = 0; j < 32; j++) {
             const double d = (double)v[j];
