@@ -340,7 +340,8 @@ static hipError_t launch_mmvq(MmvqGroup grp, const int8_t *xq, const float4 *dsf
  *   2-4 tokens: 8 where more rows per loaded activation slice pay for a
  *     smaller grid - a long K (down, 25600: 19.4 / 20.7 / 23.0 at 2 / 3 /
  *     4 tokens against 19.5 / 21.9 / 24.3 with 4) or a very tall matrix
- *     (LM head at 2: 75.1 against 81.9) - and 4 elsewhere (gate/up 16.0
+ *     (LM head at 2: 75.1 against 81.9), or 3-4 tokens on 8192 rows and
+ *     more (q: 7.5 / 8.4 against 7.8 / 9.1) - and 4 elsewhere (gate/up 16.0
  *     against 16.2, o 5.7 / 6.6 / 8.2 against 6.6 / 7.8 / 8.7, k/v 2.8 /
  *     3.1 / 3.5 against 3.4 / 4.0 / 4.5);
  *   5 tokens: 4 (k/v 3.8 against 4.1 with 2);
@@ -348,7 +349,7 @@ static hipError_t launch_mmvq(MmvqGroup grp, const int8_t *xq, const float4 *dsf
  *     k/v at 8 tokens 5.3 against 18.7). */
 extern "C" int sera_mmvq_rows_per_wave(int N, int K, int M) {
     if (M <= 1) return 4;
-    if (M <= 4) return (K >= 16384 || N >= 65536) ? 8 : 4;
+    if (M <= 4) return (K >= 16384 || N >= 65536 || (M >= 3 && N >= 8192)) ? 8 : 4;
     if (M == 5) return 4;
     return 2;
 }

@@ -223,9 +223,11 @@ def test_vec_dispatch_rule(L):
     for N in (5120, 8192):
         assert [f(M, N, 25600) for M in range(1, 9)] == [0, 0, 0, 0, 1, 1, 1, 1]
         assert [f(M, N, 5120) for M in range(1, 9)] == [0, 0, 0, 0, 0, 1, 1, 1]
-    assert [L.sera_q4k_mmvq_rows_per_tile(M, 25600, 5120) for M in range(1, 9)] == [4, 4, 4, 4, 4, 2, 2, 2]
+    assert [L.sera_q4k_mmvq_rows_per_tile(M, 25600, 5120) for M in range(1, 9)] == [4, 4, 8, 8, 4, 2, 2, 2]
     assert [L.sera_q4k_mmvq_rows_per_tile(M, 5120, 25600) for M in range(1, 9)] == [4, 8, 8, 8, 4, 2, 2, 2]
     assert L.sera_q4k_mmvq_rows_per_tile(2, 151936, 5120) == 8
+    assert [L.sera_q4k_mmvq_rows_per_tile(M, 8192, 5120) for M in range(1, 6)] == [4, 4, 8, 8, 4]
+    assert [L.sera_q4k_mmvq_rows_per_tile(M, 5120, 8192) for M in range(1, 6)] == [4, 4, 4, 4, 4]
     assert [f(M, 1024, 5120) for M in range(1, 9)] == [0] * 8
     assert f(0, 25600, 5120) == 0 and f(9, 25600, 5120) == 0
 
