@@ -53,12 +53,32 @@ typedef __attribute__((address_space(1))) const void ft_global_cvoid;
 
 #define SERA_FEWTOK_MAX_TOKENS 16
 #define SERA_FEWTOK_LDS_CHUNK_TOKENS 320   /* chunk x staged tokens: 40 super-blocks of 8, 20 of 16 */
+#define SERA_FEWTOK_XROW (Q4K_QK + 16)     /* LDS bytes per staged token and super-block: 16 columns + a pad */
+
+/* Zero bytes read by the lanes whose MFMA operand is zero: they address
+ * the zero area with the same immediate offsets as the real lanes (up to
+ * one token group of rows and 160 bytes of columns, plus 16). */
+static constexpr __host__ __device__ int fewtok_zero_bytes(int tok) { return (tok / 8 - 1) * 8 * SERA_FEWTOK_XROW + 176; }
+
+/* LDS byte offset of the zero area: after the scale factors, moved up to
+ * 224 mod 256. A 16-byte read of 8 real lanes covers 32 consecutive banks
+ * starting at 32 j + 8 h + {0, 4, 16, 20} (mod 64, 4-byte banks); the zero
+ * lanes of the same 16 read 4 banks at 56 + 32 j + 8 h, outside all four. */
+static inline __host__ __device__ int fewtok_zero_offset(int chunk, int tok) {
+    const int end = chunk * tok * (SERA_FEWTOK_XROW + 2 * 8 * (int)sizeof(float));
+    return end + ((224 - end) & 255);
+}
 
 /* LDS bytes of a workgroup for `chunk` super-blocks of `tok` staged tokens:
- * quants, d8, the min-term activation factor, and a 16-byte zero operand. */
-static inline size_t fewtok_lds_bytes(int chunk, int tok) {
-    return (size_t)chunk * tok * (Q4K_QK + 2 * 8 * sizeof(float)) + 16;
+ * quants (padded rows), d8, the min-term activation factor, the zero area. */
+static inline __host__ __device__ size_t fewtok_lds_bytes(int chunk, int tok) {
+    return (size_t)fewtok_zero_offset(chunk, tok) + fewtok_zero_bytes(tok);
 }
+
+/* Row of sub-block b in the min-term factors [u][row][token]: sub-blocks g
+ * and 4 + g, which one lane reads together, sit in adjacent rows (one
+ * token row apart, so the pair never shares a bank). */
+__device__ __forceinline__ int fewtok_mslot(int b) { return (b & 3) * 2 + (b >> 2); }
 
 struct FewtokW {
     ft_v4u hd;      /* d | dmin, 12 scale bytes */
@@ -86,20 +106,21 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     const int nkb = K / Q4K_QK;
     const int kb0 = blockIdx.y * chunk;
     const int C = min(nkb - kb0, chunk);
-    /* LDS: quants [u][t][256] | d8 [u][b][t] | min factor [u][b][t] | zero */
+    /* LDS: quants [u][t][272] | d8 [u][b][t] | min factor [u][mslot(b)][t] | zero */
     int8_t *xs = (int8_t *)ft_smem;
-    float *d8s = (float *)(ft_smem + (size_t)chunk * TOK * Q4K_QK);
+    float *d8s = (float *)(ft_smem + (size_t)chunk * TOK * SERA_FEWTOK_XROW);
     float *mns = d8s + (size_t)chunk * 8 * TOK;
-    uint8_t *zero = (uint8_t *)(mns + (size_t)chunk * 8 * TOK);
+    uint8_t *zero = ft_smem + fewtok_zero_offset(chunk, TOK);
 
     constexpr int RW = 16 * NW;       /* weight rows per workgroup */
     int row = blockIdx.x * RW + 16 * wave + n;
     const bool row_ok = row < N;
     if (!row_ok) row = N - 1;         /* clamp; never stored */
     const uint8_t *wr = W + ((size_t)row * nkb + kb0) * Q4K_BLOCK_BYTES;
-    /* super-block u of the chunk; u past the chunk re-reads the last one
-     * (its contribution is scaled by zero), so the loop has no branches
-     * around loads and the compiler's load counting stays exact */
+    /* super-block u of the chunk; u past the chunk (the prefetch after the
+     * last pair) re-reads the last one and is never used, so the loop has
+     * no branches around loads and the compiler's load counting stays
+     * exact */
     auto load = [&](int u, FewtokW &w) {
         const uint8_t *b = wr + (size_t)min(u, C - 1) * Q4K_BLOCK_BYTES;
         w.hd = *(const ft_v4u *)b;
@@ -111,14 +132,21 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
 
     /* --- stage the chunk's activations --- */
     {
-        /* quants: 16-byte piece (u, token t, column c) at LDS column c ^ t;
-         * one wave-instruction writes 1 KB; tokens past M copy the last */
-        const int pieces = C * TOK * 16;
-        for (int base = wave * 64; base < pieces; base += NW * 64) {
-            const int q = min(base + lane, pieces - 1);
-            const int u = q / (TOK * 16), t = (q >> 4) % TOK, col = q & 15;
-            const int8_t *src = xq + (size_t)min(t, M - 1) * K + (size_t)(kb0 + u) * Q4K_QK + 16 * (col ^ t);
-            __builtin_amdgcn_global_load_lds((ft_global_cvoid *)src, (ft_lds_void *)(xs + (size_t)base * 16), 16, 0, 0);
+        /* quants: 16-byte slot s of token row (u, t) holds column s (slot
+         * 16 is the row's pad, filled with a copy of column 15 and never
+         * read); one wave-instruction writes 64 consecutive slots (1 KB),
+         * lanes past the chunk are masked off; tokens past M copy the last.
+         * The 272-byte rows put 8 consecutive tokens' reads of one column on
+         * distinct banks, and every operand of a lane sits at a constant
+         * offset from one base. */
+        const int slots = C * TOK * 17;
+        for (int base = wave * 64; base < slots; base += NW * 64) {
+            const int q = base + lane;
+            const int u = q / (TOK * 17), r = q - u * (TOK * 17), t = r / 17, col = min(r - t * 17, 15);
+            const int8_t *src = xq + (size_t)min(t, M - 1) * K + (size_t)(kb0 + u) * Q4K_QK + 16 * col;
+            if (q < slots)
+                __builtin_amdgcn_global_load_lds((ft_global_cvoid *)src, (ft_lds_void *)(xs + (size_t)base * 16), 16, 0,
+                                                 0);
         }
         /* scales, transposed to [u][sub-block][token]: all loads first, then
          * the LDS writes. FORM 0: float4 (d_2p, d_2p+1, dS_2p, dS_2p+1) per
@@ -149,8 +177,8 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
                     float *d8u = d8s + u * 8 * TOK, *mnu = mns + u * 8 * TOK;
                     d8u[(2 * p) * TOK + t] = __uint_as_float(f[r].x);
                     d8u[(2 * p + 1) * TOK + t] = __uint_as_float(f[r].y);
-                    mnu[(2 * p) * TOK + t] = __uint_as_float(f[r].z);
-                    mnu[(2 * p + 1) * TOK + t] = __uint_as_float(f[r].w);
+                    mnu[fewtok_mslot(2 * p) * TOK + t] = __uint_as_float(f[r].z);
+                    mnu[fewtok_mslot(2 * p + 1) * TOK + t] = __uint_as_float(f[r].w);
                 } else {
                     const int u = i / (TOK * 2), t = (i >> 1) % TOK, p = i & 1;
                     float *d8u = d8s + u * 8 * TOK, *mnu = mns + u * 8 * TOK;
@@ -158,44 +186,63 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         d8u[(4 * p + e) * TOK + t] = h2f_bits(ds[e] & 0xffffu);
-                        mnu[(4 * p + e) * TOK + t] = h2f_bits(ds[e] >> 16);
+                        mnu[fewtok_mslot(4 * p + e) * TOK + t] = h2f_bits(ds[e] >> 16);
                     }
                 }
             }
         }
-        if (tid == 0) *(ft_v4u *)zero = (ft_v4u){0u, 0u, 0u, 0u};
+        for (int i = tid; i < fewtok_zero_bytes(TOK) / 16; i += NW * 64) ((ft_v4u *)zero)[i] = (ft_v4u){0u, 0u, 0u, 0u};
     }
     __builtin_amdgcn_s_waitcnt(0);    /* this thread's loads to LDS have landed */
     __syncthreads();
 
-    /* A operand offsets: lane (row i = n, group g) is real when (i < 8) ==
-     * (g < 2): token 8 tg + (i & 7) on sub-block 4j + 2 (i >> 3) + h, 16
-     * bytes at k-half hq; other lanes read the zero operand */
-    int aoff[TG][4];
-    bool m_real[TG];
-#pragma unroll
-    for (int tg = 0; tg < TG; tg++) {
-        const int t = 8 * tg + (n & 7);
-        const bool a_real = ((n < 8) == (g < 2)) && t < M;
-#pragma unroll
-        for (int jh = 0; jh < 4; jh++) {
-            const int sbk = 4 * (jh >> 1) + 2 * (n >> 3) + (jh & 1);
-            aoff[tg][jh] = a_real ? t * Q4K_QK + 16 * ((2 * sbk + hq) ^ t) : -1;
-        }
-        m_real[tg] = n < 8 && 8 * tg + n < M;
-    }
+    /* A operand: lane (row i = n, group g) is real when (i < 8) == (g < 2):
+     * token 8 tg + (i & 7) on sub-block 4j + 2 (i >> 3) + h, 16 bytes at
+     * k-half hq, i.e. column 2 (4j + 2 (i >> 3) + h) + hq of the token row.
+     * Every (tg, j, h) is a constant offset from the lane's base for super-
+     * block u, a_base + u * a_step; the other lanes have step 0 and a base
+     * in the zero area, so they read zeros at the same offsets. Staged
+     * tokens past M hold copies of the last token; their results are never
+     * stored. The min-term A (FORM 0 d8*S, FORM 1 the fp16 sum of x) works
+     * the same way: lanes n < 8 read token 8 tg + n of sub-blocks g, 4 + g. */
+    const bool a_real = (n < 8) == (g < 2);
+    const int zoff = (int)(zero - (uint8_t *)ft_smem);
+    const int a_base = a_real ? (n & 7) * SERA_FEWTOK_XROW + 16 * (4 * (n >> 3) + hq) : zoff;
+    const int a_step = a_real ? TOK * SERA_FEWTOK_XROW : 0;
+    const int m_base = n < 8 ? (int)((uint8_t *)mns - (uint8_t *)ft_smem) + 4 * (2 * g * TOK + n) : zoff;
+    const int m_step = n < 8 ? 4 * 8 * TOK : 0;
     const int sg = g >> 1;            /* result sub-block: 4j + 2 sg + h */
     const int tq = 4 * hq;            /* result tokens 8 tg + tq .. + 3 */
+    /* FORM 1 scale bytes as fp16 1024 + v: v_perm puts sub-block bytes
+     * (2 sg, 2 sg + 1) under exponent byte 0x64 (selector bytes 0-3 pick
+     * the scale word, 4 the 0x64 word) */
+    const uint32_t sel_sc = (2u * sg) | (4u << 8) | ((2u * sg + 1u) << 16) | (4u << 24);
     ft_v4f acc[TG];
 #pragma unroll
     for (int tg = 0; tg < TG; tg++) acc[tg] = (ft_v4f){0.f, 0.f, 0.f, 0.f};
     const v4i magic = sera_magic_seed<4>();
 
     auto compute = [&](int u, const FewtokW &w) {
-        const float live = u < C ? 1.0f : 0.0f;
-        const int uu = min(u, C - 1);
-        const int8_t *xu = xs + (size_t)uu * TOK * Q4K_QK;
-        const float *d8u = d8s + uu * 8 * TOK, *mnu = mns + uu * 8 * TOK;
+        const uint8_t *au = ft_smem + a_base + u * a_step;
+        const uint8_t *mu = ft_smem + m_base + u * m_step;
+        const float *d8u = d8s + u * 8 * TOK;
+        /* the super-block's LDS operands first: they do not wait for the
+         * weights, so their latency overlaps the wait for the header */
+        v4i Ar[4][TG];
+        ft_v4f D8r[4][TG];
+        float am0[TG], am1[TG];
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) {
+            am0[tg] = *(const float *)(mu + 32 * tg);
+            am1[tg] = *(const float *)(mu + 4 * TOK + 32 * tg);
+        }
+#pragma unroll
+        for (int jh = 0; jh < 4; jh++)
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++) {
+                Ar[jh][tg] = *(const v4i *)(au + 8 * SERA_FEWTOK_XROW * tg + 32 * (jh & 1) + 128 * (jh >> 1));
+                D8r[jh][tg] = *(const ft_v4f *)&d8u[(4 * (jh >> 1) + 2 * sg + (jh & 1)) * TOK + 8 * tg + tq];
+            }
         /* (scale, min) bytes of sub-blocks 0-3 and 4-7 (src/q3_quant.c:44-55) */
         const ft_v4u hd = w.hd;
         const uint32_t sc03 = hd.y & 0x3F3F3F3Fu;
@@ -204,31 +251,45 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         const uint32_t m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
         /* sub-block scale and min products: FORM 0 exact in fp32 (d*sc,
          * -dmin*m); FORM 1 one fp16 rounding each, as the reference's half2
-         * store (d, dmin) * (1, -1) * (sc, m) */
-        auto scale = [&](uint32_t v) -> float {
-            if (FORM == 0) return h2f_bits(hd.x & 0xffffu) * (float)v;
-            return (float)((_Float16)v * (_Float16)h2f_bits(hd.x & 0xffffu));
-        };
-        auto minp = [&](uint32_t v) -> float {
-            if (FORM == 0) return -h2f_bits(hd.x >> 16) * (float)v;
-            return (float)((_Float16)v * (_Float16)(-h2f_bits(hd.x >> 16)));
-        };
+         * store (d, dmin) * (1, -1) * (sc, m): the bytes become fp16 1024 + v,
+         * an exact subtraction leaves v, one packed RNE multiply the product */
+        float swv[4], bm0, bm1;
+        if constexpr (FORM == 0) {
+            const float d = h2f_bits(hd.x & 0xffffu), ndmin = -h2f_bits(hd.x >> 16);
+            const uint32_t s03 = sc03 >> (16 * sg), s47 = sc47 >> (16 * sg);
+            swv[0] = d * (float)(s03 & 0xffu);
+            swv[1] = d * (float)((s03 >> 8) & 0xffu);
+            swv[2] = d * (float)(s47 & 0xffu);
+            swv[3] = d * (float)((s47 >> 8) & 0xffu);
+            bm0 = ndmin * (float)((m03 >> (8 * g)) & 0xffu);
+            bm1 = ndmin * (float)((m47 >> (8 * g)) & 0xffu);
+        } else {
+            typedef _Float16 ft_h2 __attribute__((ext_vector_type(2)));
+            const ft_h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+            const uint32_t dd = (hd.x & 0xffffu) * 0x10001u, nm = (hd.x >> 16) * 0x10001u ^ 0x80008000u;
+            const ft_h2 d2 = __builtin_bit_cast(ft_h2, dd), nm2 = __builtin_bit_cast(ft_h2, nm);
+            const ft_h2 p03 = (__builtin_bit_cast(ft_h2, __builtin_amdgcn_perm(0x64646464u, sc03, sel_sc)) - bias) * d2;
+            const ft_h2 p47 = (__builtin_bit_cast(ft_h2, __builtin_amdgcn_perm(0x64646464u, sc47, sel_sc)) - bias) * d2;
+            const uint32_t mg = __builtin_amdgcn_perm(m47, m03, (uint32_t)g | ((4u + g) << 8));
+            const ft_h2 pm = (__builtin_bit_cast(ft_h2, __builtin_amdgcn_perm(0x64646464u, mg, 0x04010400u)) - bias) * nm2;
+            swv[0] = (float)p03.x;
+            swv[1] = (float)p03.y;
+            swv[2] = (float)p47.x;
+            swv[3] = (float)p47.y;
+            bm0 = (float)pm.x;
+            bm1 = (float)pm.y;
+        }
         /* min term: lane (n, g) gives A[n][g] and B[g][n] for sub-blocks g
-         * and 4 + g (A: FORM 0 d8*S, FORM 1 the fp16 sum of x) */
-        const float bm0 = live * minp((m03 >> (8 * g)) & 0xffu);
-        const float bm1 = live * minp((m47 >> (8 * g)) & 0xffu);
+         * and 4 + g */
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
-            const float am0 = m_real[tg] ? mnu[g * TOK + 8 * tg + n] : 0.0f;
-            const float am1 = m_real[tg] ? mnu[(4 + g) * TOK + 8 * tg + n] : 0.0f;
-            acc[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(am0, bm0, acc[tg], 0, 0, 0);
-            acc[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(am1, bm1, acc[tg], 0, 0, 0);
+            acc[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(am0[tg], bm0, acc[tg], 0, 0, 0);
+            acc[tg] = __builtin_amdgcn_mfma_f32_16x16x4f32(am1[tg], bm1, acc[tg], 0, 0, 0);
         }
 #pragma unroll
         for (int jh = 0; jh < 4; jh++) {
             const int j = jh >> 1, h = jh & 1;
-            const int sbl = 4 * j + 2 * sg + h;
-            const float swb = live * scale(((j ? sc47 : sc03) >> (8 * (2 * sg + h))) & 0xffu);
+            const float swb = swv[jh];
             const float nswb = -SERA_MAGIC_F * swb;
             const ft_v4u q = w.q[j];
             v4i B;
@@ -238,9 +299,8 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             B.w = (int)((q.w >> (4 * h)) & 0x0F0F0F0Fu);
 #pragma unroll
             for (int tg = 0; tg < TG; tg++) {
-                const v4i A = *(const v4i *)(aoff[tg][jh] >= 0 ? (const void *)(xu + aoff[tg][jh])
-                                                               : (const void *)zero);
-                const ft_v4f D8 = *(const ft_v4f *)&d8u[sbl * TOK + 8 * tg + tq];
+                const v4i A = Ar[jh][tg];
+                const ft_v4f D8 = D8r[jh][tg];
                 /* magic-seeded: (I * scale) rounded once, then * d8 into acc */
                 const v4i F = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, magic, 0, 0, 0);
 #pragma unroll
@@ -254,7 +314,8 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
      * each compute): 4-6% faster at 4-8 tokens (gate/up 19.6 -> 18.5 us,
      * down 25.3 -> 23.9), equal at 16; deeper prefetch, in groups of 2-5
      * super-blocks or only before the staging, was slower at every size. */
-    for (int u0 = 0; u0 < C; u0 += 2) {
+    int u0 = 0;
+    for (; u0 + 1 < C; u0 += 2) {
         load(u0 + 1, wb);
         __builtin_amdgcn_sched_barrier(0);
         compute(u0, wa);
@@ -264,6 +325,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         compute(u0 + 1, wb);
         __builtin_amdgcn_sched_barrier(0);
     }
+    if (u0 < C) compute(u0, wa);   /* odd chunk: the last super-block */
     /* lanes g and g ^ 2 hold the two sub-block halves of the same outputs */
 #pragma unroll
     for (int tg = 0; tg < TG; tg++)
