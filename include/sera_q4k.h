@@ -180,6 +180,13 @@ int sera_q4k_fewtok(int form, const void *W, const void *stage, float *Y, float 
                     int K, int chunk, int accum, void *stream);
 int sera_q4k_fewtok_splits(int M, int N, int K, int chunk);
 int sera_q4k_fewtok_groups(int M, int N, int K);
+/* Workgroups along the rows of that launch on the current device: the row
+ * groups, or fewer when the grid is persistent (one K split, an even number
+ * of super-blocks, more row groups than the device holds at once: each
+ * workgroup stages the activations once for a balanced range of 16-row
+ * tiles); -1 for a chunk past the limit, 0 for an invalid shape. No
+ * counterpart in the reference (a query of this build's launch shape). */
+int sera_q4k_fewtok_grid(int form, int M, int N, int K, int chunk);
 
 /* Device Q4_K dequant, w = (d*sc)*q - (dmin*m) per weight; replaces
  * q3_cuda_dequantize_row (src/q3_cuda_primitives.h, cuda/q3_cuda_primitives.cu:13-95). */

@@ -89,11 +89,11 @@ struct FewtokW {
  * (dsf: d8, d8*S as fp32); FORM 1: MMQ formula on an MMQ stage (ds: fp16
  * d8, fp16 sum of x), cuda/mmq/mmq.cuh:2269-2283,1440-1472:
  *   y = sum_b fp16(d*sc_b) * d8_b * I_b + fp16(-dmin*m_b) * s8_b */
-template <int NW, int TG, int FORM>
+template <int NW, int TG, int FORM, bool PERSIST>
 __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq, const void *__restrict__ xsc,
         float *__restrict__ y, float *__restrict__ slots, int *__restrict__ counters, int M, int N, int K,
-        int chunk, int accum) {
+        int chunk, int accum, int out_tiles) {
     constexpr int TOK = 8 * TG;                          /* staged tokens */
     extern __shared__ __attribute__((aligned(16))) uint8_t ft_smem[];
     __shared__ int s_last;
@@ -111,24 +111,50 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     float *d8s = (float *)(ft_smem + (size_t)chunk * TOK * SERA_FEWTOK_XROW);
     float *mns = d8s + (size_t)chunk * 8 * TOK;
     uint8_t *zero = ft_smem + fewtok_zero_offset(chunk, TOK);
+    /* PERSIST: results of the workgroup's tiles, [token][row], out_tiles
+     * tiles of 16 rows per token */
+    float *outb = (float *)(ft_smem + fewtok_lds_bytes(chunk, TOK));
+    const int ocap = 16 * out_tiles;
 
-    constexpr int RW = 16 * NW;       /* weight rows per workgroup */
-    int row = blockIdx.x * RW + 16 * wave + n;
-    const bool row_ok = row < N;
-    if (!row_ok) row = N - 1;         /* clamp; never stored */
-    const uint8_t *wr = W + ((size_t)row * nkb + kb0) * Q4K_BLOCK_BYTES;
-    /* super-block u of the chunk; u past the chunk (the prefetch after the
-     * last pair) re-reads the last one and is never used, so the loop has
-     * no branches around loads and the compiler's load counting stays
-     * exact */
-    auto load = [&](int u, FewtokW &w) {
-        const uint8_t *b = wr + (size_t)min(u, C - 1) * Q4K_BLOCK_BYTES;
+    /* 16-row tiles. One tile per wave: wave w of workgroup b takes tile
+     * NW b + w (rows past N are clamped and never stored; split K's
+     * hand-off counts the NW tiles of a workgroup). PERSIST (one K split,
+     * an even chunk, a grid smaller than the tile groups): the workgroup
+     * stages its chunk once and takes a balanced range [tb, te) of all
+     * ceil(N / 16) tiles; wave w starts on tile tb + w and then takes the
+     * next free one from an LDS counter. */
+    __shared__ int s_next;
+    int tb, te;
+    if constexpr (!PERSIST) {
+        tb = blockIdx.x * NW;
+        te = tb + NW;
+    } else {
+        const long T = (N + 15) / 16;
+        tb = (int)(blockIdx.x * T / gridDim.x);
+        te = (int)((blockIdx.x + 1) * T / gridDim.x);
+    }
+    int tile = tb + wave;
+    int row;
+    bool row_ok;
+    const uint8_t *wr, *wnext;
+    auto rows_of = [&](int t, int &r, bool &ok) {
+        r = 16 * t + n;
+        ok = r < N;
+        if (!ok) r = N - 1;
+    };
+    rows_of(tile, row, row_ok);
+    wr = W + ((size_t)row * nkb + kb0) * Q4K_BLOCK_BYTES;
+    /* super-block u of the chunk (u < C; the loop never asks for more) */
+    auto load_from = [&](const uint8_t *base, int u, FewtokW &w) {
+        const uint8_t *b = base + (size_t)u * Q4K_BLOCK_BYTES;
         w.hd = *(const ft_v4u *)b;
         w.q[0] = *(const ft_v4u *)(b + 16 + 16 * g);
         w.q[1] = *(const ft_v4u *)(b + 80 + 16 * g);
     };
+    auto load = [&](int u, FewtokW &w) { load_from(wr, u, w); };
     FewtokW wa, wb;
-    load(0, wa);    /* in flight during the activation staging */
+    if (tile < te) load(0, wa);    /* in flight during the activation staging */
+    if (PERSIST && tid == 0) s_next = 0;
 
     /* --- stage the chunk's activations --- */
     {
@@ -218,8 +244,6 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
      * the scale word, 4 the 0x64 word) */
     const uint32_t sel_sc = (2u * sg) | (4u << 8) | ((2u * sg + 1u) << 16) | (4u << 24);
     ft_v4f acc[TG];
-#pragma unroll
-    for (int tg = 0; tg < TG; tg++) acc[tg] = (ft_v4f){0.f, 0.f, 0.f, 0.f};
     const v4i magic = sera_magic_seed<4>();
 
     auto compute = [&](int u, const FewtokW &w) {
@@ -308,82 +332,145 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             }
         }
     };
+    /* one tile's results: split K hands partials to the last split; one
+     * tile per wave stores directly; PERSIST keeps them in LDS, so its loop
+     * issues no global stores and the load counting stays exact across
+     * tiles. Returns false when this workgroup's split is not the last. */
+    auto finish = [&]() -> bool {
+        /* lanes g and g ^ 2 hold the two sub-block halves of the same outputs */
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[tg][r] += __shfl_xor(acc[tg][r], 32, 64);
+        const bool owner = g < 2 && row_ok;
+
+        if (gridDim.y > 1) {
+            /* split K: this split's partial of the tile goes to
+             * slots[split][t][row] with device-scope stores, so the hand-off
+             * needs no cache-wide fence */
+            const int S = gridDim.y;
+            if (owner) {
+                float *mine = slots + (size_t)blockIdx.y * M * N;
+#pragma unroll
+                for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int t = 8 * tg + tq + r;
+                        if (t < M)
+                            __hip_atomic_store(&mine[(size_t)t * N + row], acc[tg][r], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    }
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0)
+                s_last = __hip_atomic_fetch_add(&counters[blockIdx.x], 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+            __syncthreads();
+            if (!s_last) return false;
+            if (tid == 0) __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (owner) {
+#pragma unroll
+                for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int t = 8 * tg + tq + r;
+                        if (t >= M) continue;
+                        const size_t at = (size_t)t * N + row;
+                        float v = __hip_atomic_load(&slots[at], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        for (int k = 1; k < S; k++)
+                            v += __hip_atomic_load(&slots[(size_t)k * M * N + at], __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                        acc[tg][r] = v;
+                    }
+            }
+        }
+        if constexpr (!PERSIST) {
+            if (owner) {
+#pragma unroll
+                for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int t = 8 * tg + tq + r;
+                        if (t < M) {
+                            float *dst = y + (size_t)t * N + row;
+                            *dst = accum ? *dst + acc[tg][r] : acc[tg][r];
+                        }
+                    }
+            }
+        } else if (g < 2) {
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) outb[(8 * tg + tq + r) * ocap + 16 * (tile - tb) + n] = acc[tg][r];
+        }
+        return true;
+    };
     /* One super-block in flight, issued before the current one's compute
      * (the scheduling barriers keep each load group ahead of the compute it
      * overlaps). Measured against two in flight (the next two issued after
      * each compute): 4-6% faster at 4-8 tokens (gate/up 19.6 -> 18.5 us,
      * down 25.3 -> 23.9), equal at 16; deeper prefetch, in groups of 2-5
      * super-blocks or only before the staging, was slower at every size. */
-    int u0 = 0;
-    for (; u0 + 1 < C; u0 += 2) {
-        load(u0 + 1, wb);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(u0, wa);
-        __builtin_amdgcn_sched_barrier(0);
-        load(u0 + 2, wa);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(u0 + 1, wb);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    if (u0 < C) compute(u0, wa);   /* odd chunk: the last super-block */
-    /* lanes g and g ^ 2 hold the two sub-block halves of the same outputs */
+    if constexpr (!PERSIST) {
 #pragma unroll
-    for (int tg = 0; tg < TG; tg++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) acc[tg][r] += __shfl_xor(acc[tg][r], 32, 64);
-    const bool owner = g < 2 && row_ok;
-
-    if (gridDim.y > 1) {
-        /* split K: this split's partial of the tile goes to slots[split][t][row]
-         * with device-scope stores, so the hand-off needs no cache-wide fence */
-        const int S = gridDim.y;
-        if (owner) {
-            float *mine = slots + (size_t)blockIdx.y * M * N;
-#pragma unroll
-            for (int tg = 0; tg < TG; tg++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int t = 8 * tg + tq + r;
-                    if (t < M)
-                        __hip_atomic_store(&mine[(size_t)t * N + row], acc[tg][r], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
+        for (int tg = 0; tg < TG; tg++) acc[tg] = (ft_v4f){0.f, 0.f, 0.f, 0.f};
+        int u0 = 0;
+        for (; u0 + 1 < C; u0 += 2) {
+            load(u0 + 1, wb);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(u0, wa);
+            __builtin_amdgcn_sched_barrier(0);
+            load(min(u0 + 2, C - 1), wa);   /* past the chunk: re-read, unused */
+            __builtin_amdgcn_sched_barrier(0);
+            compute(u0 + 1, wb);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0)
-            s_last = __hip_atomic_fetch_add(&counters[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                     S - 1;
-        __syncthreads();
-        if (!s_last) return;
-        if (tid == 0) __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (owner) {
+        if (u0 < C) compute(u0, wa);   /* odd chunk: the last super-block */
+        finish();
+    } else {
+        while (tile < te) {
 #pragma unroll
-            for (int tg = 0; tg < TG; tg++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int t = 8 * tg + tq + r;
-                    if (t >= M) continue;
-                    const size_t at = (size_t)t * N + row;
-                    float v = __hip_atomic_load(&slots[at], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    for (int k = 1; k < S; k++)
-                        v += __hip_atomic_load(&slots[(size_t)k * M * N + at], __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                    acc[tg][r] = v;
-                }
-        }
-    }
-    if (owner) {
-#pragma unroll
-        for (int tg = 0; tg < TG; tg++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = 8 * tg + tq + r;
-                if (t < M) {
-                    float *dst = y + (size_t)t * N + row;
-                    *dst = accum ? *dst + acc[tg][r] : acc[tg][r];
-                }
+            for (int tg = 0; tg < TG; tg++) acc[tg] = (ft_v4f){0.f, 0.f, 0.f, 0.f};
+            /* the wave's next tile; its first super-block is the last pair's
+             * second load (past the range it re-reads this tile's rows) */
+            int next = 0;
+            if (lane == 0)
+                next = tb + NW + __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            next = __builtin_amdgcn_readfirstlane(next);
+            int nrow;
+            bool nrow_ok;
+            rows_of(next < te ? next : tile, nrow, nrow_ok);
+            wnext = W + ((size_t)nrow * nkb + kb0) * Q4K_BLOCK_BYTES;
+            /* even chunk: the select on an opaque flag keeps one loop body and
+             * its exact load counting (the compiler would peel the last pair) */
+            for (int u0 = 0; u0 < C; u0 += 2) {
+                load(u0 + 1, wb);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(u0, wa);
+                __builtin_amdgcn_sched_barrier(0);
+                int last = u0 + 2 == C;
+                __asm__ volatile("" : "+v"(last));
+                load_from(last ? wnext : wr + (size_t)(u0 + 2) * Q4K_BLOCK_BYTES, 0, wa);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(u0 + 1, wb);
+                __builtin_amdgcn_sched_barrier(0);
             }
+            finish();
+            tile = next;
+            row = nrow;
+            row_ok = nrow_ok;
+            wr = wnext;
+        }
+        /* the workgroup's rows [16 tb, 16 te) of every token, coalesced */
+        __syncthreads();
+        const int r0 = 16 * tb, nr = min(16 * te, N) - r0;
+        for (int i = tid; i < nr * M; i += NW * 64) {
+            const int t = i / nr, r = i - t * nr;
+            float *dst = y + (size_t)t * N + r0 + r;
+            const float v = outb[t * ocap + r];
+            *dst = accum ? *dst + v : v;
+        }
     }
 }
 
@@ -435,14 +522,74 @@ extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk) {
 }
 
 
+/* Workgroups of one launch that the device holds at once (CUs times the
+ * occupancy the kernel's registers and LDS allow), per device. */
+template <int NW, int TG, int FORM>
+static int fewtok_resident(size_t lds) {
+    constexpr bool PERSIST = true;
+    static int cus[16];                /* per device */
+    static int cache[16][8][2];        /* [device][slot] -> (lds bytes, workgroups per CU) */
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
+    if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    const int slot = (int)((lds >> 4) & 7);
+    if (cache[dev][slot][0] != (int)lds || cache[dev][slot][1] <= 0) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sera_q4k_fewtok_kernel<NW, TG, FORM, PERSIST>,
+                                                          NW * 64, lds) != hipSuccess)
+            return 0;
+        cache[dev][slot][0] = (int)lds;
+        cache[dev][slot][1] = per_cu;
+    }
+    return cus[dev] * cache[dev][slot][1];
+}
+
+/* Grid (workgroups along the rows), persistent-buffer tiles (0: one tile
+ * per wave) and LDS bytes of a launch on the current device. */
+template <int NW, int TG, int FORM>
+static void fewtok_grid(int N, int K, int chunk, int *groups_out, int *out_tiles_out, size_t *lds_out) {
+    const int nkb = K / Q4K_QK;
+    const int splits = (nkb + chunk - 1) / chunk;
+    const size_t base = fewtok_lds_bytes(chunk, 8 * TG);
+    const int tiles = (N + 15) / 16;
+    int groups = (N + 16 * NW - 1) / (16 * NW), out_tiles = 0;
+    size_t lds = base;
+    if (splits == 1 && (nkb & 1) == 0) {
+        /* more tile groups than resident workgroups: a persistent grid, each
+         * workgroup staging the activations once for its range of tiles and
+         * keeping the results in LDS until its last tile (the buffer's size
+         * feeds back into the occupancy, hence the two rounds) */
+        auto out_bytes = [&](int g) { return (size_t)((tiles + g - 1) / g) * 16 * 8 * TG * sizeof(float); };
+        const int natural = groups;
+        for (int round = 0; round < 2; round++) {
+            const int resident = fewtok_resident<NW, TG, FORM>(base + out_bytes(groups));
+            if (resident > 0 && groups > resident) groups = resident;
+        }
+        if (groups < natural) {
+            out_tiles = (tiles + groups - 1) / groups;
+            lds = base + out_bytes(groups);
+        }
+    }
+    *groups_out = groups;
+    *out_tiles_out = out_tiles;
+    *lds_out = lds;
+}
+
 template <int NW, int TG, int FORM>
 static hipError_t launch_fewtok(const uint8_t *W, const int8_t *xq, const void *xsc, float *y, float *slots,
                                 int *counters, int M, int N, int K, int chunk, int accum, hipStream_t s) {
-    const int nkb = K / Q4K_QK;
-    const int splits = (nkb + chunk - 1) / chunk;
-    dim3 grid((N + 16 * NW - 1) / (16 * NW), splits);
-    hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM>), grid, dim3(NW * 64), fewtok_lds_bytes(chunk, 8 * TG),
-                       s, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum);
+    const int splits = (K / Q4K_QK + chunk - 1) / chunk;
+    int groups, out_tiles;
+    size_t lds;
+    fewtok_grid<NW, TG, FORM>(N, K, chunk, &groups, &out_tiles, &lds);
+    dim3 grid(groups, splits);
+    if (out_tiles > 0)
+        hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM, true>), grid, dim3(NW * 64), lds, s, W, xq, xsc, y,
+                           slots, counters, M, N, K, chunk, accum, out_tiles);
+    else
+        hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM, false>), grid, dim3(NW * 64), lds, s, W, xq, xsc, y,
+                           slots, counters, M, N, K, chunk, accum, 0);
     return hipGetLastError();
 }
 
@@ -479,4 +626,27 @@ extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const 
                                       c, accum, s);
     return launch_fewtok_nw<1, 1>(nw, w, (const int8_t *)(base + L.qs), base + L.ds, y, slots, counters, M, N, K, c,
                                   accum, s);
+}
+
+/* Workgroups along the rows of the launch sera_launch_q4k_fewtok_acc makes
+ * on the current device (fewer than the row groups when the grid is
+ * persistent), or -1 for an invalid chunk. */
+extern "C" int sera_fewtok_grid(int form, int M, int N, int K, int chunk) {
+    int nw, c;
+    sera_fewtok_plan(M, N, K, &nw, &c);
+    if (chunk > 0) c = chunk;
+    if (c > sera_fewtok_max_chunk(M)) return -1;
+    int groups = 0, out_tiles = 0;
+    size_t lds = 0;
+    const bool tg2 = form == 1 && M > 8;
+    if (nw == 8) {
+        if (tg2) fewtok_grid<8, 2, 1>(N, K, c, &groups, &out_tiles, &lds);
+        else if (form == 1) fewtok_grid<8, 1, 1>(N, K, c, &groups, &out_tiles, &lds);
+        else fewtok_grid<8, 1, 0>(N, K, c, &groups, &out_tiles, &lds);
+    } else {
+        if (tg2) fewtok_grid<4, 2, 1>(N, K, c, &groups, &out_tiles, &lds);
+        else if (form == 1) fewtok_grid<4, 1, 1>(N, K, c, &groups, &out_tiles, &lds);
+        else fewtok_grid<4, 1, 0>(N, K, c, &groups, &out_tiles, &lds);
+    }
+    return groups;
 }

@@ -60,6 +60,7 @@ void sera_fewtok_plan(int M, int N, int K, int *nwave, int *chunk);
 int sera_fewtok_max_chunk(int M);
 int sera_fewtok_groups(int M, int N, int K);
 int sera_fewtok_splits(int M, int N, int K, int chunk);
+int sera_fewtok_grid(int form, int M, int N, int K, int chunk);
 hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
                                       int *counters, int M, int N, int K, int chunk, int accum, hipStream_t s);
 

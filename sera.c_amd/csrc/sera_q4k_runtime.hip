@@ -275,6 +275,13 @@ extern "C" int sera_q4k_fewtok_groups(int M, int N, int K) {
     return sera_fewtok_groups(M, N, K);
 }
 
+extern "C" int sera_q4k_fewtok_grid(int form, int M, int N, int K, int chunk) {
+    if (M <= 0 || M > SERA_Q4K_FEWTOK_MMQ_MAX_BATCH || (form == 0 && M > 8) || (form != 0 && form != 1) || N <= 0 ||
+        K <= 0 || K % Q4K_QK || chunk < 0)
+        return 0;
+    return sera_fewtok_grid(form, M, N, K, chunk);
+}
+
 extern "C" int sera_q4k_fewtok(int form, const void *W, const void *stage, float *Y, float *slots, int *counters,
                                int M, int N, int K, int chunk, int accum, void *stream) {
     if (!W || !stage || !Y) return fail(-1, "sera_q4k_fewtok: null pointer");

@@ -105,6 +105,7 @@ def load():
         "sera_q4k_fewtok": ([I, P, P, P, P, P, I, I, I, I, I, P], I),
         "sera_q4k_fewtok_splits": ([I, I, I, I], I),
         "sera_q4k_fewtok_groups": ([I, I, I], I),
+        "sera_q4k_fewtok_grid": ([I, I, I, I, I], I),
         "sera_q4k_kernel_launches": ([I, I, I], I),
         "sera_q4k_vec_uses_fewtok": ([I, I, I], I),
         "sera_q6k_vec_uses_tile": ([I, I, I], I),
@@ -293,6 +294,12 @@ def fewtok_splits(M, N, K, chunk=0):
 
 def fewtok_groups(M, N, K):
     return load().sera_q4k_fewtok_groups(M, N, K)
+
+
+def fewtok_grid(form, M, N, K, chunk=0):
+    """Workgroups along the rows of the launch on the current device (fewer
+    than fewtok_groups when the grid is persistent)."""
+    return load().sera_q4k_fewtok_grid(form, M, N, K, chunk)
 
 
 def dequantize(W, nblocks, out, stream=None):

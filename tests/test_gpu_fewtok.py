@@ -8,8 +8,9 @@ another order, so it also sits within 2e-5 * rms, far inside the gap between
 the two formulas (the fp16 rounding of d*sc alone moves y by ~1e-4 * rms):
 that pins which formula runs. Split-K results repeat bit for bit and leave
 the row-group counters at zero; accumulate adds exactly the product; the
-boundary (q3_cuda_q4k_linear) runs this kernel where sera_q4k_vec_uses_fewtok
-says so (2-8 tokens) and at 9 tokens.
+persistent grid (more tiles than resident workgroups) matches the oracle and
+repeats; the boundary (q3_cuda_q4k_linear) runs this kernel where
+sera_q4k_vec_uses_fewtok says so (2-8 tokens) and at 9 tokens.
 """
 import sys
 
@@ -149,6 +150,51 @@ def test_fewtok_split_repeats_and_accumulates(torch):
         acc = base.clone()
         run_fewtok(torch, Wd, stage, M, N, K, chunk, y=acc, accum=True)
         assert torch.equal(acc, base + a), "accumulate is not y + product"
+
+
+# (N, K): more 16-row tiles than the device's resident workgroups take in
+# one pass, so the launch is persistent when the K chunk is one even split
+# (ragged N; 2 and 10 super-blocks); the odd 3-super-block K keeps one tile
+# per wave
+PERSIST_SHAPES = [(70001, 512), (40000, 2560), (70001, 768)]
+
+
+@pytest.mark.parametrize("N,K", PERSIST_SHAPES)
+def test_fewtok_persistent_grid(torch, N, K):
+    """Workgroups that stage the activations once and walk a range of tiles
+    (results held in LDS, written out at the end): both formulas against the
+    oracle, repeats bit for bit, accumulate adds exactly the product."""
+    rng = np.random.default_rng(17 * N + K)
+    W = rand_weights(rng, N, K)
+    Wd = dev(torch, W)
+    nkb = K // 256
+    ran_persistent = False
+    for form, M in ((0, 4), (0, 8), (1, 9), (1, 16)):
+        x = outlier_activations(rng, M, K)
+        if form == 0:
+            stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+            q3q4.quantize_row(dev(torch, x), stage)
+            xq, xd, _ = oracle.q8_1_row(x)
+            ref = oracle.gemm_mmvq(W, xq, xd, N, K)
+        else:
+            stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+            q3q4.quantize_mmq(dev(torch, x), stage)
+            xq, xd, xs = oracle.q8_1_mmq(x)
+            ref = oracle.gemm_mmq(W, xq, xd, xs, N, K)
+        grid, groups = q3q4.fewtok_grid(form, M, N, K), q3q4.fewtok_groups(M, N, K)
+        persistent = q3q4.fewtok_splits(M, N, K) == 1 and grid < groups
+        ran_persistent |= persistent
+        assert persistent or nkb % 2 or q3q4.fewtok_splits(M, N, K) > 1 or grid == groups
+        say(f"case fewtok persistent={persistent} form={form} M={M} N={N} K={K} grid={grid} groups={groups}")
+        y, _ = run_fewtok(torch, Wd, stage, M, N, K, 0, form=form)
+        check_close(y.cpu().numpy(), ref, f"fewtok form {form} M={M} N={N} K={K}", TIGHT)
+        b, _ = run_fewtok(torch, Wd, stage, M, N, K, 0, form=form)
+        assert torch.equal(y, b), "repeat differs"
+        base = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
+        acc = base.clone()
+        run_fewtok(torch, Wd, stage, M, N, K, 0, y=acc, accum=True, form=form)
+        assert torch.equal(acc, base + y), "accumulate is not y + product"
+    assert ran_persistent == (nkb % 2 == 0), "the persistent grid was not exercised"
 
 
 def test_fewtok_matches_dot4_mmvq(torch):
