@@ -54,6 +54,10 @@ typedef __attribute__((address_space(1))) const void ft_global_cvoid;
 #define SERA_FEWTOK_MAX_TOKENS 16
 #define SERA_FEWTOK_LDS_CHUNK_TOKENS 320   /* chunk x staged tokens: 40 super-blocks of 8, 20 of 16 */
 #define SERA_FEWTOK_XROW (Q4K_QK + 16)     /* LDS bytes per staged token and super-block: 16 columns + a pad */
+/* waves per workgroup of a persistent grid (one workgroup per CU: 2 waves
+ * per SIMD); 12 waves for one token group, 3 per SIMD, measured 8% slower
+ * on the LM head */
+template <int TG> constexpr int fewtok_persist_waves() { return 8; }
 
 /* Zero bytes read by the lanes whose MFMA operand is zero: they address
  * the zero area with the same immediate offsets as the real lanes (up to
@@ -548,27 +552,31 @@ static int fewtok_resident(size_t lds) {
 /* Grid (workgroups along the rows), persistent-buffer tiles (0: one tile
  * per wave) and LDS bytes of a launch on the current device. */
 template <int NW, int TG, int FORM>
-static void fewtok_grid(int N, int K, int chunk, int *groups_out, int *out_tiles_out, size_t *lds_out) {
+static void fewtok_grid(int N, int K, int chunk, bool allow_persist, int *groups_out, int *out_tiles_out,
+                        size_t *lds_out) {
     const int nkb = K / Q4K_QK;
     const int splits = (nkb + chunk - 1) / chunk;
     const size_t base = fewtok_lds_bytes(chunk, 8 * TG);
     const int tiles = (N + 15) / 16;
     int groups = (N + 16 * NW - 1) / (16 * NW), out_tiles = 0;
     size_t lds = base;
-    if (splits == 1 && (nkb & 1) == 0) {
-        /* more tile groups than resident workgroups: a persistent grid, each
-         * workgroup staging the activations once for its range of tiles and
-         * keeping the results in LDS until its last tile (the buffer's size
-         * feeds back into the occupancy, hence the two rounds) */
-        auto out_bytes = [&](int g) { return (size_t)((tiles + g - 1) / g) * 16 * 8 * TG * sizeof(float); };
-        const int natural = groups;
-        for (int round = 0; round < 2; round++) {
-            const int resident = fewtok_resident<NW, TG, FORM>(base + out_bytes(groups));
-            if (resident > 0 && groups > resident) groups = resident;
-        }
-        if (groups < natural) {
-            out_tiles = (tiles + groups - 1) / groups;
-            lds = base + out_bytes(groups);
+    if constexpr (NW == fewtok_persist_waves<TG>()) {
+        if (allow_persist && splits == 1 && (nkb & 1) == 0) {
+            /* more tile groups than resident workgroups: a persistent grid,
+             * each workgroup staging the activations once for its range of
+             * tiles and keeping the results in LDS until its last tile (the
+             * buffer's size feeds back into the occupancy, hence the two
+             * rounds) */
+            auto out_bytes = [&](int g) { return (size_t)((tiles + g - 1) / g) * 16 * 8 * TG * sizeof(float); };
+            const int natural = groups;
+            for (int round = 0; round < 2; round++) {
+                const int resident = fewtok_resident<NW, TG, FORM>(base + out_bytes(groups));
+                if (resident > 0 && groups > resident) groups = resident;
+            }
+            if (groups < natural) {
+                out_tiles = (tiles + groups - 1) / groups;
+                lds = base + out_bytes(groups);
+            }
         }
     }
     *groups_out = groups;
@@ -576,20 +584,13 @@ static void fewtok_grid(int N, int K, int chunk, int *groups_out, int *out_tiles
     *lds_out = lds;
 }
 
-template <int NW, int TG, int FORM>
+template <int NW, int TG, int FORM, bool PERSIST>
 static hipError_t launch_fewtok(const uint8_t *W, const int8_t *xq, const void *xsc, float *y, float *slots,
-                                int *counters, int M, int N, int K, int chunk, int accum, hipStream_t s) {
-    const int splits = (K / Q4K_QK + chunk - 1) / chunk;
-    int groups, out_tiles;
-    size_t lds;
-    fewtok_grid<NW, TG, FORM>(N, K, chunk, &groups, &out_tiles, &lds);
-    dim3 grid(groups, splits);
-    if (out_tiles > 0)
-        hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM, true>), grid, dim3(NW * 64), lds, s, W, xq, xsc, y,
-                           slots, counters, M, N, K, chunk, accum, out_tiles);
-    else
-        hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM, false>), grid, dim3(NW * 64), lds, s, W, xq, xsc, y,
-                           slots, counters, M, N, K, chunk, accum, 0);
+                                int *counters, int M, int N, int K, int chunk, int accum, int groups, int out_tiles,
+                                size_t lds, hipStream_t s) {
+    dim3 grid(groups, (K / Q4K_QK + chunk - 1) / chunk);
+    hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM, PERSIST>), grid, dim3(NW * 64), lds, s, W, xq, xsc, y,
+                       slots, counters, M, N, K, chunk, accum, out_tiles);
     return hipGetLastError();
 }
 
@@ -597,8 +598,21 @@ template <int TG, int FORM>
 static hipError_t launch_fewtok_nw(int nw, const uint8_t *W, const int8_t *xq, const void *xsc, float *y,
                                    float *slots, int *counters, int M, int N, int K, int chunk, int accum,
                                    hipStream_t s) {
-    if (nw == 8) return launch_fewtok<8, TG, FORM>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, s);
-    return launch_fewtok<4, TG, FORM>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, s);
+    constexpr int P = fewtok_persist_waves<TG>();
+    int groups, out_tiles;
+    size_t lds;
+    fewtok_grid<P, TG, FORM>(N, K, chunk, true, &groups, &out_tiles, &lds);
+    if (out_tiles > 0)
+        return launch_fewtok<P, TG, FORM, true>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups,
+                                                out_tiles, lds, s);
+    if (nw == 8) {
+        fewtok_grid<8, TG, FORM>(N, K, chunk, false, &groups, &out_tiles, &lds);
+        return launch_fewtok<8, TG, FORM, false>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups, 0,
+                                                 lds, s);
+    }
+    fewtok_grid<4, TG, FORM>(N, K, chunk, false, &groups, &out_tiles, &lds);
+    return launch_fewtok<4, TG, FORM, false>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups, 0, lds,
+                                             s);
 }
 
 /* y (+)= X . W^T for 1 <= M <= 16. form 0: row stage, MMVQ formula (M <= 8);
@@ -639,14 +653,9 @@ extern "C" int sera_fewtok_grid(int form, int M, int N, int K, int chunk) {
     int groups = 0, out_tiles = 0;
     size_t lds = 0;
     const bool tg2 = form == 1 && M > 8;
-    if (nw == 8) {
-        if (tg2) fewtok_grid<8, 2, 1>(N, K, c, &groups, &out_tiles, &lds);
-        else if (form == 1) fewtok_grid<8, 1, 1>(N, K, c, &groups, &out_tiles, &lds);
-        else fewtok_grid<8, 1, 0>(N, K, c, &groups, &out_tiles, &lds);
-    } else {
-        if (tg2) fewtok_grid<4, 2, 1>(N, K, c, &groups, &out_tiles, &lds);
-        else if (form == 1) fewtok_grid<4, 1, 1>(N, K, c, &groups, &out_tiles, &lds);
-        else fewtok_grid<4, 1, 0>(N, K, c, &groups, &out_tiles, &lds);
-    }
-    return groups;
+    if (tg2) fewtok_grid<fewtok_persist_waves<2>(), 2, 1>(N, K, c, true, &groups, &out_tiles, &lds);
+    else if (form == 1) fewtok_grid<fewtok_persist_waves<1>(), 1, 1>(N, K, c, true, &groups, &out_tiles, &lds);
+    else fewtok_grid<fewtok_persist_waves<1>(), 1, 0>(N, K, c, true, &groups, &out_tiles, &lds);
+    if (out_tiles > 0) return groups;
+    return (N + 16 * nw - 1) / (16 * nw);
 }
