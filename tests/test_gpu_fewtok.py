@@ -169,7 +169,7 @@ def test_fewtok_persistent_grid(torch, N, K):
     Wd = dev(torch, W)
     nkb = K // 256
     ran_persistent = False
-    for form, M in ((0, 4), (0, 8), (1, 9), (1, 16)):
+    for form, M in ((0, 4), (0, 8), (1, 4), (1, 9), (1, 16)):
         x = outlier_activations(rng, M, K)
         if form == 0:
             stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")

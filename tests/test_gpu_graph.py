@@ -73,7 +73,8 @@ def kernel_of(qtype, M, N, K):
 # split K on the row stage (form 0: a 4096-row matrix from 5 tokens, a tall
 # one from 3) and on the MMQ stage (form 1, 9 tokens); the paired MMQ tile
 # with split-K + reduce; stream-K; the 64-token tile with split-K + reduce;
-# Q6_K MMVQ and the Q6_K tile kernel on the row-formula stage
+# Q6_K MMVQ and the Q6_K tile kernel on the row-formula stage; the few-token
+# kernel's persistent grid (more 16-row tiles than resident workgroups)
 CASES = [
     (12, 1, 4096, 5120, "dot4"),
     (12, 6, 2048, 5120, "dot4"),
@@ -86,14 +87,21 @@ CASES = [
     (14, 1, 2048, 5120, "q6k-mmvq"),
     (14, 8, 2048, 5120, "q6k-mmvq"),
     (14, 8, 4096, 5120, "q6k-tile"),
+    (12, 16, 70001, 512, "fewtok-mmq-persistent"),
 ]
 
 
 @pytest.mark.parametrize("qtype,M,N,K,kernel", CASES)
 def test_graph_replay_matches_eager(torch, linear, qtype, M, N, K, kernel):
     say(f"case graph qtype={qtype} M={M} N={N} K={K} kernel={kernel}")
+    persistent = kernel.endswith("-persistent")
+    kernel = kernel.replace("-persistent", "")
     assert kernel_of(qtype, M, N, K) == kernel, "dispatch moved: choose a case that reaches this kernel"
-    if kernel.startswith("fewtok"):
+    if persistent:
+        form = 1 if kernel == "fewtok-mmq" else 0
+        assert q3q4.fewtok_splits(M, N, K) == 1 and q3q4.fewtok_grid(form, M, N, K) < q3q4.fewtok_groups(M, N, K), \
+            "case meant to run the few-token kernel's persistent grid"
+    elif kernel.startswith("fewtok"):
         assert q3q4.fewtok_splits(M, N, K) > 1, "case meant to split K inside the few-token kernel"
     rng = np.random.default_rng(1000 * M + qtype)
     Wd = torch.from_numpy(weights(rng, qtype, N, K)).cuda()
