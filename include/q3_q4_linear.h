@@ -54,7 +54,9 @@ typedef struct {
 } q3_q4_linear_geometry;
 
 /* GGUF dim[0] = K (row length), dim[1] = N (row count). Fails on a qtype
- * other than Q4_K (12) / Q6_K (14), zero dims, K % 256 != 0 or dims above
+ * other than Q4_K (12) / Q6_K (14) or the two device layouts of
+ * include/sera_q4k.h (SERA_QTYPE_Q4K_TILED, which also needs N % 16 == 0,
+ * and SERA_QTYPE_Q6K_SPLIT), zero dims, K % 256 != 0 or dims above
  * INT32_MAX. Pure host. Replaces src/q3_q4_linear.h:65-69
  * (src/q3_q4_linear.cu:48-91). */
 bool q3_q4_linear_bind_geometry(uint32_t qtype,
@@ -84,9 +86,9 @@ const char *q3_cuda_q4k_linear_path_for_batch(size_t token_count);
 /* Y[M][N] = X[M][K] . W^T with device pointers only; enqueue-only on
  * `stream` (no host sync, no allocation, no host copies). Returns false
  * with `error` filled on any failure. Q4_K (12) and Q6_K (14) geometries
- * both run, as in the reference (src/q3_q4_linear.cu:199-209), and so does
- * a Q6_K geometry bound to the split device layout (SERA_QTYPE_Q6K_SPLIT,
- * include/sera_q4k.h). Replaces src/q3_q4_linear.h:99-106
+ * both run, as in the reference (src/q3_q4_linear.cu:199-209), and so do
+ * geometries bound to the device layouts (SERA_QTYPE_Q4K_TILED,
+ * SERA_QTYPE_Q6K_SPLIT, include/sera_q4k.h). Replaces src/q3_q4_linear.h:99-106
  * (src/q3_q4_linear.cu:149-228). */
 bool q3_cuda_q4k_linear(const q3_q4_linear_geometry *geometry,
                         const void *weight,

@@ -65,6 +65,26 @@ int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
 int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
 
+/* Q4_K weights in the 16-row tiled device layout (no reference
+ * counterpart; the reference keeps GGUF bytes on the device,
+ * cuda/q3_model_loader_cuda.cu:290-342): block b of row r at byte
+ * ((r/16)*(K/256) + b)*2304 + (r%16)*144, i.e. 16-row tiles one after the
+ * other, each tile super-block by super-block, each super-block's 16 rows
+ * back to back. Same 144-byte blocks and byte count as GGUF; N % 16 == 0.
+ * A 16-row group of one super-block is one contiguous 2304-byte run, which
+ * the few-token and MMQ kernels read with full-line loads. Values and
+ * results are those of the GGUF bytes. sera_weight_upload /
+ * sera_weight_to_device_layout produce it; a q3_q4_linear geometry and the
+ * group, gathered-row and upload calls may carry this qtype. */
+#define SERA_QTYPE_Q4K_TILED 268u
+
+/* sera_q4k_dense / sera_q4k_dense_vec on the weight layout of qtype: 12
+ * (GGUF bytes, what the two calls above take) or SERA_QTYPE_Q4K_TILED. */
+int sera_q4k_dense_qt(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
+                      void *stream, int timed);
+int sera_q4k_dense_vec_qt(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
+                          void *stream, int timed);
+
 /* The MMVQ path of sera_q4k_dense_vec, allocating nothing and needing no
  * attached workspace. No counterpart in the reference: it is for callers
  * that cannot allocate device memory or attach a workspace (code under HIP
@@ -280,8 +300,9 @@ int sera_q6k_mmq_splits_for(int M, int N, int K);
  * Replaces the verbatim tensor copy of the reference's resident loader
  * (q3_loader_load, cuda/q3_model_loader_cuda.cu:171-373; pinned staging +
  * H2D + D2D at :290-342) for the weights of this path. qtype names the
- * device layout: 12 and 14 keep the GGUF bytes (a plain copy), and
- * SERA_QTYPE_Q6K_SPLIT repacks GGUF Q6_K bytes into the split layout on the
+ * device layout: 12 and 14 keep the GGUF bytes (a plain copy),
+ * SERA_QTYPE_Q4K_TILED repacks GGUF Q4_K bytes into the tiled layout and
+ * SERA_QTYPE_Q6K_SPLIT GGUF Q6_K bytes into the split layout, on the
  * device. The source is always the tensor's GGUF bytes (N rows of K/256
  * blocks). */
 
@@ -290,7 +311,8 @@ int sera_q6k_mmq_splits_for(int M, int N, int K);
 size_t sera_weight_bytes(uint32_t qtype, int N, int K);
 
 /* GGUF bytes already on the device -> dst in the layout of qtype (enqueue
- * only). Split: gguf 2-byte aligned, dst 16-byte aligned, no overlap. */
+ * only). Split: gguf 2-byte aligned, dst 16-byte aligned, no overlap.
+ * Tiled: both 16-byte aligned, no overlap, N % 16 == 0. */
 int sera_weight_to_device_layout(uint32_t qtype, int N, int K, const void *gguf, void *dst, void *stream);
 
 /* Host GGUF bytes -> dst in the layout of qtype, on `stream` (enqueue
@@ -298,7 +320,9 @@ int sera_weight_to_device_layout(uint32_t qtype, int N, int K, const void *gguf,
  * for hipMemcpyAsync; pinned memory makes the copies asynchronous). The
  * split layout streams the bytes through the caller's device staging
  * buffer (>= 210 bytes, 16-byte aligned; whole blocks per pass) and repacks
- * each pass into dst; GGUF layouts copy straight to dst (staging unused). */
+ * each pass into dst; the tiled layout likewise, whole 16-row groups per
+ * pass (staging >= 16 * K/256 * 144 bytes); GGUF layouts copy straight to
+ * dst (staging unused). */
 int sera_weight_upload(uint32_t qtype, int N, int K, const void *host_gguf, void *dst, void *staging,
                        size_t staging_bytes, void *stream);
 
@@ -348,7 +372,8 @@ typedef struct {
     unsigned flags;
 } sera_linear_group_call;
 
-/* ---- gathered rows of a Q4_K (12) / Q6_K (14, SERA_QTYPE_Q6K_SPLIT) matrix ---
+/* ---- gathered rows of a Q4_K (12, SERA_QTYPE_Q4K_TILED) / Q6_K (14,
+ * SERA_QTYPE_Q6K_SPLIT) matrix ---
  * fp32 dequant with the expression order of src/q3_quant.c:57-103 (Q4_K
  * (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32)) and the GGUF Q6_K byte mapping of
  * q3_quant.c. The reference's device twin q6_value_dev

@@ -14,9 +14,15 @@
 #include <string.h>
 
 enum { QTYPE_Q4_K = 12, QTYPE_Q6_K = 14 };
-/* Q6_K in the split device layout (sera_weight_upload); an extension of
- * the reference's qtype set, accepted wherever Q6_K is. */
+/* Q6_K in the split device layout and Q4_K in the 16-row tiled one
+ * (sera_weight_upload); extensions of the reference's qtype set, accepted
+ * wherever Q6_K / Q4_K is. The tiled layout needs N % 16 == 0. */
 #define QTYPE_Q6_K_SPLIT SERA_QTYPE_Q6K_SPLIT
+#define QTYPE_Q4_K_TILED SERA_QTYPE_Q4K_TILED
+
+static bool known_qtype(uint32_t qtype) {
+    return qtype == QTYPE_Q4_K || qtype == QTYPE_Q4_K_TILED || qtype == QTYPE_Q6_K || qtype == QTYPE_Q6_K_SPLIT;
+}
 #define QK_K 256
 #define Q4_K_BLOCK_BYTES 144
 #define Q6_K_BLOCK_BYTES 210
@@ -36,7 +42,7 @@ bool q3_q4_linear_bind_geometry(uint32_t qtype, uint32_t gguf_rows_dim0, uint32_
                                 q3_q4_linear_geometry *out, char *error, size_t error_len) {
     if (!out) return false;
     memset(out, 0, sizeof(*out));
-    if (qtype != QTYPE_Q4_K && qtype != QTYPE_Q6_K && qtype != QTYPE_Q6_K_SPLIT) {
+    if (!known_qtype(qtype)) {
         set_error(error, error_len, "q3_q4_linear: tensor qtype is not Q4_K/Q6_K");
         return false;
     }
@@ -57,11 +63,16 @@ bool q3_q4_linear_bind_geometry(uint32_t qtype, uint32_t gguf_rows_dim0, uint32_
         set_error(error, error_len, "q3_q4_linear: geometry exceeds int32");
         return false;
     }
+    if (qtype == QTYPE_Q4_K_TILED && N % 16 != 0) {
+        set_error(error, error_len, "q3_q4_linear: the tiled Q4_K layout needs a row count divisible by 16");
+        return false;
+    }
     out->K = (int32_t)K;
     out->N = (int32_t)N;
     out->qtype = qtype;
     out->M = 0;
-    out->weight_bytes = N * (K / QK_K) * (qtype == QTYPE_Q4_K ? Q4_K_BLOCK_BYTES : Q6_K_BLOCK_BYTES);
+    out->weight_bytes = N * (K / QK_K) *
+                        (qtype == QTYPE_Q4_K || qtype == QTYPE_Q4_K_TILED ? Q4_K_BLOCK_BYTES : Q6_K_BLOCK_BYTES);
     return true;
 }
 
@@ -131,11 +142,11 @@ bool q3_cuda_q4k_linear(const q3_q4_linear_geometry *geometry, const void *weigh
         set_error(error, error_len, "q3_q4_linear: unresolved geometry");
         return false;
     }
-    if (geometry->qtype != QTYPE_Q4_K && geometry->qtype != QTYPE_Q6_K && geometry->qtype != QTYPE_Q6_K_SPLIT) {
+    if (!known_qtype(geometry->qtype)) {
         set_error(error, error_len, "q3_q4_linear: tensor qtype is not Q4_K/Q6_K");
         return false;
     }
-    const bool q6 = geometry->qtype != QTYPE_Q4_K;
+    const bool q6 = geometry->qtype == QTYPE_Q6_K || geometry->qtype == QTYPE_Q6_K_SPLIT;
 
     q3_q4_linear_stats local;
     q3_q4_linear_stats *s = stats ? stats : &local;
@@ -152,13 +163,13 @@ bool q3_cuda_q4k_linear(const q3_q4_linear_geometry *geometry, const void *weigh
     if (tokens <= SERA_Q4K_MMVQ_MAX_BATCH) {
         rc = q6 ? sera_q6k_dense_vec(geometry->qtype, weight, device_input, device_output, tokens, features, K,
                                      stream, stats != NULL)
-                : sera_q4k_dense_vec(weight, device_input, device_output, tokens, features, K, stream,
-                                     stats != NULL);
+                : sera_q4k_dense_vec_qt(geometry->qtype, weight, device_input, device_output, tokens, features, K,
+                                        stream, stats != NULL);
     } else {
         rc = q6 ? sera_q6k_dense(geometry->qtype, weight, device_input, device_output, tokens, features, K,
                                  stream, stats != NULL)
-                : sera_q4k_dense(weight, device_input, device_output, tokens, features, K, stream,
-                                 stats != NULL);
+                : sera_q4k_dense_qt(geometry->qtype, weight, device_input, device_output, tokens, features, K,
+                                    stream, stats != NULL);
     }
     s->kernel_launches = (uint64_t)(q6 ? sera_q6k_kernel_launches(tokens, features, K)
                                        : sera_q4k_kernel_launches(tokens, features, K));

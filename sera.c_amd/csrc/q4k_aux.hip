@@ -294,6 +294,30 @@ __global__ __launch_bounds__(256) void sera_q4k_subblock_dots_kernel(
     }
 }
 
+/* GGUF Q4_K rows [row0, row0 + rows) (back to back at src) into the tiled
+ * layout of a matrix of nkb super-blocks per row. The 144-byte blocks move
+ * whole, as nine 16-byte pieces: thread (row r, block b, piece c) copies
+ * one piece. Reads are contiguous; a 16-row group's writes land in one
+ * 16 x nkb x 144-byte run. rows and row0 are multiples of 16. */
+__global__ __launch_bounds__(256) void sera_q4k_tile_kernel(const uint4 *__restrict__ src, uint8_t *__restrict__ dst,
+                                                            uint64_t row0, uint64_t rows, uint64_t nkb) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * nkb * 9) return;
+    const uint64_t rb = i / 9;                  /* r * nkb + b within the source rows */
+    const int c = (int)(i - rb * 9);
+    const uint64_t r = rb / nkb, b = rb - r * nkb;
+    *(uint4 *)(dst + q4k_block_offset(1, row0 + r, b, nkb) + 16 * c) = src[i];
+}
+
+extern "C" hipError_t sera_launch_q4k_tile(const void *src, void *dst, uint64_t row0, uint64_t rows, uint64_t nkb,
+                                           hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    const uint64_t threads = rows * nkb * 9;
+    hipLaunchKernelGGL(sera_q4k_tile_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       (const uint4 *)src, (uint8_t *)dst, row0, rows, nkb);
+    return hipGetLastError();
+}
+
 extern "C" hipError_t sera_launch_q4k_quantize(const float *x, int64_t rows, int64_t K, void *out,
                                                hipStream_t s) {
     const int64_t nblocks = rows * (K / Q4K_QK);

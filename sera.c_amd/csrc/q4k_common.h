@@ -33,6 +33,31 @@
 #define Q4K_BLOCK_BYTES 144
 #define Q8_QK 32
 
+/* Q4_K weight layouts: qtype 12 keeps the GGUF bytes, row after row;
+ * SERA_QTYPE_Q4K_TILED is this library's 16-row tiled device layout, the
+ * same blocks reordered so that super-block b of 16 consecutive rows is one
+ * 2304-byte run: block (row r, super-block b) at
+ * ((r / 16) * (K / 256) + b) * 2304 + (r % 16) * 144. N must be a multiple
+ * of 16. */
+#ifndef SERA_QTYPE_Q4K_TILED
+#define SERA_QTYPE_Q4K_TILED 268u
+#endif
+#define Q4K_TILE_ROWS 16
+
+/* Byte offset of block (r, b) of an N x K matrix with nkb = K / 256. */
+__host__ __device__ static inline size_t q4k_block_offset(int tiled, size_t r, size_t b, size_t nkb) {
+    return tiled ? (((r >> 4) * nkb + b) * Q4K_TILE_ROWS + (r & 15)) * Q4K_BLOCK_BYTES
+                 : (r * nkb + b) * Q4K_BLOCK_BYTES;
+}
+/* Bytes from block (r, b) to block (r, b + 1), and from row r to row r + 1
+ * of the same tile (tiled) or of the matrix (GGUF). */
+__host__ __device__ static inline int q4k_block_stride(int tiled) {
+    return tiled ? Q4K_TILE_ROWS * Q4K_BLOCK_BYTES : Q4K_BLOCK_BYTES;
+}
+__host__ __device__ static inline int q4k_row_stride(int tiled, int nkb) {
+    return tiled ? Q4K_BLOCK_BYTES : nkb * Q4K_BLOCK_BYTES;
+}
+
 /* Byte offsets of the sub-arrays of a stage, 256-byte aligned. */
 static inline size_t sera_align256(size_t v) { return (v + 255u) & ~(size_t)255u; }
 

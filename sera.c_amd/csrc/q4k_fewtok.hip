@@ -97,7 +97,7 @@ template <int NW, int TG, int FORM, bool PERSIST>
 __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq, const void *__restrict__ xsc,
         float *__restrict__ y, float *__restrict__ slots, int *__restrict__ counters, int M, int N, int K,
-        int chunk, int accum, int out_tiles) {
+        int chunk, int accum, int out_tiles, int tiled) {
     constexpr int TOK = 8 * TG;                          /* staged tokens */
     extern __shared__ __attribute__((aligned(16))) uint8_t ft_smem[];
     __shared__ int s_last;
@@ -147,10 +147,11 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         if (!ok) r = N - 1;
     };
     rows_of(tile, row, row_ok);
-    wr = W + ((size_t)row * nkb + kb0) * Q4K_BLOCK_BYTES;
+    const int bstride = q4k_block_stride(tiled);   /* super-block to super-block of one row */
+    wr = W + q4k_block_offset(tiled, row, kb0, nkb);
     /* super-block u of the chunk (u < C; the loop never asks for more) */
     auto load_from = [&](const uint8_t *base, int u, FewtokW &w) {
-        const uint8_t *b = base + (size_t)u * Q4K_BLOCK_BYTES;
+        const uint8_t *b = base + (size_t)u * bstride;
         w.hd = *(const ft_v4u *)b;
         w.q[0] = *(const ft_v4u *)(b + 16 + 16 * g);
         w.q[1] = *(const ft_v4u *)(b + 80 + 16 * g);
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             int nrow;
             bool nrow_ok;
             rows_of(next < te ? next : tile, nrow, nrow_ok);
-            wnext = W + ((size_t)nrow * nkb + kb0) * Q4K_BLOCK_BYTES;
+            wnext = W + q4k_block_offset(tiled, nrow, kb0, nkb);
             /* even chunk: the select on an opaque flag keeps one loop body and
              * its exact load counting (the compiler would peel the last pair) */
             for (int u0 = 0; u0 < C; u0 += 2) {
@@ -455,7 +456,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
                 __builtin_amdgcn_sched_barrier(0);
                 int last = u0 + 2 == C;
                 __asm__ volatile("" : "+v"(last));
-                load_from(last ? wnext : wr + (size_t)(u0 + 2) * Q4K_BLOCK_BYTES, 0, wa);
+                load_from(last ? wnext : wr + (size_t)(u0 + 2) * bstride, 0, wa);
                 __builtin_amdgcn_sched_barrier(0);
                 compute(u0 + 1, wb);
                 __builtin_amdgcn_sched_barrier(0);
@@ -585,17 +586,17 @@ static void fewtok_grid(int N, int K, int chunk, bool allow_persist, int *groups
 }
 
 template <int NW, int TG, int FORM, bool PERSIST>
-static hipError_t launch_fewtok(const uint8_t *W, const int8_t *xq, const void *xsc, float *y, float *slots,
-                                int *counters, int M, int N, int K, int chunk, int accum, int groups, int out_tiles,
-                                size_t lds, hipStream_t s) {
+static hipError_t launch_fewtok(int tiled, const uint8_t *W, const int8_t *xq, const void *xsc, float *y,
+                                float *slots, int *counters, int M, int N, int K, int chunk, int accum, int groups,
+                                int out_tiles, size_t lds, hipStream_t s) {
     dim3 grid(groups, (K / Q4K_QK + chunk - 1) / chunk);
     hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM, PERSIST>), grid, dim3(NW * 64), lds, s, W, xq, xsc, y,
-                       slots, counters, M, N, K, chunk, accum, out_tiles);
+                       slots, counters, M, N, K, chunk, accum, out_tiles, tiled);
     return hipGetLastError();
 }
 
 template <int TG, int FORM>
-static hipError_t launch_fewtok_nw(int nw, const uint8_t *W, const int8_t *xq, const void *xsc, float *y,
+static hipError_t launch_fewtok_nw(int nw, int tiled, const uint8_t *W, const int8_t *xq, const void *xsc, float *y,
                                    float *slots, int *counters, int M, int N, int K, int chunk, int accum,
                                    hipStream_t s) {
     constexpr int P = fewtok_persist_waves<TG>();
@@ -603,26 +604,29 @@ static hipError_t launch_fewtok_nw(int nw, const uint8_t *W, const int8_t *xq, c
     size_t lds;
     fewtok_grid<P, TG, FORM>(N, K, chunk, true, &groups, &out_tiles, &lds);
     if (out_tiles > 0)
-        return launch_fewtok<P, TG, FORM, true>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups,
+        return launch_fewtok<P, TG, FORM, true>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups,
                                                 out_tiles, lds, s);
     if (nw == 8) {
         fewtok_grid<8, TG, FORM>(N, K, chunk, false, &groups, &out_tiles, &lds);
-        return launch_fewtok<8, TG, FORM, false>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups, 0,
-                                                 lds, s);
+        return launch_fewtok<8, TG, FORM, false>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum,
+                                                 groups, 0, lds, s);
     }
     fewtok_grid<4, TG, FORM>(N, K, chunk, false, &groups, &out_tiles, &lds);
-    return launch_fewtok<4, TG, FORM, false>(W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups, 0, lds,
-                                             s);
+    return launch_fewtok<4, TG, FORM, false>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups, 0,
+                                             lds, s);
 }
 
-/* y (+)= X . W^T for 1 <= M <= 16. form 0: row stage, MMVQ formula (M <= 8);
- * form 1: MMQ stage, MMQ formula. chunk: super-blocks per workgroup
+/* y (+)= X . W^T for 1 <= M <= 16, W in the layout of qtype (12 or
+ * SERA_QTYPE_Q4K_TILED). form 0: row stage, MMVQ formula (M <= 8); form 1:
+ * MMQ stage, MMQ formula. chunk: super-blocks per workgroup
  * (1..sera_fewtok_max_chunk(M), 0 = planned); when it splits K, slots holds
  * splits*M*N floats and counters sera_fewtok_groups() ints, zero on entry
  * and zero again after the kernel. */
-extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
-                                                 int *counters, int M, int N, int K, int chunk, int accum,
-                                                 hipStream_t s) {
+extern "C" hipError_t sera_launch_q4k_fewtok_acc(uint32_t qtype, int form, const void *W, const void *stage,
+                                                 float *y, float *slots, int *counters, int M, int N, int K,
+                                                 int chunk, int accum, hipStream_t s) {
+    const int tiled = qtype == SERA_QTYPE_Q4K_TILED;
+    if ((!tiled && qtype != 12u) || (tiled && N % Q4K_TILE_ROWS)) return hipErrorInvalidValue;
     int nw, c;
     sera_fewtok_plan(M, N, K, &nw, &c);
     if (chunk > 0) c = chunk;
@@ -631,15 +635,15 @@ extern "C" hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const 
     const uint8_t *w = (const uint8_t *)W;
     if (form == 0) {
         const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
-        return launch_fewtok_nw<1, 0>(nw, w, (const int8_t *)(base + L.qs), base + L.dsf, y, slots, counters, M, N,
-                                      K, c, accum, s);
+        return launch_fewtok_nw<1, 0>(nw, tiled, w, (const int8_t *)(base + L.qs), base + L.dsf, y, slots, counters,
+                                      M, N, K, c, accum, s);
     }
     const sera_stage_layout L = sera_mmq_stage_layout((size_t)sera_mmq_padded_rows(M), (size_t)K);
     if (M > 8)
-        return launch_fewtok_nw<2, 1>(nw, w, (const int8_t *)(base + L.qs), base + L.ds, y, slots, counters, M, N, K,
-                                      c, accum, s);
-    return launch_fewtok_nw<1, 1>(nw, w, (const int8_t *)(base + L.qs), base + L.ds, y, slots, counters, M, N, K, c,
-                                  accum, s);
+        return launch_fewtok_nw<2, 1>(nw, tiled, w, (const int8_t *)(base + L.qs), base + L.ds, y, slots, counters,
+                                      M, N, K, c, accum, s);
+    return launch_fewtok_nw<1, 1>(nw, tiled, w, (const int8_t *)(base + L.qs), base + L.ds, y, slots, counters, M, N,
+                                  K, c, accum, s);
 }
 
 /* Workgroups along the rows of the launch sera_launch_q4k_fewtok_acc makes

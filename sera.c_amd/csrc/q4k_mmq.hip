@@ -151,7 +151,7 @@ template <int TT, int WGT, int WGN, int PR = 0, bool AHEAD = false>
 __device__ __forceinline__ void mmq_segment(
         MmqSmem<MmqShape<TT, WGT, WGN, PR>::BM> &sm, const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, int N, int K, int m0, int n0, int kb_begin, int kb_end,
-        v16f (&acc)[TT][2]) {
+        v16f (&acc)[TT][2], int tiled) {
     using S = MmqShape<TT, WGT, WGN, PR>;
     constexpr int BMW = S::BMW, BM = S::BM;
     const int tid = threadIdx.x;
@@ -170,8 +170,9 @@ __device__ __forceinline__ void mmq_segment(
     for (int nt = 0; nt < 2; nt++) {
         int row = n0 + 64 * wn + 32 * nt + l32;
         if (row > N - 1) row = N - 1;          /* clamp; rows >= N are never stored */
-        wbase[nt] = W + (size_t)row * nkb_total * Q4K_BLOCK_BYTES;
+        wbase[nt] = W + q4k_block_offset(tiled, row, 0, nkb_total);
     }
+    const int bstride = q4k_block_stride(tiled);   /* super-block to super-block of one row */
 
     /* --- activation staging: BM tokens x 256 int8 go global -> LDS directly
      * (16-byte loads to LDS, one KB per wave-instruction, XOR-swizzled
@@ -212,7 +213,7 @@ __device__ __forceinline__ void mmq_segment(
     auto load_w = [&](int kb, v4u *hdr, v4u (*q)[4]) {
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
-            const uint8_t *b = wbase[nt] + (size_t)kb * Q4K_BLOCK_BYTES;
+            const uint8_t *b = wbase[nt] + (size_t)kb * bstride;
             hdr[nt] = *(const v4u *)b;
 #pragma unroll
             for (int j2 = 0; j2 < 4; j2++) q[nt][j2] = *(const v4u *)(b + 16 + 32 * j2 + 16 * h);
@@ -220,12 +221,12 @@ __device__ __forceinline__ void mmq_segment(
     };
     auto load_hdr = [&](int kb, v4u *hdr) {
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) hdr[nt] = *(const v4u *)(wbase[nt] + (size_t)kb * Q4K_BLOCK_BYTES);
+        for (int nt = 0; nt < 2; nt++) hdr[nt] = *(const v4u *)(wbase[nt] + (size_t)kb * bstride);
     };
     auto load_piece = [&](int kb, int j2, v4u *q) {
 #pragma unroll
         for (int nt = 0; nt < 2; nt++)
-            q[nt] = *(const v4u *)(wbase[nt] + (size_t)kb * Q4K_BLOCK_BYTES + 16 + 32 * j2 + 16 * h);
+            q[nt] = *(const v4u *)(wbase[nt] + (size_t)kb * bstride + 16 + 32 * j2 + 16 * h);
     };
 
 #pragma unroll
@@ -449,7 +450,7 @@ template <int TT, int WGT, int WGN, int WPE = 2, int PR = 0>
 __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ partial,
-        int M, int N, int K, int kb_per_split, int accum) {
+        int M, int N, int K, int kb_per_split, int accum, int tiled) {
     static_assert(WGT * WGN == 4, "4 waves per workgroup");
     using S = MmqShape<TT, WGT, WGN, PR>;
     __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
@@ -462,7 +463,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
     const int kb_begin = blockIdx.y * kb_per_split;
     const int kb_end = min(nkb_total, kb_begin + kb_per_split);
     v16f acc[TT][2];
-    mmq_segment<TT, WGT, WGN, PR, TT == 1 && WPE <= 2>(sm, W, xq, xds, N, K, m0, n0, kb_begin, kb_end, acc);
+    mmq_segment<TT, WGT, WGN, PR, TT == 1 && WPE <= 2>(sm, W, xq, xds, N, K, m0, n0, kb_begin, kb_end, acc, tiled);
     float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
     mmq_store<TT, WGT, WGN, PR>(out, M, N, m0, n0, acc, partial ? 0 : accum);
 }
@@ -485,7 +486,7 @@ template <int TT, int WGT, int WGN, int WPE = 2, int PR = 0>
 __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, float *__restrict__ y, float *__restrict__ slots,
-        int *__restrict__ counters, int M, int N, int K, int accum) {
+        int *__restrict__ counters, int M, int N, int K, int accum, int tiled) {
     static_assert(WGT * WGN == 4, "4 waves per workgroup");
     using S = MmqShape<TT, WGT, WGN, PR>;
     __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         const int kb1 = (int)min<int64_t>(nkb, kb0 + (myu1 - u));
         const int m0 = (t % ntt) * S::BM, n0 = (t / ntt) * S::BN;
         v16f acc[TT][2];
-        mmq_segment<TT, WGT, WGN, PR, TT == 1 && WPE <= 2>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc);
+        mmq_segment<TT, WGT, WGN, PR, TT == 1 && WPE <= 2>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc, tiled);
         if (kb0 == 0 && kb1 == nkb) {
             mmq_store<TT, WGT, WGN, PR>(y, M, N, m0, n0, acc, accum);
         } else {
@@ -625,7 +626,7 @@ extern "C" int sera_mmq_padded_rows(int M) {
 }
 
 template <int TT, int WGT, int WGN, int WPE, int PR = 0>
-static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
+static hipError_t launch_mmq_cfg(int tiled, const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
                                  float *partial, int M, int N, int K, int splits, int accum, hipStream_t s) {
     constexpr int BM = MmqShape<TT, WGT, WGN, PR>::BM, BN = MmqShape<TT, WGT, WGN, PR>::BN;
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
@@ -633,7 +634,7 @@ static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint3
     const int per = (nkb + splits - 1) / splits;
     dim3 grid(tiles, splits);
     hipLaunchKernelGGL((sera_q4k_mmq_kernel<TT, WGT, WGN, WPE, PR>), grid, dim3(256), 0, s, W, xq, xds, y,
-                       splits > 1 ? partial : nullptr, M, N, K, per, accum);
+                       splits > 1 ? partial : nullptr, M, N, K, per, accum, tiled);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
     return sera_launch_splitk_reduce_acc(partial, y, (size_t)M * N, splits, accum, s);
@@ -641,13 +642,16 @@ static hipError_t launch_mmq_cfg(const uint8_t *W, const int8_t *xq, const uint3
 
 /* partial: M*N*splits floats of scratch when splits > 1 (M*N % 4 == 0);
  * accum != 0 adds the product to y. */
-extern "C" hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial,
+extern "C" hipError_t sera_launch_q4k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial,
                                           int M, int N, int K, int splits, hipStream_t s) {
-    return sera_launch_q4k_mmq_acc(W, stage, y, partial, M, N, K, splits, 0, s);
+    return sera_launch_q4k_mmq_acc(qtype, W, stage, y, partial, M, N, K, splits, 0, s);
 }
 
-extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, float *y, float *partial,
-                                              int M, int N, int K, int splits, int accum, hipStream_t s) {
+extern "C" hipError_t sera_launch_q4k_mmq_acc(uint32_t qtype, const void *W, const void *stage, float *y,
+                                              float *partial, int M, int N, int K, int splits, int accum,
+                                              hipStream_t s) {
+    const int tiled = qtype == SERA_QTYPE_Q4K_TILED;
+    if ((!tiled && qtype != 12u) || (tiled && N % Q4K_TILE_ROWS)) return hipErrorInvalidValue;
     const int Mpad = sera_mmq_padded_rows(M);
     const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
     const char *base = (const char *)stage;
@@ -655,10 +659,10 @@ extern "C" hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, 
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
     if (sera_mmq_bm(M) == 16)
-        return launch_mmq_cfg<1, 1, 4, 2, 1>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
+        return launch_mmq_cfg<1, 1, 4, 2, 1>(tiled, w, xq, xds, y, partial, M, N, K, splits, accum, s);
     if (sera_mmq_bm(M) == 32)
-        return launch_mmq_cfg<1, 1, 4, 2>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
-    return launch_mmq_cfg<2, 1, 4, 2>(w, xq, xds, y, partial, M, N, K, splits, accum, s);
+        return launch_mmq_cfg<1, 1, 4, 2>(tiled, w, xq, xds, y, partial, M, N, K, splits, accum, s);
+    return launch_mmq_cfg<2, 1, 4, 2>(tiled, w, xq, xds, y, partial, M, N, K, splits, accum, s);
 }
 
 /* ---- stream-K schedule ---------------------------------------------------- */
@@ -678,11 +682,11 @@ extern "C" int sera_mmq_slot_floats(int M) {
 }
 
 template <int TT, int WGT, int WGN, int WPE, int PR = 0>
-static hipError_t launch_mmq_streamk_cfg(const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
-                                         float *slots, int *counters, int M, int N, int K, int P, int accum,
+static hipError_t launch_mmq_streamk_cfg(int tiled, const uint8_t *W, const int8_t *xq, const uint32_t *xds,
+                                         float *y, float *slots, int *counters, int M, int N, int K, int P, int accum,
                                          hipStream_t s) {
     hipLaunchKernelGGL((sera_q4k_mmq_streamk_kernel<TT, WGT, WGN, WPE, PR>), dim3(P), dim3(256), 0, s, W, xq, xds, y,
-                       slots, counters, M, N, K, accum);
+                       slots, counters, M, N, K, accum, tiled);
     return hipGetLastError();
 }
 
@@ -690,14 +694,17 @@ static hipError_t launch_mmq_streamk_cfg(const uint8_t *W, const int8_t *xq, con
  * workgroups the device keeps resident, and ntiles*K/256 >= P).
  * slots: 2*P*sera_mmq_slot_floats(M) floats; counters: sera_mmq_tiles(M,N)
  * ints, zero on entry and zero again on exit. */
-extern "C" hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots,
-                                                  int *counters, int M, int N, int K, int P, hipStream_t s) {
-    return sera_launch_q4k_mmq_streamk_acc(W, stage, y, slots, counters, M, N, K, P, 0, s);
+extern "C" hipError_t sera_launch_q4k_mmq_streamk(uint32_t qtype, const void *W, const void *stage, float *y,
+                                                  float *slots, int *counters, int M, int N, int K, int P,
+                                                  hipStream_t s) {
+    return sera_launch_q4k_mmq_streamk_acc(qtype, W, stage, y, slots, counters, M, N, K, P, 0, s);
 }
 
-extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots,
-                                                      int *counters, int M, int N, int K, int P, int accum,
-                                                      hipStream_t s) {
+extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(uint32_t qtype, const void *W, const void *stage, float *y,
+                                                      float *slots, int *counters, int M, int N, int K, int P,
+                                                      int accum, hipStream_t s) {
+    const int tiled = qtype == SERA_QTYPE_Q4K_TILED;
+    if ((!tiled && qtype != 12u) || (tiled && N % Q4K_TILE_ROWS)) return hipErrorInvalidValue;
     const int Mpad = sera_mmq_padded_rows(M);
     const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
     const char *base = (const char *)stage;
@@ -705,8 +712,8 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void 
     const uint32_t *xds = (const uint32_t *)(base + L.ds);
     const uint8_t *w = (const uint8_t *)W;
     if (sera_mmq_bm(M) == 16)
-        return launch_mmq_streamk_cfg<1, 1, 4, 2, 1>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
+        return launch_mmq_streamk_cfg<1, 1, 4, 2, 1>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
     if (sera_mmq_bm(M) == 32)
-        return launch_mmq_streamk_cfg<1, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
-    return launch_mmq_streamk_cfg<2, 1, 4, 2>(w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
+        return launch_mmq_streamk_cfg<1, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
+    return launch_mmq_streamk_cfg<2, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
 }

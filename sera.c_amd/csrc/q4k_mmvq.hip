@@ -84,6 +84,7 @@ struct MmvqGroup {
     int tile_end[SERA_MMVQ_GROUP];
     int count;
     int accum;
+    int tiled;      /* weights in the 16-row tiled layout (every matrix) */
 };
 
 template <int NCOLS, int R, int NW, bool GROUPED>
@@ -91,8 +92,8 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
         MmvqGroup grp, const int8_t *__restrict__ xq, const float4 *__restrict__ dsf, int K) {
     {
         const void *a0 = grp.W[0], *a1 = grp.y[0], *a2 = xq, *a3 = dsf;
-        const int a4 = grp.N[0], a5 = K, a6 = grp.accum;
-        __asm__ volatile("" : : "s"(a0), "s"(a1), "s"(a2), "s"(a3), "s"(a4), "s"(a5), "s"(a6));
+        const int a4 = grp.N[0], a5 = K, a6 = grp.accum, a7 = grp.tiled;
+        __asm__ volatile("" : : "s"(a0), "s"(a1), "s"(a2), "s"(a3), "s"(a4), "s"(a5), "s"(a6), "s"(a7));
     }
     /* one matrix: its pointers come straight from the kernel arguments, so
      * the first loads issue without the dependent scalar loads of the
@@ -123,12 +124,17 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
     const int row0 = tile0 + R > N && N >= R ? N - R : tile0;
     const int nb = K / Q4K_QK;
     const int ngroups = (nb + 7) >> 3;
-    const int rowbytes = nb * Q4K_BLOCK_BYTES;
+    /* row and block strides of the layout; a tile of R <= 16 rows never
+     * crosses a 16-row tile of the tiled layout (N % 16 == 0 there) */
+    const int rowbytes = q4k_row_stride(grp.tiled, nb);
+    const int bstride = q4k_block_stride(grp.tiled);
     const int nrows = min(R, N - row0);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + (size_t)row0 * rowbytes, (uint32_t)(nrows * rowbytes));
+    const __amdgpu_buffer_rsrc_t rw =
+        make_rsrc(W + q4k_block_offset(grp.tiled, row0, 0, nb),
+                  (uint32_t)(grp.tiled ? (nb - 1) * bstride + nrows * Q4K_BLOCK_BYTES : nrows * rowbytes));
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, (uint32_t)(NCOLS * K));
     const __amdgpu_buffer_rsrc_t rf = make_rsrc(dsf, (uint32_t)(NCOLS * (K / 64) * 16));
-    const int vo_w = rs * rowbytes + g * Q4K_BLOCK_BYTES;
+    const int vo_w = rs * rowbytes + g * bstride;
     const int vo_hdr = vo_w + 4 * q;
     const int vo_qs = vo_w + 16 + 32 * q;
     const int vo_xh = g * Q4K_QK + 64 * q + 32 * rs;
@@ -147,7 +153,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
         }
 #pragma unroll
         for (int r = 0; r < HR; r++) {
-            const int so = 2 * r * rowbytes + bg * 8 * Q4K_BLOCK_BYTES;
+            const int so = 2 * r * rowbytes + bg * 8 * bstride;
             t.hw[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vo_hdr, so, 0);
             t.qa[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qs, so, 0);
             t.qc[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qs + 16, so, 0);
@@ -175,7 +181,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
         }
 #pragma unroll
         for (int r = 0; r < HR; r++) {
-            const int so = 2 * r * rowbytes + bg * 8 * Q4K_BLOCK_BYTES;
+            const int so = 2 * r * rowbytes + bg * 8 * bstride;
             t.hw[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vo_hdr, so, 0);
             t.qa[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qs, so, 0);
             t.qc[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_qs + 16, so, 0);
@@ -394,10 +400,14 @@ static hipError_t dispatch_r(int r, const MmvqGroup &grp, const int8_t *xq, cons
 
 /* count weight matrices (W[i], N[i] rows, output y[i]) of one K on one row
  * stage; rows = 0 picks the rows per workgroup from the smallest N. */
-extern "C" hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W, float *const *y, const int *N,
-                                                 const void *stage, int M, int K, int rows, int accum,
+extern "C" hipError_t sera_launch_q4k_mmvq_group(uint32_t qtype, int count, const void *const *W, float *const *y,
+                                                 const int *N, const void *stage, int M, int K, int rows, int accum,
                                                  hipStream_t s) {
     if (count < 1 || count > SERA_MMVQ_GROUP) return hipErrorInvalidValue;
+    const int tiled = qtype == SERA_QTYPE_Q4K_TILED;
+    if (!tiled && qtype != 12u) return hipErrorInvalidValue;
+    for (int i = 0; i < count; i++)
+        if (tiled && N[i] % Q4K_TILE_ROWS) return hipErrorInvalidValue;
     const sera_stage_layout L = sera_row_stage_layout((size_t)M, (size_t)K);
     const char *base = (const char *)stage;
     const int8_t *xq = (const int8_t *)(base + L.qs);
@@ -412,8 +422,10 @@ extern "C" hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W
     }
     grp.count = count;
     grp.accum = accum;
+    grp.tiled = tiled;
     if (rows <= 0) rows = sera_mmvq_rows_per_wave(nmin, K, M);
     while (rows > 2 && rows > nmin) rows >>= 1;   /* the shifted last tile needs R <= N */
+    if (tiled && rows > Q4K_TILE_ROWS) rows = Q4K_TILE_ROWS;
     switch (M) {
         case 1: return dispatch_r<1>(rows, grp, xq, dsf, K, s);
         case 2: return dispatch_r<2>(rows, grp, xq, dsf, K, s);
@@ -427,7 +439,7 @@ extern "C" hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W
     }
 }
 
-extern "C" hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y,
+extern "C" hipError_t sera_launch_q4k_mmvq(uint32_t qtype, const void *W, const void *stage, float *y,
                                            int M, int N, int K, int rows, hipStream_t s) {
-    return sera_launch_q4k_mmvq_group(1, &W, &y, &N, stage, M, K, rows, 0, s);
+    return sera_launch_q4k_mmvq_group(qtype, 1, &W, &y, &N, stage, M, K, rows, 0, s);
 }

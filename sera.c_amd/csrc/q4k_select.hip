@@ -20,7 +20,10 @@
  *
  * Q6_K rows come as GGUF bytes (qtype 14) or in the split device layout
  * (SERA_QTYPE_Q6K_SPLIT: 208-byte aligned ql/qh/sc blocks and a separate
- * fp16 d array); both give the same values.
+ * fp16 d array); Q4_K rows as GGUF bytes (12) or in the 16-row tiled layout
+ * (SERA_QTYPE_Q4K_TILED: the same blocks, ordered by 16-row tile, then
+ * super-block, then row). Each layout gives the same values as its GGUF
+ * bytes.
  *
  * gfx950 mapping: one wave per output row; lane l takes weights 4l..4l+3 of
  * each 256-weight block (one sub-block, one group scale), reads its bytes as
@@ -60,7 +63,23 @@ __device__ __forceinline__ uint32_t sel_load4(__amdgpu_buffer_rsrc_t r, uint32_t
  * 208 (ql, qh, sc; d in the separate array). */
 template <int QT>
 __host__ __device__ constexpr uint32_t sel_block_bytes() {
-    return QT == 12 ? Q4K_BLOCK_BYTES : QT == 14 ? Q6K_GGUF_BYTES : Q6K_SPLIT_QBYTES;
+    return QT == 12 || QT == (int)SERA_QTYPE_Q4K_TILED ? Q4K_BLOCK_BYTES
+           : QT == 14                                   ? Q6K_GGUF_BYTES
+                                                        : Q6K_SPLIT_QBYTES;
+}
+
+/* From one block of a row to the next: the block size, or a 16-row tile of
+ * blocks in the tiled Q4_K layout. */
+template <int QT>
+__host__ __device__ constexpr uint32_t sel_block_step() {
+    return QT == (int)SERA_QTYPE_Q4K_TILED ? Q4K_TILE_ROWS * Q4K_BLOCK_BYTES : sel_block_bytes<QT>();
+}
+
+/* Byte offset of row id's first block. */
+template <int QT>
+__device__ __forceinline__ uint64_t sel_row_offset(uint32_t id, int nb) {
+    return QT == (int)SERA_QTYPE_Q4K_TILED ? (uint64_t)q4k_block_offset(1, id, 0, (size_t)nb)
+                                           : (uint64_t)id * nb * sel_block_bytes<QT>();
 }
 
 /* Weights e0..e0+3 (e0 % 4 == 0) of block `blk` of the row starting at byte
@@ -69,8 +88,8 @@ __host__ __device__ constexpr uint32_t sel_block_bytes() {
 template <int QT>
 __device__ __forceinline__ void sel_dequant4(__amdgpu_buffer_rsrc_t r, uint32_t row, int blk, int e0, uint32_t dsplit,
                                              float w[4]) {
-    if (QT == 12) {
-        const uint32_t b = row + (uint32_t)blk * Q4K_BLOCK_BYTES;
+    if (QT == 12 || QT == (int)SERA_QTYPE_Q4K_TILED) {
+        const uint32_t b = row + (uint32_t)blk * sel_block_step<QT>();
         const uint32_t h0 = __builtin_amdgcn_raw_buffer_load_b32(r, b, 0, 0);
         const uint32_t s0 = __builtin_amdgcn_raw_buffer_load_b32(r, b + 4, 0, 0);
         const uint32_t s1 = __builtin_amdgcn_raw_buffer_load_b32(r, b + 8, 0, 0);
@@ -130,10 +149,10 @@ __global__ __launch_bounds__(256) void sera_candidate_logits_kernel(
         return;
     }
     const int nb = K / Q4K_QK;
-    const uint64_t rb = (uint64_t)nb * sel_block_bytes<QT>();
-    const uint64_t base = ((uint64_t)id * rb) & ~(uint64_t)15;
+    const uint64_t start = sel_row_offset<QT>(id, nb);
+    const uint64_t base = start & ~(uint64_t)15;
     const __amdgpu_buffer_rsrc_t r = sel_rsrc(W + base, wbytes - base);
-    const uint32_t row = (uint32_t)((uint64_t)id * rb - base);
+    const uint32_t row = (uint32_t)(start - base);
     const float *x = hidden + (size_t)(index / per_branch) * K;
     const uint16_t *drow = QT == SERA_QTYPE_Q6K_SPLIT ? Wd + (size_t)id * nb : nullptr;
     float acc = 0.0f;
@@ -164,11 +183,11 @@ __global__ __launch_bounds__(256) void sera_embedding_kernel(
     const int t = (int)(unit / nb), blk = (int)(unit - (int64_t)t * nb);
     const uint32_t id = ids[t];
     if (id >= (uint32_t)N) return;
-    const uint64_t rb = (uint64_t)nb * sel_block_bytes<QT>();
-    const uint64_t base = ((uint64_t)id * rb) & ~(uint64_t)15;
+    const uint64_t start = sel_row_offset<QT>(id, nb);
+    const uint64_t base = start & ~(uint64_t)15;
     const __amdgpu_buffer_rsrc_t r = sel_rsrc(W + base, wbytes - base);
     float w[4];
-    sel_dequant4<QT>(r, (uint32_t)((uint64_t)id * rb - base), blk, 4 * lane,
+    sel_dequant4<QT>(r, (uint32_t)(start - base), blk, 4 * lane,
                      QT == SERA_QTYPE_Q6K_SPLIT ? Wd[(size_t)id * nb + blk] : 0u, w);
     *(float4 *)(hidden + (size_t)t * K + (size_t)blk * Q4K_QK + 4 * lane) = make_float4(w[0], w[1], w[2], w[3]);
 }
@@ -177,11 +196,14 @@ namespace {
 /* bytes the kernels address through the resource, and the d array */
 uint64_t sel_qbytes(int qtype, int N, int K) {
     const uint64_t nblk = (uint64_t)N * (uint64_t)(K / Q4K_QK);
-    return nblk * (qtype == 12 ? Q4K_BLOCK_BYTES : qtype == 14 ? Q6K_GGUF_BYTES : Q6K_SPLIT_QBYTES);
+    return nblk * (qtype == 12 || qtype == (int)SERA_QTYPE_Q4K_TILED ? Q4K_BLOCK_BYTES
+                   : qtype == 14                                        ? Q6K_GGUF_BYTES
+                                                                        : Q6K_SPLIT_QBYTES);
 }
 }  // namespace
 
-/* qtype 12 (Q4_K), 14 (Q6_K GGUF bytes) or SERA_QTYPE_Q6K_SPLIT. */
+/* qtype 12 (Q4_K), SERA_QTYPE_Q4K_TILED, 14 (Q6_K GGUF bytes) or
+ * SERA_QTYPE_Q6K_SPLIT. */
 extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int N, int K, const float *hidden,
                                                    const uint32_t *ids, int branches, int per_branch,
                                                    float *logits, hipStream_t s) {
@@ -193,6 +215,9 @@ extern "C" hipError_t sera_launch_candidate_logits(int qtype, const void *W, int
     if (qtype == 12)
         hipLaunchKernelGGL(sera_candidate_logits_kernel<12>, grid, dim3(256), 0, s, w, wd, qb, N, K, hidden, ids,
                            per_branch, total, logits);
+    else if (qtype == (int)SERA_QTYPE_Q4K_TILED)
+        hipLaunchKernelGGL(sera_candidate_logits_kernel<(int)SERA_QTYPE_Q4K_TILED>, grid, dim3(256), 0, s, w, wd, qb,
+                           N, K, hidden, ids, per_branch, total, logits);
     else if (qtype == 14)
         hipLaunchKernelGGL(sera_candidate_logits_kernel<14>, grid, dim3(256), 0, s, w, wd, qb, N, K, hidden, ids,
                            per_branch, total, logits);
@@ -211,6 +236,9 @@ extern "C" hipError_t sera_launch_embedding(int qtype, const void *W, int N, int
     const dim3 grid((unsigned)((units + 3) / 4));
     if (qtype == 12)
         hipLaunchKernelGGL(sera_embedding_kernel<12>, grid, dim3(256), 0, s, w, wd, qb, N, K, ids, tokens, hidden);
+    else if (qtype == (int)SERA_QTYPE_Q4K_TILED)
+        hipLaunchKernelGGL(sera_embedding_kernel<(int)SERA_QTYPE_Q4K_TILED>, grid, dim3(256), 0, s, w, wd, qb, N, K,
+                           ids, tokens, hidden);
     else if (qtype == 14)
         hipLaunchKernelGGL(sera_embedding_kernel<14>, grid, dim3(256), 0, s, w, wd, qb, N, K, ids, tokens, hidden);
     else

@@ -31,9 +31,11 @@ hipError_t sera_launch_q8_1_q6k_stage_p(const float *x, const sera_producer *pro
 
 /* ---- q4k_mmvq.hip: dot4 MMVQ ------------------------------------------ */
 int sera_mmvq_rows_per_wave(int N, int K, int M);
-hipError_t sera_launch_q4k_mmvq(const void *W, const void *stage, float *y, int M, int N, int K, int rpw,
-                                hipStream_t s);
-hipError_t sera_launch_q4k_mmvq_group(int count, const void *const *W, float *const *y, const int *N,
+/* qtype: 12 (GGUF bytes) or SERA_QTYPE_Q4K_TILED (N % 16 == 0) for every
+ * Q4_K weight launcher below */
+hipError_t sera_launch_q4k_mmvq(uint32_t qtype, const void *W, const void *stage, float *y, int M, int N, int K,
+                                int rpw, hipStream_t s);
+hipError_t sera_launch_q4k_mmvq_group(uint32_t qtype, int count, const void *const *W, float *const *y, const int *N,
                                       const void *stage, int M, int K, int rows, int accum, hipStream_t s);
 
 /* ---- q4k_mmq.hip: MMQ tiles, split-K reduce, stream-K ------------------ */
@@ -46,14 +48,14 @@ int sera_mmq_slot_floats(int M);
 hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits, hipStream_t s);
 hipError_t sera_launch_splitk_reduce_acc(const float *partial, float *y, size_t n, int splits, int accum,
                                          hipStream_t s);
-hipError_t sera_launch_q4k_mmq(const void *W, const void *stage, float *y, float *partial, int M, int N, int K,
-                               int splits, hipStream_t s);
-hipError_t sera_launch_q4k_mmq_acc(const void *W, const void *stage, float *y, float *partial, int M, int N, int K,
-                                   int splits, int accum, hipStream_t s);
-hipError_t sera_launch_q4k_mmq_streamk(const void *W, const void *stage, float *y, float *slots, int *counters, int M,
-                                       int N, int K, int P, hipStream_t s);
-hipError_t sera_launch_q4k_mmq_streamk_acc(const void *W, const void *stage, float *y, float *slots, int *counters,
-                                           int M, int N, int K, int P, int accum, hipStream_t s);
+hipError_t sera_launch_q4k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial, int M, int N,
+                               int K, int splits, hipStream_t s);
+hipError_t sera_launch_q4k_mmq_acc(uint32_t qtype, const void *W, const void *stage, float *y, float *partial, int M,
+                                   int N, int K, int splits, int accum, hipStream_t s);
+hipError_t sera_launch_q4k_mmq_streamk(uint32_t qtype, const void *W, const void *stage, float *y, float *slots,
+                                       int *counters, int M, int N, int K, int P, hipStream_t s);
+hipError_t sera_launch_q4k_mmq_streamk_acc(uint32_t qtype, const void *W, const void *stage, float *y, float *slots,
+                                           int *counters, int M, int N, int K, int P, int accum, hipStream_t s);
 
 /* ---- q4k_fewtok.hip: few-token MFMA kernel ----------------------------- */
 void sera_fewtok_plan(int M, int N, int K, int *nwave, int *chunk);
@@ -61,8 +63,9 @@ int sera_fewtok_max_chunk(int M);
 int sera_fewtok_groups(int M, int N, int K);
 int sera_fewtok_splits(int M, int N, int K, int chunk);
 int sera_fewtok_grid(int form, int M, int N, int K, int chunk);
-hipError_t sera_launch_q4k_fewtok_acc(int form, const void *W, const void *stage, float *y, float *slots,
-                                      int *counters, int M, int N, int K, int chunk, int accum, hipStream_t s);
+hipError_t sera_launch_q4k_fewtok_acc(uint32_t qtype, int form, const void *W, const void *stage, float *y,
+                                      float *slots, int *counters, int M, int N, int K, int chunk, int accum,
+                                      hipStream_t s);
 
 /* ---- q6k_mmvq.hip / q6k_mmq.hip / q6k_layout.hip: Q6_K ---------------- */
 int sera_q6k_mmvq_rows(int N, int M);
@@ -89,6 +92,8 @@ hipError_t sera_launch_embedding(int qtype, const void *W, int N, int K, const u
 /* ---- q4k_aux.hip: weight quantizer, dequant, integer-dot test hook ----- */
 hipError_t sera_launch_q4k_quantize(const float *x, int64_t rows, int64_t K, void *out, hipStream_t s);
 hipError_t sera_launch_q4k_dequant(const void *W, int64_t nblocks, float *out, hipStream_t s);
+hipError_t sera_launch_q4k_tile(const void *src, void *dst, uint64_t row0, uint64_t rows, uint64_t nkb,
+                                hipStream_t s);
 hipError_t sera_launch_q4k_subblock_dots(const void *W, const int8_t *xq, int32_t *I, int M, int N, int K,
                                          hipStream_t s);
 

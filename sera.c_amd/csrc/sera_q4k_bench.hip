@@ -46,7 +46,8 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
  * on Q6_K weights in the split layout (path 9: param = rows per workgroup),
  * 12 / 13 = few-token kernel on a row stage (MMVQ formula) / an MMQ stage
  * (MMQ formula) (param = chunk, 0 = planned; partial = split slots followed
- * by the zeroed row-group counters).
+ * by the zeroed row-group counters). path | 256: the Q4_K paths (0, 1, 4,
+ * 8, 12, 13) on weights in the tiled layout (SERA_QTYPE_Q4K_TILED).
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
  * elapsed time over iters (each launch's duration plus the dispatch gap to
@@ -57,11 +58,13 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
                                      double *avg_kernel_ms, double *elapsed_ms) {
     if (!weights || nweights <= 0 || iters <= 0) return -1;
     hipStream_t s = (hipStream_t)stream;
+    const uint32_t q4 = (path & 256) ? SERA_QTYPE_Q4K_TILED : 12u;
+    path &= 255;
     auto launch = [&](int i) -> hipError_t {
         const void *w = weights[i % nweights];
         switch (path) {
-            case 0: return sera_launch_q4k_mmvq(w, stage, y, M, N, K, param, s);
-            case 1: return sera_launch_q4k_mmq(w, stage, y, partial, M, N, K, param, s);
+            case 0: return sera_launch_q4k_mmvq(q4, w, stage, y, M, N, K, param, s);
+            case 1: return sera_launch_q4k_mmq(q4, w, stage, y, partial, M, N, K, param, s);
             case 5:
             case 9: return sera_launch_q6k_mmvq(path == 5 ? 14u : SERA_QTYPE_Q6K_SPLIT, w, stage, y, M, N, K, param,
                                                 s);
@@ -70,15 +73,15 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
                                                 param, s);
             case 7:
             case 8:
-            case 11: return sera_launch_candidate_logits(path == 7 ? 14 : path == 8 ? 12 : (int)SERA_QTYPE_Q6K_SPLIT,
+            case 11: return sera_launch_candidate_logits(path == 7 ? 14 : path == 8 ? (int)q4 : (int)SERA_QTYPE_Q6K_SPLIT,
                                                          w, N, K, (const float *)stage, (const uint32_t *)partial, M,
                                                          param, y, s);
             case 12:
             case 13: return sera_launch_q4k_fewtok_acc(
-                         path - 12, w, stage, y, partial,
+                         q4, path - 12, w, stage, y, partial,
                          (int *)(partial + (size_t)sera_fewtok_splits(M, N, K, param) * M * N), M, N, K, param, 0, s);
             case 4: return sera_launch_q4k_mmq_streamk(
-                        w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),
+                        q4, w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),
                         M, N, K, param, s);
             default: return hipErrorInvalidValue;
         }

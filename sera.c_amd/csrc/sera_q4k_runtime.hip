@@ -259,7 +259,7 @@ extern "C" int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int
     if (rows_per_tile != 0 && rows_per_tile != 2 && rows_per_tile != 4 && rows_per_tile != 8 &&
         rows_per_tile != 16)
         return fail(-1, "sera_q4k_mmvq: rows_per_tile=%d not in {0,2,4,8,16}", rows_per_tile);
-    return sera_launch_q4k_mmvq(W, row_stage, Y, M, N, K, rows_per_tile, (hipStream_t)stream) == hipSuccess
+    return sera_launch_q4k_mmvq(12u, W, row_stage, Y, M, N, K, rows_per_tile, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q4k_mmvq: launch failed");
 }
 
@@ -295,7 +295,7 @@ extern "C" int sera_q4k_fewtok(int form, const void *W, const void *stage, float
         return fail(-1, "sera_q4k_fewtok: chunk=%d outside 0..%d", chunk, sera_fewtok_max_chunk(M));
     if (sera_fewtok_splits(M, N, K, chunk) > 1 && (!slots || !counters))
         return fail(-1, "sera_q4k_fewtok: a split K needs slots and counters");
-    return sera_launch_q4k_fewtok_acc(form, W, stage, Y, slots, counters, M, N, K, chunk, accum ? 1 : 0,
+    return sera_launch_q4k_fewtok_acc(12u, form, W, stage, Y, slots, counters, M, N, K, chunk, accum ? 1 : 0,
                                       (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q4k_fewtok: launch failed");
 }
@@ -308,7 +308,7 @@ extern "C" int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, floa
     if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q4k_mmq: splits=%d outside 1..K/256", splits);
     if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
         return fail(-1, "sera_q4k_mmq: split-K needs a partial buffer and M*N %% 4 == 0");
-    return sera_launch_q4k_mmq(W, mmq_stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
+    return sera_launch_q4k_mmq(12u, W, mmq_stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q4k_mmq: launch failed");
 }
 
@@ -335,8 +335,9 @@ namespace {
 /* The few-token kernel on `stage` (form 0: row stage, 1: MMQ stage): split
  * partials go to `slots` (cap floats), row-group counters to `counters`
  * (ncounters ints, zero between calls). */
-int fewtok_launch_on(const char *tag, int form, const void *W, const void *stage, float *Y, float *slots, size_t cap,
-                     int *counters, int ncounters, int M, int N, int K, int accum, hipStream_t s) {
+int fewtok_launch_on(const char *tag, uint32_t qtype, int form, const void *W, const void *stage, float *Y,
+                     float *slots, size_t cap, int *counters, int ncounters, int M, int N, int K, int accum,
+                     hipStream_t s) {
     const int splits = sera_fewtok_splits(M, N, K, 0);
     if (splits > 1) {
         if ((size_t)splits * M * N > cap)
@@ -344,23 +345,23 @@ int fewtok_launch_on(const char *tag, int form, const void *W, const void *stage
         if (sera_fewtok_groups(M, N, K) > ncounters)
             return fail(-1, "%s: N=%d needs more row-group counters than the scratch holds", tag, N);
     }
-    return sera_launch_q4k_fewtok_acc(form, W, stage, Y, slots, counters, M, N, K, 0, accum, s) == hipSuccess
+    return sera_launch_q4k_fewtok_acc(qtype, form, W, stage, Y, slots, counters, M, N, K, 0, accum, s) == hipSuccess
                ? 0 : fail(-3, "%s: few-token kernel launch failed", tag);
 }
 
 /* The same on the caller's arena: the stage at its start, the counters in
  * the second half of the counter region. */
-int fewtok_launch(const char *tag, int form, const void *W, float *Y, float *slots, size_t cap, int M, int N, int K,
-                  int accum, hipStream_t s) {
-    return fewtok_launch_on(tag, form, W, g_arena, Y, slots, cap, g_counters + kFewtokCounterBase, kFewtokMaxCounters,
+int fewtok_launch(const char *tag, uint32_t qtype, int form, const void *W, float *Y, float *slots, size_t cap, int M,
+                  int N, int K, int accum, hipStream_t s) {
+    return fewtok_launch_on(tag, qtype, form, W, g_arena, Y, slots, cap, g_counters + kFewtokCounterBase, kFewtokMaxCounters,
                             M, N, K, accum, s);
 }
 
 /* The MMVQ path (quantize + dot4 MMVQ or the few-token kernel) on explicit
  * scratch: the row stage at `stage`, split slots after it (slot_cap
  * floats), row-group counters at `counters`. */
-int dense_vec_on(const char *tag, const void *W, const float *X, float *Y, int M, int N, int K, hipStream_t s,
-                 int timed, unsigned char *stage, size_t stage_cap, int *counters, int ncounters) {
+int dense_vec_on(const char *tag, uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
+                 hipStream_t s, int timed, unsigned char *stage, size_t stage_cap, int *counters, int ncounters) {
     const size_t stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
     if (stage_bytes > stage_cap) return fail(-1, "%s: scratch too small (%zu > %zu)", tag, stage_bytes, stage_cap);
     if (timed) record(g_ev.quant_begin, s);
@@ -368,10 +369,10 @@ int dense_vec_on(const char *tag, const void *W, const float *X, float *Y, int M
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
     if (sera_q4k_vec_uses_fewtok(M, N, K)) {
-        const int rc = fewtok_launch_on(tag, 0, W, stage, Y, (float *)(stage + stage_bytes),
+        const int rc = fewtok_launch_on(tag, qtype, 0, W, stage, Y, (float *)(stage + stage_bytes),
                                         (stage_cap - stage_bytes) / sizeof(float), counters, ncounters, M, N, K, 0, s);
         if (rc) return rc;
-    } else if (sera_launch_q4k_mmvq(W, stage, Y, M, N, K, 0, s) != hipSuccess) {
+    } else if (sera_launch_q4k_mmvq(qtype, W, stage, Y, M, N, K, 0, s) != hipSuccess) {
         return fail(-3, "%s: mmvq launch failed", tag);
     }
     if (timed) record(g_ev.kernel_end, s);
@@ -379,9 +380,31 @@ int dense_vec_on(const char *tag, const void *W, const float *X, float *Y, int M
 }
 }  // namespace
 
+namespace {
+/* The weight layouts of the Q4_K path: 12 (GGUF bytes) or the 16-row tiled
+ * layout, which needs N % 16 == 0. */
+bool q4k_layout_ok(const char *tag, uint32_t qtype, int N) {
+    if (qtype != 12u && qtype != SERA_QTYPE_Q4K_TILED) {
+        fail(-1, "%s: qtype %u is not Q4_K (12) or Q4_K tiled (%u)", tag, qtype, SERA_QTYPE_Q4K_TILED);
+        return false;
+    }
+    if (qtype == SERA_QTYPE_Q4K_TILED && N % Q4K_TILE_ROWS) {
+        fail(-1, "%s: the tiled layout needs N %% 16 == 0 (N=%d)", tag, N);
+        return false;
+    }
+    return true;
+}
+}  // namespace
+
 extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
                               int timed) {
+    return sera_q4k_dense_qt(12u, W, X, Y, M, N, K, stream, timed);
+}
+
+extern "C" int sera_q4k_dense_qt(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
+                                 void *stream, int timed) {
     if (!check_shape("sera_q4k_dense", W, X, Y, M, N, K)) return -1;
+    if (!q4k_layout_ok("sera_q4k_dense", qtype, N)) return -1;
     if (!g_arena) return fail(-1, "sera_q4k_dense: no arena attached");
     hipStream_t s = (hipStream_t)stream;
     const int Mpad = sera_mmq_padded_rows(M);
@@ -395,7 +418,7 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
             return fail(-2, "sera_q4k_dense: quantize launch failed");
         if (timed) record(g_ev.quant_end, s);
         if (timed) record(g_ev.kernel_begin, s);
-        const int rc = fewtok_launch("sera_q4k_dense", 1, W, Y, (float *)(g_arena + stage_bytes),
+        const int rc = fewtok_launch("sera_q4k_dense", qtype, 1, W, Y, (float *)(g_arena + stage_bytes),
                                      (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s);
         if (rc) return rc;
         if (timed) record(g_ev.kernel_end, s);
@@ -416,8 +439,9 @@ extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, in
         return fail(-2, "sera_q4k_dense: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    const hipError_t e = sk ? sera_launch_q4k_mmq_streamk(W, stage, Y, partial, g_counters, M, N, K, streamk_wgs(M), s)
-                            : sera_launch_q4k_mmq(W, stage, Y, partial, M, N, K, splits, s);
+    const hipError_t e = sk ? sera_launch_q4k_mmq_streamk(qtype, W, stage, Y, partial, g_counters, M, N, K,
+                                                          streamk_wgs(M), s)
+                            : sera_launch_q4k_mmq(qtype, W, stage, Y, partial, M, N, K, splits, s);
     if (e != hipSuccess) return fail(-3, "sera_q4k_dense: mmq launch failed");
     if (timed) record(g_ev.kernel_end, s);
     return 0;
@@ -440,7 +464,7 @@ extern "C" int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float 
         return fail(-1, "sera_q4k_mmq_streamk: workgroups=%d must be a positive multiple of 8", wgs);
     if ((int64_t)sera_mmq_tiles(M, N) * (K / Q4K_QK) < wgs)
         return fail(-1, "sera_q4k_mmq_streamk: fewer (tile, super-block) units than workgroups=%d", wgs);
-    return sera_launch_q4k_mmq_streamk(W, mmq_stage, Y, slots, counters, M, N, K, wgs, (hipStream_t)stream) ==
+    return sera_launch_q4k_mmq_streamk(12u, W, mmq_stage, Y, slots, counters, M, N, K, wgs, (hipStream_t)stream) ==
                    hipSuccess
                ? 0 : fail(-3, "sera_q4k_mmq_streamk: launch failed");
 }
@@ -457,12 +481,18 @@ extern "C" int sera_q4k_kernel_launches(int M, int N, int K) {
 
 extern "C" int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
                                   int timed) {
+    return sera_q4k_dense_vec_qt(12u, W, X, Y, M, N, K, stream, timed);
+}
+
+extern "C" int sera_q4k_dense_vec_qt(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
+                                     void *stream, int timed) {
     if (!check_shape("sera_q4k_dense_vec", W, X, Y, M, N, K)) return -1;
+    if (!q4k_layout_ok("sera_q4k_dense_vec", qtype, N)) return -1;
     if (M > SERA_Q4K_MMVQ_MAX_BATCH)
         return fail(-1, "sera_q4k_dense_vec: batch M=%d exceeds MMVQ cap %d", M, SERA_Q4K_MMVQ_MAX_BATCH);
     if (!g_arena) return fail(-1, "sera_q4k_dense_vec: no arena attached");
-    return dense_vec_on("sera_q4k_dense_vec", W, X, Y, M, N, K, (hipStream_t)stream, timed, g_arena, g_arena_bytes,
-                        g_counters + kFewtokCounterBase, kFewtokMaxCounters);
+    return dense_vec_on("sera_q4k_dense_vec", qtype, W, X, Y, M, N, K, (hipStream_t)stream, timed, g_arena,
+                        g_arena_bytes, g_counters + kFewtokCounterBase, kFewtokMaxCounters);
 }
 
 extern "C" size_t sera_q4k_dense_vec_static_bytes(int M, int N, int K) {
@@ -491,7 +521,7 @@ extern "C" int sera_q4k_dense_vec_static(const void *W, const float *X, float *Y
     if (hipGetDevice(&device) != hipSuccess) return fail(-1, "%s: hipGetDevice failed", tag);
     if (static_scratch_setup(device, s) != 0) return -1;
     unsigned char *base = g_scratch_ptr[device];
-    return dense_vec_on(tag, W, X, Y, M, N, K, s, 0, base + kStaticCounterBytes,
+    return dense_vec_on(tag, 12u, W, X, Y, M, N, K, s, 0, base + kStaticCounterBytes,
                         SERA_Q4K_STATIC_SCRATCH_BYTES - kStaticCounterBytes, (int *)base,
                         (int)(kStaticCounterBytes / sizeof(int)));
 }
@@ -682,12 +712,17 @@ extern "C" int sera_q6k_dense(uint32_t qtype, const void *W, const float *X, flo
 
 namespace {
 bool layout_args_ok(const char *tag, uint32_t qtype, int N, int K) {
-    if (qtype != 12u && qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) {
-        fail(-1, "%s: qtype %u is not Q4_K (12), Q6_K (14) or Q6_K split (%u)", tag, qtype, SERA_QTYPE_Q6K_SPLIT);
+    if (qtype != 12u && qtype != SERA_QTYPE_Q4K_TILED && qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) {
+        fail(-1, "%s: qtype %u is not Q4_K (12), Q4_K tiled (%u), Q6_K (14) or Q6_K split (%u)", tag, qtype,
+             SERA_QTYPE_Q4K_TILED, SERA_QTYPE_Q6K_SPLIT);
         return false;
     }
     if (N <= 0 || K <= 0 || K % Q4K_QK) {
         fail(-1, "%s: bad shape N=%d K=%d", tag, N, K);
+        return false;
+    }
+    if (qtype == SERA_QTYPE_Q4K_TILED && N % Q4K_TILE_ROWS) {
+        fail(-1, "%s: the tiled layout needs N %% 16 == 0 (N=%d)", tag, N);
         return false;
     }
     return true;
@@ -695,8 +730,10 @@ bool layout_args_ok(const char *tag, uint32_t qtype, int N, int K) {
 }  // namespace
 
 extern "C" size_t sera_weight_bytes(uint32_t qtype, int N, int K) {
-    if ((qtype != 12u && qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
-    return (size_t)N * (size_t)(K / Q4K_QK) * (qtype == 12u ? Q4K_BLOCK_BYTES : Q6K_GGUF_BYTES);
+    const bool q4 = qtype == 12u || qtype == SERA_QTYPE_Q4K_TILED;
+    if ((!q4 && qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
+    if (qtype == SERA_QTYPE_Q4K_TILED && N % Q4K_TILE_ROWS) return 0;
+    return (size_t)N * (size_t)(K / Q4K_QK) * (q4 ? Q4K_BLOCK_BYTES : Q6K_GGUF_BYTES);
 }
 
 extern "C" int sera_weight_to_device_layout(uint32_t qtype, int N, int K, const void *gguf, void *dst, void *stream) {
@@ -705,13 +742,19 @@ extern "C" int sera_weight_to_device_layout(uint32_t qtype, int N, int K, const 
     if (!layout_args_ok(tag, qtype, N, K)) return -1;
     const size_t bytes = sera_weight_bytes(qtype, N, K);
     hipStream_t s = (hipStream_t)stream;
-    if (qtype != SERA_QTYPE_Q6K_SPLIT) {
+    if (qtype == 12u || qtype == 14u) {
         if (gguf == dst) return 0;
         return hipMemcpyAsync(dst, gguf, bytes, hipMemcpyDeviceToDevice, s) == hipSuccess
                    ? 0 : fail(-3, "%s: copy failed", tag);
     }
     const char *a = (const char *)gguf, *b = (const char *)dst;
     if (a < b + bytes && b < a + bytes) return fail(-1, "%s: source and destination overlap", tag);
+    if (qtype == SERA_QTYPE_Q4K_TILED) {
+        if (((uintptr_t)gguf & 15u) || ((uintptr_t)dst & 15u))
+            return fail(-1, "%s: GGUF bytes and dst must be 16-byte aligned", tag);
+        return sera_launch_q4k_tile(gguf, dst, 0, (uint64_t)N, (uint64_t)(K / Q4K_QK), s) == hipSuccess
+                   ? 0 : fail(-3, "%s: launch failed", tag);
+    }
     if (((uintptr_t)gguf & 1u) || ((uintptr_t)dst & 15u))
         return fail(-1, "%s: GGUF bytes must be 2-byte and dst 16-byte aligned", tag);
     const uint64_t total = (uint64_t)N * (uint64_t)(K / Q4K_QK);
@@ -725,9 +768,30 @@ extern "C" int sera_weight_upload(uint32_t qtype, int N, int K, const void *host
     if (!layout_args_ok(tag, qtype, N, K)) return -1;
     const size_t bytes = sera_weight_bytes(qtype, N, K);
     hipStream_t s = (hipStream_t)stream;
-    if (qtype != SERA_QTYPE_Q6K_SPLIT)
+    if (qtype == 12u || qtype == 14u)
         return hipMemcpyAsync(dst, host_gguf, bytes, hipMemcpyHostToDevice, s) == hipSuccess
                    ? 0 : fail(-3, "%s: host-to-device copy failed", tag);
+    if (qtype == SERA_QTYPE_Q4K_TILED) {
+        /* whole 16-row groups through the staging buffer */
+        const uint64_t nkb = (uint64_t)(K / Q4K_QK);
+        const uint64_t group_bytes = Q4K_TILE_ROWS * nkb * Q4K_BLOCK_BYTES;
+        if (!staging || staging_bytes < group_bytes)
+            return fail(-1, "%s: the tiled layout needs a device staging buffer of at least %llu bytes", tag,
+                        (unsigned long long)group_bytes);
+        if (((uintptr_t)staging & 15u) || ((uintptr_t)dst & 15u))
+            return fail(-1, "%s: staging and dst must be 16-byte aligned", tag);
+        const uint64_t per = (staging_bytes / group_bytes) * Q4K_TILE_ROWS;
+        const char *src = (const char *)host_gguf;
+        for (uint64_t row0 = 0; row0 < (uint64_t)N; row0 += per) {
+            const uint64_t rows = (uint64_t)N - row0 < per ? (uint64_t)N - row0 : per;
+            if (hipMemcpyAsync(staging, src + row0 * nkb * Q4K_BLOCK_BYTES, rows * nkb * Q4K_BLOCK_BYTES,
+                               hipMemcpyHostToDevice, s) != hipSuccess)
+                return fail(-3, "%s: host-to-device copy failed", tag);
+            if (sera_launch_q4k_tile(staging, dst, row0, rows, nkb, s) != hipSuccess)
+                return fail(-3, "%s: repack launch failed", tag);
+        }
+        return 0;
+    }
     if (!staging || staging_bytes < Q6K_GGUF_BYTES)
         return fail(-1, "%s: the split layout needs a device staging buffer of at least %d bytes", tag,
                     Q6K_GGUF_BYTES);
@@ -754,8 +818,13 @@ extern "C" int sera_weight_upload(uint32_t qtype, int N, int K, const void *host
 namespace {
 bool rows_shape_ok(const char *tag, int qtype, const void *W, int N, int K) {
     if (!W) { fail(-1, "%s: null weight pointer", tag); return false; }
-    if (qtype != 12 && qtype != 14 && qtype != (int)SERA_QTYPE_Q6K_SPLIT) {
-        fail(-1, "%s: qtype %d is not Q4_K (12), Q6_K (14) or Q6_K split (%u)", tag, qtype, SERA_QTYPE_Q6K_SPLIT);
+    if (qtype != 12 && qtype != (int)SERA_QTYPE_Q4K_TILED && qtype != 14 && qtype != (int)SERA_QTYPE_Q6K_SPLIT) {
+        fail(-1, "%s: qtype %d is not Q4_K (12), Q4_K tiled (%u), Q6_K (14) or Q6_K split (%u)", tag, qtype,
+             SERA_QTYPE_Q4K_TILED, SERA_QTYPE_Q6K_SPLIT);
+        return false;
+    }
+    if (qtype == (int)SERA_QTYPE_Q4K_TILED && N % Q4K_TILE_ROWS) {
+        fail(-1, "%s: the tiled layout needs N %% 16 == 0 (N=%d)", tag, N);
         return false;
     }
     if (N <= 0 || K <= 0 || K % Q4K_QK) { fail(-1, "%s: bad shape N=%d K=%d", tag, N, K); return false; }
@@ -817,8 +886,14 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         if (!check_shape(tag, weights[i], X, outputs[i], M, g->N, K)) return -1;
         N[i] = g->N;
     }
-    if (qt != 12 && qt != 14 && qt != SERA_QTYPE_Q6K_SPLIT) return fail(-1, "%s: qtype %u is not Q4_K/Q6_K", tag, qt);
-    if (qt != 12 && !q6k_shape_ok(tag, qt, K)) return -1;
+    if (qt != 12 && qt != SERA_QTYPE_Q4K_TILED && qt != 14 && qt != SERA_QTYPE_Q6K_SPLIT)
+        return fail(-1, "%s: qtype %u is not Q4_K/Q6_K", tag, qt);
+    /* q4: the Q4_K kernels, on GGUF bytes or the tiled layout */
+    const bool q4 = qt == 12 || qt == SERA_QTYPE_Q4K_TILED;
+    if (q4)
+        for (int i = 0; i < count; i++)
+            if (!q4k_layout_ok(tag, qt, N[i])) return -1;
+    if (!q4 && !q6k_shape_ok(tag, qt, K)) return -1;
     hipStream_t s = (hipStream_t)stream;
     const int accum = (flags & SERA_LIN_ACCUMULATE) ? 1 : 0;
     sera_producer prod = {0, X2, gamma, eps};
@@ -834,7 +909,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
     /* stage, then per-matrix split-K partials or stream-K slots */
     size_t stage_bytes;
     int Mpad = M;
-    if (qt == 12) {
+    if (q4) {
         if (M <= SERA_Q4K_MMVQ_MAX_BATCH) {
             stage_bytes = sera_row_stage_layout((size_t)M, (size_t)K).total;
         } else {
@@ -853,7 +928,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
 
     /* quantize once */
     hipError_t qe;
-    if (qt == 12)
+    if (q4)
         qe = M <= SERA_Q4K_MMVQ_MAX_BATCH ? sera_launch_q8_1_row_p(X, &prod, M, K, g_arena, s)
                                           : sera_launch_q8_1_mmq_p(X, &prod, M, Mpad, K, g_arena, s);
     else
@@ -864,7 +939,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
     if (qe != hipSuccess) return fail(-2, "%s: quantize launch failed", tag);
 
     /* the products */
-    if (qt == 12 && M <= SERA_Q4K_MMVQ_MAX_BATCH) {
+    if (q4 && M <= SERA_Q4K_MMVQ_MAX_BATCH) {
         /* the matrices the dot4 kernel takes share one grouped launch; the
          * few-token kernel runs the others one by one */
         const void *gw[SERA_LINEAR_GROUP_MAX];
@@ -878,11 +953,11 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
                 gn[g] = N[i];
                 g++;
             }
-        if (g > 0 && sera_launch_q4k_mmvq_group(g, gw, gy, gn, g_arena, M, K, 0, accum, s) != hipSuccess)
+        if (g > 0 && sera_launch_q4k_mmvq_group(qt, g, gw, gy, gn, g_arena, M, K, 0, accum, s) != hipSuccess)
             return fail(-3, "%s: grouped mmvq launch failed", tag);
         for (int i = 0; i < count; i++)
             if (sera_q4k_vec_uses_fewtok(M, N[i], K)) {
-                const int rc = fewtok_launch(tag, 0, weights[i], outputs[i], partial, partial_cap, M, N[i], K,
+                const int rc = fewtok_launch(tag, qt, 0, weights[i], outputs[i], partial, partial_cap, M, N[i], K,
                                              accum, s);
                 if (rc) return rc;
             }
@@ -892,19 +967,19 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         hipError_t e;
         const int n = N[i];
         const bool mn4 = ((size_t)M * n) % 4 == 0;
-        if (qt == 12 && sera_q4k_mmq_uses_fewtok(M, n, K)) {
-            const int rc = fewtok_launch(tag, 1, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
+        if (q4 && sera_q4k_mmq_uses_fewtok(M, n, K)) {
+            const int rc = fewtok_launch(tag, qt, 1, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
             if (rc) return rc;
             continue;
-        } else if (qt == 12) {
+        } else if (q4) {
             const size_t slot_floats = (size_t)2 * streamk_wgs(M) * sera_mmq_slot_floats(M);
             if (use_streamk(M, n, K) && slot_floats <= partial_cap) {
-                e = sera_launch_q4k_mmq_streamk_acc(weights[i], g_arena, outputs[i], partial, g_counters, M, n, K,
-                                                    streamk_wgs(M), accum, s);
+                e = sera_launch_q4k_mmq_streamk_acc(qt, weights[i], g_arena, outputs[i], partial, g_counters, M, n,
+                                                    K, streamk_wgs(M), accum, s);
             } else {
                 int sp = mn4 ? sera_mmq_splits(M, n, K) : 1;
                 if ((size_t)sp * M * n > partial_cap) sp = 1;
-                e = sera_launch_q4k_mmq_acc(weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
+                e = sera_launch_q4k_mmq_acc(qt, weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
             }
         } else if (!q6_tile) {
             e = sera_launch_q6k_mmvq_acc(qt, weights[i], g_arena, outputs[i], M, n, K, 0, accum, s);

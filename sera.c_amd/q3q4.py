@@ -87,6 +87,8 @@ def load():
         "sera_q4k_set_arena": ([P, SZ], I),
         "sera_q4k_dense": ([P, P, P, I, I, I, P, I], I),
         "sera_q4k_dense_vec": ([P, P, P, I, I, I, P, I], I),
+        "sera_q4k_dense_qt": ([U32, P, P, P, I, I, I, P, I], I),
+        "sera_q4k_dense_vec_qt": ([U32, P, P, P, I, I, I, P, I], I),
         "sera_q4k_dense_vec_static": ([P, P, P, I, I, I, P], I),
         "sera_q4k_dense_vec_static_bytes": ([I, I, I], SZ),
         "sera_q4k_read_timings": ([ctypes.POINTER(ctypes.c_double)] * 3, None),
@@ -344,6 +346,17 @@ def quantize_row_q6k(x, stage, stream=None):
 
 
 QTYPE_Q6K_SPLIT = 270   # SERA_QTYPE_Q6K_SPLIT: Q6_K in the split device layout
+QTYPE_Q4K_TILED = 268   # SERA_QTYPE_Q4K_TILED: Q4_K in the 16-row tiled device layout
+
+
+def q4k_tiled_bytes(gguf, N, K):
+    """Host-side statement of the tiled layout (numpy uint8 in, uint8 out):
+    block (r, b) of the GGUF rows lands at ((r//16)*(K//256) + b)*2304 +
+    (r%16)*144. The device repack must give exactly these bytes."""
+    import numpy as np
+    nkb = K // 256
+    blocks = np.asarray(gguf, dtype=np.uint8).reshape(N // 16, 16, nkb, 144)
+    return np.ascontiguousarray(blocks.transpose(0, 2, 1, 3)).reshape(-1)
 
 
 def q6k_mmvq(W, stage, out, M, N, K, rows_per_wave=0, stream=None, qtype=14):

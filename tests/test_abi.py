@@ -48,6 +48,7 @@ def test_struct_layouts_match_reference():
     (12, 25600, 5120, 73_728_000),     # down
     (12, 5120, 151936, 437_575_680),   # LM head
     (14, 5120, 1024, 1024 * 20 * 210), # Q6_K: 210-byte blocks, run by the same call
+    (268, 5120, 151936, 437_575_680),  # Q4_K tiled: the same bytes reordered
 ])
 def test_bind_geometry(qtype, dim0, dim1, wbytes):
     g = q3q4.bind_geometry(qtype, dim0, dim1)
@@ -60,10 +61,28 @@ def test_bind_geometry(qtype, dim0, dim1, wbytes):
     (12, 512, 0, "degenerate"),
     (12, 5000, 100, "multiple of 256"),
     (12, 2 ** 31 + 256, 4, "exceeds int32"),
+    (268, 5120, 100, "divisible by 16"),
 ])
 def test_bind_geometry_errors(qtype, dim0, dim1, msg):
     with pytest.raises(q3q4.Q3Q4Error, match=msg):
         q3q4.bind_geometry(qtype, dim0, dim1)
+
+
+def test_tiled_layout_host_statement_and_sizes(L):
+    """q3q4.q4k_tiled_bytes against the offset formula written block by
+    block, and sera_weight_bytes for the tiled qtype (pure host)."""
+    import numpy as np
+    rng = np.random.default_rng(5)
+    for N, K in ((16, 256), (48, 768), (32, 2304)):
+        W = rng.integers(0, 256, N * K // 256 * 144, dtype=np.uint8)
+        want = np.empty_like(W)
+        for r in range(N):
+            for b in range(K // 256):
+                o = ((r // 16) * (K // 256) + b) * 2304 + (r % 16) * 144
+                want[o:o + 144] = W[(r * (K // 256) + b) * 144:(r * (K // 256) + b + 1) * 144]
+        assert np.array_equal(q3q4.q4k_tiled_bytes(W, N, K), want)
+        assert L.sera_weight_bytes(q3q4.QTYPE_Q4K_TILED, N, K) == W.size
+    assert L.sera_weight_bytes(q3q4.QTYPE_Q4K_TILED, 40, 256) == 0
 
 
 def test_bind_geometry_null_out(L):
