@@ -314,6 +314,9 @@ def main():
         # at 16 tokens the LM head is bound by its 437 MB of weights
         lm["kernel_frac_hbm"] = round(lm["kernel_GBps"] / HBM_PEAK_GBS, 4)
         results["config4_lm_head_m16"] = lm
+        results["q4k_tiled_layout"] = tiled_cases(torch, q3q4, L, dev, activations, bench_linear, bench_kernel,
+                                                  {"gate_up": (gN, gK, gws), "down": (5120, 25600, sets["down"][2][0]),
+                                                   "lm_head": (151936, 5120, lmw)}, args)
         del lmw
         results["config5_decode_stream"] = decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr)
 
@@ -348,6 +351,64 @@ def main():
         "results": results,
     }
     print(json.dumps(out), flush=True)
+
+
+def tiled_cases(torch, q3q4, L, dev, activations, bench_linear, bench_kernel, mats, args):
+    """The same Q4_K matrices in the 16-row tiled layout (qtype 268, made
+    on the device from the GGUF copies): the whole q3_cuda_q4k_linear call
+    and the kernel alone on the tiled copies, and the kernel alone on the
+    GGUF copies measured right after for an A/B on the same box (the GGUF
+    rule's own kernel choice is in mmvq_sweep and mmq_few_tokens). Decode
+    batch sizes where the few-token kernel runs (2-16 tokens), M=1 (dot4
+    MMVQ), and the LM head at 4-16 tokens."""
+    T = q3q4.QTYPE_Q4K_TILED
+    rows = []
+    plan = {"gate_up": (1, 2, 4, 8, 16), "down": (1, 4, 8, 16), "lm_head": (4, 8, 16)}
+    for name, (N, K, gbufs) in mats.items():
+        tbufs = []
+        for w in gbufs:
+            t = torch.empty(w.numel(), dtype=torch.uint8, device=dev)
+            q3q4.weight_to_device_layout(T, N, K, w, t)
+            tbufs.append(t)
+        torch.cuda.synchronize()
+        n = len(gbufs)
+        garr = (ctypes.c_void_p * n)(*[w.data_ptr() for w in gbufs])
+        tarr = (ctypes.c_void_p * n)(*[w.data_ptr() for w in tbufs])
+        geo = q3q4.bind_geometry(T, K, N)
+        iters = 20 if name == "lm_head" else max(50, args.steps // 2)
+        for M in plan[name]:
+            x = activations(M, K, 60 + M)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            step_ms = bench_linear(geo, tarr, n, x, y, 5, iters)
+            if M <= 8:
+                stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
+                q3q4.quantize_row(x, stage)
+                path = 12 if L.sera_q4k_vec_uses_fewtok_qt(T, M, N, K) else 0
+            else:
+                stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
+                q3q4.quantize_mmq(x, stage)
+                path = 13
+                assert L.sera_q4k_mmq_uses_fewtok(M, N, K)
+            part = None
+            if path != 0:
+                part = torch.zeros(q3q4.fewtok_splits(M, N, K) * M * N + q3q4.fewtok_groups(M, N, K),
+                                   dtype=torch.float32, device=dev)
+            kt, _ = bench_kernel(256 + path, tarr, n, stage, y, part, M, N, K, 0, 5, iters)
+            kg, _ = bench_kernel(path, garr, n, stage, y, part, M, N, K, 0, 5, iters)
+            b = alg_bytes(M, N, K)
+            row = {"proj": name, "M": M, "N": N, "K": K,
+                   "kernel": "dot4 MMVQ" if path == 0 else f"few-token (form {path - 12})",
+                   "step_us": round(step_ms * 1e3, 2), "kernel_us": round(kt * 1e3, 2),
+                   "kernel_frac_hbm": round(b / (kt * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "same_kernel_on_gguf_us": round(kg * 1e3, 2),
+                   "same_kernel_on_gguf_frac_hbm": round(b / (kg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            log(f"[bench] tiled {name} M={M}: step {row['step_us']} us, {row['kernel']} {row['kernel_us']} us "
+                f"({100 * row['kernel_frac_hbm']:.1f}% of HBM); the same kernel on GGUF bytes "
+                f"{row['same_kernel_on_gguf_us']} us ({100 * row['same_kernel_on_gguf_frac_hbm']:.1f}%)")
+            rows.append(row)
+        del tbufs
+        torch.cuda.empty_cache()
+    return rows
 
 
 def lm_head_rows(torch, dev, bench_kernel):

@@ -60,7 +60,8 @@ int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K,
 
 /* Same contract through the MMVQ path (MMVQ arithmetic), 1 <= M <= 8:
  * the dot4 MMVQ kernel or the few-token MFMA kernel (form 0), as
- * sera_q4k_vec_uses_fewtok chooses. Replaces q3_mmq_q4_K_dense_vec
+ * sera_q4k_vec_uses_fewtok (sera_q4k_vec_uses_fewtok_qt for the _qt call
+ * below) chooses. Replaces q3_mmq_q4_K_dense_vec
  * (cuda/q3_mmq.cu:408-506). */
 int sera_q4k_dense_vec(const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
@@ -113,6 +114,13 @@ int sera_q4k_kernel_launches(int M, int N, int K);
  * MMVQ kernel. No counterpart in the reference (cuda/mmq/mmvq.cu has one
  * kernel); a dispatch query. */
 int sera_q4k_vec_uses_fewtok(int M, int N, int K);
+
+/* The same query for the weight layout of qtype: 12 as above; on
+ * SERA_QTYPE_Q4K_TILED the few-token kernel takes over earlier (matrices of
+ * 16384+ rows from 2 tokens; 4096-16383 rows from 3 when K >= 16384, else
+ * from 5 at 8192+ rows and from 6 below), as it gains more from the tiled
+ * bytes than dot4 does. 0 for any other qtype. */
+int sera_q4k_vec_uses_fewtok_qt(uint32_t qtype, int M, int N, int K);
 
 /* 1 if a Q6_K call on the MMVQ path (1 <= M <= 8) runs the tile kernel on a
  * row-formula stage for an N x K matrix (from 4 tokens at 16384 or more

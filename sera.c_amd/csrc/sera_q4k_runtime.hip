@@ -66,6 +66,21 @@ extern "C" int sera_q4k_vec_uses_fewtok(int M, int N, int K) {
     return 0;
 }
 
+/* The same choice on the tiled layout, where the few-token kernel reads each
+ * 16-row group of a super-block as one 2304-byte run (15-19% faster than on
+ * GGUF bytes) and dot4 loses 0-6%. Kernel us, dot4 / few-token, both on the
+ * tiled bytes: gate/up 2 tokens 17.3 / 15.9; LM head 2: 79.3 / 76.8;
+ * down 3: 20.9 / 20.7, 4: 23.1 / 21.3; q 5: 10.8 / 9.8; o 5: 9.3 / 12.1,
+ * 6: 14.9 / 12.1; k/v dot4 at every batch (8: 5.3 / 9.2). At one token
+ * dot4 stays ahead everywhere (gate/up 14.2 / 15.7). */
+extern "C" int sera_q4k_vec_uses_fewtok_qt(uint32_t qtype, int M, int N, int K) {
+    if (qtype != SERA_QTYPE_Q4K_TILED) return qtype == 12u ? sera_q4k_vec_uses_fewtok(M, N, K) : 0;
+    if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH || N <= 0) return 0;
+    if (N >= 16384) return M >= 2;
+    if (N >= 4096) return M >= (K >= 16384 ? 3 : N >= 8192 ? 5 : 6);
+    return 0;
+}
+
 /* The MMQ path runs the same kernel with the MMQ formula on the MMQ stage
  * at 1-8 tokens, and at 9-16 tokens on the matrices whose rows or K reach
  * 16384 (its 8-wave plan). Against the paired 16-token MMQ tile, measured
@@ -368,7 +383,7 @@ int dense_vec_on(const char *tag, uint32_t qtype, const void *W, const float *X,
     if (sera_launch_q8_1_row(X, M, K, stage, s) != hipSuccess) return fail(-2, "%s: quantize launch failed", tag);
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    if (sera_q4k_vec_uses_fewtok(M, N, K)) {
+    if (sera_q4k_vec_uses_fewtok_qt(qtype, M, N, K)) {
         const int rc = fewtok_launch_on(tag, qtype, 0, W, stage, Y, (float *)(stage + stage_bytes),
                                         (stage_cap - stage_bytes) / sizeof(float), counters, ncounters, M, N, K, 0, s);
         if (rc) return rc;
@@ -947,7 +962,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         int gn[SERA_LINEAR_GROUP_MAX];
         int g = 0;
         for (int i = 0; i < count; i++)
-            if (!sera_q4k_vec_uses_fewtok(M, N[i], K)) {
+            if (!sera_q4k_vec_uses_fewtok_qt(qt, M, N[i], K)) {
                 gw[g] = weights[i];
                 gy[g] = outputs[i];
                 gn[g] = N[i];
@@ -956,7 +971,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         if (g > 0 && sera_launch_q4k_mmvq_group(qt, g, gw, gy, gn, g_arena, M, K, 0, accum, s) != hipSuccess)
             return fail(-3, "%s: grouped mmvq launch failed", tag);
         for (int i = 0; i < count; i++)
-            if (sera_q4k_vec_uses_fewtok(M, N[i], K)) {
+            if (sera_q4k_vec_uses_fewtok_qt(qt, M, N[i], K)) {
                 const int rc = fewtok_launch(tag, qt, 0, weights[i], outputs[i], partial, partial_cap, M, N[i], K,
                                              accum, s);
                 if (rc) return rc;

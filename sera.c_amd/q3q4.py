@@ -110,6 +110,7 @@ def load():
         "sera_q4k_fewtok_grid": ([I, I, I, I, I], I),
         "sera_q4k_kernel_launches": ([I, I, I], I),
         "sera_q4k_vec_uses_fewtok": ([I, I, I], I),
+        "sera_q4k_vec_uses_fewtok_qt": ([U32, I, I, I], I),
         "sera_q6k_vec_uses_tile": ([I, I, I], I),
         "sera_q4k_mmq_streamk": ([P, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_streamk_wgs": ([I], I),

@@ -251,6 +251,25 @@ def test_vec_dispatch_rule(L):
     assert f(0, 25600, 5120) == 0 and f(9, 25600, 5120) == 0
 
 
+def test_vec_dispatch_rule_tiled_layout(L):
+    """On the tiled layout the few-token kernel takes over earlier: tall
+    matrices from 2 tokens, down (K 25600) from 3, q (8192 rows) from 5, o
+    (5120 rows, K 8192) from 6, k/v never; qtype 12 answers as the GGUF
+    query and other qtypes 0."""
+    T = q3q4.QTYPE_Q4K_TILED
+    f = L.sera_q4k_vec_uses_fewtok_qt
+    assert [f(T, M, 25600, 5120) for M in range(1, 9)] == [0, 1, 1, 1, 1, 1, 1, 1]
+    assert [f(T, M, 151936, 5120) for M in range(1, 9)] == [0, 1, 1, 1, 1, 1, 1, 1]
+    assert [f(T, M, 5120, 25600) for M in range(1, 9)] == [0, 0, 1, 1, 1, 1, 1, 1]
+    assert [f(T, M, 8192, 5120) for M in range(1, 9)] == [0, 0, 0, 0, 1, 1, 1, 1]
+    assert [f(T, M, 5120, 8192) for M in range(1, 9)] == [0, 0, 0, 0, 0, 1, 1, 1]
+    assert [f(T, M, 1024, 5120) for M in range(1, 9)] == [0] * 8
+    for M in range(0, 10):
+        for N, K in ((25600, 5120), (5120, 25600), (8192, 5120), (1024, 5120)):
+            assert f(12, M, N, K) == L.sera_q4k_vec_uses_fewtok(M, N, K)
+    assert f(14, 4, 25600, 5120) == 0 and f(T, 9, 25600, 5120) == 0
+
+
 def test_q6k_vec_dispatch_rule(L):
     """Q6_K on the MMVQ path: the tile kernel on tall matrices from 4 tokens,
     on 4096-16383 rows from 6, never below 4096 rows; launch counts follow."""

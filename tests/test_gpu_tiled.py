@@ -249,7 +249,12 @@ def test_tiled_mmq_bit_identical(torch, linear, M, N, K):
 def test_tiled_linear_boundary(torch, linear, N, K):
     """q3_cuda_q4k_linear with a tiled geometry, every path the batch size
     picks (MMVQ, few-token in both formulas, MMQ split-K / stream-K), is
-    bit-identical to the GGUF geometry."""
+    bit-identical to the GGUF geometry where both pick the same kernel.
+    Where the tiled rule picks the few-token kernel and the GGUF rule dot4
+    (sera_q4k_vec_uses_fewtok_qt), the tiled output is bit-identical to the
+    few-token kernel on the GGUF bytes and within 2e-5 * rms of the dot4
+    output (the same MMVQ formula summed in another order)."""
+    L = q3q4.load()
     rng = np.random.default_rng(N + 3 * K)
     Wg = device_blocks(torch, N, K, 11 * N + K)
     Wt = to_tiled(torch, Wg, N, K)
@@ -262,7 +267,22 @@ def test_tiled_linear_boundary(torch, linear, N, K):
         linear(gg, Wg, x, yg)
         linear(gt, Wt, x, yt)
         torch.cuda.synchronize()
-        same_bits(yg, yt, f"boundary M={M} N={N} K={K}")
+        if M <= 8 and L.sera_q4k_vec_uses_fewtok_qt(TILED, M, N, K) != L.sera_q4k_vec_uses_fewtok(M, N, K):
+            assert L.sera_q4k_vec_uses_fewtok_qt(TILED, M, N, K) == 1
+            stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+            q3q4.quantize_row(x, stage)
+            part = torch.zeros(q3q4.fewtok_splits(M, N, K) * M * N + q3q4.fewtok_groups(M, N, K),
+                               dtype=torch.float32, device="cuda")
+            yk = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+            kernel_once(torch, 12, Wg, stage, yk, part, M, N, K, 0)
+            same_bits(yk, yt, f"boundary M={M} N={N} K={K} (few-token on both layouts)")
+            a, b = yt.cpu().numpy().astype(np.float64), yg.cpu().numpy().astype(np.float64)
+            rms = float(np.sqrt(np.mean(b * b)))
+            err = float(np.max(np.abs(a - b)))
+            say(f"  tiled few-token vs GGUF dot4: max|diff| = {err:.3e}, rms = {rms:.3e}")
+            assert err <= 2e-5 * rms
+        else:
+            same_bits(yg, yt, f"boundary M={M} N={N} K={K}")
 
 
 def test_tiled_lm_head_boundary(torch, linear):
@@ -272,7 +292,7 @@ def test_tiled_lm_head_boundary(torch, linear):
     Wg = device_blocks(torch, N, K, 4242)
     Wt = to_tiled(torch, Wg, N, K)
     gg, gt = q3q4.bind_geometry(12, K, N), q3q4.bind_geometry(TILED, K, N)
-    for M in (1, 4, 8, 16):
+    for M in (1, 3, 4, 8, 16):
         say(f"case tiled LM head M={M}")
         x = dev(torch, activations(rng, M, K))
         yg = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
@@ -354,3 +374,34 @@ def test_tiled_gathered_rows_bit_identical(torch, N, K):
     ref = oracle.dequant(Wg.cpu().numpy(), N, K)
     assert np.array_equal(et[0].view(np.uint32), ref[ids[0]].view(np.uint32))
     assert np.all(et[3] == 7.25) and np.isnan(lgt[3])
+
+
+def test_tiled_group_gate_up_two_tokens(torch, linear):
+    """gate and up at 2 tokens: on the tiled layout both run the few-token
+    kernel (the GGUF rule would group them on dot4). The group's outputs are
+    bit-identical to one boundary call per matrix on the same tiled bytes,
+    and with SERA_LIN_ACCUMULATE add exactly that product."""
+    N, K, M = 25600, 5120, 2
+    rng = np.random.default_rng(77)
+    assert q3q4.load().sera_q4k_vec_uses_fewtok_qt(TILED, M, N, K) == 1
+    Wt = [to_tiled(torch, device_blocks(torch, N, K, 90 + i), N, K) for i in range(2)]
+    geo = q3q4.bind_geometry(TILED, K, N)
+    x = dev(torch, activations(rng, M, K))
+    say("case tiled group gate/up M=2")
+    ref = []
+    for w in Wt:
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        linear(geo, w, x, y)
+        ref.append(y)
+    ys = [torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda") for _ in Wt]
+    q3q4.linear_group([geo, geo], Wt, ys, x)
+    torch.cuda.synchronize()
+    for a, b in zip(ys, ref):
+        same_bits(a, b, "group vs boundary")
+    y0 = [rng.standard_normal((M, N)).astype(np.float32) for _ in Wt]
+    ya = [dev(torch, a) for a in y0]
+    q3q4.linear_group([geo, geo], Wt, ya, x, None, None, 0.0, q3q4.LIN_ACCUMULATE)
+    torch.cuda.synchronize()
+    for a, b, c in zip(ya, ref, y0):
+        want = (torch.from_numpy(c).cuda() + b)
+        same_bits(a, want, "group accumulate")
