@@ -360,10 +360,11 @@ def tiled_cases(torch, q3q4, L, dev, activations, bench_linear, bench_kernel, ma
     GGUF copies measured right after for an A/B on the same box (the GGUF
     rule's own kernel choice is in mmvq_sweep and mmq_few_tokens). Decode
     batch sizes where the few-token kernel runs (2-16 tokens), M=1 (dot4
-    MMVQ), and the LM head at 4-16 tokens."""
+    MMVQ), the LM head at 4-16 tokens, and the whole call at 512 tokens
+    (MMQ path) on both layouts."""
     T = q3q4.QTYPE_Q4K_TILED
     rows = []
-    plan = {"gate_up": (1, 2, 4, 8, 16), "down": (1, 4, 8, 16), "lm_head": (4, 8, 16)}
+    plan = {"gate_up": (1, 2, 4, 8, 16, 512), "down": (1, 4, 8, 16, 512), "lm_head": (4, 8, 16)}
     for name, (N, K, gbufs) in mats.items():
         tbufs = []
         for w in gbufs:
@@ -379,6 +380,22 @@ def tiled_cases(torch, q3q4, L, dev, activations, bench_linear, bench_kernel, ma
         for M in plan[name]:
             x = activations(M, K, 60 + M)
             y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            if M > 16:
+                # prefill: the whole call (quantize + MMQ schedule) on either layout
+                gg = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+                ts, gs = [], []
+                for _ in range(3):   # interleaved, median of three
+                    ts.append(bench_linear(geo, tarr, n, x, y, 2, 10))
+                    gs.append(bench_linear(gg, garr, n, x, y, 2, 10))
+                st, sg = sorted(ts)[1], sorted(gs)[1]
+                ops = 2.0 * M * N * K
+                row = {"proj": name, "M": M, "N": N, "K": K, "kernel": "MMQ path (whole call)",
+                       "step_us": round(st * 1e3, 2), "step_TOPS": round(ops / (st * 1e-3) / 1e12, 1),
+                       "gguf_step_us": round(sg * 1e3, 2), "gguf_step_TOPS": round(ops / (sg * 1e-3) / 1e12, 1)}
+                log(f"[bench] tiled {name} M={M}: step {row['step_us']} us ({row['step_TOPS']} TOPS); "
+                    f"GGUF bytes {row['gguf_step_us']} us ({row['gguf_step_TOPS']} TOPS)")
+                rows.append(row)
+                continue
             step_ms = bench_linear(geo, tarr, n, x, y, 5, iters)
             if M <= 8:
                 stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)

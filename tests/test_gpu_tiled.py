@@ -405,3 +405,23 @@ def test_tiled_group_gate_up_two_tokens(torch, linear):
     for a, b, c in zip(ya, ref, y0):
         want = (torch.from_numpy(c).cuda() + b)
         same_bits(a, want, "group accumulate")
+
+
+@pytest.mark.parametrize("N,K", [(16, 256), (48, 768), (272, 2304)])
+def test_tiled_small_matrices_boundary(torch, linear, N, K):
+    """One to 17 tiles: the dot4 kernel's shifted last tile, the MMQ row
+    clamp and the few-token row clamp all stay inside whole 16-row tiles;
+    every batch size is bit-identical to the GGUF bytes."""
+    rng = np.random.default_rng(N * 7 + K)
+    Wg = device_blocks(torch, N, K, 5 * N + K)
+    Wt = to_tiled(torch, Wg, N, K)
+    gg, gt = q3q4.bind_geometry(12, K, N), q3q4.bind_geometry(TILED, K, N)
+    for M in (1, 2, 3, 5, 8, 9, 16, 33, 100):
+        say(f"case tiled small boundary N={N} K={K} M={M}")
+        x = dev(torch, activations(rng, M, K))
+        yg = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        yt = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        linear(gg, Wg, x, yg)
+        linear(gt, Wt, x, yt)
+        torch.cuda.synchronize()
+        same_bits(yg, yt, f"small boundary N={N} K={K} M={M}")
