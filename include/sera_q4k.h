@@ -206,6 +206,18 @@ int sera_q4k_mmq_slot_floats(int M);
  * product to Y. */
 int sera_q4k_fewtok(int form, const void *W, const void *stage, float *Y, float *slots, int *counters, int M, int N,
                     int K, int chunk, int accum, void *stream);
+
+/* The four kernel calls above on the weight layout of qtype: 12 (GGUF
+ * bytes, what the calls above take) or SERA_QTYPE_Q4K_TILED (N % 16 == 0).
+ * Same arguments, kernels and results otherwise. */
+int sera_q4k_mmvq_qt(uint32_t qtype, const void *W, const void *row_stage, float *Y, int M, int N, int K,
+                     int rows_per_tile, void *stream);
+int sera_q4k_mmq_qt(uint32_t qtype, const void *W, const void *mmq_stage, float *Y, float *partial, int M, int N,
+                    int K, int splits, void *stream);
+int sera_q4k_mmq_streamk_qt(uint32_t qtype, const void *W, const void *mmq_stage, float *Y, float *slots,
+                            int *counters, int M, int N, int K, int wgs, void *stream);
+int sera_q4k_fewtok_qt(uint32_t qtype, int form, const void *W, const void *stage, float *Y, float *slots,
+                       int *counters, int M, int N, int K, int chunk, int accum, void *stream);
 int sera_q4k_fewtok_splits(int M, int N, int K, int chunk);
 int sera_q4k_fewtok_groups(int M, int N, int K);
 /* Workgroups along the rows of that launch on the current device: the row

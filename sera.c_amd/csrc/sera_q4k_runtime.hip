@@ -266,15 +266,37 @@ extern "C" int sera_q4k_mmvq_rows_per_tile(int M, int N, int K) {
     return sera_mmvq_rows_per_wave(N, K, M);
 }
 
+namespace {
+/* The weight layouts of the Q4_K path: 12 (GGUF bytes) or the 16-row tiled
+ * layout, which needs N % 16 == 0. */
+bool q4k_layout_ok(const char *tag, uint32_t qtype, int N) {
+    if (qtype != 12u && qtype != SERA_QTYPE_Q4K_TILED) {
+        fail(-1, "%s: qtype %u is not Q4_K (12) or Q4_K tiled (%u)", tag, qtype, SERA_QTYPE_Q4K_TILED);
+        return false;
+    }
+    if (qtype == SERA_QTYPE_Q4K_TILED && N % Q4K_TILE_ROWS) {
+        fail(-1, "%s: the tiled layout needs N %% 16 == 0 (N=%d)", tag, N);
+        return false;
+    }
+    return true;
+}
+}  // namespace
+
 extern "C" int sera_q4k_mmvq(const void *W, const void *row_stage, float *Y, int M, int N, int K,
                              int rows_per_tile, void *stream) {
+    return sera_q4k_mmvq_qt(12u, W, row_stage, Y, M, N, K, rows_per_tile, stream);
+}
+
+extern "C" int sera_q4k_mmvq_qt(uint32_t qtype, const void *W, const void *row_stage, float *Y, int M, int N, int K,
+                                int rows_per_tile, void *stream) {
     if (!W || !row_stage || !Y) return fail(-1, "sera_q4k_mmvq: null pointer");
     if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q4k_mmvq: batch M=%d outside 1..8", M);
     if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_mmvq: bad shape N=%d K=%d", N, K);
     if (rows_per_tile != 0 && rows_per_tile != 2 && rows_per_tile != 4 && rows_per_tile != 8 &&
         rows_per_tile != 16)
         return fail(-1, "sera_q4k_mmvq: rows_per_tile=%d not in {0,2,4,8,16}", rows_per_tile);
-    return sera_launch_q4k_mmvq(12u, W, row_stage, Y, M, N, K, rows_per_tile, (hipStream_t)stream) == hipSuccess
+    if (!q4k_layout_ok("sera_q4k_mmvq", qtype, N)) return -1;
+    return sera_launch_q4k_mmvq(qtype, W, row_stage, Y, M, N, K, rows_per_tile, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q4k_mmvq: launch failed");
 }
 
@@ -299,6 +321,11 @@ extern "C" int sera_q4k_fewtok_grid(int form, int M, int N, int K, int chunk) {
 
 extern "C" int sera_q4k_fewtok(int form, const void *W, const void *stage, float *Y, float *slots, int *counters,
                                int M, int N, int K, int chunk, int accum, void *stream) {
+    return sera_q4k_fewtok_qt(12u, form, W, stage, Y, slots, counters, M, N, K, chunk, accum, stream);
+}
+
+extern "C" int sera_q4k_fewtok_qt(uint32_t qtype, int form, const void *W, const void *stage, float *Y, float *slots,
+                                  int *counters, int M, int N, int K, int chunk, int accum, void *stream) {
     if (!W || !stage || !Y) return fail(-1, "sera_q4k_fewtok: null pointer");
     if (form != 0 && form != 1) return fail(-1, "sera_q4k_fewtok: form=%d not 0 (row stage) or 1 (MMQ stage)", form);
     const int mmax = form == 0 ? SERA_Q4K_MMVQ_MAX_BATCH : SERA_Q4K_FEWTOK_MAX_BATCH;
@@ -310,20 +337,27 @@ extern "C" int sera_q4k_fewtok(int form, const void *W, const void *stage, float
         return fail(-1, "sera_q4k_fewtok: chunk=%d outside 0..%d", chunk, sera_fewtok_max_chunk(M));
     if (sera_fewtok_splits(M, N, K, chunk) > 1 && (!slots || !counters))
         return fail(-1, "sera_q4k_fewtok: a split K needs slots and counters");
-    return sera_launch_q4k_fewtok_acc(12u, form, W, stage, Y, slots, counters, M, N, K, chunk, accum ? 1 : 0,
+    if (!q4k_layout_ok("sera_q4k_fewtok", qtype, N)) return -1;
+    return sera_launch_q4k_fewtok_acc(qtype, form, W, stage, Y, slots, counters, M, N, K, chunk, accum ? 1 : 0,
                                       (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q4k_fewtok: launch failed");
 }
 
 extern "C" int sera_q4k_mmq(const void *W, const void *mmq_stage, float *Y, float *partial, int M, int N,
                             int K, int splits, void *stream) {
+    return sera_q4k_mmq_qt(12u, W, mmq_stage, Y, partial, M, N, K, splits, stream);
+}
+
+extern "C" int sera_q4k_mmq_qt(uint32_t qtype, const void *W, const void *mmq_stage, float *Y, float *partial, int M,
+                               int N, int K, int splits, void *stream) {
     if (!W || !mmq_stage || !Y) return fail(-1, "sera_q4k_mmq: null pointer");
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_mmq: bad shape M=%d N=%d K=%d", M, N, K);
     if (splits == 0) splits = sera_mmq_splits(M, N, K);
     if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q4k_mmq: splits=%d outside 1..K/256", splits);
     if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
         return fail(-1, "sera_q4k_mmq: split-K needs a partial buffer and M*N %% 4 == 0");
-    return sera_launch_q4k_mmq(12u, W, mmq_stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
+    if (!q4k_layout_ok("sera_q4k_mmq", qtype, N)) return -1;
+    return sera_launch_q4k_mmq(qtype, W, mmq_stage, Y, partial, M, N, K, splits, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-3, "sera_q4k_mmq: launch failed");
 }
 
@@ -395,21 +429,6 @@ int dense_vec_on(const char *tag, uint32_t qtype, const void *W, const float *X,
 }
 }  // namespace
 
-namespace {
-/* The weight layouts of the Q4_K path: 12 (GGUF bytes) or the 16-row tiled
- * layout, which needs N % 16 == 0. */
-bool q4k_layout_ok(const char *tag, uint32_t qtype, int N) {
-    if (qtype != 12u && qtype != SERA_QTYPE_Q4K_TILED) {
-        fail(-1, "%s: qtype %u is not Q4_K (12) or Q4_K tiled (%u)", tag, qtype, SERA_QTYPE_Q4K_TILED);
-        return false;
-    }
-    if (qtype == SERA_QTYPE_Q4K_TILED && N % Q4K_TILE_ROWS) {
-        fail(-1, "%s: the tiled layout needs N %% 16 == 0 (N=%d)", tag, N);
-        return false;
-    }
-    return true;
-}
-}  // namespace
 
 extern "C" int sera_q4k_dense(const void *W, const float *X, float *Y, int M, int N, int K, void *stream,
                               int timed) {
@@ -471,6 +490,11 @@ extern "C" int sera_q4k_mmq_schedule(int M, int N, int K) {
 
 extern "C" int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
                                     int M, int N, int K, int wgs, void *stream) {
+    return sera_q4k_mmq_streamk_qt(12u, W, mmq_stage, Y, slots, counters, M, N, K, wgs, stream);
+}
+
+extern "C" int sera_q4k_mmq_streamk_qt(uint32_t qtype, const void *W, const void *mmq_stage, float *Y, float *slots,
+                                       int *counters, int M, int N, int K, int wgs, void *stream) {
     if (!W || !mmq_stage || !Y || !slots || !counters) return fail(-1, "sera_q4k_mmq_streamk: null pointer");
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK)
         return fail(-1, "sera_q4k_mmq_streamk: bad shape M=%d N=%d K=%d", M, N, K);
@@ -479,7 +503,8 @@ extern "C" int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float 
         return fail(-1, "sera_q4k_mmq_streamk: workgroups=%d must be a positive multiple of 8", wgs);
     if ((int64_t)sera_mmq_tiles(M, N) * (K / Q4K_QK) < wgs)
         return fail(-1, "sera_q4k_mmq_streamk: fewer (tile, super-block) units than workgroups=%d", wgs);
-    return sera_launch_q4k_mmq_streamk(12u, W, mmq_stage, Y, slots, counters, M, N, K, wgs, (hipStream_t)stream) ==
+    if (!q4k_layout_ok("sera_q4k_mmq_streamk", qtype, N)) return -1;
+    return sera_launch_q4k_mmq_streamk(qtype, W, mmq_stage, Y, slots, counters, M, N, K, wgs, (hipStream_t)stream) ==
                    hipSuccess
                ? 0 : fail(-3, "sera_q4k_mmq_streamk: launch failed");
 }

@@ -101,6 +101,10 @@ def load():
         "sera_q8_1_mmq_stage_offsets": ([I, I, ctypes.POINTER(SZ), ctypes.POINTER(SZ)], None),
         "sera_q8_1_quantize_mmq": ([P, I, I, P, P], I),
         "sera_q4k_mmvq": ([P, P, P, I, I, I, I, P], I),
+        "sera_q4k_mmvq_qt": ([U32, P, P, P, I, I, I, I, P], I),
+        "sera_q4k_mmq_qt": ([U32, P, P, P, P, I, I, I, I, P], I),
+        "sera_q4k_mmq_streamk_qt": ([U32, P, P, P, P, P, I, I, I, I, P], I),
+        "sera_q4k_fewtok_qt": ([U32, I, P, P, P, P, P, I, I, I, I, I, P], I),
         "sera_q4k_mmvq_rows_per_tile": ([I, I, I], I),
         "sera_q4k_mmq": ([P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_splits": ([I, I, I], I),
@@ -261,34 +265,37 @@ def quantize_mmq(x, stage, stream=None):
            "sera_q8_1_quantize_mmq")
 
 
-def mmvq(W, stage, out, M, N, K, rows_per_tile=0, stream=None):
-    _check(load().sera_q4k_mmvq(_ptr(W), _ptr(stage), _ptr(out), M, N, K, rows_per_tile,
-                                _stream(stream)), "sera_q4k_mmvq")
+def mmvq(W, stage, out, M, N, K, rows_per_tile=0, stream=None, qtype=QTYPE_Q4_K):
+    """qtype: QTYPE_Q4_K (GGUF bytes) or QTYPE_Q4K_TILED, as for the other
+    Q4_K kernel calls below."""
+    _check(load().sera_q4k_mmvq_qt(qtype, _ptr(W), _ptr(stage), _ptr(out), M, N, K, rows_per_tile,
+                                   _stream(stream)), "sera_q4k_mmvq")
 
 
-def mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None):
-    _check(load().sera_q4k_mmq(_ptr(W), _ptr(stage), _ptr(out), _ptr(partial), M, N, K, splits,
-                               _stream(stream)), "sera_q4k_mmq")
+def mmq(W, stage, out, M, N, K, splits=0, partial=None, stream=None, qtype=QTYPE_Q4_K):
+    _check(load().sera_q4k_mmq_qt(qtype, _ptr(W), _ptr(stage), _ptr(out), _ptr(partial), M, N, K, splits,
+                                  _stream(stream)), "sera_q4k_mmq")
 
 
 def mmq_splits(M, N, K):
     return load().sera_q4k_mmq_splits(M, N, K)
 
 
-def mmq_streamk(W, stage, out, M, N, K, slots, counters, wgs=0, stream=None):
+def mmq_streamk(W, stage, out, M, N, K, slots, counters, wgs=0, stream=None, qtype=QTYPE_Q4_K):
     """MMQ under a stream-K schedule; counters (int32, sera_q4k_mmq_tiles)
     must be zero and are zero again afterwards."""
-    _check(load().sera_q4k_mmq_streamk(_ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N, K,
-                                       wgs, _stream(stream)), "sera_q4k_mmq_streamk")
+    _check(load().sera_q4k_mmq_streamk_qt(qtype, _ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M,
+                                          N, K, wgs, _stream(stream)), "sera_q4k_mmq_streamk")
 
 
-def fewtok(W, stage, out, M, N, K, chunk=0, slots=None, counters=None, accum=False, form=0, stream=None):
+def fewtok(W, stage, out, M, N, K, chunk=0, slots=None, counters=None, accum=False, form=0, stream=None,
+           qtype=QTYPE_Q4_K):
     """Few-token MFMA kernel: form 0 on a row stage (MMVQ formula, M <= 8),
     form 1 on an MMQ stage (MMQ formula, M <= 16); a split K needs slots
     (splits*M*N float32) and counters (fewtok_groups int32, zero before and
     after)."""
-    _check(load().sera_q4k_fewtok(form, _ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N, K,
-                                  chunk, 1 if accum else 0, _stream(stream)), "sera_q4k_fewtok")
+    _check(load().sera_q4k_fewtok_qt(qtype, form, _ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M,
+                                     N, K, chunk, 1 if accum else 0, _stream(stream)), "sera_q4k_fewtok")
 
 
 def fewtok_splits(M, N, K, chunk=0):

@@ -85,6 +85,20 @@ def test_tiled_layout_host_statement_and_sizes(L):
     assert L.sera_weight_bytes(q3q4.QTYPE_Q4K_TILED, 40, 256) == 0
 
 
+def test_tiled_kernel_calls_reject_bad_layouts(L):
+    """The _qt kernel calls check the qtype and the tiled row count on the
+    host, before any launch."""
+    d = ctypes.c_void_p(256)
+    assert L.sera_q4k_mmvq_qt(q3q4.QTYPE_Q4K_TILED, d, d, d, 1, 40, 256, 0, None) == -1
+    assert b"16" in L.sera_q4k_last_error()
+    assert L.sera_q4k_mmvq_qt(14, d, d, d, 1, 48, 256, 0, None) == -1
+    assert b"qtype" in L.sera_q4k_last_error()
+    assert L.sera_q4k_mmq_qt(q3q4.QTYPE_Q4K_TILED, d, d, d, None, 16, 40, 256, 1, None) == -1
+    assert L.sera_q4k_fewtok_qt(q3q4.QTYPE_Q4K_TILED, 0, d, d, d, None, None, 4, 40, 256, 0, 0, None) == -1
+    assert L.sera_q4k_mmq_streamk_qt(q3q4.QTYPE_Q4K_TILED, d, d, d, d, ctypes.c_void_p(512), 64, 40, 5120, 8,
+                                     None) == -1
+
+
 def test_bind_geometry_null_out(L):
     assert not L.q3_q4_linear_bind_geometry(12, 256, 4, None, None, 0)
 

@@ -92,17 +92,18 @@ def same_bits(a, b, what):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), what
 
 
-def kernel_once(torch, path, W, stage, y, partial, M, N, K, param):
-    """One launch of a Q4_K kernel through the library's kernel loop
-    (sera_q4k_bench_kernel with no warm-up and one iteration)."""
-    L = q3q4.load()
-    arr = (ctypes.c_void_p * 1)(W.data_ptr())
-    avg, tot = ctypes.c_double(), ctypes.c_double()
-    rc = L.sera_q4k_bench_kernel(path, arr, 1, ctypes.c_void_p(stage.data_ptr()), ctypes.c_void_p(y.data_ptr()),
-                                 ctypes.c_void_p(partial.data_ptr() if partial is not None else 0), M, N, K, param,
-                                 q3q4._stream(None), 0, 1, ctypes.byref(avg), ctypes.byref(tot))
-    assert rc == 0, L.sera_q4k_last_error().decode()
+def fewtok_once(torch, qtype, form, W, stage, M, N, K, chunk):
+    """One few-token launch (sera_q4k_fewtok_qt) with fresh split slots and
+    zeroed row-group counters, which must be zero again afterwards."""
+    sp = q3q4.fewtok_splits(M, N, K, chunk)
+    slots = torch.empty(sp * M * N, dtype=torch.float32, device="cuda") if sp > 1 else None
+    counters = torch.zeros(q3q4.fewtok_groups(M, N, K), dtype=torch.int32, device="cuda") if sp > 1 else None
+    y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    q3q4.fewtok(W, stage, y, M, N, K, chunk=chunk, slots=slots, counters=counters, form=form, qtype=qtype)
     torch.cuda.synchronize()
+    if counters is not None:
+        assert int(counters.abs().sum()) == 0, "row-group counters not reset"
+    return y
 
 
 # ---------------------------------------------------------------------------
@@ -165,8 +166,9 @@ def test_tiled_mmvq_bit_identical(torch, N, K):
             say(f"case tiled mmvq M={M} N={N} K={K} rows={rows}")
             yg = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
             yt = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-            kernel_once(torch, 0, Wg, stage, yg, None, M, N, K, rows)
-            kernel_once(torch, 256, Wt, stage, yt, None, M, N, K, rows)
+            q3q4.mmvq(Wg, stage, yg, M, N, K, rows_per_tile=rows)
+            q3q4.mmvq(Wt, stage, yt, M, N, K, rows_per_tile=rows, qtype=TILED)
+            torch.cuda.synchronize()
             same_bits(yg, yt, f"mmvq M={M} N={N} K={K} rows={rows}")
 
 
@@ -193,15 +195,9 @@ def test_tiled_fewtok_bit_identical(torch, form, M, N, K):
         sp = q3q4.fewtok_splits(M, N, K, chunk)
         say(f"case tiled fewtok form={form} M={M} N={N} K={K} chunk={chunk} splits={sp} "
             f"grid={q3q4.fewtok_grid(form, M, N, K, chunk)}")
-        outs = []
-        for path, W in ((12 + form, Wg), (256 + 12 + form, Wt)):
-            part = torch.zeros(sp * M * N + q3q4.fewtok_groups(M, N, K), dtype=torch.float32, device="cuda")
-            y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-            kernel_once(torch, path, W, stage, y, part, M, N, K, chunk)
-            if sp > 1:
-                assert int(part[sp * M * N:].abs().sum()) == 0, "row-group counters not reset"
-            outs.append(y)
-        same_bits(outs[0], outs[1], f"fewtok form={form} M={M} N={N} K={K} chunk={chunk}")
+        yg = fewtok_once(torch, 12, form, Wg, stage, M, N, K, chunk)
+        yt = fewtok_once(torch, TILED, form, Wt, stage, M, N, K, chunk)
+        same_bits(yg, yt, f"fewtok form={form} M={M} N={N} K={K} chunk={chunk}")
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (200, 1008, 2304), (512, 25600, 5120), (33, 4096, 25600)])
@@ -219,24 +215,26 @@ def test_tiled_mmq_bit_identical(torch, linear, M, N, K):
         if s > 1 and (M * N) % 4:
             continue
         say(f"case tiled mmq M={M} N={N} K={K} splits={s}")
-        part = torch.empty(max(s, 1) * M * N, dtype=torch.float32, device="cuda")
+        part = torch.empty(s * M * N, dtype=torch.float32, device="cuda") if s > 1 else None
         ys = []
-        for path, W in ((1, Wg), (257, Wt)):
+        for qt, W in ((12, Wg), (TILED, Wt)):
             y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-            kernel_once(torch, path, W, stage, y, part, M, N, K, s)
+            q3q4.mmq(W, stage, y, M, N, K, splits=s, partial=part, qtype=qt)
+            torch.cuda.synchronize()
             ys.append(y)
         same_bits(ys[0], ys[1], f"mmq M={M} N={N} K={K} splits={s}")
     wgs = L.sera_q4k_mmq_streamk_wgs(M)
     assert wgs >= 8
     if L.sera_q4k_mmq_tiles(M, N) * (K // 256) >= wgs:
         say(f"case tiled mmq stream-K M={M} N={N} K={K} wgs={wgs}")
-        nslot = 2 * wgs * L.sera_q4k_mmq_slot_floats(M)
+        slots = torch.empty(2 * wgs * L.sera_q4k_mmq_slot_floats(M), dtype=torch.float32, device="cuda")
         ys = []
-        for path, W in ((4, Wg), (260, Wt)):
-            part = torch.zeros(nslot + L.sera_q4k_mmq_tiles(M, N), dtype=torch.float32, device="cuda")
+        for qt, W in ((12, Wg), (TILED, Wt)):
+            counters = torch.zeros(L.sera_q4k_mmq_tiles(M, N), dtype=torch.int32, device="cuda")
             y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-            kernel_once(torch, path, W, stage, y, part, M, N, K, wgs)
-            assert int(part[nslot:].abs().sum()) == 0, "tile counters not reset"
+            q3q4.mmq_streamk(W, stage, y, M, N, K, slots, counters, wgs=wgs, qtype=qt)
+            torch.cuda.synchronize()
+            assert int(counters.abs().sum()) == 0, "tile counters not reset"
             ys.append(y)
         same_bits(ys[0], ys[1], f"mmq stream-K M={M} N={N} K={K}")
 
@@ -271,10 +269,7 @@ def test_tiled_linear_boundary(torch, linear, N, K):
             assert L.sera_q4k_vec_uses_fewtok_qt(TILED, M, N, K) == 1
             stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
             q3q4.quantize_row(x, stage)
-            part = torch.zeros(q3q4.fewtok_splits(M, N, K) * M * N + q3q4.fewtok_groups(M, N, K),
-                               dtype=torch.float32, device="cuda")
-            yk = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-            kernel_once(torch, 12, Wg, stage, yk, part, M, N, K, 0)
+            yk = fewtok_once(torch, 12, 0, Wg, stage, M, N, K, 0)
             same_bits(yk, yt, f"boundary M={M} N={N} K={K} (few-token on both layouts)")
             a, b = yt.cpu().numpy().astype(np.float64), yg.cpu().numpy().astype(np.float64)
             rms = float(np.sqrt(np.mean(b * b)))
