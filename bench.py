@@ -83,6 +83,10 @@ def main():
     ap.add_argument("--linear-case", default="", metavar="M,N,K",
                     help="only time q3_cuda_q4k_linear on one Q4_K shape over --copies weight copies, "
                          "--steps calls (for counter-collection runs and batch sweeps)")
+    ap.add_argument("--no-tiled", action="store_true",
+                    help="skip the tiled-layout A/B cases (kernel traces that group launches by kernel name)")
+    ap.add_argument("--tiled", action="store_true",
+                    help="with --linear-case: the weights in the tiled Q4_K layout (qtype 268)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -152,11 +156,21 @@ def main():
     if args.linear_case:
         M, N, K = (int(v) for v in args.linear_case.split(","))
         ws, arr = weight_set(N, K, 7, args.copies)
-        geo = q3q4.bind_geometry(q3q4.QTYPE_Q4_K, K, N)
+        qt = q3q4.QTYPE_Q4K_TILED if args.tiled else q3q4.QTYPE_Q4_K
+        if args.tiled:
+            tw = []
+            for w in ws:
+                t = torch.empty(w.numel(), dtype=torch.uint8, device=dev)
+                q3q4.weight_to_device_layout(qt, N, K, w, t)
+                tw.append(t)
+            ws = tw
+            arr = (ctypes.c_void_p * len(ws))(*[w.data_ptr() for w in ws])
+        geo = q3q4.bind_geometry(qt, K, N)
         x = activations(M, K, 3)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
         ms = bench_linear(geo, arr, args.copies, x, y, 2, args.steps)
-        log(f"[bench] linear case M={M} N={N} K={K} ({L.q3_cuda_q4k_linear_path_for_batch(M).decode()}, "
+        log(f"[bench] linear case M={M} N={N} K={K}{' tiled' if args.tiled else ''} "
+            f"({L.q3_cuda_q4k_linear_path_for_batch(M).decode()}, "
             f"{L.sera_q4k_kernel_launches(M, N, K)} launches, {args.copies} weight copies): "
             f"{ms * 1e3:.2f} us per call over {args.steps} calls")
         return
@@ -314,9 +328,11 @@ def main():
         # at 16 tokens the LM head is bound by its 437 MB of weights
         lm["kernel_frac_hbm"] = round(lm["kernel_GBps"] / HBM_PEAK_GBS, 4)
         results["config4_lm_head_m16"] = lm
-        results["q4k_tiled_layout"] = tiled_cases(torch, q3q4, L, dev, activations, bench_linear, bench_kernel,
-                                                  {"gate_up": (gN, gK, gws), "down": (5120, 25600, sets["down"][2][0]),
-                                                   "lm_head": (151936, 5120, lmw)}, args)
+        if not args.no_tiled:
+            results["q4k_tiled_layout"] = tiled_cases(
+                torch, q3q4, L, dev, activations, bench_linear, bench_kernel,
+                {"gate_up": (gN, gK, gws), "down": (5120, 25600, sets["down"][2][0]), "lm_head": (151936, 5120, lmw)},
+                args)
         del lmw
         results["config5_decode_stream"] = decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr)
 
