@@ -43,6 +43,9 @@ def linear(torch):
 def weights(rng, qtype, N, K):
     if qtype == q3q4.QTYPE_Q4_K:
         return oracle.quantize_q4k((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    if qtype == q3q4.QTYPE_Q4K_TILED:
+        gguf = oracle.quantize_q4k((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+        return q3q4.q4k_tiled_bytes(gguf, N, K)
     return oracle.q6k_weights(rng, N, K)
 
 
@@ -60,9 +63,9 @@ def kernel_of(qtype, M, N, K):
     """The kernel the boundary runs for this call, from the library's own
     dispatch queries."""
     L = q3q4.load()
-    if qtype == q3q4.QTYPE_Q4_K:
+    if qtype in (q3q4.QTYPE_Q4_K, q3q4.QTYPE_Q4K_TILED):
         if M <= 8:
-            return "fewtok" if L.sera_q4k_vec_uses_fewtok(M, N, K) else "dot4"
+            return "fewtok" if L.sera_q4k_vec_uses_fewtok_qt(qtype, M, N, K) else "dot4"
         if L.sera_q4k_mmq_uses_fewtok(M, N, K):
             return "fewtok-mmq"
         return "mmq-streamk" if L.sera_q4k_mmq_schedule(M, N, K) == 1 else "mmq"
@@ -74,7 +77,9 @@ def kernel_of(qtype, M, N, K):
 # one from 3) and on the MMQ stage (form 1, 9 tokens); the paired MMQ tile
 # with split-K + reduce; stream-K; the 64-token tile with split-K + reduce;
 # Q6_K MMVQ and the Q6_K tile kernel on the row-formula stage; the few-token
-# kernel's persistent grid (more 16-row tiles than resident workgroups)
+# kernel's persistent grid (more 16-row tiles than resident workgroups); the
+# same kernels on Q4_K weights in the tiled layout (268), where the few-token
+# kernel takes tall matrices from 2 tokens
 CASES = [
     (12, 1, 4096, 5120, "dot4"),
     (12, 6, 2048, 5120, "dot4"),
@@ -88,6 +93,10 @@ CASES = [
     (14, 8, 2048, 5120, "q6k-mmvq"),
     (14, 8, 4096, 5120, "q6k-tile"),
     (12, 16, 70001, 512, "fewtok-mmq-persistent"),
+    (268, 1, 4096, 5120, "dot4"),
+    (268, 2, 16384, 5120, "fewtok"),
+    (268, 64, 16384, 2048, "mmq-streamk"),
+    (268, 16, 70000, 512, "fewtok-mmq-persistent"),
 ]
 
 
