@@ -242,7 +242,8 @@ def test_mmq_exact_streamk(torch, M, N, K, wgs):
 def test_linear_boundary_exact(torch, linear, M, N, K):
     """q3_cuda_q4k_linear: dot4 MMVQ, the few-token kernel (tall and
     4096-row matrices), the MMQ-path few-token kernel (9 tokens), the paired
-    tile and the 64-token tile, each bit-exact on exact inputs."""
+    tile and the 64-token tile, each bit-exact on exact inputs; and the same
+    on the tiled layout, with its own few-token rule."""
     L = q3q4.load()
     rng = np.random.default_rng(M * 17 + N + K)
     W, X = exact_inputs(rng, M, N, K)
@@ -253,3 +254,11 @@ def test_linear_boundary_exact(torch, linear, M, N, K):
     linear(q3q4.bind_geometry(12, K, N), dev(torch, W), dev(torch, X), y)
     torch.cuda.synchronize()
     assert_bits(y, ref, f"linear M={M} N={N} K={K} ({kern})")
+    # the same bytes in the tiled layout (its own kernel choice at M <= 8)
+    T = q3q4.QTYPE_Q4K_TILED
+    kern_t = ("fewtok" if L.sera_q4k_vec_uses_fewtok_qt(T, M, N, K) else "dot4") if M <= 8 else "mmq-path"
+    say(f"case exact linear tiled M={M} N={N} K={K} ({kern_t})")
+    y = nan_out(torch, M, N)
+    linear(q3q4.bind_geometry(T, K, N), dev(torch, q3q4.q4k_tiled_bytes(W, N, K)), dev(torch, X), y)
+    torch.cuda.synchronize()
+    assert_bits(y, ref, f"linear tiled M={M} N={N} K={K} ({kern_t})")
