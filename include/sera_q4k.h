@@ -231,6 +231,9 @@ int sera_q4k_fewtok_grid(int form, int M, int N, int K, int chunk);
 /* Device Q4_K dequant, w = (d*sc)*q - (dmin*m) per weight; replaces
  * q3_cuda_dequantize_row (src/q3_cuda_primitives.h, cuda/q3_cuda_primitives.cu:13-95). */
 int sera_q4k_dequantize(const void *W, size_t nblocks, float *out, void *stream);
+/* The N x K matrix in the layout of qtype (12 or SERA_QTYPE_Q4K_TILED)
+ * dequantized to row-major fp32 out[N][K], same values as above. */
+int sera_q4k_dequantize_qt(uint32_t qtype, const void *W, int N, int K, float *out, void *stream);
 
 /* Exact per-32 int32 dots I[m][n][b] = sum q4*q8 for the first M rows of a
  * stage's qs array (int8 [rows][K]). Test hook for the integer core shared

@@ -241,13 +241,18 @@ __global__ __launch_bounds__(64) void sera_q4k_quantize_kernel(
     }
 }
 
-/* One thread per weight, (d*sc)*q - (dmin*m) rounded step by step. */
+/* One thread per weight, (d*sc)*q - (dmin*m) rounded step by step. out is
+ * row-major [N][K]: weight i sits in block i / 256 of row order, read from
+ * the GGUF bytes (tiled = 0) or from its place in the tiled layout of a
+ * matrix with nkb super-blocks per row. */
 __global__ __launch_bounds__(256) void sera_q4k_dequant_kernel(
-        const uint8_t *__restrict__ W, int64_t nweights, float *__restrict__ out) {
+        const uint8_t *__restrict__ W, int64_t nweights, float *__restrict__ out, int tiled, int64_t nkb) {
 #pragma clang fp contract(off)
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= nweights) return;
-    const uint8_t *b = W + (i >> 8) * Q4K_BLOCK_BYTES;
+    const int64_t blk = i >> 8;
+    const uint8_t *b = W + (tiled ? q4k_block_offset(1, (size_t)(blk / nkb), (size_t)(blk % nkb), (size_t)nkb)
+                                  : (size_t)blk * Q4K_BLOCK_BYTES);
     const int e = (int)(i & 255), j = e >> 5, l = e & 31;
     const uint4 hv = *(const uint4 *)b;
     const float d = h2f_bits(hv.x & 0xffffu), dmin = h2f_bits(hv.x >> 16);
@@ -329,7 +334,15 @@ extern "C" hipError_t sera_launch_q4k_quantize(const float *x, int64_t rows, int
 extern "C" hipError_t sera_launch_q4k_dequant(const void *W, int64_t nblocks, float *out, hipStream_t s) {
     const int64_t n = nblocks * Q4K_QK;
     hipLaunchKernelGGL(sera_q4k_dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                       (const uint8_t *)W, n, out);
+                       (const uint8_t *)W, n, out, 0, (int64_t)1);
+    return hipGetLastError();
+}
+
+/* The whole N x K matrix in the tiled layout, out row-major. */
+extern "C" hipError_t sera_launch_q4k_dequant_tiled(const void *W, int64_t N, int64_t K, float *out, hipStream_t s) {
+    const int64_t n = N * K;
+    hipLaunchKernelGGL(sera_q4k_dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       (const uint8_t *)W, n, out, 1, K / Q4K_QK);
     return hipGetLastError();
 }
 

@@ -92,6 +92,7 @@ hipError_t sera_launch_embedding(int qtype, const void *W, int N, int K, const u
 /* ---- q4k_aux.hip: weight quantizer, dequant, integer-dot test hook ----- */
 hipError_t sera_launch_q4k_quantize(const float *x, int64_t rows, int64_t K, void *out, hipStream_t s);
 hipError_t sera_launch_q4k_dequant(const void *W, int64_t nblocks, float *out, hipStream_t s);
+hipError_t sera_launch_q4k_dequant_tiled(const void *W, int64_t N, int64_t K, float *out, hipStream_t s);
 hipError_t sera_launch_q4k_tile(const void *src, void *dst, uint64_t row0, uint64_t rows, uint64_t nkb,
                                 hipStream_t s);
 hipError_t sera_launch_q4k_subblock_dots(const void *W, const int8_t *xq, int32_t *I, int M, int N, int K,

@@ -1051,6 +1051,15 @@ extern "C" int sera_q4k_dequantize(const void *W, size_t nblocks, float *out, vo
                ? 0 : fail(-3, "sera_q4k_dequantize: launch failed");
 }
 
+extern "C" int sera_q4k_dequantize_qt(uint32_t qtype, const void *W, int N, int K, float *out, void *stream) {
+    if (!W || !out || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_dequantize: bad arguments");
+    if (!q4k_layout_ok("sera_q4k_dequantize", qtype, N)) return -1;
+    const hipError_t e = qtype == SERA_QTYPE_Q4K_TILED
+                             ? sera_launch_q4k_dequant_tiled(W, N, K, out, (hipStream_t)stream)
+                             : sera_launch_q4k_dequant(W, (int64_t)N * (K / Q4K_QK), out, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : fail(-3, "sera_q4k_dequantize: launch failed");
+}
+
 extern "C" int sera_q4k_subblock_dots(const void *W, const void *stage_qs, int32_t *I, int M, int N, int K,
                                       void *stream) {
     if (!W || !stage_qs || !I || M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK)

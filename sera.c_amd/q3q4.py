@@ -123,6 +123,7 @@ def load():
         "sera_q4k_mmq_tiles": ([I, I], I),
         "sera_q4k_mmq_slot_floats": ([I], I),
         "sera_q4k_dequantize": ([P, SZ, P, P], I),
+        "sera_q4k_dequantize_qt": ([U32, P, I, I, P, P], I),
         "sera_q4k_subblock_dots": ([P, P, P, I, I, I, P], I),
         "sera_q4k_quantize": ([P, I64, I64, P, P], I),
         "sera_q4k_last_error": ([], CP),
@@ -314,6 +315,13 @@ def fewtok_grid(form, M, N, K, chunk=0):
 
 def dequantize(W, nblocks, out, stream=None):
     _check(load().sera_q4k_dequantize(_ptr(W), nblocks, _ptr(out), _stream(stream)),
+           "sera_q4k_dequantize")
+
+
+def dequantize_matrix(qtype, W, N, K, out, stream=None):
+    """The N x K matrix in the layout of qtype (QTYPE_Q4_K or QTYPE_Q4K_TILED)
+    to row-major fp32 out [N, K]."""
+    _check(load().sera_q4k_dequantize_qt(qtype, _ptr(W), N, K, _ptr(out), _stream(stream)),
            "sera_q4k_dequantize")
 
 

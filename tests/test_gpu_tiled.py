@@ -420,3 +420,19 @@ def test_tiled_small_matrices_boundary(torch, linear, N, K):
         linear(gt, Wt, x, yt)
         torch.cuda.synchronize()
         same_bits(yg, yt, f"small boundary N={N} K={K} M={M}")
+
+
+@pytest.mark.parametrize("N,K", [(16, 256), (272, 2304), (1008, 5120)])
+def test_tiled_dequant_row_major(torch, N, K):
+    """sera_q4k_dequantize_qt on the tiled bytes gives the row-major matrix
+    the oracle dequantizes from the GGUF bytes, bit for bit; on GGUF bytes
+    the same as sera_q4k_dequantize."""
+    say(f"case tiled dequant N={N} K={K}")
+    Wg = device_blocks(torch, N, K, 3 * N + K)
+    Wt = to_tiled(torch, Wg, N, K)
+    ref = oracle.dequant(Wg.cpu().numpy(), N, K)
+    for qt, W in ((TILED, Wt), (12, Wg)):
+        out = torch.full((N, K), float("nan"), dtype=torch.float32, device="cuda")
+        q3q4.dequantize_matrix(qt, W, N, K, out)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32)), qt
