@@ -73,7 +73,9 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
                                                 param, s);
             case 7:
             case 8:
-            case 11: return sera_launch_candidate_logits(path == 7 ? 14 : path == 8 ? (int)q4 : (int)SERA_QTYPE_Q6K_SPLIT,
+            case 11: return sera_launch_candidate_logits(path == 7   ? 14
+                                                         : path == 8 ? (int)q4
+                                                                     : (int)SERA_QTYPE_Q6K_SPLIT,
                                                          w, N, K, (const float *)stage, (const uint32_t *)partial, M,
                                                          param, y, s);
             case 12:

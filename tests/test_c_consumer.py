@@ -37,7 +37,8 @@ int main(void) {
            sera_weight_bytes(SERA_QTYPE_Q4K_TILED, 25600, 5120), sera_weight_bytes(14, 1024, 5120),
            sera_weight_bytes(SERA_QTYPE_Q6K_SPLIT, 1024, 5120));
     printf("fewtok %d %d %d\n", sera_q4k_vec_uses_fewtok(2, 25600, 5120),
-           sera_q4k_vec_uses_fewtok_qt(SERA_QTYPE_Q4K_TILED, 2, 25600, 5120), sera_q4k_mmq_uses_fewtok(16, 151936, 5120));
+           sera_q4k_vec_uses_fewtok_qt(SERA_QTYPE_Q4K_TILED, 2, 25600, 5120),
+           sera_q4k_mmq_uses_fewtok(16, 151936, 5120));
     return 0;
 }
 """
