@@ -403,8 +403,7 @@ int fewtok_launch_on(const char *tag, uint32_t qtype, int form, const void *W, c
 int fewtok_launch(const char *tag, uint32_t qtype, int form, const void *W, float *Y, float *slots, size_t cap, int M,
                   int N, int K, int accum, hipStream_t s) {
     return fewtok_launch_on(tag, qtype, form, W, g_arena, Y, slots, cap, g_counters + kFewtokCounterBase,
-                            kFewtokMaxCounters,
-                            M, N, K, accum, s);
+                            kFewtokMaxCounters, M, N, K, accum, s);
 }
 
 /* The MMVQ path (quantize + dot4 MMVQ or the few-token kernel) on explicit
