@@ -215,7 +215,7 @@ def main():
             row = {"proj": name, "M": M, "N": N, "K": K,
                    "kernel": (f"sera_q4k_fewtok_kernel<{8 if N >= 16384 or K >= 16384 else 4}> "
                               f"(splits {q3q4.fewtok_splits(M, N, K)})") if rpw is None else
-                             f"sera_q4k_mmvq_kernel<{M}, {rpw}, {mmvq_waves(M, K)}, false>",
+                             f"sera_q4k_mmvq_kernel<{M}, {rpw}, {mmvq_waves(M, K)}, false, false>",
                    "step_us": round(step_ms * 1e3, 3),
                    "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),
                    "kernel_us": round(kavg * 1e3, 3),
@@ -243,7 +243,8 @@ def main():
         kavg, _ = bench_kernel(0, qarr, ncopy, stage, y, None, 1, N, K, 0, args.warmup, args.steps)
         b = alg_bytes(1, N, K)
         row = {"proj": "q", "M": 1, "N": N, "K": K,
-               "kernel": f"sera_q4k_mmvq_kernel<1, {L.sera_q4k_mmvq_rows_per_tile(1, N, K)}, {mmvq_waves(1, K)}, false>",
+               "kernel": (f"sera_q4k_mmvq_kernel<1, {L.sera_q4k_mmvq_rows_per_tile(1, N, K)}, "
+                          f"{mmvq_waves(1, K)}, false, false>"),
                "step_us": round(step_ms * 1e3, 3), "step_GBps": round(b / (step_ms * 1e-3) / 1e9, 1),
                "kernel_us": round(kavg * 1e3, 3), "kernel_GBps": round(b / (kavg * 1e-3) / 1e9, 1),
                "kernel_frac_hbm": round(b / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -87,13 +87,13 @@ struct MmvqGroup {
     int tiled;      /* weights in the 16-row tiled layout (every matrix) */
 };
 
-template <int NCOLS, int R, int NW, bool GROUPED>
+template <int NCOLS, int R, int NW, bool GROUPED, bool TILED>
 __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
         MmvqGroup grp, const int8_t *__restrict__ xq, const float4 *__restrict__ dsf, int K) {
     {
         const void *a0 = grp.W[0], *a1 = grp.y[0], *a2 = xq, *a3 = dsf;
-        const int a4 = grp.N[0], a5 = K, a6 = grp.accum, a7 = grp.tiled;
-        __asm__ volatile("" : : "s"(a0), "s"(a1), "s"(a2), "s"(a3), "s"(a4), "s"(a5), "s"(a6), "s"(a7));
+        const int a4 = grp.N[0], a5 = K, a6 = grp.accum;
+        __asm__ volatile("" : : "s"(a0), "s"(a1), "s"(a2), "s"(a3), "s"(a4), "s"(a5), "s"(a6));
     }
     /* one matrix: its pointers come straight from the kernel arguments, so
      * the first loads issue without the dependent scalar loads of the
@@ -126,12 +126,12 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_mmvq_kernel(
     const int ngroups = (nb + 7) >> 3;
     /* row and block strides of the layout; a tile of R <= 16 rows never
      * crosses a 16-row tile of the tiled layout (N % 16 == 0 there) */
-    const int rowbytes = q4k_row_stride(grp.tiled, nb);
-    const int bstride = q4k_block_stride(grp.tiled);
+    const int rowbytes = q4k_row_stride(TILED, nb);
+    constexpr int bstride = TILED ? Q4K_TILE_ROWS * Q4K_BLOCK_BYTES : Q4K_BLOCK_BYTES;
     const int nrows = min(R, N - row0);
     const __amdgpu_buffer_rsrc_t rw =
-        make_rsrc(W + q4k_block_offset(grp.tiled, row0, 0, nb),
-                  (uint32_t)(grp.tiled ? (nb - 1) * bstride + nrows * Q4K_BLOCK_BYTES : nrows * rowbytes));
+        make_rsrc(W + q4k_block_offset(TILED, row0, 0, nb),
+                  (uint32_t)(TILED ? (nb - 1) * bstride + nrows * Q4K_BLOCK_BYTES : nrows * rowbytes));
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, (uint32_t)(NCOLS * K));
     const __amdgpu_buffer_rsrc_t rf = make_rsrc(dsf, (uint32_t)(NCOLS * (K / 64) * 16));
     const int vo_w = rs * rowbytes + g * bstride;
@@ -331,12 +331,20 @@ static hipError_t launch_mmvq(MmvqGroup grp, const int8_t *xq, const float4 *dsf
         tiles += (grp.N[i] + R - 1) / R;
         grp.tile_end[i] = tiles;
     }
-    if (grp.count == 1)
-        hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW, false>), dim3(tiles), dim3(NW * 64), 0, s, grp, xq,
-                           dsf, K);
+    /* the layout is a template argument: runtime strides cost the GGUF
+     * instance 4 VGPRs, one wave per SIMD of occupancy */
+    if (grp.count == 1 && grp.tiled)
+        hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW, false, true>), dim3(tiles), dim3(NW * 64), 0, s, grp,
+                           xq, dsf, K);
+    else if (grp.count == 1)
+        hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW, false, false>), dim3(tiles), dim3(NW * 64), 0, s, grp,
+                           xq, dsf, K);
+    else if (grp.tiled)
+        hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW, true, true>), dim3(tiles), dim3(NW * 64), 0, s, grp,
+                           xq, dsf, K);
     else
-        hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW, true>), dim3(tiles), dim3(NW * 64), 0, s, grp, xq,
-                           dsf, K);
+        hipLaunchKernelGGL((sera_q4k_mmvq_kernel<NCOLS, R, NW, true, false>), dim3(tiles), dim3(NW * 64), 0, s, grp,
+                           xq, dsf, K);
     return hipGetLastError();
 }
 
