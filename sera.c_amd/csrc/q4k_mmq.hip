@@ -607,16 +607,37 @@ static int mmq_bn(int bm) { (void)bm; return 256; }
  * slower. */
 extern "C" int sera_mmq_wgs_per_cu(int M) { (void)M; return 2; }
 
-/* Split-K factor: enough workgroups to give every CU at least two, but
- * never fewer than 2 super-blocks per split. */
+/* Split-K factor: the split count in {1, 2, 4, 8, 16} (never fewer than 2
+ * super-blocks per split, at most 2048 workgroups) of least modelled time.
+ * The model is per CU: the busiest of the 256 CUs holds L = ceil(wgs / 256)
+ * workgroups and runs them two at a time, a pair costing kPairUs and a lone
+ * workgroup kLoneUs per super-block of a 64 x 256 tile (x0.6 for the 32-token
+ * tile, x0.5 for the paired 16-token tile); a split adds the partial sums'
+ * write and read, 8 bytes per output per split at 8 TB/s, and the reduce
+ * launch. Fitted to MI355X timings of 43 Qwen3-32B shapes (q, k/v, o,
+ * gate/up, down at 16-2048 tokens, every split count): its pick is within
+ * 3.2% of the fastest split count on every one of them. */
+static constexpr float kLoneUs = 3.2f, kPairUs = 5.75f;
+static constexpr float kPartialBytesPerUs = 8.0e6f, kReduceUs = 1.0f;
+static constexpr int kModelCUs = 256, kMaxSplitWgs = 2048;
+
 extern "C" int sera_mmq_splits(int M, int N, int K) {
     const int bm = sera_mmq_bm(M);
     const int bn = mmq_bn(bm);
     const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int nkb = K / Q4K_QK;
-    int s = 1;
-    while (tiles * s < 512 && nkb / (s * 2) >= 2 && s < 16) s *= 2;
-    return s;
+    const float tile_scale = bm == 16 ? 0.5f : bm == 32 ? 0.6f : 1.0f;
+    int best = 1;
+    float best_us = 0.0f;
+    for (int s = 1; s <= 16; s *= 2) {
+        if (s > 1 && (nkb / s < 2 || (int64_t)tiles * s > kMaxSplitWgs)) break;
+        const int64_t L = ((int64_t)tiles * s + kModelCUs - 1) / kModelCUs;
+        const int kb = (nkb + s - 1) / s;
+        float us = (float)((L / 2) * kPairUs + (L % 2) * kLoneUs) * kb * tile_scale;
+        if (s > 1) us += kReduceUs + (float)s * M * N * 8.0f / kPartialBytesPerUs;
+        if (s == 1 || us < best_us) { best = s; best_us = us; }
+    }
+    return best;
 }
 
 /* Rows of the MMQ activation stage: M rounded up to the token tile. */

@@ -99,13 +99,13 @@ extern "C" int sera_q4k_mmq_uses_fewtok(int M, int N, int K) {
  * count, a multiple of 8. */
 int streamk_wgs(int M) { return g_cus > 0 ? sera_mmq_wgs_per_cu(M) * g_cus / 8 * 8 : 0; }
 
-/* Partial-sum floats never exceed this. Split-K: the split count stops
- * doubling once tiles*splits >= 512, so tiles*splits < 1024, and an MMQ
- * tile holds at most 64*256 outputs, so splits*M*N < 1024 * 16384.
- * Stream-K: two tile slots per resident workgroup, at most 2*(2*CUs)*16384
- * = 4*CUs*16384 (64 x 256 tiles) or 2*(3*CUs)*8192 (32 x 256 tiles). */
+/* Partial-sum floats never exceed this. Split-K: at most 2048 workgroups
+ * (tiles * splits), and an MMQ tile holds at most 64*256 outputs, so
+ * splits*M*N <= 2048 * 16384. Stream-K: two tile slots per resident
+ * workgroup, at most 2*(2*CUs)*16384 = 4*CUs*16384 (64 x 256 tiles) or
+ * 2*(3*CUs)*8192 (32 x 256 tiles). */
 size_t partial_floats_bound(size_t max_tokens, int64_t max_features) {
-    size_t by_tiles = (size_t)1024 * 16384;
+    size_t by_tiles = (size_t)2048 * 16384;
     const size_t by_slots = (size_t)4 * (g_cus > 0 ? g_cus : 256) * 16384;
     if (by_slots > by_tiles) by_tiles = by_slots;
     const size_t by_shape = (size_t)16 * max_tokens * (size_t)(max_features > 0 ? max_features : 0);
@@ -362,19 +362,18 @@ extern "C" int sera_q4k_mmq_qt(uint32_t qtype, const void *W, const void *mmq_st
 }
 
 namespace {
-/* The schedule rule, from MI355X measurements over the Qwen3-32B shapes:
- * stream-K for 64-token tiles when there are at least 64 tiles and fewer
- * than four rounds of resident workgroups (beyond that the last round's idle
- * share is small and plain tiles are faster). 32-token tiles (M <= 32) take
- * stream-K only from one full round of tiles on (the 151936-row LM head:
- * 152 against 157 us); below that split-K wins by 10-90%, since each tile
- * would be cut into many short pieces. */
+/* The schedule rule, from MI355X measurements over the Qwen3-32B shapes.
+ * For 64-token tiles the fitted split-K choice beats stream-K on all 43
+ * measured shapes (q, k/v, o, gate/up, down at 48-2048 tokens; stream-K
+ * 0.3-90% slower), so 64-token tiles never take it. 32-token tiles (M <= 32)
+ * take stream-K from one full round of tiles on (the 151936-row LM head);
+ * below that split-K wins, since each tile would be cut into many short
+ * pieces. */
 bool streamk_rule(int M, int N, int K) {
     const int P = streamk_wgs(M);
-    if (P < 8) return false;
+    if (P < 8 || M > 32) return false;
     const int tiles = sera_mmq_tiles(M, N);
-    if (M <= 32 && tiles < P) return false;
-    return tiles >= 64 && tiles < 4 * P && tiles <= kFewtokCounterBase && (int64_t)tiles * (K / Q4K_QK) >= P;
+    return tiles >= P && tiles < 4 * P && tiles <= kFewtokCounterBase && (int64_t)tiles * (K / Q4K_QK) >= P;
 }
 bool use_streamk(int M, int N, int K) { return g_counters && streamk_rule(M, N, K); }
 }  // namespace

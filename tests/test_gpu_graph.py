@@ -75,7 +75,8 @@ def kernel_of(qtype, M, N, K):
 # (qtype, M, N, K, kernel): dot4 MMVQ; the few-token kernel with in-kernel
 # split K on the row stage (form 0: a 4096-row matrix from 5 tokens, a tall
 # one from 3) and on the MMQ stage (form 1, 9 tokens); the paired MMQ tile
-# with split-K + reduce; stream-K; the 64-token tile with split-K + reduce;
+# with split-K + reduce; stream-K (32-token tiles over a 131328-row matrix);
+# the 64-token tile with split-K + reduce;
 # Q6_K MMVQ and the Q6_K tile kernel on the row-formula stage; the few-token
 # kernel's persistent grid (more 16-row tiles than resident workgroups); the
 # same kernels on Q4_K weights in the tiled layout (268), where the few-token
@@ -87,7 +88,8 @@ CASES = [
     (12, 3, 16384, 5120, "fewtok"),
     (12, 9, 1000, 25600, "fewtok-mmq"),
     (12, 10, 1000, 2560, "mmq"),
-    (12, 64, 16384, 2048, "mmq-streamk"),
+    (12, 20, 131328, 256, "mmq-streamk"),
+    (12, 64, 16384, 2048, "mmq"),
     (12, 100, 4096, 5120, "mmq"),
     (14, 1, 2048, 5120, "q6k-mmvq"),
     (14, 8, 2048, 5120, "q6k-mmvq"),
@@ -95,7 +97,8 @@ CASES = [
     (12, 16, 70001, 512, "fewtok-mmq-persistent"),
     (268, 1, 4096, 5120, "dot4"),
     (268, 2, 16384, 5120, "fewtok"),
-    (268, 64, 16384, 2048, "mmq-streamk"),
+    (268, 20, 131328, 256, "mmq-streamk"),
+    (268, 64, 16384, 2048, "mmq"),
     (268, 16, 70000, 512, "fewtok-mmq-persistent"),
 ]
 
