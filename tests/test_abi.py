@@ -221,6 +221,29 @@ def test_stage_layouts_and_workspace_sizing():
                 assert need <= L.sera_q4k_arena_bytes(mt, 151936, 128 * 1024) - (256 << 10), (mt, M, N, K, s)
 
 
+def test_mmq_split_rule_picks_measured_best():
+    """The split-K cost model picks, on Qwen3-32B shapes, the split count
+    that measured fastest on MI355X (q, k/v, o, gate/up, down at 64-2048
+    tokens), and keeps every choice within its bounds: at least 2
+    super-blocks per split, at most 2048 workgroups, 16 splits at most."""
+    measured_best = {(64, 8192, 5120): 8, (128, 8192, 5120): 4, (512, 8192, 5120): 1,
+                     (512, 1024, 5120): 8, (1024, 1024, 5120): 4,
+                     (256, 5120, 8192): 8, (1024, 5120, 8192): 4,
+                     (512, 25600, 5120): 1, (2048, 25600, 5120): 1,
+                     (128, 5120, 25600): 16, (512, 5120, 25600): 8, (1024, 5120, 25600): 4,
+                     (2048, 5120, 25600): 2}
+    for (M, N, K), s in measured_best.items():
+        assert q3q4.mmq_splits(M, N, K) == s, (M, N, K)
+    L = q3q4.load()
+    for M in (9, 16, 17, 32, 33, 64, 100, 256, 777, 2048, 8192):
+        for N in (256, 1000, 5120, 25600, 151936):
+            for K in (256, 512, 2304, 5120, 25600):
+                s = q3q4.mmq_splits(M, N, K)
+                assert s in (1, 2, 4, 8, 16), (M, N, K, s)
+                if s > 1:
+                    assert K // 256 // s >= 2 and L.sera_q4k_mmq_tiles(M, N) * s <= 2048, (M, N, K, s)
+
+
 def test_kernel_launch_counts(L):
     """quantize + matmul (+ the split-K reduce when an MMQ launch splits K)."""
     assert L.sera_q4k_kernel_launches(1, 25600, 5120) == 2          # dot4 MMVQ
