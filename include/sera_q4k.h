@@ -179,8 +179,11 @@ int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *
                          int M, int N, int K, int wgs, void *stream);
 int sera_q4k_mmq_streamk_wgs(int M);   /* resident workgroups for M tokens (after init) */
 /* Schedule of the MMQ tile kernels for this shape (after init): 1 =
- * stream-K, 0 = plain tiles / split-K (sera_q4k_mmq_splits); -1 for a bad
- * shape. sera_q4k_dense runs it where sera_q4k_mmq_uses_fewtok is 0. */
+ * stream-K (16- and 32-token tiles, M <= 32, from one full round of
+ * resident workgroups of tiles), 0 = plain tiles / split-K with the split
+ * count of sera_q4k_mmq_splits (a per-CU cost model fitted to MI355X
+ * timings); -1 for a bad shape. sera_q4k_dense runs it where
+ * sera_q4k_mmq_uses_fewtok is 0. */
 int sera_q4k_mmq_schedule(int M, int N, int K);
 /* 1 if sera_q4k_dense (the boundary's MMQ path) runs the few-token MFMA
  * kernel with the MMQ formula for this shape instead of the MMQ tiles: 1-8
