@@ -595,8 +595,8 @@ extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, 
  * epilogue: its 16 seed registers made that budget spill (37 -> 52 us on
  * gate/up at 32 tokens), while at 2 waves with the next step's weights
  * issued ahead it measures 37 us. Measured on MI355X against 128 x
- * 128 tiles: the 64 x 256 tile under the stream-K schedule is the fastest at
- * 512 tokens for both the 5120 -> 25600 and the 25600 -> 5120 shapes. */
+ * 128 tiles (both under stream-K): the 64 x 256 tile is the fastest at 512
+ * tokens for both the 5120 -> 25600 and the 25600 -> 5120 shapes. */
 extern "C" int sera_mmq_bm(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : 64; }
 
 static int mmq_bn(int bm) { (void)bm; return 256; }
