@@ -229,6 +229,30 @@ def main():
                 headline = (row, step_ms, b)
     results["mmvq_sweep"] = sweep
 
+    # ---------------- the achievable read rate: a plain streaming read ------
+    # of the same weight copies (73,728,000 B each, walked round robin, no
+    # compute, no output), the ceiling the MMVQ kernel is judged against
+    ceiling = []
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    dummy = torch.zeros(16, dtype=torch.uint8, device=dev)
+    for name, (N, K, (ws, arr)) in sets.items():
+        wbytes = N * (K // 256) * 144
+        for lpt in (2, 4, 8, 16):
+            kavg, _ = bench_kernel(14, arr, args.copies, dummy, sink, None, 1, N, K, lpt, args.warmup, args.steps)
+            ceiling.append({"proj": name, "bytes": wbytes, "loads_per_thread": lpt,
+                            "kernel": f"sera_stream_read_kernel<{lpt}>",
+                            "workgroups": -(-wbytes // (16 * 256 * lpt)),
+                            "us": round(kavg * 1e3, 3),
+                            "GBps": round(wbytes / (kavg * 1e-3) / 1e9, 1)})
+            log(f"[bench] plain read of {name} ({wbytes} B, {lpt} loads per thread): "
+                f"{ceiling[-1]['us']} us, {ceiling[-1]['GBps']} GB/s")
+    results["hbm_read_ceiling"] = ceiling
+    read_best = {name: max((c for c in ceiling if c["proj"] == name), key=lambda c: c["GBps"])
+                 for name in sets}
+    for row in sweep:
+        best = read_best[row["proj"]]
+        row["frac_of_read_ceiling"] = round(row["kernel_GBps"] / best["GBps"], 4)
+
     # ---------------- config 1: q_proj 8192 x 5120 at M=1 ------------------
     if not args.quick:
         N, K = SHAPES["q"]
@@ -345,7 +369,11 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(kname),
                 "kernel": kname,
-                "avg_launch_us": row["kernel_us"], "algorithmic_bytes_per_launch": b}
+                "avg_launch_us": row["kernel_us"], "algorithmic_bytes_per_launch": b,
+                # the same kernel against the device's measured plain-read rate
+                # of the same weight copies (results.hbm_read_ceiling)
+                "read_ceiling_GBps": read_best["gate_up"]["GBps"],
+                "frac_of_read_ceiling": row["frac_of_read_ceiling"]}
 
     # ---------------- CPU baseline ------------------------------------------
     cpu = None

@@ -146,6 +146,9 @@ __device__ __forceinline__ uint32_t f2h_bits(float f) {
  * Then fma(F, sw, -1.5 * 2^23 * sw) is I * sw rounded once, with no
  * integer-to-float convert; -1.5 * 2^23 * sw is exact whenever sw has at
  * most 22 significant bits (fp16 products and d * sc with sc < 64). The
+ * caller then accumulates fma(t, d8, acc): two roundings per term, where a
+ * single fma(sw * d8, I, acc) rounds once (relative difference at most
+ * 2^-24 of the term; none when I * sw fits 24 bits). The
  * seed comes from an opaque register so that the compiler keeps one copy
  * live for every MFMA instead of rematerializing the moves per use. */
 #define SERA_MAGIC_BITS 0x4B400000

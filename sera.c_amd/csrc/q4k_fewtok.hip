@@ -46,6 +46,8 @@
  */
 #include "sera_launch.h"
 
+#include <mutex>
+
 typedef uint32_t ft_v4u __attribute__((ext_vector_type(4)));
 typedef float ft_v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void ft_lds_void;
@@ -527,27 +529,63 @@ extern "C" int sera_fewtok_splits(int M, int N, int K, int chunk) {
 }
 
 
+/* Per-device facts the persistent grid is sized from: the CU count, the
+ * LDS one workgroup may use, and the occupancy of each kernel instance per
+ * LDS size (cached on the exact byte count; guarded by a mutex, since
+ * several host threads may launch). */
+struct FewtokDevice {
+    int cus = 0;
+    int max_lds = 0;
+};
+static std::mutex g_fewtok_mu;
+
+static bool fewtok_device(int *dev_out, FewtokDevice *out) {
+    static FewtokDevice devs[16];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return false;
+    std::lock_guard<std::mutex> lock(g_fewtok_mu);
+    FewtokDevice &d = devs[dev];
+    if (d.cus == 0) {
+        int cus = 0, lds = 0, optin = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0 ||
+            hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds <= 0)
+            return false;
+        if (hipDeviceGetAttribute(&optin, hipDeviceAttributeSharedMemPerBlockOptin, dev) == hipSuccess && optin > lds)
+            lds = optin;
+        d.cus = cus;
+        d.max_lds = lds;
+    }
+    *dev_out = dev;
+    *out = d;
+    return true;
+}
+
 /* Workgroups of one launch that the device holds at once (CUs times the
- * occupancy the kernel's registers and LDS allow), per device. */
+ * occupancy the kernel's registers and LDS allow), or 0 if unknown. */
 template <int NW, int TG, int FORM>
 static int fewtok_resident(size_t lds) {
     constexpr bool PERSIST = true;
-    static int cus[16];                /* per device */
-    static int cache[16][8][2];        /* [device][slot] -> (lds bytes, workgroups per CU) */
+    constexpr int kEntries = 8;
+    static int cache[16][kEntries][2];   /* [device][entry] -> (lds bytes, workgroups per CU) */
+    static int next[16];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
-    if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 0;
-    const int slot = (int)((lds >> 4) & 7);
-    if (cache[dev][slot][0] != (int)lds || cache[dev][slot][1] <= 0) {
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sera_q4k_fewtok_kernel<NW, TG, FORM, PERSIST>,
-                                                          NW * 64, lds) != hipSuccess)
-            return 0;
-        cache[dev][slot][0] = (int)lds;
-        cache[dev][slot][1] = per_cu;
+    FewtokDevice d;
+    if (!fewtok_device(&dev, &d)) return 0;
+    if (lds > (size_t)d.max_lds) return 0;
+    {
+        std::lock_guard<std::mutex> lock(g_fewtok_mu);
+        for (int e = 0; e < kEntries; e++)
+            if (cache[dev][e][0] == (int)lds && cache[dev][e][1] > 0) return d.cus * cache[dev][e][1];
     }
-    return cus[dev] * cache[dev][slot][1];
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sera_q4k_fewtok_kernel<NW, TG, FORM, PERSIST>, NW * 64,
+                                                      lds) != hipSuccess || per_cu <= 0)
+        return 0;
+    std::lock_guard<std::mutex> lock(g_fewtok_mu);
+    const int e = next[dev]++ % kEntries;
+    cache[dev][e][0] = (int)lds;
+    cache[dev][e][1] = per_cu;
+    return d.cus * per_cu;
 }
 
 /* Grid (workgroups along the rows), persistent-buffer tiles (0: one tile
@@ -562,7 +600,9 @@ static void fewtok_grid(int N, int K, int chunk, bool allow_persist, int *groups
     int groups = (N + 16 * NW - 1) / (16 * NW), out_tiles = 0;
     size_t lds = base;
     if constexpr (NW == fewtok_persist_waves<TG>()) {
-        if (allow_persist && splits == 1 && (nkb & 1) == 0) {
+        int dev = 0;
+        FewtokDevice d;
+        if (allow_persist && splits == 1 && (nkb & 1) == 0 && fewtok_device(&dev, &d)) {
             /* more tile groups than resident workgroups: a persistent grid,
              * each workgroup staging the activations once for its range of
              * tiles and keeping the results in LDS until its last tile (the
@@ -574,9 +614,21 @@ static void fewtok_grid(int N, int K, int chunk, bool allow_persist, int *groups
                 const int resident = fewtok_resident<NW, TG, FORM>(base + out_bytes(groups));
                 if (resident > 0 && groups > resident) groups = resident;
             }
+            /* the result buffer must fit the workgroup's LDS: with more
+             * tiles per workgroup than that allows (a very tall matrix),
+             * take more workgroups, each with a shorter range (they need
+             * not all be resident: no workgroup waits on another) */
+            while (groups < natural && base + out_bytes(groups) > (size_t)d.max_lds) {
+                const size_t room = (size_t)d.max_lds > base ? (size_t)d.max_lds - base : 0;
+                const int per = (int)(room / ((size_t)16 * 8 * TG * sizeof(float)));   /* tiles that fit */
+                groups = per > 0 ? (tiles + per - 1) / per : natural;
+                if (groups > natural) groups = natural;
+            }
             if (groups < natural) {
                 out_tiles = (tiles + groups - 1) / groups;
                 lds = base + out_bytes(groups);
+            } else {
+                groups = natural;
             }
         }
     }

@@ -22,8 +22,13 @@
  *     1.5 * 2^23 + I (|I| <= 32*15*127 < 2^22 keeps the exponent fixed);
  *     t = fma(F, sw, -1.5 * 2^23 * sw) is then I * sw rounded once (the
  *     offset product is exact: sw is an fp16 value), and acc = fma(t, d8,
- *     acc). The reference rounds sw * d8 first and multiplies by I; both are
- *     single fp32 roundings of the same exact products.
+ *     acc). This rounds each term twice where the reference rounds it once:
+ *     the reference's sw * d8 is exact (two fp16 values), and its
+ *     fma(sw * d8, I, sum) rounds only into the sum. Here I * sw is rounded
+ *     to fp32 first (relative error at most 2^-24 per term) and then
+ *     accumulated, so per-term results do not follow the reference's single
+ *     rounding; they are exact whenever I * sw fits 24 bits (integer-exact
+ *     inputs), and otherwise differ by about 2^-24 of the term.
  *   - the min term is a plain matrix product over the sub-block index,
  *     [tokens x 8] fp16 s8 times [8 x rows] fp16(-dmin*m_b), done once per
  *     super-block by one v_mfma_f32_32x32x16_f16 accumulating into the same

@@ -38,6 +38,45 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
     return 0;
 }
 
+/* The achievable read rate of this device: a plain streaming read of a
+ * weight copy's bytes with no compute and no output (the floor the MMVQ
+ * kernel's time is judged against). Workgroup b reads the 16-byte vectors
+ * [b * 256 * LPT, (b + 1) * 256 * LPT) of the buffer, LPT per thread, all
+ * loads issued before the first is used; the folded value is stored only in
+ * the impossible case that it equals a sentinel, so nothing is written but
+ * the loads cannot be dropped. */
+template <int LPT>
+__global__ __launch_bounds__(256) void sera_stream_read_kernel(const uint4 *__restrict__ p, size_t n16,
+                                                               uint32_t *__restrict__ sink) {
+    const size_t base = (size_t)blockIdx.x * 256 * LPT + threadIdx.x;
+    uint4 v[LPT];
+#pragma unroll
+    for (int i = 0; i < LPT; i++) {
+        const size_t j = base + (size_t)i * 256;
+        v[i] = j < n16 ? p[j] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    uint32_t acc = 0u;
+#pragma unroll
+    for (int i = 0; i < LPT; i++) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    if (acc == 0x9E3779B9u && threadIdx.x == 0) sink[blockIdx.x & 255] = acc;
+}
+
+namespace {
+hipError_t launch_stream_read(const void *p, size_t bytes, int lpt, uint32_t *sink, hipStream_t s) {
+    const size_t n16 = bytes / 16;
+    const size_t per = (size_t)256 * lpt;
+    const dim3 grid((unsigned)((n16 + per - 1) / per));
+    switch (lpt) {
+        case 2: hipLaunchKernelGGL(sera_stream_read_kernel<2>, grid, dim3(256), 0, s, (const uint4 *)p, n16, sink); break;
+        case 4: hipLaunchKernelGGL(sera_stream_read_kernel<4>, grid, dim3(256), 0, s, (const uint4 *)p, n16, sink); break;
+        case 8: hipLaunchKernelGGL(sera_stream_read_kernel<8>, grid, dim3(256), 0, s, (const uint4 *)p, n16, sink); break;
+        case 16: hipLaunchKernelGGL(sera_stream_read_kernel<16>, grid, dim3(256), 0, s, (const uint4 *)p, n16, sink); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+}  // namespace
+
 /* Kernel-only loop on a prepared stage: path 0 = MMVQ, 1 = MMQ, 4 = stream-K MMQ (partial = slots, then
  * the zeroed tile counters), 5 = Q6_K MMVQ (param = rows per wave), 6 = Q6_K
  * MMQ (param = splits), 7 / 8 = selected-row LM head on Q6_K / Q4_K rows
@@ -48,6 +87,9 @@ extern "C" int sera_q4k_bench_linear(const void *geometry, const void *const *we
  * (MMQ formula) (param = chunk, 0 = planned; partial = split slots followed
  * by the zeroed row-group counters). path | 256: the Q4_K paths (0, 1, 4,
  * 8, 12, 13) on weights in the tiled layout (SERA_QTYPE_Q4K_TILED).
+ * Path 14: the plain streaming read of each weight copy's N*K/256*144 bytes
+ * (param = 16-byte loads per thread: 2, 4, 8 or 16; y receives nothing but
+ * must be 1 KB of device memory).
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
  * elapsed time over iters (each launch's duration plus the dispatch gap to
@@ -82,6 +124,7 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
             case 13: return sera_launch_q4k_fewtok_acc(
                          q4, path - 12, w, stage, y, partial,
                          (int *)(partial + (size_t)sera_fewtok_splits(M, N, K, param) * M * N), M, N, K, param, 0, s);
+            case 14: return launch_stream_read(w, (size_t)N * (K / Q4K_QK) * Q4K_BLOCK_BYTES, param, (uint32_t *)y, s);
             case 4: return sera_launch_q4k_mmq_streamk(
                         q4, w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),
                         M, N, K, param, s);

@@ -112,10 +112,38 @@ size_t partial_floats_bound(size_t max_tokens, int64_t max_features) {
     return by_tiles < by_shape ? by_tiles : by_shape;
 }
 
+/* Limits of the kernels' index arithmetic, checked before any launch:
+ *   - the activation stages are addressed with 32-bit element offsets
+ *     (the MMQ staging computes (token * K + k) in 32 bits), so
+ *     Mpad * K must stay below 2^31 for the largest token padding (64);
+ *   - the quantizers put one activation row per grid row (gridDim.y),
+ *     which the device caps at 65535;
+ *   - a weight row and a 16-row group of rows stay below 2^31 bytes
+ *     (buffer-resource ranges are 32-bit), which K <= 2^24 guarantees. */
+constexpr int64_t kMaxStagedElems = (int64_t)1 << 31;
+constexpr int kMaxRows = 65535;
+constexpr int kMaxK = 1 << 24;
+
+bool stage_ok(const char *tag, int M, int K) {
+    if (K > kMaxK) { fail(-1, "%s: K=%d exceeds the supported %d", tag, K, kMaxK); return false; }
+    const int64_t mpad = ((int64_t)M + 63) / 64 * 64;
+    if (mpad > kMaxRows) {
+        fail(-1, "%s: M=%d tokens exceed the %d rows one quantize launch covers", tag, M, kMaxRows);
+        return false;
+    }
+    if (mpad * K >= kMaxStagedElems) {
+        fail(-1, "%s: staged activations Mpad*K = %lld reach 2^31 (32-bit stage offsets)", tag,
+             (long long)(mpad * K));
+        return false;
+    }
+    return true;
+}
+
 bool check_shape(const char *tag, const void *W, const float *X, const float *Y, int M, int N, int K) {
     if (!W || !X || !Y) { fail(-1, "%s: null pointer", tag); return false; }
     if (M <= 0 || N <= 0 || K <= 0) { fail(-1, "%s: bad shape M=%d N=%d K=%d", tag, M, N, K); return false; }
     if (K % Q4K_QK != 0) { fail(-1, "%s: K=%d must be a multiple of 256", tag, K); return false; }
+    if (!stage_ok(tag, M, K)) return false;
     if (((uintptr_t)X & 15u) != 0) { fail(-1, "%s: X must be 16-byte aligned", tag); return false; }
     if (((uintptr_t)W & 15u) != 0) { fail(-1, "%s: W must be 16-byte aligned", tag); return false; }
     return true;
@@ -251,12 +279,14 @@ extern "C" int sera_q4k_set_arena(void *device_ptr, size_t bytes) {
 
 extern "C" int sera_q8_1_quantize_row(const float *X, int M, int K, void *stage, void *stream) {
     if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q8_1_quantize_row: bad arguments");
+    if (!stage_ok("sera_q8_1_quantize_row", M, K)) return -1;
     return sera_launch_q8_1_row(X, M, K, stage, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-2, "sera_q8_1_quantize_row: launch failed");
 }
 
 extern "C" int sera_q8_1_quantize_mmq(const float *X, int M, int K, void *stage, void *stream) {
     if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q8_1_quantize_mmq: bad arguments");
+    if (!stage_ok("sera_q8_1_quantize_mmq", M, K)) return -1;
     if (((uintptr_t)X & 15u) != 0) return fail(-1, "sera_q8_1_quantize_mmq: X must be 16-byte aligned");
     return sera_launch_q8_1_mmq(X, M, sera_mmq_padded_rows(M), K, stage, (hipStream_t)stream) == hipSuccess
                ? 0 : fail(-2, "sera_q8_1_quantize_mmq: launch failed");
@@ -292,6 +322,7 @@ extern "C" int sera_q4k_mmvq_qt(uint32_t qtype, const void *W, const void *row_s
     if (!W || !row_stage || !Y) return fail(-1, "sera_q4k_mmvq: null pointer");
     if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q4k_mmvq: batch M=%d outside 1..8", M);
     if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_mmvq: bad shape N=%d K=%d", N, K);
+    if (!stage_ok("sera_q4k_mmvq", M, K)) return -1;
     if (rows_per_tile != 0 && rows_per_tile != 2 && rows_per_tile != 4 && rows_per_tile != 8 &&
         rows_per_tile != 16)
         return fail(-1, "sera_q4k_mmvq: rows_per_tile=%d not in {0,2,4,8,16}", rows_per_tile);
@@ -331,6 +362,7 @@ extern "C" int sera_q4k_fewtok_qt(uint32_t qtype, int form, const void *W, const
     const int mmax = form == 0 ? SERA_Q4K_MMVQ_MAX_BATCH : SERA_Q4K_FEWTOK_MAX_BATCH;
     if (M < 1 || M > mmax) return fail(-1, "sera_q4k_fewtok: batch M=%d outside 1..%d", M, mmax);
     if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_fewtok: bad shape N=%d K=%d", N, K);
+    if (!stage_ok("sera_q4k_fewtok", M, K)) return -1;
     if (((uintptr_t)W & 15u) || ((uintptr_t)stage & 15u))
         return fail(-1, "sera_q4k_fewtok: W and the stage must be 16-byte aligned");
     if (chunk < 0 || chunk > sera_fewtok_max_chunk(M))
@@ -352,6 +384,7 @@ extern "C" int sera_q4k_mmq_qt(uint32_t qtype, const void *W, const void *mmq_st
                                int N, int K, int splits, void *stream) {
     if (!W || !mmq_stage || !Y) return fail(-1, "sera_q4k_mmq: null pointer");
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q4k_mmq: bad shape M=%d N=%d K=%d", M, N, K);
+    if (!stage_ok("sera_q4k_mmq", M, K)) return -1;
     if (splits == 0) splits = sera_mmq_splits(M, N, K);
     if (splits < 1 || splits > K / Q4K_QK) return fail(-1, "sera_q4k_mmq: splits=%d outside 1..K/256", splits);
     if (splits > 1 && (!partial || ((size_t)M * N) % 4 != 0))
@@ -497,6 +530,7 @@ extern "C" int sera_q4k_mmq_streamk_qt(uint32_t qtype, const void *W, const void
     if (!W || !mmq_stage || !Y || !slots || !counters) return fail(-1, "sera_q4k_mmq_streamk: null pointer");
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK)
         return fail(-1, "sera_q4k_mmq_streamk: bad shape M=%d N=%d K=%d", M, N, K);
+    if (!stage_ok("sera_q4k_mmq_streamk", M, K)) return -1;
     if (wgs == 0) wgs = streamk_wgs(M);
     if (wgs < 8 || wgs % 8)
         return fail(-1, "sera_q4k_mmq_streamk: workgroups=%d must be a positive multiple of 8", wgs);
@@ -594,6 +628,7 @@ extern "C" int sera_q6k_mmvq(uint32_t qtype, const void *W, const void *row_stag
     if (!W || !row_stage || !Y) return fail(-1, "sera_q6k_mmvq: null pointer");
     if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH) return fail(-1, "sera_q6k_mmvq: batch M=%d outside 1..8", M);
     if (N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q6k_mmvq: bad shape N=%d K=%d", N, K);
+    if (!stage_ok("sera_q6k_mmvq", M, K)) return -1;
     if (!q6k_shape_ok("sera_q6k_mmvq", qtype, K)) return -1;
     if (qtype == SERA_QTYPE_Q6K_SPLIT) {
         if (rows != 0 && rows != 2 && rows != 4)
@@ -687,6 +722,7 @@ extern "C" void sera_q8_1_q6k_mmq_stage_offsets(int M, int K, size_t *qs, size_t
 extern "C" int sera_q8_1_quantize_mmq_d4(const float *X, int M, int K, void *stage, void *stream) {
     if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK)
         return fail(-1, "sera_q8_1_quantize_mmq_d4: bad arguments");
+    if (!stage_ok("sera_q8_1_quantize_mmq_d4", M, K)) return -1;
     if (((uintptr_t)X & 15u) != 0) return fail(-1, "sera_q8_1_quantize_mmq_d4: X must be 16-byte aligned");
     return sera_launch_q8_1_q6k_stage(X, M, sera_q6k_mmq_padded_rows(M), K, 0, stage, (hipStream_t)stream) ==
                    hipSuccess
@@ -696,6 +732,7 @@ extern "C" int sera_q8_1_quantize_mmq_d4(const float *X, int M, int K, void *sta
 extern "C" int sera_q8_1_quantize_row_q6k(const float *X, int M, int K, void *stage, void *stream) {
     if (!X || !stage || M <= 0 || K <= 0 || K % Q4K_QK)
         return fail(-1, "sera_q8_1_quantize_row_q6k: bad arguments");
+    if (!stage_ok("sera_q8_1_quantize_row_q6k", M, K)) return -1;
     if (((uintptr_t)X & 15u) != 0) return fail(-1, "sera_q8_1_quantize_row_q6k: X must be 16-byte aligned");
     return sera_launch_q8_1_q6k_stage(X, M, sera_q6k_mmq_padded_rows(M), K, 1, stage, (hipStream_t)stream) ==
                    hipSuccess
@@ -711,6 +748,7 @@ extern "C" int sera_q6k_mmq(uint32_t qtype, const void *W, const void *q6k_mmq_s
                             int M, int N, int K, int splits, void *stream) {
     if (!W || !q6k_mmq_stage || !Y) return fail(-1, "sera_q6k_mmq: null pointer");
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q6k_mmq: bad shape M=%d N=%d K=%d", M, N, K);
+    if (!stage_ok("sera_q6k_mmq", M, K)) return -1;
     if (((uintptr_t)W & 15u) != 0) return fail(-1, "sera_q6k_mmq: W must be 16-byte aligned");
     if (!q6k_shape_ok("sera_q6k_mmq", qtype, K)) return -1;
     if (splits == 0) splits = q6k_splits(M, N, K);

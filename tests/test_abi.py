@@ -156,6 +156,41 @@ def test_kernel_entry_points_validate_on_host(L):
     assert b"slots" in L.sera_q4k_last_error()
 
 
+def test_offset_and_grid_limits_rejected_on_host(L):
+    """Shapes past the kernels' 32-bit stage offsets (Mpad*K >= 2^31), the
+    quantizers' 65535-row grid or K > 2^24 fail with a message before any
+    launch (the reference indexes its quantizers in int64,
+    cuda/mmq/quantize.cu:9,28; here they are rejected, never wrapped)."""
+    d = ctypes.c_void_p(256)
+    # 60000 tokens x K=40960: Mpad*K = 60032*40960 > 2^31
+    assert L.sera_q4k_dense(d, d, d, 60000, 128, 40960, None, 0) == -1
+    assert b"2^31" in L.sera_q4k_last_error()
+    # just under the bound is not rejected by the shape check (it fails later: no arena)
+    assert L.sera_q4k_dense(d, d, d, 52416, 128, 40960, None, 0) == -1
+    assert b"arena" in L.sera_q4k_last_error()
+    # 84000 tokens: more rows than one quantize grid holds
+    assert L.sera_q4k_dense(d, d, d, 84000, 128, 5120, None, 0) == -1
+    assert b"65535" in L.sera_q4k_last_error()
+    big_k = (1 << 24) + 256
+    assert L.sera_q4k_dense_vec(d, d, d, 1, 128, big_k, None, 0) == -1
+    assert b"exceeds" in L.sera_q4k_last_error()
+    assert L.sera_q4k_dense_vec_static(d, d, d, 1, 128, big_k, None) == -1
+    assert b"exceeds" in L.sera_q4k_last_error()
+    assert L.sera_q8_1_quantize_mmq(d, 60000, 40960, d, None) == -1
+    assert b"2^31" in L.sera_q4k_last_error()
+    assert L.sera_q8_1_quantize_row(d, 1, big_k, d, None) == -1
+    assert L.sera_q4k_mmq_qt(12, d, d, d, d, 60000, 128, 40960, 1, None) == -1
+    assert b"2^31" in L.sera_q4k_last_error()
+    assert L.sera_q4k_mmq_streamk_qt(12, d, d, d, d, d, 60000, 128, 40960, 8, None) == -1
+    assert b"2^31" in L.sera_q4k_last_error()
+    assert L.sera_q4k_fewtok(1, d, d, d, None, None, 16, 128, big_k, 0, 0, None) == -1
+    assert b"exceeds" in L.sera_q4k_last_error()
+    assert L.sera_q6k_dense(14, d, d, d, 60000, 128, 40960, None, 0) == -1
+    assert b"2^31" in L.sera_q4k_last_error()
+    assert L.sera_q8_1_quantize_mmq_d4(d, 60000, 40960, d, None) == -1
+    assert b"2^31" in L.sera_q4k_last_error()
+
+
 def test_fewtok_plan(L):
     """Planned chunks cover K in at most 20 super-blocks each; explicit
     chunks go up to 40 (20 above 8 tokens); row groups cover N."""

@@ -197,6 +197,42 @@ def test_fewtok_persistent_grid(torch, N, K):
     assert ran_persistent == (nkb % 2 == 0), "the persistent grid was not exercised"
 
 
+def test_fewtok_persistent_grid_beyond_the_lds_of_one_range(torch, linear):
+    """A head tall enough that one resident workgroup per CU cannot hold its
+    range's results in LDS (262144 rows at 16 tokens: 256 ranges of 64
+    tiles would need 175,632 bytes): the launcher takes more, shorter ranges
+    instead of failing, and the outputs match the oracle on sampled rows,
+    through the kernel entry point and the boundary."""
+    N, K, M = 262144, 5120, 16
+    L = q3q4.load()
+    grid, groups = q3q4.fewtok_grid(1, M, N, K), q3q4.fewtok_groups(M, N, K)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    say(f"case fewtok LDS-capped persistent grid M={M} N={N} K={K} grid={grid} groups={groups} cus={cus}")
+    assert q3q4.fewtok_splits(M, N, K) == 1
+    assert cus < grid < groups, "the ranges should be shortened to fit LDS, not left at one per CU"
+    gen = torch.Generator(device="cuda").manual_seed(262144)
+    wf = torch.randn((N, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+    Wd = torch.empty((N, K // 256 * 144), dtype=torch.uint8, device="cuda")
+    q3q4.quantize_weights(wf, Wd)
+    del wf
+    rng = np.random.default_rng(5)
+    x = outlier_activations(rng, M, K)
+    stage = torch.empty(q3q4.mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
+    q3q4.quantize_mmq(dev(torch, x), stage)
+    y, _ = run_fewtok(torch, Wd, stage, M, N, K, 0, form=1)
+    yb = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    linear(q3q4.bind_geometry(12, K, N), Wd, dev(torch, x), yb)
+    torch.cuda.synchronize()
+    assert torch.equal(y, yb), "the boundary's result differs from the kernel entry point's"
+    rows = np.unique(np.concatenate([np.arange(256), np.arange(N - 256, N),
+                                     rng.choice(N, 512, replace=False)]))
+    W = Wd[torch.from_numpy(rows).cuda()].cpu().numpy()
+    xq, xd, xs = oracle.q8_1_mmq(x)
+    ref = oracle.gemm_mmq(W, xq, xd, xs, len(rows), K)
+    check_close(y.cpu().numpy()[:, rows], ref, f"LDS-capped persistent grid ({len(rows)} rows)", TIGHT)
+    del Wd
+
+
 def test_fewtok_matches_dot4_mmvq(torch):
     """The two MMVQ-path kernels agree within the tolerance at every batch
     they share (1-8 tokens) on a Qwen3-32B-width matrix."""

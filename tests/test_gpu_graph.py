@@ -148,3 +148,50 @@ def test_graph_replay_matches_eager(torch, linear, qtype, M, N, K, kernel):
         assert torch.equal(y, y_ref), f"replay {rep} differs from the eager result"
     del graph
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 5120, 25600), (1, 4096, 5120)])
+def test_graph_replay_static_entry(torch, linear, M, N, K):
+    """sera_q4k_dense_vec_static (the decode path on the library's static
+    scratch) captured into a graph: replays equal the eager call bit for bit,
+    with eager static calls on other inputs between them."""
+    L = q3q4.load()
+    kern = "few-token" if L.sera_q4k_vec_uses_fewtok(M, N, K) else "dot4"
+    say(f"case graph static M={M} N={N} K={K} ({kern}, splits {q3q4.fewtok_splits(M, N, K)})")
+    rng = np.random.default_rng(31 * M + N)
+    Wd = torch.from_numpy(weights(rng, q3q4.QTYPE_Q4_K, N, K)).cuda()
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    x_other = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+
+    def static_call(xx, yy):
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = L.sera_q4k_dense_vec_static(ctypes.c_void_p(Wd.data_ptr()), ctypes.c_void_p(xx.data_ptr()),
+                                         ctypes.c_void_p(yy.data_ptr()), M, N, K, stream)
+        assert rc == 0, L.sera_q4k_last_error().decode()
+
+    y_ref = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    static_call(x, y_ref)               # eager; also sets the scratch up on this device
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y_ref).all())
+    y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    y_other = torch.empty_like(y)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        static_call(x, y)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        static_call(x, y)
+    for rep in range(3):
+        y.fill_(float("nan"))
+        static_call(x_other, y_other)   # eager call on the same static scratch
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        say(f"  replay {rep}: equal={bool(torch.equal(y, y_ref))}")
+        assert torch.equal(y, y_ref), f"replay {rep} differs from the eager result"
+    del graph
+    torch.cuda.synchronize()

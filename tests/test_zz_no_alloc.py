@@ -9,10 +9,17 @@ split in five and uses the split slots and row-group counters, the second
 (3 tokens, 5120 -> 2048) is smaller and runs the dot4 kernel; both must
 match. Device memory in use does not change across the static calls, and a
 shape that needs more than the static scratch is rejected with a message.
-In a fresh process the static calls come before any init of the library,
-so the first one sets the scratch up itself.
+
+The first static call on a device sets the scratch up itself (looks up its
+address and clears its counters on the caller's stream) unless the
+library's init already did. In this test process other tests have called
+init first, so a second test runs the static calls in a fresh child
+process that calls nothing else in the library, and compares its outputs
+with sera_q4k_dense_vec's here.
 """
 import ctypes
+import os
+import subprocess
 import sys
 
 import numpy as np
@@ -91,3 +98,70 @@ def test_static_entry_point_matches_dense_vec():
     rc = L.sera_q4k_dense_vec_static(ctypes.c_void_p(W.data_ptr()), ctypes.c_void_p(x.data_ptr()),
                                      ctypes.c_void_p(got[0].data_ptr()), M, N, K, stream)
     assert rc == -1 and b"static" in L.sera_q4k_last_error()
+
+
+CHILD = r"""
+import ctypes, sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[2])
+import q3q4
+L = q3q4.load()
+d = sys.argv[1]
+stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+for i, (M, N, K) in enumerate([(8, 5120, 25600), (3, 2048, 5120)]):
+    W = torch.from_numpy(np.load(f"{d}/w{i}.npy")).cuda()
+    x = torch.from_numpy(np.load(f"{d}/x{i}.npy")).cuda()
+    y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    print(f"child static call M={M} N={N} K={K}", flush=True)
+    rc = L.sera_q4k_dense_vec_static(ctypes.c_void_p(W.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                     ctypes.c_void_p(y.data_ptr()), M, N, K, stream)
+    assert rc == 0, L.sera_q4k_last_error().decode()
+    torch.cuda.synchronize()
+    np.save(f"{d}/y{i}.npy", y.cpu().numpy())
+print("child done", flush=True)
+"""
+
+
+def test_static_entry_point_in_a_fresh_process(tmp_path):
+    """The static calls of a process that never initialised the library:
+    the first one sets the scratch up on the caller's stream."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("gpu test without a visible HIP device")
+    L = q3q4.load()
+    rng = np.random.default_rng(77)
+    cases = [(8, 5120, 25600), (3, 2048, 5120)]
+    data = []
+    for i, (M, N, K) in enumerate(cases):
+        g = torch.Generator(device="cuda").manual_seed(3 * N + K)
+        wf = torch.randn((N, K), generator=g, device="cuda", dtype=torch.float32) * 0.02
+        W = torch.empty((N, K // 256 * 144), dtype=torch.uint8, device="cuda")
+        q3q4.quantize_weights(wf, W)
+        del wf
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        np.save(tmp_path / f"w{i}.npy", W.cpu().numpy())
+        np.save(tmp_path / f"x{i}.npy", x)
+        data.append((M, N, K, W, torch.from_numpy(x).cuda()))
+    torch.cuda.synchronize()
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "sera.c_amd")
+    say("starting the child process")
+    r = subprocess.run([sys.executable, "-c", CHILD, str(tmp_path), pkg], capture_output=True, text=True,
+                       timeout=240)
+    sys.stdout.write(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip().splitlines()[-1] == "child done"
+    lin = q3q4.Linear(device=0, max_tokens=8, max_features=5120, max_k=25600)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for i, (M, N, K, W, x) in enumerate(data):
+        yv = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        rc = L.sera_q4k_dense_vec(ctypes.c_void_p(W.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                  ctypes.c_void_p(yv.data_ptr()), M, N, K, stream, 0)
+        assert rc == 0, L.sera_q4k_last_error().decode()
+        torch.cuda.synchronize()
+        a = np.load(tmp_path / f"y{i}.npy")
+        b = yv.cpu().numpy()
+        assert np.all(np.isfinite(a))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"M={M} N={N} K={K}"
+        say(f"  fresh process M={M} N={N} K={K}: bit-identical to sera_q4k_dense_vec")
+    del lin
