@@ -237,7 +237,7 @@ def main():
     dummy = torch.zeros(16, dtype=torch.uint8, device=dev)
     for name, (N, K, (ws, arr)) in sets.items():
         wbytes = N * (K // 256) * 144
-        for lpt in (2, 4, 8, 16):
+        for lpt in (1, 2, 4, 8, 16):
             kavg, _ = bench_kernel(14, arr, args.copies, dummy, sink, None, 1, N, K, lpt, args.warmup, args.steps)
             ceiling.append({"proj": name, "bytes": wbytes, "loads_per_thread": lpt,
                             "kernel": f"sera_stream_read_kernel<{lpt}>",
@@ -295,6 +295,13 @@ def main():
             partial = torch.zeros(-splits * M * N + q3q4.fewtok_groups(M, N, K), dtype=torch.float32,
                                   device=dev)
             kavg, _ = bench_kernel(13, arr, ncopies, stage, y, partial, M, N, K, 0, 3, iters)
+        elif L.sera_q4k_mmq_schedule(M, N, K) == 2:
+            # whole tiles + split tail: slots, then the zeroed tile counters
+            dp, pieces = q3q4.mmq_tail_plan(M, N, K)
+            splits = None
+            nslot = q3q4.mmq_tail_slot_floats(M, N, dp, pieces)
+            partial = torch.zeros(nslot + tiles, dtype=torch.float32, device=dev)
+            kavg, _ = bench_kernel(15, arr, ncopies, stage, y, partial, M, N, K, dp * 64 + pieces, 3, iters)
         elif L.sera_q4k_mmq_schedule(M, N, K) == 1:
             # stream-K schedule: slots, then the zeroed tile counters
             splits = 0
@@ -308,7 +315,8 @@ def main():
             kavg, _ = bench_kernel(1, arr, ncopies, stage, y, partial, M, N, K, splits, 3, iters)
         ops = 2.0 * M * N * K
         row = {"case": label, "M": M, "N": N, "K": K,
-               "schedule": ("stream-K" if splits == 0 else f"split-K x{splits}" if splits > 0
+               "schedule": (f"{dp} whole tiles of {tiles}, the rest in {pieces} K pieces" if splits is None
+                            else "stream-K" if splits == 0 else f"split-K x{splits}" if splits > 0
                             else f"few-token kernel, {-splits} K split(s) summed in-kernel"),
                "step_us": round(step_ms * 1e3, 2), "kernel_us": round(kavg * 1e3, 2),
                "kernel_TOPS": round(ops / (kavg * 1e-3) / 1e12, 1),

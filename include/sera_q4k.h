@@ -178,13 +178,33 @@ int sera_q4k_mmq_splits(int M, int N, int K);
 int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
                          int M, int N, int K, int wgs, void *stream);
 int sera_q4k_mmq_streamk_wgs(int M);   /* resident workgroups for M tokens (after init) */
-/* Schedule of the MMQ tile kernels for this shape (after init): 1 =
- * stream-K (16- and 32-token tiles, M <= 32, from one full round of
- * resident workgroups of tiles), 0 = plain tiles / split-K with the split
- * count of sera_q4k_mmq_splits (a per-CU cost model fitted to MI355X
- * timings); -1 for a bad shape. sera_q4k_dense runs it where
- * sera_q4k_mmq_uses_fewtok is 0. */
+/* Schedule of the MMQ tile kernels for this shape (after init): 2 = whole
+ * tiles + split tail (the 64-token tile, M > 32; below), 1 = stream-K
+ * (16- and 32-token tiles, M <= 32, from one full round of resident
+ * workgroups of tiles), 0 = plain tiles / split-K with the split count of
+ * sera_q4k_mmq_splits (a per-CU cost model fitted to MI355X timings); -1
+ * for a bad shape. sera_q4k_dense runs it where sera_q4k_mmq_uses_fewtok
+ * is 0. */
 int sera_q4k_mmq_schedule(int M, int N, int K);
+
+/* MMQ kernel under the tail schedule (the role of mul_mat_q's stream-K
+ * decomposition, cuda/mmq/mmq.cuh:3641-4352, for the last round of tiles
+ * only): the first dp_tiles workgroups each run one whole output tile; each
+ * of the remaining sera_q4k_mmq_tiles(M, N) - dp_tiles tiles is cut into
+ * `pieces` near-equal K ranges, one workgroup per (tile, range), whose
+ * partial sums are added in range order by the range that finishes last
+ * (per-tile counters), so results repeat bit for bit and no workgroup waits
+ * on another. slots: sera_q4k_mmq_tail_slot_floats() floats; counters:
+ * tiles - dp_tiles ints, zero on entry and zero again after the kernel
+ * (both may be NULL when pieces == 1 or dp_tiles == tiles). accum != 0 adds
+ * the product to Y. sera_q4k_mmq_tail_plan gives the schedule's own choice
+ * (after init; slots limited to max_slot_floats, or with 0 to what the
+ * attached arena holds after the stage: the plan sera_q4k_dense runs for
+ * M > 32). */
+int sera_q4k_mmq_tail_qt(uint32_t qtype, const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
+                         int M, int N, int K, int dp_tiles, int pieces, int accum, void *stream);
+int sera_q4k_mmq_tail_plan(int M, int N, int K, size_t max_slot_floats, int *dp_tiles, int *pieces);
+size_t sera_q4k_mmq_tail_slot_floats(int M, int N, int dp_tiles, int pieces);
 /* 1 if sera_q4k_dense (the boundary's MMQ path) runs the few-token MFMA
  * kernel with the MMQ formula for this shape instead of the MMQ tiles: 1-8
  * tokens always, 9-16 tokens on matrices with N or K of 16384 or more (gate,

@@ -57,16 +57,39 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-template <int BM>
+template <int BM, int PR>
 struct alignas(16) MmqSmem {
     /* int8 quants of one 256-wide K step; the 16-byte piece c of token t
      * sits in column c ^ (t & 15), so 16 consecutive tokens reading the same
      * piece hit 16 different bank groups */
     alignas(16) int8_t xs[2][BM][Q4K_QK];
-    alignas(16) float d8[2][8][BM];          /* fp16 d8 as float, [sub-block][token] */
+    /* d8 per [sub-block][token]: the paired tile keeps it as float; the
+     * 32-row tiles keep the fp16 value itself, each 32-token group in the
+     * order of the MFMA result rows a lane holds (token 8q + 4h + i at
+     * 16h + 4q + i), so a lane's 16 scales are one 32-byte run */
+    alignas(16) float d8[PR ? 2 : 1][8][PR ? BM : 4];
+    alignas(16) _Float16 d8h[PR ? 1 : 2][8][PR ? 8 : BM];
     alignas(16) _Float16 s8[2][BM][8];       /* fp16 s8, [token][sub-block] */
     alignas(16) _Float16 zero8[8];           /* a zero min-term operand */
 };
+
+/* acc = fma(t, d8, acc) with d8 the low (HI = 0) or high half of a packed
+ * fp16 pair: v_fma_mix_f32 converts the half exactly and rounds once, as
+ * v_fma_f32 on the converted value would. Written with the accumulator
+ * tied to the destination; left to itself the register allocator gives
+ * each result a new register and copies the accumulators back per step. */
+template <int HI>
+__device__ __forceinline__ void fma_acc_f16(float &acc, float t, uint32_t d8pair) {
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(t), "v"(d8pair));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(t), "v"(d8pair));
+}
+
+/* Position of token tok in a 32-token group of MmqSmem::d8h. */
+__device__ __forceinline__ int mmq_d8h_pos(int tok) {
+    return (tok & ~31) + 16 * ((tok >> 2) & 1) + 4 * ((tok >> 3) & 3) + (tok & 3);
+}
 
 __device__ __forceinline__ v16i magic_seed() { return sera_magic_seed<16>(); }
 
@@ -154,7 +177,7 @@ struct MmqShape {
  * 0-15 are I_sa, rows 16-31 I_sb. */
 template <int TT, int WGT, int WGN, int PR = 0, bool AHEAD = false>
 __device__ __forceinline__ void mmq_segment(
-        MmqSmem<MmqShape<TT, WGT, WGN, PR>::BM> &sm, const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
+        MmqSmem<MmqShape<TT, WGT, WGN, PR>::BM, PR> &sm, const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
         const uint32_t *__restrict__ xds, int N, int K, int m0, int n0, int kb_begin, int kb_end,
         v16f (&acc)[TT][2], int tiled) {
     using S = MmqShape<TT, WGT, WGN, PR>;
@@ -207,8 +230,13 @@ __device__ __forceinline__ void mmq_segment(
             const uint32_t dw[4] = {dr.x, dr.y, dr.z, dr.w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                sm.d8[buf][4 * part + e][tok] = h2f_bits(dw[e] & 0xffffu);
                 union { uint16_t u; _Float16 f; } cv;
+                if constexpr (PR) {
+                    sm.d8[buf][4 * part + e][tok] = h2f_bits(dw[e] & 0xffffu);
+                } else {
+                    cv.u = (uint16_t)(dw[e] & 0xffffu);
+                    sm.d8h[buf][4 * part + e][mmq_d8h_pos(tok)] = cv.f;
+                }
                 cv.u = (uint16_t)(dw[e] >> 16);
                 sm.s8[buf][tok][4 * part + e] = cv.f;
             }
@@ -294,6 +322,21 @@ __device__ __forceinline__ void mmq_segment(
                 bmin[nt][2 * p + 1] = mw[p].y;
             }
         }
+        /* min term of this super-block: one f16 MFMA per (token tile,
+         * weight tile), after the sub-blocks */
+        auto min_term = [&]() {
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                /* paired tile: the min term goes to rows 0-15 only (each token once) */
+                const int tok = PR ? (l32 & 15) : BMW * wt + 32 * t + l32;
+                const bool none = h || (PR && l32 >= 16);
+                const v8h as8 =
+                    *(const v8h *)(none ? (const void *)&sm.zero8[0] : (const void *)&sm.s8[buf][tok][0]);
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+                    acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as8, bmin[nt], acc[t][nt], 0, 0, 0);
+            }
+        };
         /* the next step's super-block; the last step reloads its own (in
          * bounds, unused), which keeps the prefetch free of branches */
         const int kb_next = more ? kb_begin + it + 1 : kb_begin + it;
@@ -371,29 +414,23 @@ __device__ __forceinline__ void mmq_segment(
                 if (i + 1 < NI) Fn = mfma_of(i + 1);
                 const float swb = (float)((b & 1) ? sw[nt][b >> 1].y : sw[nt][b >> 1].x);
                 const float nswb = -SERA_MAGIC_F * swb;
-                float d8v[16];
+                /* the lane's 16 token scales (fp16, exact as float): one
+                 * 32-byte run; v_fma_mix takes each half as it is */
+                const _Float16 *d8p = &sm.d8h[buf][b][BMW * wt + 32 * t + 16 * h];
+                const v4u d8lo = *(const v4u *)d8p, d8hi = *(const v4u *)(d8p + 8);
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const v4f f4 = *(const v4f *)&sm.d8[buf][b][BMW * wt + 32 * t + 8 * q + 4 * h];
-                    d8v[4 * q] = f4.x; d8v[4 * q + 1] = f4.y; d8v[4 * q + 2] = f4.z; d8v[4 * q + 3] = f4.w;
+                for (int r = 0; r < 16; r += 2) {
+                    const uint32_t pair = r < 8 ? d8lo[r / 2] : d8hi[r / 2 - 4];
+                    float a0 = acc[t][nt][r], a1 = acc[t][nt][r + 1];
+                    fma_acc_f16<0>(a0, scaled_dot(Fc[r], swb, nswb), pair);
+                    fma_acc_f16<1>(a1, scaled_dot(Fc[r + 1], swb, nswb), pair);
+                    acc[t][nt][r] = a0;
+                    acc[t][nt][r + 1] = a1;
                 }
-#pragma unroll
-                for (int r = 0; r < 16; r++)
-                    acc[t][nt][r] = fmaf(scaled_dot(Fc[r], swb, nswb), d8v[r], acc[t][nt][r]);
                 Fc = Fn;
             }
         }
-        /* min term of this super-block */
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-            /* paired tile: the min term goes to rows 0-15 only (each token once) */
-            const int tok = PR ? (l32 & 15) : BMW * wt + 32 * t + l32;
-            const bool none = h || (PR && l32 >= 16);
-            const v8h as8 = *(const v8h *)(none ? (const void *)&sm.zero8[0] : (const void *)&sm.s8[buf][tok][0]);
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-                acc[t][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as8, bmin[nt], acc[t][nt], 0, 0, 0);
-        }
+        min_term();
         if (more) {
             if constexpr (!kWeightsAhead && !kProgressive) load_w(kb_begin + it + 1, hdr, qw);
             store_x(buf ^ 1, dr);
@@ -458,7 +495,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_kernel(
         int M, int N, int K, int kb_per_split, int accum, int tiled) {
     static_assert(WGT * WGN == 4, "4 waves per workgroup");
     using S = MmqShape<TT, WGT, WGN, PR>;
-    __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
+    __shared__ __attribute__((aligned(16))) MmqSmem<S::BM, PR> sm;
     const int ntt = (M + S::BM - 1) / S::BM;
     const int nrt = (N + S::BN - 1) / S::BN;
     const int tile = mmq_tile_of(blockIdx.x, ntt * nrt);
@@ -494,7 +531,7 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         int *__restrict__ counters, int M, int N, int K, int accum, int tiled) {
     static_assert(WGT * WGN == 4, "4 waves per workgroup");
     using S = MmqShape<TT, WGT, WGN, PR>;
-    __shared__ __attribute__((aligned(16))) MmqSmem<S::BM> sm;
+    __shared__ __attribute__((aligned(16))) MmqSmem<S::BM, PR> sm;
     __shared__ int s_last;
     const int tid = threadIdx.x;
     const int P = gridDim.x;                       /* multiple of 8 */
@@ -559,6 +596,98 @@ __global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_streamk_kernel(
         }
         u += kb1 - kb0;
     }
+}
+
+/* Whole tiles, then a split tail. The first dp_tiles workgroups each run
+ * one whole output tile (the full rounds of resident workgroups, tiles in
+ * the XCD-contiguous order of mmq_tile_of). The remaining R = ntiles -
+ * dp_tiles tiles are cut along K into `pieces` ranges of near-equal length,
+ * one workgroup per (tile, range), so the last round of tiles is spread
+ * over every workgroup slot instead of leaving most of them idle. Pieces
+ * are ordered range-major, tiles (token tiles fastest) within a range, so
+ * the token tiles that share a range's weight bytes run together on one
+ * XCD. The pieces of a tile hand off as in the stream-K kernel: each writes
+ * its accumulators to its own slot with device-scope stores, waits for
+ * them, and bumps the tile's counter; the piece that completes the count
+ * sums the slots in piece order, stores the tile and resets the counter. No workgroup waits on another, and the result
+ * does not depend on which piece finishes last. */
+/* Buffer-resource word 3 for raw 32-bit accesses on gfx950 (the DATA_FORMAT
+ * field set to 32 bits, as the MMVQ kernels' resources) and the sc1 cache
+ * policy bit of the buffer builtins' aux operand. */
+#define MMQ_SLOT_RSRC_FLAGS 0x00020000
+#define MMQ_SC1 16
+
+template <int TT, int WGT, int WGN, int WPE = 2, int PR = 0>
+__global__ __launch_bounds__(256, WPE) void sera_q4k_mmq_tail_kernel(
+        const uint8_t *__restrict__ W, const int8_t *__restrict__ xq, const uint32_t *__restrict__ xds,
+        float *__restrict__ y, float *__restrict__ slots, int *__restrict__ counters, int M, int N, int K,
+        int dp_tiles, int pieces, int accum, int tiled) {
+    static_assert(WGT * WGN == 4, "4 waves per workgroup");
+    using S = MmqShape<TT, WGT, WGN, PR>;
+    __shared__ __attribute__((aligned(16))) MmqSmem<S::BM, PR> sm;
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+    const int ntt = (M + S::BM - 1) / S::BM;
+    const int nrt = (N + S::BN - 1) / S::BN;
+    const int ntiles = ntt * nrt;
+    const int nkb = K / Q4K_QK;
+    const int wg = blockIdx.x;
+    int t, piece = 0, kb0 = 0, kb1 = nkb;
+    if (wg < dp_tiles) {
+        t = mmq_tile_of(wg, dp_tiles);
+    } else {
+        const int R = ntiles - dp_tiles;
+        const int L = mmq_tile_of(wg - dp_tiles, R * pieces);
+        piece = L / R;
+        t = dp_tiles + (L - piece * R);
+        kb0 = piece * nkb / pieces;
+        kb1 = (piece + 1) * nkb / pieces;
+    }
+    const int m0 = (t % ntt) * S::BM, n0 = (t / ntt) * S::BN;
+    v16f acc[TT][2];
+    mmq_segment<TT, WGT, WGN, PR, TT == 1 && WPE <= 2>(sm, W, xq, xds, N, K, m0, n0, kb0, kb1, acc, tiled);
+    if (wg < dp_tiles || pieces == 1) {
+        mmq_store<TT, WGT, WGN, PR>(y, M, N, m0, n0, acc, accum);
+        return;
+    }
+    const int r = t - dp_tiles;
+    /* slot (r, p): S::NACC / 4 chunks of 16 bytes per thread, chunk j of
+     * thread tid at byte (j * 256 + tid) * 16 of the slot, written and read
+     * with 16-byte buffer accesses carrying the sc1 (agent coherence) cache
+     * policy, the policy the agent-scope atomic accesses of the stream-K
+     * hand-off use, so no stale line of another XCD's L2 is read */
+    constexpr int kChunks = S::NACC / 4;
+    constexpr int kSlotBytes = S::NACC * 256 * 4;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        slots + (size_t)r * pieces * (S::NACC * 256), (short)0, pieces * kSlotBytes, MMQ_SLOT_RSRC_FLAGS);
+#pragma unroll
+    for (int j = 0; j < kChunks; j++) {
+        const int tt = j / 8, nt = (j / 4) & 1, q0 = 4 * (j & 3);
+        const v4f v = {acc[tt][nt][q0], acc[tt][nt][q0 + 1], acc[tt][nt][q0 + 2], acc[tt][nt][q0 + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), rs, (j * 256 + tid) * 16,
+                                               piece * kSlotBytes, MMQ_SC1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&counters[r], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == pieces - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(&counters[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    /* every piece's sums, this one's included, are read back from the
+     * slots (this one's stores were acknowledged before the counter moved),
+     * which keeps one set of accumulators live instead of two */
+    for (int p = 0; p < pieces; p++) {
+#pragma unroll
+        for (int j = 0; j < kChunks; j++) {
+            const int tt = j / 8, nt = (j / 4) & 1, q0 = 4 * (j & 3);
+            const v4f v = __builtin_bit_cast(
+                v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, (j * 256 + tid) * 16, p * kSlotBytes, MMQ_SC1));
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[tt][nt][q0 + e] = p == 0 ? v[e] : acc[tt][nt][q0 + e] + v[e];
+        }
+    }
+    mmq_store<TT, WGT, WGN, PR>(y, M, N, m0, n0, acc, accum);
 }
 
 /* Sums the split-K partials in split order: y = ((p0 + p1) + p2) + ... */
@@ -742,4 +871,100 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(uint32_t qtype, const void
     if (sera_mmq_bm(M) == 32)
         return launch_mmq_streamk_cfg<1, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
     return launch_mmq_streamk_cfg<2, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
+}
+
+/* ---- whole tiles + split tail ---------------------------------------------- */
+
+/* Whole-tile workgroups and K pieces of the tail schedule for M tokens of an
+ * N x K matrix on `cus` compute units (64-token tiles, M > 32). The device
+ * keeps 2 workgroups per CU resident, so P = 2 * cus run per round. The
+ * whole tiles are a multiple of P (all full rounds, or one round fewer);
+ * the R tiles left are cut into c K ranges (c = 1: whole as well). Each
+ * choice is priced by a rounds model of the greedy dispatch: rounds of P
+ * workgroups at kTailPairUs per super-block, a last partial round at
+ * kTailLoneUs when it fills no more than one workgroup per CU, and
+ * kTailFixUs per piece of a split tile (the hand-off and the last piece's
+ * reads). Fitted to a sweep of (whole tiles, c) on 14 Qwen3-32B shapes
+ * (q, k/v, o, gate/up, down at 64-2048 tokens) on MI355X: its pick is
+ * within 1.6% of the fastest measured choice on every shape where the
+ * schedule is used (sera_q4k_mmq_schedule). The split tiles' slots must
+ * fit max_slot_floats. */
+static constexpr float kTailPairUs = 5.0f, kTailLoneUs = 3.2f, kTailFixUs = 1.5f;
+
+static float tail_cost(int64_t dp_rounds, int64_t R, int c, int nkb, int P, int C) {
+    const int64_t n = R * c;
+    const int w = (nkb + c - 1) / c;
+    const int64_t full = n / P, rem = n % P;
+    float us = (float)dp_rounds * nkb * kTailPairUs + (float)full * w * kTailPairUs;
+    if (rem) us += (float)w * (rem > C ? kTailPairUs : kTailLoneUs);
+    if (c > 1) us += kTailFixUs * c;
+    return us;
+}
+
+extern "C" void sera_mmq_tail_plan(int M, int N, int K, int cus, size_t max_slot_floats, int *dp_tiles,
+                                   int *pieces) {
+    const int bm = sera_mmq_bm(M);
+    const int bn = mmq_bn(bm);
+    const int T = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const int nkb = K / Q4K_QK;
+    const int C = cus > 0 ? cus : kModelCUs;
+    const int P = 2 * C;
+    const int rounds = T / P;
+    int best_dp = T, best_c = 1;
+    float best = tail_cost(rounds, T - (int64_t)rounds * P, 1, nkb, P, C);
+    for (int fold = 0; fold <= (rounds > 0 ? 1 : 0); fold++) {
+        const int dp = (rounds - fold) * P;
+        const int R = T - dp;
+        if (R == 0) continue;
+        for (int c = 2; c <= (nkb < 16 ? nkb : 16); c++) {
+            if ((size_t)R * c * sera_mmq_slot_floats(M) > max_slot_floats) break;
+            const float us = tail_cost(rounds - fold, R, c, nkb, P, C);
+            if (us < best) { best = us; best_dp = dp; best_c = c; }
+        }
+    }
+    *dp_tiles = best_dp;
+    *pieces = best_c;
+}
+
+/* Floats of the tail schedule's slots and ints of its counters. */
+extern "C" size_t sera_mmq_tail_slot_floats(int M, int N, int dp_tiles, int pieces) {
+    const int R = sera_mmq_tiles(M, N) - dp_tiles;
+    return pieces > 1 && R > 0 ? (size_t)R * pieces * sera_mmq_slot_floats(M) : 0;
+}
+
+template <int TT, int WGT, int WGN, int WPE, int PR = 0>
+static hipError_t launch_mmq_tail_cfg(int tiled, const uint8_t *W, const int8_t *xq, const uint32_t *xds, float *y,
+                                      float *slots, int *counters, int M, int N, int K, int dp_tiles, int pieces,
+                                      int accum, hipStream_t s) {
+    const int T = sera_mmq_tiles(M, N);
+    const int grid = dp_tiles + (T - dp_tiles) * pieces;
+    hipLaunchKernelGGL((sera_q4k_mmq_tail_kernel<TT, WGT, WGN, WPE, PR>), dim3(grid), dim3(256), 0, s, W, xq, xds, y,
+                       slots, counters, M, N, K, dp_tiles, pieces, accum, tiled);
+    return hipGetLastError();
+}
+
+/* Tail-scheduled MMQ: dp_tiles whole tiles (0..tiles), the rest in `pieces`
+ * K ranges (1..K/256). slots: sera_mmq_tail_slot_floats() floats; counters:
+ * tiles - dp_tiles ints, zero on entry and zero again on exit. */
+extern "C" hipError_t sera_launch_q4k_mmq_tail_acc(uint32_t qtype, const void *W, const void *stage, float *y,
+                                                   float *slots, int *counters, int M, int N, int K, int dp_tiles,
+                                                   int pieces, int accum, hipStream_t s) {
+    const int tiled = qtype == SERA_QTYPE_Q4K_TILED;
+    if ((!tiled && qtype != 12u) || (tiled && N % Q4K_TILE_ROWS)) return hipErrorInvalidValue;
+    const int T = sera_mmq_tiles(M, N);
+    if (dp_tiles < 0 || dp_tiles > T || pieces < 1 || pieces > K / Q4K_QK) return hipErrorInvalidValue;
+    const int Mpad = sera_mmq_padded_rows(M);
+    const sera_stage_layout L = sera_mmq_stage_layout((size_t)Mpad, (size_t)K);
+    const char *base = (const char *)stage;
+    const int8_t *xq = (const int8_t *)(base + L.qs);
+    const uint32_t *xds = (const uint32_t *)(base + L.ds);
+    const uint8_t *w = (const uint8_t *)W;
+    if (sera_mmq_bm(M) == 16)
+        return launch_mmq_tail_cfg<1, 1, 4, 2, 1>(tiled, w, xq, xds, y, slots, counters, M, N, K, dp_tiles, pieces,
+                                                   accum, s);
+    if (sera_mmq_bm(M) == 32)
+        return launch_mmq_tail_cfg<1, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, dp_tiles, pieces,
+                                                accum, s);
+    return launch_mmq_tail_cfg<2, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, dp_tiles, pieces, accum,
+                                            s);
 }

@@ -56,6 +56,11 @@ hipError_t sera_launch_q4k_mmq_streamk(uint32_t qtype, const void *W, const void
                                        int *counters, int M, int N, int K, int P, hipStream_t s);
 hipError_t sera_launch_q4k_mmq_streamk_acc(uint32_t qtype, const void *W, const void *stage, float *y, float *slots,
                                            int *counters, int M, int N, int K, int P, int accum, hipStream_t s);
+void sera_mmq_tail_plan(int M, int N, int K, int cus, size_t max_slot_floats, int *dp_tiles, int *pieces);
+size_t sera_mmq_tail_slot_floats(int M, int N, int dp_tiles, int pieces);
+hipError_t sera_launch_q4k_mmq_tail_acc(uint32_t qtype, const void *W, const void *stage, float *y, float *slots,
+                                        int *counters, int M, int N, int K, int dp_tiles, int pieces, int accum,
+                                        hipStream_t s);
 
 /* ---- q4k_fewtok.hip: few-token MFMA kernel ----------------------------- */
 void sera_fewtok_plan(int M, int N, int K, int *nwave, int *chunk);

@@ -67,6 +67,7 @@ hipError_t launch_stream_read(const void *p, size_t bytes, int lpt, uint32_t *si
     const size_t per = (size_t)256 * lpt;
     const dim3 grid((unsigned)((n16 + per - 1) / per));
     switch (lpt) {
+        case 1: hipLaunchKernelGGL(sera_stream_read_kernel<1>, grid, dim3(256), 0, s, (const uint4 *)p, n16, sink); break;
         case 2: hipLaunchKernelGGL(sera_stream_read_kernel<2>, grid, dim3(256), 0, s, (const uint4 *)p, n16, sink); break;
         case 4: hipLaunchKernelGGL(sera_stream_read_kernel<4>, grid, dim3(256), 0, s, (const uint4 *)p, n16, sink); break;
         case 8: hipLaunchKernelGGL(sera_stream_read_kernel<8>, grid, dim3(256), 0, s, (const uint4 *)p, n16, sink); break;
@@ -87,8 +88,10 @@ hipError_t launch_stream_read(const void *p, size_t bytes, int lpt, uint32_t *si
  * (MMQ formula) (param = chunk, 0 = planned; partial = split slots followed
  * by the zeroed row-group counters). path | 256: the Q4_K paths (0, 1, 4,
  * 8, 12, 13) on weights in the tiled layout (SERA_QTYPE_Q4K_TILED).
+ * Path 15: MMQ under the tail schedule (param = dp_tiles * 64 + pieces;
+ * partial = slots followed by the zeroed counters).
  * Path 14: the plain streaming read of each weight copy's N*K/256*144 bytes
- * (param = 16-byte loads per thread: 2, 4, 8 or 16; y receives nothing but
+ * (param = 16-byte loads per thread: 1, 2, 4, 8 or 16; y receives nothing but
  * must be 1 KB of device memory).
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
@@ -124,6 +127,12 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
             case 13: return sera_launch_q4k_fewtok_acc(
                          q4, path - 12, w, stage, y, partial,
                          (int *)(partial + (size_t)sera_fewtok_splits(M, N, K, param) * M * N), M, N, K, param, 0, s);
+            case 15: {
+                const int dp = param / 64, pc = param % 64;
+                return sera_launch_q4k_mmq_tail_acc(
+                    q4, w, stage, y, partial, (int *)(partial + sera_mmq_tail_slot_floats(M, N, dp, pc)), M, N, K,
+                    dp, pc, 0, s);
+            }
             case 14: return launch_stream_read(w, (size_t)N * (K / Q4K_QK) * Q4K_BLOCK_BYTES, param, (uint32_t *)y, s);
             case 4: return sera_launch_q4k_mmq_streamk(
                         q4, w, stage, y, partial, (int *)(partial + (size_t)2 * param * sera_mmq_slot_floats(M)),

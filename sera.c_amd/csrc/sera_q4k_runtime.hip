@@ -409,6 +409,61 @@ bool streamk_rule(int M, int N, int K) {
     return tiles >= P && tiles < 4 * P && tiles <= kFewtokCounterBase && (int64_t)tiles * (K / Q4K_QK) >= P;
 }
 bool use_streamk(int M, int N, int K) { return g_counters && streamk_rule(M, N, K); }
+
+/* The tail schedule (whole tiles, then the last round's tiles cut along K)
+ * serves the 64-token tile (M > 32) from more than P/8 tiles (P = 2 * CUs
+ * resident workgroups); below that the fitted split-K with its reduce
+ * launch was faster on every measured shape (k/v at 256-1024 tokens, q at
+ * 96-128: split-K 22.7-30.3 us against the best tail 24.1-34.3; from 80
+ * tiles the tail won: o at 256 tokens 50.6 against 54.4, gate/up at 64
+ * 44.1 against 48.8, at 512 215.9 against 232.9, down at 512 206.5 against
+ * 217.9). Its counters share the stream-K half of the counter region (the
+ * two never run at once; both leave it zero). */
+bool tail_rule(int M, int N) {
+    return g_cus > 0 && sera_mmq_bm(M) == 64 && sera_mmq_tiles(M, N) * 8 > 2 * g_cus;
+}
+
+struct MmqPlan {
+    int kind;        /* 0 split-K (splits), 1 stream-K, 2 tail (dp_tiles, pieces) */
+    int splits, dp_tiles, pieces;
+    size_t partial_floats;
+};
+
+/* The MMQ schedule for M x N x K with cap floats of partial/slot scratch. */
+MmqPlan mmq_plan(int M, int N, int K, size_t cap, bool have_counters) {
+    MmqPlan p = {0, 1, 0, 1, 0};
+    if (have_counters && tail_rule(M, N)) {
+        sera_mmq_tail_plan(M, N, K, g_cus, cap, &p.dp_tiles, &p.pieces);
+        const int R = sera_mmq_tiles(M, N) - p.dp_tiles;
+        if (p.pieces == 1 || R <= kFewtokCounterBase) {
+            p.kind = 2;
+            p.partial_floats = sera_mmq_tail_slot_floats(M, N, p.dp_tiles, p.pieces);
+            return p;
+        }
+    }
+    const size_t slot_floats = (size_t)2 * streamk_wgs(M) * sera_mmq_slot_floats(M);
+    if (have_counters && streamk_rule(M, N, K) && slot_floats <= cap) {
+        p.kind = 1;
+        p.partial_floats = slot_floats;
+        return p;
+    }
+    int sp = ((size_t)M * N) % 4 == 0 ? sera_mmq_splits(M, N, K) : 1;
+    if ((size_t)sp * M * N > cap) sp = 1;
+    p.splits = sp;
+    p.partial_floats = sp > 1 ? (size_t)sp * M * N : 0;
+    return p;
+}
+
+hipError_t mmq_launch(const MmqPlan &p, uint32_t qt, const void *W, const void *stage, float *Y, float *partial,
+                      int M, int N, int K, int accum, hipStream_t s) {
+    if (p.kind == 2)
+        return sera_launch_q4k_mmq_tail_acc(qt, W, stage, Y, partial, g_counters, M, N, K, p.dp_tiles, p.pieces,
+                                            accum, s);
+    if (p.kind == 1)
+        return sera_launch_q4k_mmq_streamk_acc(qt, W, stage, Y, partial, g_counters, M, N, K, streamk_wgs(M), accum,
+                                               s);
+    return sera_launch_q4k_mmq_acc(qt, W, stage, Y, partial, M, N, K, p.splits, accum, s);
+}
 }  // namespace
 
 
@@ -490,24 +545,17 @@ extern "C" int sera_q4k_dense_qt(uint32_t qtype, const void *W, const float *X, 
         if (timed) record(g_ev.kernel_end, s);
         return 0;
     }
-    const size_t slot_bytes = (size_t)2 * streamk_wgs(M) * sera_mmq_slot_floats(M) * sizeof(float);
-    const bool sk = use_streamk(M, N, K) && stage_bytes + slot_bytes <= g_arena_bytes;
-    int splits = sk ? 1 : sera_mmq_splits(M, N, K);
-    if (((size_t)M * N) % 4 != 0) splits = 1;
-    const size_t partial_bytes = sk ? slot_bytes : splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
-    if (stage_bytes + partial_bytes > g_arena_bytes)
-        return fail(-1, "sera_q4k_dense: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
-                    g_arena_bytes);
+    if (stage_bytes > g_arena_bytes)
+        return fail(-1, "sera_q4k_dense: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
+    const MmqPlan plan = mmq_plan(M, N, K, (g_arena_bytes - stage_bytes) / sizeof(float), g_counters != nullptr);
     void *stage = g_arena;
-    float *partial = partial_bytes ? (float *)(g_arena + stage_bytes) : nullptr;
+    float *partial = plan.partial_floats ? (float *)(g_arena + stage_bytes) : nullptr;
     if (timed) record(g_ev.quant_begin, s);
     if (sera_launch_q8_1_mmq(X, M, Mpad, K, stage, s) != hipSuccess)
         return fail(-2, "sera_q4k_dense: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    const hipError_t e = sk ? sera_launch_q4k_mmq_streamk(qtype, W, stage, Y, partial, g_counters, M, N, K,
-                                                          streamk_wgs(M), s)
-                            : sera_launch_q4k_mmq(qtype, W, stage, Y, partial, M, N, K, splits, s);
+    const hipError_t e = mmq_launch(plan, qtype, W, stage, Y, partial, M, N, K, 0, s);
     if (e != hipSuccess) return fail(-3, "sera_q4k_dense: mmq launch failed");
     if (timed) record(g_ev.kernel_end, s);
     return 0;
@@ -517,7 +565,44 @@ extern "C" int sera_q4k_mmq_streamk_wgs(int M) { return M > 0 ? streamk_wgs(M) :
 
 extern "C" int sera_q4k_mmq_schedule(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return -1;
+    if (tail_rule(M, N)) return 2;
     return streamk_rule(M, N, K) ? 1 : 0;
+}
+
+extern "C" int sera_q4k_mmq_tail_plan(int M, int N, int K, size_t max_slot_floats, int *dp_tiles, int *pieces) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK || !dp_tiles || !pieces)
+        return fail(-1, "sera_q4k_mmq_tail_plan: bad arguments");
+    if (g_cus <= 0) return fail(-1, "sera_q4k_mmq_tail_plan: not initialised (the CU count is unknown)");
+    if (max_slot_floats == 0) {
+        /* what sera_q4k_dense would use: the attached arena after the stage */
+        const size_t stage = sera_mmq_stage_layout((size_t)sera_mmq_padded_rows(M), (size_t)K).total;
+        max_slot_floats = g_arena && g_arena_bytes > stage ? (g_arena_bytes - stage) / sizeof(float) : 0;
+    }
+    sera_mmq_tail_plan(M, N, K, g_cus, max_slot_floats, dp_tiles, pieces);
+    return 0;
+}
+
+extern "C" size_t sera_q4k_mmq_tail_slot_floats(int M, int N, int dp_tiles, int pieces) {
+    if (M <= 0 || N <= 0) return 0;
+    return sera_mmq_tail_slot_floats(M, N, dp_tiles, pieces);
+}
+
+extern "C" int sera_q4k_mmq_tail_qt(uint32_t qtype, const void *W, const void *mmq_stage, float *Y, float *slots,
+                                    int *counters, int M, int N, int K, int dp_tiles, int pieces, int accum,
+                                    void *stream) {
+    const char *tag = "sera_q4k_mmq_tail";
+    if (!W || !mmq_stage || !Y) return fail(-1, "%s: null pointer", tag);
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "%s: bad shape M=%d N=%d K=%d", tag, M, N, K);
+    if (!stage_ok(tag, M, K)) return -1;
+    const int T = sera_mmq_tiles(M, N);
+    if (dp_tiles < 0 || dp_tiles > T) return fail(-1, "%s: dp_tiles=%d outside 0..%d", tag, dp_tiles, T);
+    if (pieces < 1 || pieces > K / Q4K_QK) return fail(-1, "%s: pieces=%d outside 1..K/256", tag, pieces);
+    if (pieces > 1 && dp_tiles < T && (!slots || !counters))
+        return fail(-1, "%s: a split tail needs slots and counters", tag);
+    if (!q4k_layout_ok(tag, qtype, N)) return -1;
+    return sera_launch_q4k_mmq_tail_acc(qtype, W, mmq_stage, Y, slots, counters, M, N, K, dp_tiles, pieces,
+                                        accum ? 1 : 0, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "%s: launch failed", tag);
 }
 
 extern "C" int sera_q4k_mmq_streamk(const void *W, const void *mmq_stage, float *Y, float *slots, int *counters,
@@ -548,6 +633,7 @@ extern "C" int sera_q4k_mmq_slot_floats(int M) { return M > 0 ? sera_mmq_slot_fl
 extern "C" int sera_q4k_kernel_launches(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
     if (sera_q4k_mmq_uses_fewtok(M, N, K)) return 2;   /* the few-token kernel sums split K inside */
+    if (g_counters && tail_rule(M, N)) return 2;
     if (use_streamk(M, N, K)) return 2;
     return sera_mmq_splits(M, N, K) > 1 && ((size_t)M * N) % 4 == 0 ? 3 : 2;
 }
@@ -1049,15 +1135,8 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
             if (rc) return rc;
             continue;
         } else if (q4) {
-            const size_t slot_floats = (size_t)2 * streamk_wgs(M) * sera_mmq_slot_floats(M);
-            if (use_streamk(M, n, K) && slot_floats <= partial_cap) {
-                e = sera_launch_q4k_mmq_streamk_acc(qt, weights[i], g_arena, outputs[i], partial, g_counters, M, n,
-                                                    K, streamk_wgs(M), accum, s);
-            } else {
-                int sp = mn4 ? sera_mmq_splits(M, n, K) : 1;
-                if ((size_t)sp * M * n > partial_cap) sp = 1;
-                e = sera_launch_q4k_mmq_acc(qt, weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
-            }
+            const MmqPlan plan = mmq_plan(M, n, K, partial_cap, g_counters != nullptr);
+            e = mmq_launch(plan, qt, weights[i], g_arena, outputs[i], partial, M, n, K, accum, s);
         } else if (!q6_tile) {
             e = sera_launch_q6k_mmvq_acc(qt, weights[i], g_arena, outputs[i], M, n, K, 0, accum, s);
         } else {

@@ -119,6 +119,9 @@ def load():
         "sera_q4k_mmq_streamk": ([P, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_streamk_wgs": ([I], I),
         "sera_q4k_mmq_schedule": ([I, I, I], I),
+        "sera_q4k_mmq_tail_qt": ([U32, P, P, P, P, P, I, I, I, I, I, I, P], I),
+        "sera_q4k_mmq_tail_plan": ([I, I, I, SZ, ctypes.POINTER(I), ctypes.POINTER(I)], I),
+        "sera_q4k_mmq_tail_slot_floats": ([I, I, I, I], SZ),
         "sera_q4k_mmq_uses_fewtok": ([I, I, I], I),
         "sera_q4k_mmq_tiles": ([I, I], I),
         "sera_q4k_mmq_slot_floats": ([I], I),
@@ -287,6 +290,28 @@ def mmq_streamk(W, stage, out, M, N, K, slots, counters, wgs=0, stream=None, qty
     must be zero and are zero again afterwards."""
     _check(load().sera_q4k_mmq_streamk_qt(qtype, _ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M,
                                           N, K, wgs, _stream(stream)), "sera_q4k_mmq_streamk")
+
+
+def mmq_tail(W, stage, out, M, N, K, dp_tiles, pieces, slots=None, counters=None, accum=False, stream=None,
+             qtype=QTYPE_Q4_K):
+    """MMQ under the tail schedule: dp_tiles whole tiles, the rest cut into
+    `pieces` K ranges; slots (mmq_tail_slot_floats float32) and counters
+    (tiles - dp_tiles int32, zero before and after) when a tail is split."""
+    _check(load().sera_q4k_mmq_tail_qt(qtype, _ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N,
+                                       K, dp_tiles, pieces, 1 if accum else 0, _stream(stream)), "sera_q4k_mmq_tail")
+
+
+def mmq_tail_plan(M, N, K, max_slot_floats=0):
+    """(dp_tiles, pieces) of the tail schedule on the current device (after
+    init); max_slot_floats 0: the attached arena's room, as the boundary."""
+    dp, pc = ctypes.c_int(), ctypes.c_int()
+    _check(load().sera_q4k_mmq_tail_plan(M, N, K, max_slot_floats, ctypes.byref(dp), ctypes.byref(pc)),
+           "sera_q4k_mmq_tail_plan")
+    return dp.value, pc.value
+
+
+def mmq_tail_slot_floats(M, N, dp_tiles, pieces):
+    return load().sera_q4k_mmq_tail_slot_floats(M, N, dp_tiles, pieces)
 
 
 def fewtok(W, stage, out, M, N, K, chunk=0, slots=None, counters=None, accum=False, form=0, stream=None,

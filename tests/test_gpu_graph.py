@@ -68,7 +68,7 @@ def kernel_of(qtype, M, N, K):
             return "fewtok" if L.sera_q4k_vec_uses_fewtok_qt(qtype, M, N, K) else "dot4"
         if L.sera_q4k_mmq_uses_fewtok(M, N, K):
             return "fewtok-mmq"
-        return "mmq-streamk" if L.sera_q4k_mmq_schedule(M, N, K) == 1 else "mmq"
+        return {1: "mmq-streamk", 2: "mmq-tail"}.get(L.sera_q4k_mmq_schedule(M, N, K), "mmq")
     return "q6k-tile" if M > 8 or L.sera_q6k_vec_uses_tile(M, N, K) else "q6k-mmvq"
 
 
@@ -76,7 +76,8 @@ def kernel_of(qtype, M, N, K):
 # split K on the row stage (form 0: a 4096-row matrix from 5 tokens, a tall
 # one from 3) and on the MMQ stage (form 1, 9 tokens); the paired MMQ tile
 # with split-K + reduce; stream-K (32-token tiles over a 131328-row matrix);
-# the 64-token tile with split-K + reduce;
+# the 64-token tile with split-K + reduce and under the tail schedule (whole
+# tiles, then split tiles handed off through counters);
 # Q6_K MMVQ and the Q6_K tile kernel on the row-formula stage; the few-token
 # kernel's persistent grid (more 16-row tiles than resident workgroups); the
 # same kernels on Q4_K weights in the tiled layout (268), where the few-token
@@ -91,6 +92,8 @@ CASES = [
     (12, 20, 131328, 256, "mmq-streamk"),
     (12, 64, 16384, 2048, "mmq"),
     (12, 100, 4096, 5120, "mmq"),
+    (12, 200, 25600, 2048, "mmq-tail"),
+    (12, 600, 25600, 1024, "mmq-tail"),
     (14, 1, 2048, 5120, "q6k-mmvq"),
     (14, 8, 2048, 5120, "q6k-mmvq"),
     (14, 8, 4096, 5120, "q6k-tile"),
@@ -99,6 +102,7 @@ CASES = [
     (268, 2, 16384, 5120, "fewtok"),
     (268, 20, 131328, 256, "mmq-streamk"),
     (268, 64, 16384, 2048, "mmq"),
+    (268, 200, 25600, 2048, "mmq-tail"),
     (268, 16, 70000, 512, "fewtok-mmq-persistent"),
 ]
 
