@@ -55,7 +55,8 @@ typedef __attribute__((address_space(1))) const void ft_global_cvoid;
 
 #define SERA_FEWTOK_MAX_TOKENS 16
 #define SERA_FEWTOK_LDS_CHUNK_TOKENS 320   /* chunk x staged tokens: 40 super-blocks of 8, 20 of 16 */
-#define SERA_FEWTOK_XROW (Q4K_QK + 16)     /* LDS bytes per staged token and super-block: 16 columns + a pad */
+#define SERA_FEWTOK_XROW (Q4K_QK + 32)     /* LDS bytes per staged token and super-block: 16 columns + 2 pads */
+#define SERA_FEWTOK_XSLOTS (SERA_FEWTOK_XROW / 16)
 /* waves per workgroup of a persistent grid (one workgroup per CU: 2 waves
  * per SIMD); 12 waves for one token group, 3 per SIMD, measured 8% slower
  * on the LM head */
@@ -63,16 +64,31 @@ template <int TG> constexpr int fewtok_persist_waves() { return 8; }
 
 /* Zero bytes read by the lanes whose MFMA operand is zero: they address
  * the zero area with the same immediate offsets as the real lanes (up to
- * one token group of rows and 160 bytes of columns, plus 16). */
-static constexpr __host__ __device__ int fewtok_zero_bytes(int tok) { return (tok / 8 - 1) * 8 * SERA_FEWTOK_XROW + 176; }
+ * one token group of rows and 160 bytes of columns, plus 16), from one of
+ * two bases 16 bytes apart. */
+static constexpr __host__ __device__ int fewtok_zero_bytes(int tok) { return (tok / 8 - 1) * 8 * SERA_FEWTOK_XROW + 192; }
 
-/* LDS byte offset of the zero area: after the scale factors, moved up to
- * 224 mod 256. A 16-byte read of 8 real lanes covers 32 consecutive banks
- * starting at 32 j + 8 h + {0, 4, 16, 20} (mod 64, 4-byte banks); the zero
- * lanes of the same 16 read 4 banks at 56 + 32 j + 8 h, outside all four. */
+/* LDS byte offset of the zero area: after the scale factors, at 0 mod 256.
+ *
+ * Bank conflicts of the A reads (64 banks of 4 bytes). gfx950 serves a
+ * 16-byte LDS read in four passes of 16 lanes: within each half wave, the
+ * lane quads (lane >> 2 & 7) of even bit count {0, 3, 5, 6} form one pass
+ * and {1, 2, 4, 7} the other (measured with SQ_LDS_BANK_CONFLICT on lane
+ * pairs). In a pass, two lanes reading different addresses in one bank
+ * cost a cycle; lanes reading one address share it. The 288-byte token
+ * rows shift a token's bank by 8 and a column by 4, so a pass's 8 real
+ * lanes (tokens 0-3 on one column and 4-7 on another, the columns 1 apart
+ * or, past the first column pair, 4 apart) read 8 disjoint 4-bank runs,
+ * e.g. starts {0,8,16,24,36,44,52,60} for quads {0, 3, 5, 6}. Relative to
+ * the zero area, every even-quad pass leaves banks 4-7 free and every
+ * odd-quad pass banks 0-3 (super-block, token group and column offsets
+ * move every lane alike: multiples of 256 bytes or common immediates), so
+ * the zero lanes of an even-quad pass read at zero + 16 and the others at
+ * zero + 0, one address per pass. (With 272-byte rows two reads per
+ * instruction conflicted.) */
 static inline __host__ __device__ int fewtok_zero_offset(int chunk, int tok) {
     const int end = chunk * tok * (SERA_FEWTOK_XROW + 2 * 8 * (int)sizeof(float));
-    return end + ((224 - end) & 255);
+    return (end + 255) & ~255;
 }
 
 /* LDS bytes of a workgroup for `chunk` super-blocks of `tok` staged tokens:
@@ -112,7 +128,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     const int nkb = K / Q4K_QK;
     const int kb0 = blockIdx.y * chunk;
     const int C = min(nkb - kb0, chunk);
-    /* LDS: quants [u][t][272] | d8 [u][b][t] | min factor [u][mslot(b)][t] | zero */
+    /* LDS: quants [u][t][288] | d8 [u][b][t] | min factor [u][mslot(b)][t] | zero */
     int8_t *xs = (int8_t *)ft_smem;
     float *d8s = (float *)(ft_smem + (size_t)chunk * TOK * SERA_FEWTOK_XROW);
     float *mns = d8s + (size_t)chunk * 8 * TOK;
@@ -165,17 +181,18 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
 
     /* --- stage the chunk's activations --- */
     {
-        /* quants: 16-byte slot s of token row (u, t) holds column s (slot
-         * 16 is the row's pad, filled with a copy of column 15 and never
+        /* quants: 16-byte slot s of token row (u, t) holds column s (slots
+         * 16-17 are the row's pad, filled with copies of column 15 and never
          * read); one wave-instruction writes 64 consecutive slots (1 KB),
          * lanes past the chunk are masked off; tokens past M copy the last.
-         * The 272-byte rows put 8 consecutive tokens' reads of one column on
-         * distinct banks, and every operand of a lane sits at a constant
-         * offset from one base. */
-        const int slots = C * TOK * 17;
+         * The 288-byte rows keep the A reads free of bank conflicts (at the
+         * zero area's offset), and every operand of a lane sits at a
+         * constant offset from one base. */
+        constexpr int XS = SERA_FEWTOK_XSLOTS;
+        const int slots = C * TOK * XS;
         for (int base = wave * 64; base < slots; base += NW * 64) {
             const int q = base + lane;
-            const int u = q / (TOK * 17), r = q - u * (TOK * 17), t = r / 17, col = min(r - t * 17, 15);
+            const int u = q / (TOK * XS), r = q - u * (TOK * XS), t = r / XS, col = min(r - t * XS, 15);
             const int8_t *src = xq + (size_t)min(t, M - 1) * K + (size_t)(kb0 + u) * Q4K_QK + 16 * col;
             if (q < slots)
                 __builtin_amdgcn_global_load_lds((ft_global_cvoid *)src, (ft_lds_void *)(xs + (size_t)base * 16), 16, 0,
@@ -234,13 +251,15 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
      * k-half hq, i.e. column 2 (4j + 2 (i >> 3) + h) + hq of the token row.
      * Every (tg, j, h) is a constant offset from the lane's base for super-
      * block u, a_base + u * a_step; the other lanes have step 0 and a base
-     * in the zero area, so they read zeros at the same offsets. Staged
+     * in the zero area (16 bytes up for the lane quads of even bit count,
+     * see fewtok_zero_offset), so they read zeros at the same offsets. Staged
      * tokens past M hold copies of the last token; their results are never
      * stored. The min-term A (FORM 0 d8*S, FORM 1 the fp16 sum of x) works
      * the same way: lanes n < 8 read token 8 tg + n of sub-blocks g, 4 + g. */
     const bool a_real = (n < 8) == (g < 2);
     const int zoff = (int)(zero - (uint8_t *)ft_smem);
-    const int a_base = a_real ? (n & 7) * SERA_FEWTOK_XROW + 16 * (4 * (n >> 3) + hq) : zoff;
+    const int a_base = a_real ? (n & 7) * SERA_FEWTOK_XROW + 16 * (4 * (n >> 3) + hq)
+                              : zoff + 16 * (1 - (__builtin_popcount((lane >> 2) & 7) & 1));
     const int a_step = a_real ? TOK * SERA_FEWTOK_XROW : 0;
     const int m_base = n < 8 ? (int)((uint8_t *)mns - (uint8_t *)ft_smem) + 4 * (2 * g * TOK + n) : zoff;
     const int m_step = n < 8 ? 4 * 8 * TOK : 0;
