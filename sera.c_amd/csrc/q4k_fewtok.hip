@@ -97,6 +97,29 @@ static inline __host__ __device__ size_t fewtok_lds_bytes(int chunk, int tok) {
     return (size_t)fewtok_zero_offset(chunk, tok) + fewtok_zero_bytes(tok);
 }
 
+/* s_waitcnt operands (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+ * 6:4, lgkmcnt 11:8; a field at its maximum is not waited on) */
+#define SERA_WAITCNT_LGKM0 0xC07F
+#define SERA_WAITCNT_VM0 0x0F70
+static constexpr int sera_waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+/* Staged weights (WS > 0 super-blocks per copy): each wave copies its 16
+ * rows' next WS super-blocks into one of two LDS buffers with 16-byte loads
+ * to LDS, all issued at once, while it computes from the other. On GGUF
+ * bytes a copy reads 16 runs of WS * 144 bytes (one per row) instead of the
+ * 16 x 64-byte pieces per instruction of the direct loads. Loads-only
+ * kernels measured that order 14-16% faster with 2-4 super-blocks per copy
+ * and 2-3 workgroups per CU (gate/up, 74 MB: 13.3-14.0 against 15.8 us);
+ * in this kernel the staged activations leave LDS for one copy in flight
+ * per wave, and the gain is 4% (the launcher). A buffer holds row n's WS
+ * blocks at 16 n * RS bytes: an odd slot count per row puts the 16 rows'
+ * headers on 16 distinct 4-bank groups. */
+template <int WS> struct FewtokWs {
+    static constexpr int RS = 9 * WS + ((9 * WS) % 2 == 0 ? 1 : 2);   /* 16-byte slots per row */
+    static constexpr int NI = (16 * RS + 63) / 64;                     /* copy instructions */
+    static constexpr int BUF = NI * 1024;                              /* LDS bytes of one buffer */
+};
+
 /* Row of sub-block b in the min-term factors [u][row][token]: sub-blocks g
  * and 4 + g, which one lane reads together, sit in adjacent rows (one
  * token row apart, so the pair never shares a bank). */
@@ -111,7 +134,7 @@ struct FewtokW {
  * (dsf: d8, d8*S as fp32); FORM 1: MMQ formula on an MMQ stage (ds: fp16
  * d8, fp16 sum of x), cuda/mmq/mmq.cuh:2269-2283,1440-1472:
  *   y = sum_b fp16(d*sc_b) * d8_b * I_b + fp16(-dmin*m_b) * s8_b */
-template <int NW, int TG, int FORM, bool PERSIST>
+template <int NW, int TG, int FORM, bool PERSIST, int WS = 0>
 __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         const uint8_t *__restrict__ W, const int8_t *__restrict__ xq, const void *__restrict__ xsc,
         float *__restrict__ y, float *__restrict__ slots, int *__restrict__ counters, int M, int N, int K,
@@ -121,7 +144,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     __shared__ int s_last;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   /* wave-uniform: LDS copy targets need no waterfall */
     const int n = lane & 15;          /* B column (weight row), A row */
     const int g = lane >> 4;          /* 16-wide K group */
     const int hq = g & 1;
@@ -176,7 +199,52 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     };
     auto load = [&](int u, FewtokW &w) { load_from(wr, u, w); };
     FewtokW wa, wb;
-    if (tile < te) load(0, wa);    /* in flight during the activation staging */
+    /* WS: the wave's two weight buffers after the staged activations, and
+     * the copy of sub-chunk sc (super-blocks WS sc .. WS sc + WS - 1 of the
+     * chunk, clamped to the chunk: a partial last copy re-reads its last
+     * super-block) into buffer bf. Slot q = 64 i + lane of the buffer is
+     * piece q % RS of row q / RS (pieces past the row's 9 WS, the pad, and
+     * slots past row 15 copy a valid piece and are never read). */
+    using Ws = FewtokWs<WS ? WS : 1>;
+    uint8_t *wbuf = ft_smem + fewtok_lds_bytes(chunk, TOK) + (size_t)wave * 2 * Ws::BUF;
+    /* per copy instruction i: the lane's source in the chunk's first
+     * sub-chunk and its super-block there */
+    const uint8_t *wsp[WS ? Ws::NI : 1];
+    int wsu[WS ? Ws::NI : 1];
+    if constexpr (WS > 0) {
+#pragma unroll
+        for (int i = 0; i < Ws::NI; i++) {
+            const int q = 64 * i + lane;
+            const int r = min(q / Ws::RS, 15), o = min(q - (q / Ws::RS) * Ws::RS, 9 * WS - 1);
+            wsu[i] = o / 9;
+            wsp[i] = W + q4k_block_offset(tiled, min(16 * tile + r, N - 1), kb0 + min(wsu[i], C - 1), nkb) +
+                     16 * (o - 9 * wsu[i]);
+        }
+    }
+    auto ws_issue = [&](int sc, int bf) {
+        const bool whole = WS * sc + WS <= C;
+#pragma unroll
+        for (int i = 0; i < Ws::NI; i++) {
+            /* a whole sub-chunk moves every lane alike; the last one clamps */
+            const int du = whole ? WS * sc : min(WS * sc + wsu[i], C - 1) - min(wsu[i], C - 1);
+            __builtin_amdgcn_global_load_lds((ft_global_cvoid *)(wsp[i] + (size_t)du * bstride),
+                                             (ft_lds_void *)(wbuf + bf * Ws::BUF + 1024 * i), 16, 0, 0);
+        }
+    };
+    /* super-block ul of the sub-chunk in buffer bf, in the layout load() gives */
+    auto ws_read = [&](int bf, int ul, FewtokW &w) {
+        const uint8_t *b = wbuf + bf * Ws::BUF + n * (16 * Ws::RS) + ul * Q4K_BLOCK_BYTES;
+        w.hd = *(const ft_v4u *)b;
+        w.q[0] = *(const ft_v4u *)(b + 16 + 16 * g);
+        w.q[1] = *(const ft_v4u *)(b + 80 + 16 * g);
+    };
+    const int nsub = WS ? (C + WS - 1) / WS : 0;
+    if constexpr (WS > 0) {
+        ws_issue(0, 0);                /* in flight during the activation staging */
+        if (nsub > 1) ws_issue(1, 1);
+    } else {
+        if (tile < te) load(0, wa);    /* in flight during the activation staging */
+    }
     if (PERSIST && tid == 0) s_next = 0;
 
     /* --- stage the chunk's activations --- */
@@ -438,7 +506,35 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
      * each compute): 4-6% faster at 4-8 tokens (gate/up 19.6 -> 18.5 us,
      * down 25.3 -> 23.9), equal at 16; deeper prefetch, in groups of 2-5
      * super-blocks or only before the staging, was slower at every size. */
-    if constexpr (!PERSIST) {
+    if constexpr (WS > 0) {
+        static_assert(!PERSIST, "staged weights serve one tile per wave");
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) acc[tg] = (ft_v4f){0.f, 0.f, 0.f, 0.f};
+        /* the barrier above waited for sub-chunks 0 and 1 */
+        for (int sc = 0; sc < nsub; sc++) {
+            const int bf = sc & 1;
+            const int nu = min(WS, C - WS * sc);
+#pragma unroll
+            for (int ul = 0; ul < WS; ul++) {
+                if (ul < nu) {
+                    ws_read(bf, ul, wa);
+                    compute(WS * sc + ul, wa);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (sc + 2 < nsub) {
+                /* buffer bf is free once its LDS reads have returned; then
+                 * sub-chunk sc + 1 (issued before this copy) is waited for */
+                __builtin_amdgcn_s_waitcnt(SERA_WAITCNT_LGKM0);
+                ws_issue(sc + 2, bf);
+                __builtin_amdgcn_s_waitcnt(sera_waitcnt_vm(Ws::NI));
+            } else {
+                __builtin_amdgcn_s_waitcnt(SERA_WAITCNT_VM0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        finish();
+    } else if constexpr (!PERSIST) {
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) acc[tg] = (ft_v4f){0.f, 0.f, 0.f, 0.f};
         int u0 = 0;
@@ -656,14 +752,44 @@ static void fewtok_grid(int N, int K, int chunk, bool allow_persist, int *groups
     *lds_out = lds;
 }
 
-template <int NW, int TG, int FORM, bool PERSIST>
+template <int NW, int TG, int FORM, bool PERSIST, int WS = 0>
 static hipError_t launch_fewtok(int tiled, const uint8_t *W, const int8_t *xq, const void *xsc, float *y,
                                 float *slots, int *counters, int M, int N, int K, int chunk, int accum, int groups,
                                 int out_tiles, size_t lds, hipStream_t s) {
     dim3 grid(groups, (K / Q4K_QK + chunk - 1) / chunk);
-    hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM, PERSIST>), grid, dim3(NW * 64), lds, s, W, xq, xsc, y,
-                       slots, counters, M, N, K, chunk, accum, out_tiles, tiled);
+    hipLaunchKernelGGL((sera_q4k_fewtok_kernel<NW, TG, FORM, PERSIST, WS>), grid, dim3(NW * 64), lds, s, W, xq, xsc,
+                       y, slots, counters, M, N, K, chunk, accum, out_tiles, tiled);
     return hipGetLastError();
+}
+
+/* One tile per wave. GGUF bytes in 8-wave workgroups (the matrices whose
+ * rows or K reach 16384) take the staged-weight kernel with 2-super-block
+ * copies when its buffers fit the device's LDS beside the staged
+ * activations; everything else loads straight into registers. Measured
+ * (us, staged against direct, GGUF bytes): gate/up 2-8 tokens 18.6-19.0
+ * against 19.4-19.8, down 21.8-24.4 against 22.7-25.2, 16 tokens equal;
+ * on the 4-wave shapes (q, o) 2-7 us slower, and on the tiled layout 1.6-2
+ * us slower on every shape. Copies of 3 or 4 super-blocks leave no LDS for
+ * two buffers of 8 waves at 20-block chunks; 10-block chunks (2 splits)
+ * were slower with either kernel. */
+static constexpr int kFewtokWs = 2;
+template <int NW, int TG, int FORM>
+static hipError_t launch_fewtok_tiles(int tiled, const uint8_t *W, const int8_t *xq, const void *xsc, float *y,
+                                      float *slots, int *counters, int M, int N, int K, int chunk, int accum,
+                                      hipStream_t s) {
+    int groups, out_tiles;
+    size_t lds;
+    fewtok_grid<NW, TG, FORM>(N, K, chunk, false, &groups, &out_tiles, &lds);
+    if constexpr (NW == 8) {
+        const size_t lds_ws = lds + (size_t)NW * 2 * FewtokWs<kFewtokWs>::BUF;
+        int dev = 0;
+        FewtokDevice d;
+        if (!tiled && fewtok_device(&dev, &d) && lds_ws <= (size_t)d.max_lds)
+            return launch_fewtok<NW, TG, FORM, false, kFewtokWs>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk,
+                                                                 accum, groups, 0, lds_ws, s);
+    }
+    return launch_fewtok<NW, TG, FORM, false>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups, 0,
+                                              lds, s);
 }
 
 template <int TG, int FORM>
@@ -677,14 +803,9 @@ static hipError_t launch_fewtok_nw(int nw, int tiled, const uint8_t *W, const in
     if (out_tiles > 0)
         return launch_fewtok<P, TG, FORM, true>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups,
                                                 out_tiles, lds, s);
-    if (nw == 8) {
-        fewtok_grid<8, TG, FORM>(N, K, chunk, false, &groups, &out_tiles, &lds);
-        return launch_fewtok<8, TG, FORM, false>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum,
-                                                 groups, 0, lds, s);
-    }
-    fewtok_grid<4, TG, FORM>(N, K, chunk, false, &groups, &out_tiles, &lds);
-    return launch_fewtok<4, TG, FORM, false>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, groups, 0,
-                                             lds, s);
+    if (nw == 8)
+        return launch_fewtok_tiles<8, TG, FORM>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, s);
+    return launch_fewtok_tiles<4, TG, FORM>(tiled, W, xq, xsc, y, slots, counters, M, N, K, chunk, accum, s);
 }
 
 /* y (+)= X . W^T for 1 <= M <= 16, W in the layout of qtype (12 or
