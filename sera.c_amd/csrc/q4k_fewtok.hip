@@ -68,6 +68,13 @@ template <int TG> constexpr int fewtok_persist_waves() { return 8; }
  * two bases 16 bytes apart. */
 static constexpr __host__ __device__ int fewtok_zero_bytes(int tok) { return (tok / 8 - 1) * 8 * SERA_FEWTOK_XROW + 192; }
 
+/* Floats per row of the min-term factors [u][row][token]: the tokens plus
+ * 4 per extra token group. A 4-byte LDS read is served in two passes of 32
+ * lanes over 32 banks; its real lanes (n < 8 of K groups g) read rows 2 g
+ * (+ 1) at n, so with 16 tokens the rows 0 and 2 of one pass would share
+ * banks; 20-float rows put the pass's two 8-lane runs 8 banks apart. */
+static constexpr __host__ __device__ int fewtok_mrow(int tok) { return tok + 4 * (tok / 8 - 1); }
+
 /* LDS byte offset of the zero area: after the scale factors, at 0 mod 256.
  *
  * Bank conflicts of the A reads (64 banks of 4 bytes). gfx950 serves a
@@ -87,7 +94,7 @@ static constexpr __host__ __device__ int fewtok_zero_bytes(int tok) { return (to
  * zero + 0, one address per pass. (With 272-byte rows two reads per
  * instruction conflicted.) */
 static inline __host__ __device__ int fewtok_zero_offset(int chunk, int tok) {
-    const int end = chunk * tok * (SERA_FEWTOK_XROW + 2 * 8 * (int)sizeof(float));
+    const int end = chunk * (tok * SERA_FEWTOK_XROW + 8 * (tok + fewtok_mrow(tok)) * (int)sizeof(float));
     return (end + 255) & ~255;
 }
 
@@ -155,6 +162,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     int8_t *xs = (int8_t *)ft_smem;
     float *d8s = (float *)(ft_smem + (size_t)chunk * TOK * SERA_FEWTOK_XROW);
     float *mns = d8s + (size_t)chunk * 8 * TOK;
+    constexpr int MR = fewtok_mrow(TOK);                 /* floats per min-factor row */
     uint8_t *zero = ft_smem + fewtok_zero_offset(chunk, TOK);
     /* PERSIST: results of the workgroup's tiles, [token][row], out_tiles
      * tiles of 16 rows per token */
@@ -292,19 +300,19 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             if (i < items) {
                 if (FORM == 0) {
                     const int u = i / (TOK * 4), t = (i >> 2) % TOK, p = i & 3;
-                    float *d8u = d8s + u * 8 * TOK, *mnu = mns + u * 8 * TOK;
+                    float *d8u = d8s + u * 8 * TOK, *mnu = mns + u * 8 * MR;
                     d8u[(2 * p) * TOK + t] = __uint_as_float(f[r].x);
                     d8u[(2 * p + 1) * TOK + t] = __uint_as_float(f[r].y);
-                    mnu[fewtok_mslot(2 * p) * TOK + t] = __uint_as_float(f[r].z);
-                    mnu[fewtok_mslot(2 * p + 1) * TOK + t] = __uint_as_float(f[r].w);
+                    mnu[fewtok_mslot(2 * p) * MR + t] = __uint_as_float(f[r].z);
+                    mnu[fewtok_mslot(2 * p + 1) * MR + t] = __uint_as_float(f[r].w);
                 } else {
                     const int u = i / (TOK * 2), t = (i >> 1) % TOK, p = i & 1;
-                    float *d8u = d8s + u * 8 * TOK, *mnu = mns + u * 8 * TOK;
+                    float *d8u = d8s + u * 8 * TOK, *mnu = mns + u * 8 * MR;
                     const uint32_t ds[4] = {f[r].x, f[r].y, f[r].z, f[r].w};
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         d8u[(4 * p + e) * TOK + t] = h2f_bits(ds[e] & 0xffffu);
-                        mnu[fewtok_mslot(4 * p + e) * TOK + t] = h2f_bits(ds[e] >> 16);
+                        mnu[fewtok_mslot(4 * p + e) * MR + t] = h2f_bits(ds[e] >> 16);
                     }
                 }
             }
@@ -329,8 +337,12 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     const int a_base = a_real ? (n & 7) * SERA_FEWTOK_XROW + 16 * (4 * (n >> 3) + hq)
                               : zoff + 16 * (1 - (__builtin_popcount((lane >> 2) & 7) & 1));
     const int a_step = a_real ? TOK * SERA_FEWTOK_XROW : 0;
-    const int m_base = n < 8 ? (int)((uint8_t *)mns - (uint8_t *)ft_smem) + 4 * (2 * g * TOK + n) : zoff;
-    const int m_step = n < 8 ? 4 * 8 * TOK : 0;
+    /* min-term A: zero lanes read the zero area at a bank the real lanes of
+     * their 32-lane pass leave free (8 with one token group; 16 for lanes
+     * 0-31 and 0 for 32-63 with two) */
+    const int m_zero = zoff + (TG == 1 ? 32 : lane < 32 ? 64 : 0);
+    const int m_base = n < 8 ? (int)((uint8_t *)mns - (uint8_t *)ft_smem) + 4 * (2 * g * MR + n) : m_zero;
+    const int m_step = n < 8 ? 4 * 8 * MR : 0;
     const int sg = g >> 1;            /* result sub-block: 4j + 2 sg + h */
     const int tq = 4 * hq;            /* result tokens 8 tg + tq .. + 3 */
     /* FORM 1 scale bytes as fp16 1024 + v: v_perm puts sub-block bytes
@@ -352,7 +364,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
             am0[tg] = *(const float *)(mu + 32 * tg);
-            am1[tg] = *(const float *)(mu + 4 * TOK + 32 * tg);
+            am1[tg] = *(const float *)(mu + 4 * MR + 32 * tg);
         }
 #pragma unroll
         for (int jh = 0; jh < 4; jh++)
