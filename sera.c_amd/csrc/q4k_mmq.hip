@@ -733,7 +733,21 @@ extern "C" hipError_t sera_launch_splitk_reduce(const float *partial, float *y, 
  * tokens for both the 5120 -> 25600 and the 25600 -> 5120 shapes. */
 extern "C" int sera_mmq_bm(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : 64; }
 
-static int mmq_bn(int bm) { (void)bm; return 256; }
+/* Weight rows per tile: 256, or 128 for the 64-token tile when 256-row
+ * tiles would leave at most 64 tiles (k/v at up to 1024 tokens, q and o up
+ * to 128). The 128-row tile is 4 waves of 32 tokens x 64 rows (each weight
+ * row unpacked by two waves, so it is slower on large grids: gate/up at
+ * 512 tokens 242 against 207 us, o 100 against 78) and doubles the grid of
+ * the narrow matrices (us, best schedule of each against the 256-row tile:
+ * k/v at 256 / 512 / 1024 tokens 18.8 / 24.0 / 31.4 against 23.1 / 26.9 /
+ * 32.4; q at 128 tokens 30.2 against 31.7; o at 256 tokens, 80 tiles, 55.7
+ * against 50.6). */
+static constexpr int kNarrowTileMax = 64;
+static int mmq_bn(int M, int N) {
+    const int bm = sera_mmq_bm(M);
+    if (bm == 64 && ((M + 63) / 64) * ((N + 255) / 256) <= kNarrowTileMax) return 128;
+    return 256;
+}
 
 /* Workgroups of the stream-K MMQ kernel one CU keeps resident: two for
  * either tile. The 32-token stream-K kernel is built for 2 waves per SIMD:
@@ -757,7 +771,7 @@ static constexpr int kModelCUs = 256, kMaxSplitWgs = 2048;
 
 extern "C" int sera_mmq_splits(int M, int N, int K) {
     const int bm = sera_mmq_bm(M);
-    const int bn = mmq_bn(bm);
+    const int bn = mmq_bn(M, N);
     const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int nkb = K / Q4K_QK;
     const float tile_scale = bm == 16 ? 0.5f : bm == 32 ? 0.6f : 1.0f;
@@ -817,6 +831,8 @@ extern "C" hipError_t sera_launch_q4k_mmq_acc(uint32_t qtype, const void *W, con
         return launch_mmq_cfg<1, 1, 4, 2, 1>(tiled, w, xq, xds, y, partial, M, N, K, splits, accum, s);
     if (sera_mmq_bm(M) == 32)
         return launch_mmq_cfg<1, 1, 4, 2>(tiled, w, xq, xds, y, partial, M, N, K, splits, accum, s);
+    if (mmq_bn(M, N) == 128)
+        return launch_mmq_cfg<1, 2, 2, 2>(tiled, w, xq, xds, y, partial, M, N, K, splits, accum, s);
     return launch_mmq_cfg<2, 1, 4, 2>(tiled, w, xq, xds, y, partial, M, N, K, splits, accum, s);
 }
 
@@ -825,15 +841,16 @@ extern "C" hipError_t sera_launch_q4k_mmq_acc(uint32_t qtype, const void *W, con
 /* Output tiles of the MMQ grid for M tokens. */
 extern "C" int sera_mmq_tiles(int M, int N) {
     const int bm = sera_mmq_bm(M);
-    const int bn = mmq_bn(bm);
+    const int bn = mmq_bn(M, N);
     return ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
 }
 
-/* Floats of one stream-K partial slot (a whole tile's accumulators; the
- * paired 16-token tile keeps its 32 MFMA rows). */
+/* Floats of one stream-K or tail partial slot: the largest tile's
+ * accumulators for M tokens (the paired 16-token tile keeps its 32 MFMA
+ * rows); a 128-row tile uses half of its slot. */
 extern "C" int sera_mmq_slot_floats(int M) {
     const int bm = sera_mmq_bm(M);
-    return (bm < 32 ? 32 : bm) * mmq_bn(bm);
+    return (bm < 32 ? 32 : bm) * 256;
 }
 
 template <int TT, int WGT, int WGN, int WPE, int PR = 0>
@@ -870,6 +887,8 @@ extern "C" hipError_t sera_launch_q4k_mmq_streamk_acc(uint32_t qtype, const void
         return launch_mmq_streamk_cfg<1, 1, 4, 2, 1>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
     if (sera_mmq_bm(M) == 32)
         return launch_mmq_streamk_cfg<1, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
+    if (mmq_bn(M, N) == 128)
+        return launch_mmq_streamk_cfg<1, 2, 2, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
     return launch_mmq_streamk_cfg<2, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, P, accum, s);
 }
 
@@ -903,9 +922,7 @@ static float tail_cost(int64_t dp_rounds, int64_t R, int c, int nkb, int P, int 
 
 extern "C" void sera_mmq_tail_plan(int M, int N, int K, int cus, size_t max_slot_floats, int *dp_tiles,
                                    int *pieces) {
-    const int bm = sera_mmq_bm(M);
-    const int bn = mmq_bn(bm);
-    const int T = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const int T = sera_mmq_tiles(M, N);
     const int nkb = K / Q4K_QK;
     const int C = cus > 0 ? cus : kModelCUs;
     const int P = 2 * C;
@@ -964,6 +981,9 @@ extern "C" hipError_t sera_launch_q4k_mmq_tail_acc(uint32_t qtype, const void *W
                                                    accum, s);
     if (sera_mmq_bm(M) == 32)
         return launch_mmq_tail_cfg<1, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, dp_tiles, pieces,
+                                                accum, s);
+    if (mmq_bn(M, N) == 128)
+        return launch_mmq_tail_cfg<1, 2, 2, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, dp_tiles, pieces,
                                                 accum, s);
     return launch_mmq_tail_cfg<2, 1, 4, 2>(tiled, w, xq, xds, y, slots, counters, M, N, K, dp_tiles, pieces, accum,
                                             s);

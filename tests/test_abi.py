@@ -259,10 +259,11 @@ def test_stage_layouts_and_workspace_sizing():
 def test_mmq_split_rule_picks_measured_best():
     """The split-K cost model picks, on Qwen3-32B shapes, the split count
     that measured fastest on MI355X (q, k/v, o, gate/up, down at 64-2048
-    tokens), and keeps every choice within its bounds: at least 2
-    super-blocks per split, at most 2048 workgroups, 16 splits at most."""
-    measured_best = {(64, 8192, 5120): 8, (128, 8192, 5120): 4, (512, 8192, 5120): 1,
-                     (512, 1024, 5120): 8, (1024, 1024, 5120): 4,
+    tokens; 128-row tiles where 256-row ones would leave at most 64), and
+    keeps every choice within its bounds: at least 2 super-blocks per split,
+    at most 2048 workgroups, 16 splits at most."""
+    measured_best = {(64, 8192, 5120): 4, (128, 8192, 5120): 4, (512, 8192, 5120): 1,
+                     (512, 1024, 5120): 4, (1024, 1024, 5120): 4, (256, 1024, 5120): 8,
                      (256, 5120, 8192): 8, (1024, 5120, 8192): 4,
                      (512, 25600, 5120): 1, (2048, 25600, 5120): 1,
                      (128, 5120, 25600): 16, (512, 5120, 25600): 8, (1024, 5120, 25600): 4,

@@ -189,9 +189,12 @@ def test_fewtok_exact(torch, N, K):
 # MMQ tiles and schedules
 # ---------------------------------------------------------------------------
 
-# M <= 16: paired 16-token tile; 17-32: 32-token tile; above: 64-token tile
+# M <= 16: paired 16-token tile; 17-32: 32-token tile; above: 64-token
+# tile, of 128 weight rows up to 64 tiles of 256 rows (the shapes up to
+# (64, 64, 25600)) and of 256 rows past that (the last two)
 MMQ_EXACT = [(1, 700, 5120), (7, 300, 2304), (16, 512, 5120), (20, 300, 2304), (32, 640, 1024),
-             (33, 384, 5120), (100, 256, 2048), (200, 640, 1024), (64, 64, 25600)]
+             (33, 384, 5120), (100, 256, 2048), (200, 640, 1024), (64, 64, 25600), (64, 16640, 512),
+             (130, 8448, 256)]
 
 
 @pytest.mark.parametrize("M,N,K", MMQ_EXACT)

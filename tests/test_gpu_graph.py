@@ -90,7 +90,7 @@ CASES = [
     (12, 9, 1000, 25600, "fewtok-mmq"),
     (12, 10, 1000, 2560, "mmq"),
     (12, 20, 131328, 256, "mmq-streamk"),
-    (12, 64, 16384, 2048, "mmq"),
+    (12, 64, 8192, 2048, "mmq"),
     (12, 100, 4096, 5120, "mmq"),
     (12, 200, 25600, 2048, "mmq-tail"),
     (12, 600, 25600, 1024, "mmq-tail"),
@@ -101,7 +101,7 @@ CASES = [
     (268, 1, 4096, 5120, "dot4"),
     (268, 2, 16384, 5120, "fewtok"),
     (268, 20, 131328, 256, "mmq-streamk"),
-    (268, 64, 16384, 2048, "mmq"),
+    (268, 64, 8192, 2048, "mmq"),
     (268, 200, 25600, 2048, "mmq-tail"),
     (268, 16, 70000, 512, "fewtok-mmq-persistent"),
 ]

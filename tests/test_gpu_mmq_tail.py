@@ -8,7 +8,8 @@ are the MMQ kernel's own (cuda/mmq/mmq.cuh:1440-1472,2269-2283). So:
   * on the exact-input construction of test_gpu_exact (every partial sum an
     exact fp32 value) the output equals the dequant GEMM bit for bit, for
     any split: whole tiles only, a split tail after whole tiles, everything
-    split, one piece per super-block, on all three token tiles (16, 32, 64)
+    split, one piece per super-block, on all three token tiles (16, 32, 64;
+    the 64-token tile at 128 and 256 weight rows)
     and on the tiled weight layout;
   * on random inputs it sits within 2e-5 * rms of the MMQ oracle (the same
     terms summed in another order), repeats bit for bit, leaves its
@@ -72,8 +73,10 @@ def tail_cases(M, N, K):
     return sorted(set(out))
 
 
-# (M, N, K): paired 16-token tile, 32-token tile, 64-token tile (ragged M and N)
-EXACT = [(16, 512, 5120), (20, 300, 2304), (33, 384, 5120), (100, 256, 2048), (200, 640, 1024), (64, 64, 25600)]
+# (M, N, K): paired 16-token tile, 32-token tile, 64-token tile of 128 rows
+# (up to 64 tiles of 256 rows) and of 256 rows (the last), ragged M and N
+EXACT = [(16, 512, 5120), (20, 300, 2304), (33, 384, 5120), (100, 256, 2048), (200, 640, 1024), (64, 64, 25600),
+         (65, 16640, 1024)]
 
 
 @pytest.mark.parametrize("M,N,K", EXACT)
