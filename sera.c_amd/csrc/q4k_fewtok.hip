@@ -570,7 +570,9 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
          * first two super-blocks (past the range it re-reads this tile's
          * rows). Against one in flight (the loop below) on the 151936-row
          * LM head: 2-8 tokens 84-87 against 87-90 us, 16 tokens 97.5-98
-         * against 99-102; tiled bytes at 16 tokens 94.8 against 98.7. */
+         * against 99-102; tiled bytes at 16 tokens 94.8 against 98.7. The
+         * same loop on one tile per wave (gate/up, down, o at 2-16 tokens)
+         * was 2-6% slower than the loop below it. */
         FewtokW wc, wd;
         while (tile < te) {
 #pragma unroll
