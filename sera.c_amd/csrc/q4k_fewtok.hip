@@ -119,10 +119,14 @@ static constexpr int sera_waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 
  * and 2-3 workgroups per CU (gate/up, 74 MB: 13.3-14.0 against 15.8 us);
  * in this kernel the staged activations leave LDS for one copy in flight
  * per wave, and the gain is 4% (the launcher). A buffer holds row n's WS
- * blocks at 16 n * RS bytes: an odd slot count per row puts the 16 rows'
- * headers on 16 distinct 4-bank groups. */
+ * blocks at 16 n * RS bytes, unpadded. A 16-byte read is served in four
+ * passes of 16 lanes (lane quads of even and odd bit count per half wave);
+ * in each pass 8 rows read one piece and 8 others the next, and no row
+ * placement gives both those reads and the 16 headers distinct banks:
+ * unpadded rows (2 runs of 4 banks apart) cost 4 conflict cycles per
+ * super-block, an odd slot count per row (conflict-free headers) 8. */
 template <int WS> struct FewtokWs {
-    static constexpr int RS = 9 * WS + ((9 * WS) % 2 == 0 ? 1 : 2);   /* 16-byte slots per row */
+    static constexpr int RS = 9 * WS;                                  /* 16-byte slots per row */
     static constexpr int NI = (16 * RS + 63) / 64;                     /* copy instructions */
     static constexpr int BUF = NI * 1024;                              /* LDS bytes of one buffer */
 };
