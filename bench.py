@@ -367,7 +367,8 @@ def main():
                 {"gate_up": (gN, gK, gws), "down": (5120, 25600, sets["down"][2][0]), "lm_head": (151936, 5120, lmw)},
                 args)
         del lmw
-        results["config5_decode_stream"] = decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr)
+        results["config5_decode_stream"] = decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr,
+                                                            bench_kernel)
 
     # ---------------- roofline of the dominant kernel (MMVQ, M=1 gate/up) ---
     row, step_ms, b = headline
@@ -692,7 +693,7 @@ def cpu_baseline(np, torch, w_dev, N, K, x):
             "configs": configs}
 
 
-def decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr):
+def decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr, bench_kernel):
     """Config 5: 64 layers x 7 projections at M=1 plus the LM head, all
     resident (~18 GB); one token = 449 q3_cuda_q4k_linear calls, issued from
     C (sera_q4k_bench_stream) so no host language sits in the loop."""
@@ -769,6 +770,21 @@ def decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr):
         out.update({f"{label}ms_per_token": round(t, 3),
                     f"{label}sustained_GBps": round(total_w / (t * 1e-3) / 1e9, 1),
                     f"{label}frac_hbm": round(total_w / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    # each projection's one-token MMVQ kernel over its 64 layer copies (streamed
+    # from HBM, round robin), timed alone: where the layer's time goes
+    per = {}
+    for name in order:
+        N, K = SHAPES[name]
+        arr = (ctypes.c_void_p * 64)(*[keep[layer * 7 + order.index(name)].data_ptr() for layer in range(64)])
+        stage = torch.empty(q3q4.row_stage_layout(1, K)["total"], dtype=torch.uint8, device=dev)
+        q3q4.quantize_row(xs[K], stage)
+        kavg, _ = bench_kernel(0, arr, 64, stage, ys[name], None, 1, N, K, 0, 10, 128)
+        wb = N * K // 256 * 144
+        per[name] = {"kernel_us": round(kavg * 1e3, 2), "GBps": round(wb / (kavg * 1e-3) / 1e9, 1),
+                     "frac_hbm": round(wb / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    out["projection_kernels_m1"] = per
+    log("[bench] config 5 one-token kernels: " +
+        ", ".join(f"{n} {v['kernel_us']} us ({100 * v['frac_hbm']:.1f}%)" for n, v in per.items()))
     del keep, lm
     out["note"] = ("449 q3_cuda_q4k_linear calls (Q8_1 quantize + MMVQ each) per token, issued from C; "
                    "graph_*: the same pass captured once into a HIP graph and replayed; fused_*: the layer as "
