@@ -211,7 +211,10 @@ size_t sera_q4k_mmq_tail_slot_floats(int M, int N, int dp_tiles, int pieces);
  * up, down, the LM head); 0 otherwise. No counterpart in the reference
  * (mul_mat_q has one kernel family); a dispatch query. */
 int sera_q4k_mmq_uses_fewtok(int M, int N, int K);
+/* MMQ output tiles for M tokens of N rows: 16, 32 or 64 tokens by 256 rows,
+ * or 64 by 128 where 256-row tiles would number at most 64. */
 int sera_q4k_mmq_tiles(int M, int N);
+/* Floats of one stream-K or tail slot for M tokens (the largest tile's). */
 int sera_q4k_mmq_slot_floats(int M);
 
 /* Few-token kernel (1 <= M <= 16): Y (+)= X . W^T with two sub-blocks per
