@@ -156,7 +156,9 @@ def test_fewtok_split_repeats_and_accumulates(torch):
 # one pass, so the launch is persistent when the K chunk is one even split
 # (ragged N; 2 and 10 super-blocks); the odd 3-super-block K keeps one tile
 # per wave
-PERSIST_SHAPES = [(70001, 512), (40000, 2560), (70001, 768)]
+# chunks of 2 and 10 super-blocks (one super-block in flight per wave), 4 and
+# 12 (two to four in flight), and an odd count (no persistent grid)
+PERSIST_SHAPES = [(70001, 512), (40000, 2560), (40000, 1024), (40000, 3072), (70001, 768)]
 
 
 @pytest.mark.parametrize("N,K", PERSIST_SHAPES)
