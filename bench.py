@@ -561,7 +561,8 @@ def q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel
                 part = torch.empty(sp * M * N, dtype=torch.float32, device=dev) if sp > 1 else None
                 kavg, _ = bench_kernel(10 if split else 6, arr, copies, stage, y, part, M, N, K, sp, 5,
                                        iters if M < 512 else 10)
-                rows.append(row_of(layout, M, N, K, f"sera_q6k_mmq_kernel<1, 2, {str(split).lower()}>",
+                tt = L.sera_q6k_mmq_tile_tokens(M, N, K) // 32
+                rows.append(row_of(layout, M, N, K, f"sera_q6k_mmq_kernel<{tt}, 2, {str(split).lower()}>",
                                    step_ms, kavg))
                 continue
             stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)

@@ -344,6 +344,10 @@ int sera_q8_1_quantize_row_q6k(const float *X, int M, int K, void *stage, void *
 int sera_q6k_mmq(uint32_t qtype, const void *W, const void *q6k_mmq_stage, float *Y, float *partial, int M, int N,
                  int K, int splits, void *stream);
 int sera_q6k_mmq_splits_for(int M, int N, int K);
+/* Token tile of the Q6_K MMQ kernel for this shape: 32, or 64 when the
+ * padded rows divide by 64 and the 64-token grid has at least 1024
+ * (tile, super-block) pairs. The two give bit-identical results. */
+int sera_q6k_mmq_tile_tokens(int M, int N, int K);
 
 /* ---- weight upload into the device layout -------------------------------
  * Replaces the verbatim tensor copy of the reference's resident loader

@@ -19,24 +19,30 @@
  * sum q8 * (q-32) * sc, every product and partial sum an integer below 2^24,
  * so the fp32 result IS the integer J_b, bit for bit. The epilogue is then
  * one FMA per element and sub-block (J_b * d8_b), plus one per block (d).
- *   - weights are the B operand: lane = weight row (MFMA column), so d and
- *     the group scales are per-lane values. A lane of half h takes, for
- *     sub-block (j, q), weights l = 16h + [0, 16) of the quarter: one 16-wide
- *     group, one scale. Its bytes (4 ql runs, 2 qh runs, the 16 scales and d
- *     of the block) are loaded straight from HBM with dword-aligned buffer
- *     loads and funnel-shifted into place (rows are only 2-byte aligned),
- *     one block ahead of use. The raw quant bytes become fp16 (1024 + q) by
- *     v_perm under exponent byte 0x64, and one packed fp16 FMA per pair
- *     gives (q-32)*s.
+ *   - weights are the A operand: lane = weight row (MFMA row), so the group
+ *     scales are per-lane values. A lane of half h takes, for sub-block
+ *     (j, q), weights l = 16h + [0, 16) of the quarter: one 16-wide group,
+ *     one scale. Its runs (4 ql, 2 qh, the 16 scales and d of the block)
+ *     come from the weight tile in LDS, funnel-shifted into place on GGUF
+ *     bytes (rows are only 2-byte aligned). The raw quant bytes become fp16
+ *     (1024 + q) by v_perm under exponent byte 0x64, and one packed fp16 FMA
+ *     per pair gives (q-32)*s.
+ *   - activations are the B operand: lane = token (MFMA column), so d8 is
+ *     one LDS word per lane and sub-block; output element r of a lane is
+ *     weight row 8(r/4) + 4h + r%4, whose d the wave passes through LDS
+ *     once per K step.
  *   - activations (fp16 quants, fp32 d8) for the workgroup's tokens go
  *     global -> LDS directly (16-byte loads to LDS, 1 KB per wave
- *     instruction), double buffered per 256-wide K step; 16-byte chunk c of
- *     token t sits in column c ^ (t & 31) so a half-wave's 32 tokens reading
- *     one chunk hit distinct banks. The quantizer writes d8 transposed per K
- *     step so it lands in LDS as [sub-block][token].
- *   - tile: 32 tokens x 128 weight rows per workgroup, 4 waves along the
- *     rows (one 32 x 32 MFMA tile each), two workgroups per CU; split-K
- *     with a fixed-order reduce when tiles are few.
+ *     instruction); 16-byte chunks are XOR-swizzled by token so a
+ *     half-wave's 32 tokens reading one chunk hit distinct banks. The
+ *     quantizer writes d8 transposed per K step so it lands in LDS as
+ *     [sub-block][token].
+ *   - tiles: 32 or 64 tokens x 128 weight rows per workgroup, 4 waves along
+ *     the rows (one 32 x 32 MFMA tile per token tile), two workgroups per
+ *     CU. 32 tokens double-buffer the activations per K step; 64 tokens
+ *     (the operand build shared by twice the tokens) keep one buffer, in
+ *     two K halves, each reloaded while the other is read. Split-K with a
+ *     fixed-order reduce when tiles are few.
  */
 #include "sera_launch.h"
 
@@ -53,10 +59,11 @@ typedef float q6v4f __attribute__((ext_vector_type(4)));
 #define Q6M_WCH 15    /* 16-byte LDS chunks per weight row and K step: a 210-byte block at any
                          2-byte phase needs 14; the 15th spreads row starts over more banks */
 
-template <int BM>
+template <int BM, int XB>
 struct alignas(16) Q6MmqSmem {
-    alignas(16) _Float16 xs[2][BM][Q4K_QK];
+    alignas(16) _Float16 xs[XB][BM][Q4K_QK];
     alignas(16) float d8[2][8][BM];
+    alignas(16) float dw[4][32];   /* each wave's 32 row scales d of the K step */
     alignas(16) uint8_t w[Q6M_BN * Q6M_WCH * 16];
 };
 
@@ -96,6 +103,18 @@ __device__ __forceinline__ uint32_t q6m_raw(uint32_t ql, uint32_t qh) {
 
 __device__ __forceinline__ int q6m_sext8(uint32_t w, int sh) { return (int)(w << (24 - sh)) >> 24; }
 
+/* Workgroup barriers that wait only for what they name: this wave's LDS reads
+ * (and, for the second, all but its VM most recent global loads), never the
+ * vmcnt(0) a __syncthreads adds. The memory clobber keeps the compiler from
+ * moving loads or LDS accesses across. */
+__device__ __forceinline__ void q6m_barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int VM>
+__device__ __forceinline__ void q6m_barrier_vm() {
+    static_assert(VM >= 0 && VM < 16, "vmcnt immediate");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(VM) : "memory");
+}
+
 }  // namespace
 
 /* Grid (tiles, K splits); splits > 1 write fp32 partials per split. */
@@ -105,8 +124,11 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
         const float *__restrict__ d8t, float *__restrict__ y, float *__restrict__ partial, int M, int Mpad,
         int N, int K, int kb_per_split, int accum) {
     constexpr int BM = 32 * TT;
+    /* activation buffers: two for 32 tokens; one for 64 (the 64 KB of a
+     * second would leave one workgroup per CU) */
+    constexpr int XB = TT == 1 ? 2 : 1;
     constexpr int WINST = Q6M_BN * Q6M_WCH * 16 / 1024;   /* load-to-LDS instructions per weight tile */
-    __shared__ __attribute__((aligned(16))) Q6MmqSmem<BM> sm;
+    __shared__ __attribute__((aligned(16))) Q6MmqSmem<BM, XB> sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
     const int ntt = Mpad / BM, nrt = (N + Q6M_BN - 1) / Q6M_BN;
@@ -142,8 +164,22 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             }
         }
     };
-    /* activations of K step kb: BM tokens x 256 fp16 and 8 x BM fp32 d8 */
-    auto issue_x = [&](int kb, int buf) {
+    /* activations of K step kb: BM tokens x 256 fp16 and 8 x BM fp32 d8.
+     * Two buffers: token rows of 512 bytes, chunk c of token t in column
+     * c ^ (t & 31). One buffer: two K halves of BM rows of 256 bytes (chunk c
+     * in half c >> 4, column (c & 15) ^ (t & 15)), loaded half by half. */
+    auto issue_xh = [&](int kb, int half) {
+#pragma unroll
+        for (int i = 0; i < BM / 16; i++) {
+            const int inst = wave + 4 * i;          /* 1 KB = four tokens' half rows */
+            const int tok = 4 * inst + (lane >> 4), col = lane & 15;
+            const _Float16 *src = xh + (size_t)(m0 + tok) * K + (size_t)kb * Q4K_QK + 128 * half +
+                                  8 * (col ^ (tok & 15));
+            __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src,
+                                             (q6m_lds_void *)&sm.xs[0][0][(half * BM + 4 * inst) * 128], 16, 0, 0);
+        }
+    };
+    auto issue_xs = [&](int kb, int buf) {
 #pragma unroll
         for (int i = 0; i < BM / 8; i++) {
             const int inst = wave + 4 * i;          /* 1 KB = two tokens */
@@ -152,6 +188,8 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src, (q6m_lds_void *)&sm.xs[buf][2 * inst][0], 16,
                                              0, 0);
         }
+    };
+    auto issue_d8 = [&](int kb, int buf) {
         if (wave < BM / 32) {
             const int f = wave * 256 + lane * 4;    /* float index in [8][BM] */
             const int b = f / BM, t = f % BM;
@@ -180,13 +218,20 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
 
     if (kb0 < kb1) {
         issue_w(kb0);
-        issue_x(kb0, 0);
+        issue_d8(kb0, 0);
+        if constexpr (XB == 2) {
+            issue_xs(kb0, 0);
+        } else {
+            issue_xh(kb0, 0);
+            issue_xh(kb0, 1);
+        }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     for (int kb = kb0; kb < kb1; kb++) {
         const int buf = (kb - kb0) & 1;
+        const int kn = min(kb + 1, kb1 - 1);
         /* the lane's runs of this block from LDS: ql[64j + 32p + 16h + 0..15],
          * qh[32j + 16h + 0..15], bytes 192..207 (scales) and d */
         const uint32_t base = (uint32_t)wr * (Q6M_WCH * 16) + (SPLIT ? 0u : ((rowg + (uint32_t)kb * BB) & 15u));
@@ -215,11 +260,27 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             dword = v[4];
         }
         const float d = SPLIT ? h2f_bits(dnext) : h2f_bits((dword >> sh) & 0xffffu);
-        __syncthreads();   /* every wave has its runs: the weight buffer is free */
-        if (kb + 1 < kb1) {
-            issue_w(kb + 1);
-            issue_x(kb + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
-            if (SPLIT) dnext = drow[kb + 1];
+        sm.dw[wave][l32] = d;   /* read back by this wave only, for the rows its outputs hold */
+        /* every wave has its runs: the weight buffer is free (one activation
+         * buffer: the second K half's loads may still be in flight) */
+        if constexpr (XB == 2) {
+            __syncthreads();
+            if (kb + 1 < kb1) {
+                issue_w(kb + 1);
+                issue_d8(kb + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
+                issue_xs(kb + 1, buf ^ 1);
+                if (SPLIT) dnext = drow[kb + 1];
+            }
+        } else {
+            /* Unconditional: the last step loads its own K step again into
+             * buffers it has finished reading. The wait counts below then
+             * hold on every step, and the step body has no branch (a branch
+             * lets the compiler sink the scaling FMAs past it and spill the
+             * MFMA results they wait for). */
+            q6m_barrier_lds();
+            issue_w(kn);
+            issue_d8(kn, buf ^ 1);
+            if (SPLIT) dnext = drow[kn];
         }
 
         /* The lane's group scales sc = 16*sh + sl of sub-blocks b = 2m, 2m+1
@@ -282,78 +343,174 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                 for (int t = 0; t < TT; t++) {
                     const int tok = 32 * t + l32;
                     const int chunk = (16 * j + 4 * q + 2 * h + u) ^ (tok & 31);
-                    const q6v8h A = *(const q6v8h *)&sm.xs[buf][tok][8 * chunk];
+                    const q6v8h X = *(const q6v8h *)&sm.xs[buf][tok][8 * chunk];
                     const v16f zero = {};
-                    C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Blo, u == 0 ? zero : C[t], 0, 0, 0);
-                    C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bhi, C[t], 0, 0, 0);
+                    C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Blo, X, u == 0 ? zero : C[t], 0, 0, 0);
+                    C[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Bhi, X, C[t], 0, 0, 0);
                 }
             }
+        };
+        /* the same for one token tile, the operand build split out */
+        auto build_b = [&](int j, int q, q6v8h (&Blo)[2], q6v8h (&Bhi)[2]) {
+            const int b = 4 * j + q, m = b >> 1, odd = b & 1;
+            const _Float16 sl16 = odd ? SL16[m].y : SL16[m].x, cl = odd ? CL[m].y : CL[m].x;
+            const _Float16 shh = odd ? SH[m].y : SH[m].x, ch = odd ? CH[m].y : CH[m].x;
+            const q6h2 s_hi = {shh, shh}, s_lo = {sl16, sl16}, c_hi = {ch, ch}, c_lo = {cl, cl};
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                uint32_t v[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint32_t ql = QL[2 * j + (q & 1)][2 * u + e], qh = QH[j][2 * u + e];
+                    v[e] = q == 0 ? q6m_raw<0>(ql, qh) : q == 1 ? q6m_raw<1>(ql, qh)
+                         : q == 2 ? q6m_raw<2>(ql, qh) : q6m_raw<3>(ql, qh);
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const q6h2 t = q6m_h2(__builtin_amdgcn_perm(0x64646464u, v[k >> 1],
+                                                                (k & 1) ? 0x04030402u : 0x04010400u));
+                    const q6h2 lo = __builtin_elementwise_fma(t, s_lo, c_lo);
+                    const q6h2 hi = __builtin_elementwise_fma(t, s_hi, c_hi);
+                    Blo[u][2 * k] = lo.x;
+                    Blo[u][2 * k + 1] = lo.y;
+                    Bhi[u][2 * k] = hi.x;
+                    Bhi[u][2 * k + 1] = hi.y;
+                }
+            }
+        };
+        auto mfma_t = [&](int j, int q, int t, const q6v8h (&Blo)[2], const q6v8h (&Bhi)[2], v16f &C) {
+            const int tok = 32 * t + l32;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int col = (4 * q + 2 * h + u) ^ (tok & 15);
+                const q6v8h X = *(const q6v8h *)&sm.xs[0][0][(j * BM + tok) * 128 + 8 * col];
+                const v16f zero = {};
+                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(Blo[u], X, u == 0 ? zero : C, 0, 0, 0);
+                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(Bhi[u], X, C, 0, 0, 0);
+            }
+        };
+        auto epi_t = [&](int j, int q, int t, const v16f &C) {
+            const float f = sm.d8[buf][4 * j + q][32 * t + l32];
+#pragma unroll
+            for (int r = 0; r < 16; r++) tmp[t][r] = fmaf(C[r], f, tmp[t][r]);
         };
         /* C is the exact integer J_b; scale by the tokens' d8 */
         auto epi_sb = [&](int j, int q, const v16f (&C)[TT]) {
 #pragma unroll
             for (int t = 0; t < TT; t++) {
+                const float f = sm.d8[buf][4 * j + q][32 * t + l32];
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const q6v4f f4 = *(const q6v4f *)&sm.d8[buf][4 * j + q][32 * t + 8 * g + 4 * h];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) tmp[t][4 * g + e] = fmaf(C[t][4 * g + e], f4[e], tmp[t][4 * g + e]);
-                }
+                for (int r = 0; r < 16; r++) tmp[t][r] = fmaf(C[t][r], f, tmp[t][r]);
             }
         };
-        /* software pipeline: the MFMAs of sub-block b+1 run while the VALU
-         * scales sub-block b */
-        v16f Ca[TT], Cb[TT];
-        mfma_sb(0, 0, Ca);
-        mfma_sb(0, 1, Cb);
-        epi_sb(0, 0, Ca);
-        mfma_sb(0, 2, Ca);
-        epi_sb(0, 1, Cb);
-        mfma_sb(0, 3, Cb);
-        epi_sb(0, 2, Ca);
-        mfma_sb(1, 0, Ca);
-        epi_sb(0, 3, Cb);
-        mfma_sb(1, 1, Cb);
-        epi_sb(1, 0, Ca);
-        mfma_sb(1, 2, Ca);
-        epi_sb(1, 1, Cb);
-        mfma_sb(1, 3, Cb);
-        epi_sb(1, 2, Ca);
-        epi_sb(1, 3, Cb);
+        if constexpr (XB == 2) {
+            /* software pipeline: the MFMAs of sub-block b+1 run while the VALU
+             * scales sub-block b */
+            v16f Ca[TT], Cb[TT];
+            mfma_sb(0, 0, Ca);
+            mfma_sb(0, 1, Cb);
+            epi_sb(0, 0, Ca);
+            mfma_sb(0, 2, Ca);
+            epi_sb(0, 1, Cb);
+            mfma_sb(0, 3, Cb);
+            epi_sb(0, 2, Ca);
+            mfma_sb(1, 0, Ca);
+            epi_sb(0, 3, Cb);
+            mfma_sb(1, 1, Cb);
+            epi_sb(1, 0, Ca);
+            mfma_sb(1, 2, Ca);
+            epi_sb(1, 1, Cb);
+            mfma_sb(1, 3, Cb);
+            epi_sb(1, 2, Ca);
+            epi_sb(1, 3, Cb);
+        } else {
+            /* 64 tokens: both token tiles' MFMAs use one operand build; the
+             * MFMAs of one token tile run while the VALU scales the other's
+             * previous result (one accumulator per token tile) */
+            v16f C0, C1;
 #pragma unroll
-        for (int t = 0; t < TT; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                acc[t][r] = fmaf(tmp[t][r], d, acc[t][r]);
-                tmp[t][r] = 0.0f;
-            }
-        __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads to LDS have landed */
-        __syncthreads();
-    }
-
-    /* lane holds weight row n0 + 32*wave + l32 for tokens
-     * m0 + 32t + 8(r/4) + 4h + r%4 */
-    float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
-    const int col = n0 + 32 * wave + l32;
-    if (col < N) {
-#pragma unroll
-        for (int t = 0; t < TT; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m < M) {
-                    float *dst = out + (size_t)m * N + col;
-                    *dst = !partial && accum ? *dst + acc[t][r] : acc[t][r];
+            for (int b = 0; b < 8; b++) {
+                const int j = b >> 2, q = b & 3;
+                if (b == 4) {
+                    /* the first K half is read by every wave; the second has
+                     * landed: at least 7 loads (weight tile, d8) and, split,
+                     * d were issued after it by every wave */
+                    q6m_barrier_vm<SPLIT ? 8 : 7>();
+                    issue_xh(kn, 0);
                 }
+                q6v8h Blo[2], Bhi[2];
+                build_b(j, q, Blo, Bhi);
+                mfma_t(j, q, 0, Blo, Bhi, C0);
+                if (b > 0) epi_t((b - 1) >> 2, (b - 1) & 3, 1, C1);
+                mfma_t(j, q, 1, Blo, Bhi, C1);
+                epi_t(j, q, 0, C0);
             }
+            epi_t(1, 3, 1, C1);
+        }
+        /* output element r of a lane is weight row 8(r/4) + 4h + r%4 of the
+         * wave's 32: that row's d from the lane that decoded it */
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const q6v4f d4 = *(const q6v4f *)&sm.dw[wave][8 * g + 4 * h];
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    acc[t][4 * g + e] = fmaf(tmp[t][4 * g + e], d4[e], acc[t][4 * g + e]);
+                    tmp[t][4 * g + e] = 0.0f;
+                }
+        }
+        if constexpr (XB == 2) {
+            __builtin_amdgcn_s_waitcnt(0);   /* this thread's loads to LDS have landed */
+            __syncthreads();
+        } else {
+            q6m_barrier_vm<0>();   /* loads landed; the second K half is read by every wave */
+            issue_xh(kn, 1);
+        }
     }
+    if constexpr (XB == 1) __builtin_amdgcn_s_waitcnt(0);   /* no load to LDS outlives the workgroup */
+
+    /* lane holds token m0 + 32t + l32 for weight rows
+     * n0 + 32*wave + 8(r/4) + 4h + r%4: four consecutive outputs per g */
+    float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
+    const bool add = !partial && accum;
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        const int m = m0 + 32 * t + l32;
+        if (m >= M) continue;
+        float *row = out + (size_t)m * N;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int col = n0 + 32 * wave + 8 * g + 4 * h;
+            if ((N & 3) == 0 && col < N) {   /* 16-byte aligned, all four in range */
+                q6v4f v = {acc[t][4 * g], acc[t][4 * g + 1], acc[t][4 * g + 2], acc[t][4 * g + 3]};
+                if (add) v += *(const q6v4f *)(row + col);
+                *(q6v4f *)(row + col) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (col + e < N) row[col + e] = add ? row[col + e] + acc[t][4 * g + e] : acc[t][4 * g + e];
+            }
+        }
+    }
+}
+
+/* Token tile: 64 (the weight operand build, the VALU bound, shared by twice
+ * the tokens) when the padded rows divide by 64 and the 64-token grid holds
+ * at least 1024 (tile, super-block) pairs; below that the 32-token tile's
+ * twice as many workgroups are faster (attn_v 1024 x 5120 at 64-256 tokens). */
+extern "C" int sera_q6k_mmq_tile_tokens(int M, int N, int K) {
+    const int mp = sera_q6k_mmq_padded_rows(M);
+    if (mp % 64) return 32;
+    const long pairs = (long)(mp / 64) * ((N + Q6M_BN - 1) / Q6M_BN) * (K / Q4K_QK);
+    return pairs >= 1024 ? 64 : 32;
 }
 
 /* K splits: double while the grid holds fewer than 1024 (tile, split)
  * workgroups (two resident per CU, two rounds on 256 CUs) and each split
  * keeps at least 2 super-blocks. */
 extern "C" int sera_q6k_mmq_splits(int M, int N, int K) {
-    const int bm = 32;
+    const int bm = sera_q6k_mmq_tile_tokens(M, N, K);
     const int tiles = ((M + bm - 1) / bm) * ((N + Q6M_BN - 1) / Q6M_BN);
     const int nkb = K / Q4K_QK;
     int s = 1;
@@ -392,12 +549,18 @@ extern "C" hipError_t sera_launch_q6k_mmq_acc(uint32_t qtype, const void *W, con
     const uint8_t *w = (const uint8_t *)W;
     const uint64_t nblk = (uint64_t)N * (uint64_t)(K / Q4K_QK);
     if (splits < 1) splits = 1;
-    if (qtype == SERA_QTYPE_Q6K_SPLIT)
-        return launch_q6k_mmq<1, 2, true>(w, (const uint16_t *)(w + nblk * Q6K_SPLIT_QBYTES),
-                                          nblk * Q6K_SPLIT_QBYTES, xh, d8t, y, partial, M, Mpad, N, K, splits, accum,
-                                          s);
-    return launch_q6k_mmq<1, 2, false>(w, nullptr, nblk * Q6K_BLOCK_BYTES, xh, d8t, y, partial, M, Mpad, N, K,
-                                       splits, accum, s);
+    const bool wide = sera_q6k_mmq_tile_tokens(M, N, K) == 64;
+    if (qtype == SERA_QTYPE_Q6K_SPLIT) {
+        const uint16_t *wd = (const uint16_t *)(w + nblk * Q6K_SPLIT_QBYTES);
+        return wide ? launch_q6k_mmq<2, 2, true>(w, wd, nblk * Q6K_SPLIT_QBYTES, xh, d8t, y, partial, M, Mpad, N, K,
+                                                 splits, accum, s)
+                    : launch_q6k_mmq<1, 2, true>(w, wd, nblk * Q6K_SPLIT_QBYTES, xh, d8t, y, partial, M, Mpad, N, K,
+                                                 splits, accum, s);
+    }
+    return wide ? launch_q6k_mmq<2, 2, false>(w, nullptr, nblk * Q6K_BLOCK_BYTES, xh, d8t, y, partial, M, Mpad, N, K,
+                                              splits, accum, s)
+                : launch_q6k_mmq<1, 2, false>(w, nullptr, nblk * Q6K_BLOCK_BYTES, xh, d8t, y, partial, M, Mpad, N, K,
+                                              splits, accum, s);
 }
 
 extern "C" hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial,

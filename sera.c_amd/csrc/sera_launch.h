@@ -80,6 +80,7 @@ hipError_t sera_launch_q6k_mmvq(uint32_t qtype, const void *W, const void *stage
 hipError_t sera_launch_q6k_mmvq_acc(uint32_t qtype, const void *W, const void *stage, float *y, int M, int N, int K,
                                     int rows, int accum, hipStream_t s);
 int sera_q6k_mmq_splits(int M, int N, int K);
+int sera_q6k_mmq_tile_tokens(int M, int N, int K);
 hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial, int M,
                                int N, int K, int splits, hipStream_t s);
 hipError_t sera_launch_q6k_mmq_acc(uint32_t qtype, const void *W, const void *stage, float *y, float *partial, int M,

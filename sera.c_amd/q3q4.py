@@ -145,6 +145,7 @@ def load():
         "sera_weight_to_device_layout": ([U32, I, I, P, P, P], I),
         "sera_weight_upload": ([U32, I, I, P, P, P, SZ, P], I),
         "sera_q6k_mmq_splits_for": ([I, I, I], I),
+        "sera_q6k_mmq_tile_tokens": ([I, I, I], I),
         "sera_candidate_logits": ([I, P, I, I, P, I, P, I, P, P], I),
         "sera_linear_group": ([I, P, P, P, P, P, P, ctypes.c_float, SZ, ctypes.c_uint, P], I),
         "sera_q4k_bench_group_stream": ([P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),

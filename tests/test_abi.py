@@ -343,6 +343,23 @@ def test_vec_dispatch_rule_tiled_layout(L):
     assert f(14, 4, 25600, 5120) == 0 and f(T, 9, 25600, 5120) == 0
 
 
+def test_q6k_mmq_token_tile_rule(L):
+    """The Q6_K tile kernel takes 64 tokens per tile when the padded rows
+    divide by 64 and the 64-token grid holds >= 1024 (tile, super-block)
+    pairs, else 32; the built-in K split counts the tiles of that choice
+    (down 5120 x 25600 at 512 tokens: 320 tiles, 4 splits)."""
+    f = L.sera_q6k_mmq_tile_tokens
+    assert f(512, 5120, 25600) == 64 and f(2048, 5120, 25600) == 64 and f(64, 5120, 25600) == 64
+    assert f(512, 151936, 5120) == 64 and f(64, 151936, 5120) == 64
+    assert f(512, 1024, 5120) == 64 and f(2048, 1024, 5120) == 64     # 64 x 20, 256 x 20 pairs
+    assert f(256, 1024, 5120) == 32 and f(64, 1024, 5120) == 32       # 32 x 20, 8 x 20 pairs
+    assert f(100, 2046, 8192) == 64 and f(128, 2048, 8192) == 64      # 2 x 16 x 32 = 1024
+    assert f(96, 5120, 25600) == 32 and f(40, 77, 2304) == 32 and f(8, 5120, 25600) == 32
+    assert L.sera_q6k_mmq_splits_for(512, 5120, 25600) == 4
+    assert L.sera_q6k_mmq_splits_for(2048, 5120, 25600) == 1
+    assert L.sera_q6k_mmq_splits_for(256, 5120, 25600) == 8
+
+
 def test_q6k_vec_dispatch_rule(L):
     """Q6_K on the MMVQ path: the tile kernel on tall matrices from 4 tokens,
     on 4096-16383 rows from 6, never below 4096 rows; launch counts follow."""

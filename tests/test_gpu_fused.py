@@ -120,6 +120,25 @@ def test_accumulate_on_split_and_streamk_schedules(torch, linear, M, N, K, kind)
     check_close(y[:, idx], oracle.linear_reference(W[idx], x, 64, K), "sampled rows")
 
 
+@pytest.mark.parametrize("M,N,K,tile", [(100, 1000, 2304, 32), (128, 2048, 8192, 64), (512, 16384, 2048, 64)])
+def test_q6k_accumulate_on_both_token_tiles(torch, linear, M, N, K, tile):
+    """Q6_K tile kernel on its 32- and 64-token tiles, split-K (the first
+    two) and whole K (the last, 1024 tiles): the accumulating store stays
+    bit-identical to product + add."""
+    L = q3q4.load()
+    say(f"case q6k accumulate M={M} N={N} K={K} tile={tile} splits={L.sera_q6k_mmq_splits_for(M, N, K)}")
+    assert L.sera_q6k_mmq_tile_tokens(M, N, K) == tile
+    rng = np.random.default_rng(M + N + K)
+    W = weights(rng, 14, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    y = run_group(torch, 14, [W], [N], K, x)[0]
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    ya = run_group(torch, 14, [W], [N], K, x, flags=q3q4.LIN_ACCUMULATE, y0=[y0])[0]
+    assert np.array_equal(ya.view(np.uint32), (y0 + y).astype(np.float32).view(np.uint32))
+    idx = np.sort(np.random.default_rng(4).choice(N, 64, replace=False))
+    check_close(y[:, idx], path_oracle(14, W[idx], x, 64, K), "sampled rows")
+
+
 @pytest.mark.parametrize("qtype,M", [(12, 1), (12, 5), (12, 33), (14, 2), (14, 7), (14, 40)])
 def test_rmsnorm_producer_is_bit_identical_to_unfused(torch, linear, qtype, M):
     K = 5120

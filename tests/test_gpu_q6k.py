@@ -204,8 +204,11 @@ def test_q6k_mmvq_exact_integer_dots(torch, M):
 # MMQ (fp16-MFMA tiles)
 # ---------------------------------------------------------------------------
 
+# the last two run the 64-token tile (ragged tokens and rows, N % 4 == 2; and
+# whole tiles with 16-byte stores); the others the 32-token tile
 Q6_MMQ_CASES = [(9, 128, 256), (16, 256, 1024), (33, 1000, 512), (64, 384, 5120), (100, 250, 2048),
-                (128, 128, 25600), (200, 640, 1024), (512, 256, 5120), (40, 77, 2304)]
+                (128, 128, 25600), (200, 640, 1024), (512, 256, 5120), (40, 77, 2304), (100, 2046, 8192),
+                (128, 2048, 8192)]
 
 
 @pytest.mark.parametrize("M,N,K", Q6_MMQ_CASES)
@@ -231,12 +234,12 @@ def test_q6k_mmq_parity(torch, M, N, K):
         check_close(y.cpu().numpy(), ref, f"q6k mmq M={M} N={N} K={K} splits={s}")
 
 
-@pytest.mark.parametrize("M", [9, 64, 100])
-def test_q6k_mmq_exact_integer_dots(torch, M):
+@pytest.mark.parametrize("M,N,K", [(9, 200, 768), (64, 200, 768), (100, 200, 768), (100, 2046, 8192)])
+def test_q6k_mmq_exact_integer_dots(torch, M, N, K):
     """The fp16-MFMA products carry the exact integers sc * (q - 32) * q8:
-    on exact inputs the output equals the exact GEMM bit for bit."""
-    N, K = 200, 768
-    say(f"case q6k mmq exact M={M}")
+    on exact inputs the output equals the exact GEMM bit for bit (32-token
+    tiles; the last case the 64-token tile)."""
+    say(f"case q6k mmq exact M={M} N={N} K={K} tile={q3q4.load().sera_q6k_mmq_tile_tokens(M, N, K)}")
     rng = np.random.default_rng(91 + M)
     W, x = _exact_inputs(rng, M, N, K)
     stage = torch.empty(q3q4.q6k_mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device="cuda")
