@@ -64,6 +64,7 @@ struct alignas(16) Q6MmqSmem {
     alignas(16) _Float16 xs[XB][BM][Q4K_QK];
     alignas(16) float d8[2][8][BM];
     alignas(16) float dw[4][32];   /* each wave's 32 row scales d of the K step */
+    alignas(16) uint32_t wd[Q6M_BN];   /* split layout: the dword holding each row's d */
     alignas(16) uint8_t w[Q6M_BN * Q6M_WCH * 16];
 };
 
@@ -163,6 +164,16 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, vo, 0, 0, 0);
             }
         }
+        if constexpr (SPLIT) {
+            /* d of the 128 rows (2 bytes each in Wd [N][K/256]): the aligned
+             * dword holding it, which never leaves the page of its valid half */
+            if (wave >= 2) {
+                const int row = min(n0 + 64 * (wave - 2) + lane, N - 1);
+                const size_t idx = (size_t)row * nb + kb;
+                __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)(Wd + (idx & ~(size_t)1)),
+                                                 (q6m_lds_void *)&sm.wd[64 * (wave - 2)], 4, 0, 0);
+            }
+        }
     };
     /* activations of K step kb: BM tokens x 256 fp16 and 8 x BM fp32 d8.
      * Two buffers: token rows of 512 bytes, chunk c of token t in column
@@ -189,23 +200,24 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                                              0, 0);
         }
     };
+    /* by the last waves, which issue one weight-tile load fewer */
     auto issue_d8 = [&](int kb, int buf) {
-        if (wave < BM / 32) {
-            const int f = wave * 256 + lane * 4;    /* float index in [8][BM] */
+        constexpr int W0 = 4 - BM / 32;
+        if (wave >= W0) {
+            const int f = (wave - W0) * 256 + lane * 4;    /* float index in [8][BM] */
             const int b = f / BM, t = f % BM;
             const float *src = d8t + ((size_t)kb * 8 + b) * Mpad + m0 + t;
-            __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src, (q6m_lds_void *)&sm.d8[buf][0][wave * 256],
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src,
+                                             (q6m_lds_void *)&sm.d8[buf][0][(wave - W0) * 256], 16, 0, 0);
         }
     };
 
     /* this lane's weight row (B column) and its phase in the LDS window */
     const int wr = 32 * wave + l32;
     const uint32_t rowg = (uint32_t)((uint64_t)min(n0 + wr, N - 1) * rb - gbase);
-    /* split layout: this lane's d for the next K step, loaded a step ahead */
-    const uint16_t *drow = SPLIT ? Wd + (size_t)min(n0 + wr, N - 1) * nb : nullptr;
-    uint32_t dnext = 0;
-    if (SPLIT && kb0 < kb1) dnext = drow[kb0];
+    /* split layout: which half of its wd dword is this row's d (parity of
+     * row * nb + kb) */
+    const int dpar = SPLIT ? (min(n0 + wr, N - 1) & 1) * (nb & 1) : 0;
 
     v16f acc[TT], tmp[TT];
 #pragma unroll
@@ -259,7 +271,8 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             SC = q6m_align16(v, sh);
             dword = v[4];
         }
-        const float d = SPLIT ? h2f_bits(dnext) : h2f_bits((dword >> sh) & 0xffffu);
+        if constexpr (SPLIT) dword = sm.wd[wr] >> (16 * ((dpar + kb) & 1));
+        const float d = h2f_bits((SPLIT ? dword : dword >> sh) & 0xffffu);
         sm.dw[wave][l32] = d;   /* read back by this wave only, for the rows its outputs hold */
         /* every wave has its runs: the weight buffer is free (one activation
          * buffer: the second K half's loads may still be in flight) */
@@ -269,7 +282,6 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                 issue_w(kb + 1);
                 issue_d8(kb + 1, buf ^ 1);   /* buffer last read one step ago, freed by the barrier */
                 issue_xs(kb + 1, buf ^ 1);
-                if (SPLIT) dnext = drow[kb + 1];
             }
         } else {
             /* Unconditional: the last step loads its own K step again into
@@ -280,7 +292,6 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             q6m_barrier_lds();
             issue_w(kn);
             issue_d8(kn, buf ^ 1);
-            if (SPLIT) dnext = drow[kn];
         }
 
         /* The lane's group scales sc = 16*sh + sl of sub-blocks b = 2m, 2m+1
@@ -433,9 +444,10 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                 const int j = b >> 2, q = b & 3;
                 if (b == 4) {
                     /* the first K half is read by every wave; the second has
-                     * landed: at least 7 loads (weight tile, d8) and, split,
-                     * d were issued after it by every wave */
-                    q6m_barrier_vm<SPLIT ? 8 : 7>();
+                     * landed: every wave issued at least 8 loads after it
+                     * (waves 0-1: 8 of the weight tile; 2-3: 7, d8 and, on the
+                     * split layout, d) */
+                    q6m_barrier_vm<8>();
                     issue_xh(kn, 0);
                 }
                 q6v8h Blo[2], Bhi[2];
