@@ -123,10 +123,15 @@ int sera_q4k_vec_uses_fewtok(int M, int N, int K);
 int sera_q4k_vec_uses_fewtok_qt(uint32_t qtype, int M, int N, int K);
 
 /* 1 if a Q6_K call on the MMVQ path (1 <= M <= 8) runs the tile kernel on a
- * row-formula stage for an N x K matrix (from 4 tokens at 16384 or more
- * rows, from 6 at 4096-16383 rows, never below 4096), 0 if it runs the
- * Q6_K MMVQ kernel. No counterpart in the reference; a dispatch query. */
+ * row-formula stage for an N x K matrix of GGUF bytes (from 4 tokens at
+ * 16384 or more rows, from 6 at 4096-16383 rows, never below 4096), 0 if it
+ * runs the Q6_K MMVQ kernel. No counterpart in the reference; a dispatch
+ * query. */
 int sera_q6k_vec_uses_tile(int M, int N, int K);
+/* The same per weight layout: qtype 14 as above; SERA_QTYPE_Q6K_SPLIT from
+ * 4 tokens at 16384+ rows and from 7 at 4096-16383 (its MMVQ kernel is
+ * faster than the GGUF one); 0 for any other qtype. */
+int sera_q6k_vec_uses_tile_qt(uint32_t qtype, int M, int N, int K);
 
 /* Event timings of the last timed dense call, valid after the caller
  * synchronized its stream (q3_mmq_read_timings, cuda/q3_mmq.h:48-50). */
@@ -294,9 +299,9 @@ const char *sera_q4k_last_error(void);
 /* Y = X . W^T through the MMVQ path (MMVQ arithmetic), 1 <= M <= 8: the
  * reference quantizes Q6_K decode activations with the same
  * quantize_row_q8_1_cuda call as Q4_K. The dot4 MMVQ kernel on the row
- * stage, or, where sera_q6k_vec_uses_tile says so (tall matrices from 4
- * tokens, 4096-16383 rows from 6), the fp16-MFMA tile kernel on a
- * row-formula Q6_K stage. Replaces q3_mmq_q6_K_dense_vec (cuda/q3_mmq.cu:515-519 over
+ * stage, or, where sera_q6k_vec_uses_tile_qt says so (tall matrices from 4
+ * tokens, 4096-16383 rows from 6 on GGUF bytes and from 7 on the split
+ * layout), the fp16-MFMA tile kernel on a row-formula Q6_K stage. Replaces q3_mmq_q6_K_dense_vec (cuda/q3_mmq.cu:515-519 over
  * q3_mmq_dense_vec_impl, :408-506). */
 int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
                        void *stream, int timed);
@@ -309,8 +314,10 @@ int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X, float *Y, 
 int sera_q6k_dense(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
                    void *stream, int timed);
 
-/* Kernel launches one sera_q6k_dense / sera_q6k_dense_vec call makes. */
+/* Kernel launches one sera_q6k_dense / sera_q6k_dense_vec call makes, on
+ * GGUF bytes and (the _qt form) on either Q6_K layout. */
 int sera_q6k_kernel_launches(int M, int N, int K);
+int sera_q6k_kernel_launches_qt(uint32_t qtype, int M, int N, int K);
 
 /* MMVQ kernel on a row stage (mul_mat_vec_q<Q6_K>, cuda/mmq/mmvq.cu:907-911,
  * with vec_dot_q6_K_q8_1, cuda/mmq/vecdotq.cuh:624-643,956-980):
@@ -329,7 +336,7 @@ int sera_q6k_mmvq_rows_per_wave(int M, int N);
  * multiple of 32. sera_q8_1_quantize_row_q6k fills the same layout with the
  * row quantizer's values (cuda/mmq/quantize.cu:4-48, d8 = fp32(fp16 d)):
  * the MMVQ arithmetic on the tile kernel, which sera_q6k_dense_vec uses
- * where sera_q6k_vec_uses_tile says so. */
+ * where sera_q6k_vec_uses_tile_qt says so. */
 int sera_q8_1_q6k_mmq_padded_rows(int M);
 size_t sera_q8_1_q6k_mmq_stage_bytes(int M, int K);
 void sera_q8_1_q6k_mmq_stage_offsets(int M, int K, size_t *qs, size_t *d);
@@ -399,7 +406,7 @@ int sera_weight_upload(uint32_t qtype, int N, int K, const void *host_gguf, void
  * MMVQ kernel takes (sera_q4k_vec_uses_fewtok == 0) share one grouped
  * launch and the others run the few-token kernel one by one; a Q6_K group
  * shares one stage, so its largest matrix picks the kernel
- * (sera_q6k_vec_uses_tile). Arithmetic per product as q3_cuda_q4k_linear (MMVQ
+ * (sera_q6k_vec_uses_tile_qt). Arithmetic per product as q3_cuda_q4k_linear (MMVQ
  * formula for M <= 8, MMQ above). gamma and X2 must be 16-byte aligned.
  * Uses the arena of sera_q4k_set_arena / q3_cuda_q4k_linear_set_workspace;
  * enqueue only. */

@@ -171,7 +171,7 @@ bool q3_cuda_q4k_linear(const q3_q4_linear_geometry *geometry, const void *weigh
                 : sera_q4k_dense_qt(geometry->qtype, weight, device_input, device_output, tokens, features, K,
                                     stream, stats != NULL);
     }
-    s->kernel_launches = (uint64_t)(q6 ? sera_q6k_kernel_launches(tokens, features, K)
+    s->kernel_launches = (uint64_t)(q6 ? sera_q6k_kernel_launches_qt(geometry->qtype, tokens, features, K)
                                        : sera_q4k_kernel_launches(tokens, features, K));
     if (rc != 0) {
         char buffer[400];

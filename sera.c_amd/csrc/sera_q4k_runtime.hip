@@ -730,20 +730,26 @@ extern "C" int sera_q6k_mmvq(uint32_t qtype, const void *W, const void *row_stag
 }
 
 /* Q6_K batches on the MMVQ path (M <= 8) run the MFMA tile kernel on a
- * row-formula stage (the MMVQ arithmetic) instead of the dot4 MMVQ kernel
- * where that is faster. Measured on MI355X per shape, GGUF bytes (kernel
- * us, MMVQ / tile): the tile kernel's time is flat in M, MMVQ's grows.
- *   LM head 151936 rows: 4 tokens 252 / 235, 5: 287 / 217;
- *   q 8192 and down 5120 rows: 5: 20.7 / 21.4, 52.8 / 61.1; 6: 22.4 / 21.1,
- *     59.4 / 59.4; 8: 40.6 / 20.9, 93.3 / 58.4;
- *   v 1024 rows: 8 tokens 8.4 / 14.7 (MMVQ at every batch). */
-extern "C" int sera_q6k_vec_uses_tile(int M, int N, int K) {
+ * row-formula stage (the MMVQ arithmetic) instead of the MMVQ kernel where
+ * that is faster. Measured on MI355X per shape (kernel us, MMVQ / tile):
+ * the tile kernel's time is flat in M, MMVQ's grows.
+ *   GGUF bytes: LM head 151936 rows: 3 tokens 219 / 222, 4: 247-253 / 220;
+ *     q 8192 and down 5120 rows: 5: 20.5 / 20.6, 52.7 / 55.8; 6: 22.1 /
+ *     20.2, 58.4 / 54.4; 8: 39.3 / 20.0, 91.3 / 55.0;
+ *   split layout (its own MMVQ kernel is faster): LM head 4 tokens 182 /
+ *     180, 5: 223 / 177; q and down 6: 16.7 / 18.6, 45.3 / 48.3; 7: 20.1 /
+ *     17.8, 52.0 / 48.8;
+ *   v 1024 rows: 8 tokens 8.2 / 13.8 (MMVQ at every batch, both layouts). */
+extern "C" int sera_q6k_vec_uses_tile_qt(uint32_t qtype, int M, int N, int K) {
     (void)K;
+    if (qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) return 0;
     if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH || N <= 0) return 0;
     if (N >= 16384) return M >= 4;
-    if (N >= 4096) return M >= 6;
+    if (N >= 4096) return M >= (qtype == 14u ? 6 : 7);
     return 0;
 }
+
+extern "C" int sera_q6k_vec_uses_tile(int M, int N, int K) { return sera_q6k_vec_uses_tile_qt(14u, M, N, K); }
 
 extern "C" int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
                                   void *stream, int timed) {
@@ -753,7 +759,7 @@ extern "C" int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X,
     if (!q6k_shape_ok("sera_q6k_dense_vec", qtype, K)) return -1;
     if (!g_arena) return fail(-1, "sera_q6k_dense_vec: no arena attached");
     hipStream_t s = (hipStream_t)stream;
-    const bool mfma = sera_q6k_vec_uses_tile(M, N, K) != 0;
+    const bool mfma = sera_q6k_vec_uses_tile_qt(qtype, M, N, K) != 0;
     const int Mpad = sera_q6k_mmq_padded_rows(M);
     const size_t stage_bytes = mfma ? sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K).total
                                     : sera_row_stage_layout((size_t)M, (size_t)K).total;
@@ -785,11 +791,13 @@ int q6k_splits(int M, int N, int K) {
 }
 }  // namespace
 
-extern "C" int sera_q6k_kernel_launches(int M, int N, int K) {
+extern "C" int sera_q6k_kernel_launches_qt(uint32_t qtype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
-    if (M <= SERA_Q4K_MMVQ_MAX_BATCH && !sera_q6k_vec_uses_tile(M, N, K)) return 2;
+    if (M <= SERA_Q4K_MMVQ_MAX_BATCH && !sera_q6k_vec_uses_tile_qt(qtype, M, N, K)) return 2;
     return q6k_splits(M, N, K) > 1 ? 3 : 2;
 }
+
+extern "C" int sera_q6k_kernel_launches(int M, int N, int K) { return sera_q6k_kernel_launches_qt(14u, M, N, K); }
 
 extern "C" int sera_q8_1_q6k_mmq_padded_rows(int M) { return M > 0 ? sera_q6k_mmq_padded_rows(M) : 0; }
 
@@ -1067,7 +1075,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
      * between the MMVQ kernel (row stage) and the tile kernel */
     int n_max = 0;
     for (int i = 0; i < count; i++) n_max = N[i] > n_max ? N[i] : n_max;
-    const bool q6_tile = M > SERA_Q4K_MMVQ_MAX_BATCH || sera_q6k_vec_uses_tile(M, n_max, K);
+    const bool q6_tile = M > SERA_Q4K_MMVQ_MAX_BATCH || sera_q6k_vec_uses_tile_qt(qt, M, n_max, K);
 
     /* stage, then per-matrix split-K partials or stream-K slots */
     size_t stage_bytes;

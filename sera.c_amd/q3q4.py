@@ -116,6 +116,7 @@ def load():
         "sera_q4k_vec_uses_fewtok": ([I, I, I], I),
         "sera_q4k_vec_uses_fewtok_qt": ([U32, I, I, I], I),
         "sera_q6k_vec_uses_tile": ([I, I, I], I),
+        "sera_q6k_vec_uses_tile_qt": ([U32, I, I, I], I),
         "sera_q4k_mmq_streamk": ([P, P, P, P, P, I, I, I, I, P], I),
         "sera_q4k_mmq_streamk_wgs": ([I], I),
         "sera_q4k_mmq_schedule": ([I, I, I], I),
@@ -133,6 +134,7 @@ def load():
         "sera_q6k_dense": ([U32, P, P, P, I, I, I, P, I], I),
         "sera_q6k_dense_vec": ([U32, P, P, P, I, I, I, P, I], I),
         "sera_q6k_kernel_launches": ([I, I, I], I),
+        "sera_q6k_kernel_launches_qt": ([U32, I, I, I], I),
         "sera_q6k_mmvq": ([U32, P, P, P, I, I, I, I, P], I),
         "sera_q6k_mmvq_rows_per_wave": ([I, I], I),
         "sera_q8_1_q6k_mmq_padded_rows": ([I], I),

@@ -362,11 +362,23 @@ def test_q6k_mmq_token_tile_rule(L):
 
 def test_q6k_vec_dispatch_rule(L):
     """Q6_K on the MMVQ path: the tile kernel on tall matrices from 4 tokens,
-    on 4096-16383 rows from 6, never below 4096 rows; launch counts follow."""
+    on 4096-16383 rows from 6 (GGUF bytes) or 7 (split layout), never below
+    4096 rows; launch counts follow."""
     f = L.sera_q6k_vec_uses_tile
     assert [f(M, 151936, 5120) for M in range(1, 9)] == [0, 0, 0, 1, 1, 1, 1, 1]
     for N, K in ((5120, 25600), (8192, 5120)):
         assert [f(M, N, K) for M in range(1, 9)] == [0, 0, 0, 0, 0, 1, 1, 1]
     assert [f(M, 1024, 5120) for M in range(1, 9)] == [0] * 8
+    g = L.sera_q6k_vec_uses_tile_qt
+    S = q3q4.QTYPE_Q6K_SPLIT
+    for N, K in ((151936, 5120), (5120, 25600), (8192, 5120), (1024, 5120)):
+        assert [g(14, M, N, K) for M in range(0, 10)] == [f(M, N, K) for M in range(0, 10)]
+    assert [g(S, M, 151936, 5120) for M in range(1, 9)] == [0, 0, 0, 1, 1, 1, 1, 1]
+    for N, K in ((5120, 25600), (8192, 5120)):
+        assert [g(S, M, N, K) for M in range(1, 9)] == [0, 0, 0, 0, 0, 0, 1, 1]
+    assert [g(S, M, 1024, 5120) for M in range(1, 9)] == [0] * 8
+    assert g(12, 8, 151936, 5120) == 0 and g(S, 9, 151936, 5120) == 0
+    assert L.sera_q6k_kernel_launches_qt(S, 6, 5120, 25600) == 2    # MMVQ on the split layout
+    assert L.sera_q6k_kernel_launches_qt(14, 6, 5120, 25600) == L.sera_q6k_kernel_launches(6, 5120, 25600)
     assert L.sera_q6k_kernel_launches(8, 1024, 5120) == 2          # MMVQ
     assert L.sera_q6k_kernel_launches(5, 5120, 25600) == 2         # MMVQ

@@ -69,7 +69,7 @@ def kernel_of(qtype, M, N, K):
         if L.sera_q4k_mmq_uses_fewtok(M, N, K):
             return "fewtok-mmq"
         return {1: "mmq-streamk", 2: "mmq-tail"}.get(L.sera_q4k_mmq_schedule(M, N, K), "mmq")
-    return "q6k-tile" if M > 8 or L.sera_q6k_vec_uses_tile(M, N, K) else "q6k-mmvq"
+    return "q6k-tile" if M > 8 or L.sera_q6k_vec_uses_tile_qt(qtype, M, N, K) else "q6k-mmvq"
 
 
 # (qtype, M, N, K, kernel): dot4 MMVQ; the few-token kernel with in-kernel

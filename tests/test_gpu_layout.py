@@ -250,8 +250,8 @@ def test_split_gathered_rows_bit_identical_to_gguf(torch, N, K):
 def test_split_linear_boundary(torch, linear, M):
     """attn_v shape through q3_cuda_q4k_linear with a geometry bound to the
     split qtype: within 1e-3 * rms of the path oracle; where the tile kernel
-    runs (sera_q6k_vec_uses_tile, or the MMQ path) bit-identical to the
-    GGUF-layout call."""
+    runs on both layouts (sera_q6k_vec_uses_tile_qt, or the MMQ path)
+    bit-identical to the GGUF-layout call."""
     say(f"case q3_cuda_q4k_linear split M={M}")
     rng = np.random.default_rng(900 + M)
     N, K = 1024, 5120
@@ -266,24 +266,28 @@ def test_split_linear_boundary(torch, linear, M):
     torch.cuda.synchronize()
     a, b = ys.cpu().numpy(), yg.cpu().numpy()
     check_close(a, oracle.linear_reference_q6k(W, x.cpu().numpy(), N, K), f"split linear M={M}")
-    if M > 8 or q3q4.load().sera_q6k_vec_uses_tile(M, N, K):
+    L = q3q4.load()
+    if M > 8 or (L.sera_q6k_vec_uses_tile_qt(SPLIT, M, N, K) and L.sera_q6k_vec_uses_tile_qt(14, M, N, K)):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,N", [(4, 16384), (6, 4096), (8, 5120), (4, 4096)])
+@pytest.mark.parametrize("M,N", [(4, 16384), (6, 4096), (7, 4096), (8, 5120), (4, 4096)])
 def test_q6k_boundary_tile_branch_of_mmvq_path(torch, linear, M, N):
     """q3_cuda_q4k_linear on Q6_K matrices of 4096+ rows at 4-8 tokens, where
     sera_q6k_dense_vec may run the tile kernel on a row-formula stage (stage
     sized from the padded batch, split partials in the arena): sampled rows
     within 1e-3 * rms of the MMVQ-formula oracle, the split layout
-    bit-identical to the GGUF bytes whenever the tile kernel runs, and the
-    launch count the stats report equal to sera_q6k_kernel_launches."""
+    bit-identical to the GGUF bytes whenever both run the tile kernel (at 6
+    tokens on 4096 rows only the GGUF bytes do), and the launch count the
+    stats report equal to sera_q6k_kernel_launches_qt."""
     L = q3q4.load()
     K = 5120
-    tile = bool(L.sera_q6k_vec_uses_tile(M, N, K))
-    say(f"case q6k boundary M={M} N={N} K={K} tile={tile} launches={L.sera_q6k_kernel_launches(M, N, K)}")
+    tiles = {qt: bool(L.sera_q6k_vec_uses_tile_qt(qt, M, N, K)) for qt in (14, SPLIT)}
+    tile = tiles[14] and tiles[SPLIT]
+    say(f"case q6k boundary M={M} N={N} K={K} tile={tiles} launches={L.sera_q6k_kernel_launches(M, N, K)}")
     if (M, N) != (4, 4096):
-        assert tile, "case meant for the tile branch"
+        assert tiles[14], "case meant for the tile branch"
+    assert tiles[SPLIT] == ((M, N) not in ((6, 4096), (4, 4096)))
     rng = np.random.default_rng(70 * M + N)
     W = oracle.q6k_weights(rng, N, K)
     xh = outlier_activations(rng, M, K)
@@ -293,7 +297,7 @@ def test_q6k_boundary_tile_branch_of_mmvq_path(torch, linear, M, N):
         y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
         st = linear(q3q4.bind_geometry(qt, K, N), Wx, x, y)
         torch.cuda.synchronize()
-        assert st.kernel_launches == L.sera_q6k_kernel_launches(M, N, K)
+        assert st.kernel_launches == L.sera_q6k_kernel_launches_qt(qt, M, N, K)
         outs[qt] = y.cpu().numpy()
         del Wx
     rows = np.sort(rng.choice(N, 256, replace=False))
