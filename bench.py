@@ -87,6 +87,9 @@ def main():
                     help="skip the tiled-layout A/B cases (kernel traces that group launches by kernel name)")
     ap.add_argument("--tiled", action="store_true",
                     help="with --linear-case: the weights in the tiled Q4_K layout (qtype 268)")
+    ap.add_argument("--q6k", action="store_true",
+                    help="with --linear-case: Q6_K weights (GGUF bytes, or with --split the split layout)")
+    ap.add_argument("--split", action="store_true", help="with --q6k: the split Q6_K layout (qtype 270)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -155,9 +158,26 @@ def main():
 
     if args.linear_case:
         M, N, K = (int(v) for v in args.linear_case.split(","))
-        ws, arr = weight_set(N, K, 7, args.copies)
-        qt = q3q4.QTYPE_Q4K_TILED if args.tiled else q3q4.QTYPE_Q4_K
-        if args.tiled:
+        if args.q6k:
+            qt = q3q4.QTYPE_Q6K_SPLIT if args.split else q3q4.QTYPE_Q6_K
+            ws = []
+            for i in range(args.copies):
+                gen = torch.Generator(device=dev).manual_seed(7 + i)
+                w = torch.randint(0, 256, (N, K // 256, 210), generator=gen, device=dev, dtype=torch.uint8)
+                d = (torch.rand((N, K // 256), generator=gen, device=dev) + 0.5) * 2e-5
+                w[:, :, 208:210] = d.to(torch.float16).view(torch.uint8).view(N, K // 256, 2)
+                if args.split:
+                    sp = torch.empty(w.numel(), dtype=torch.uint8, device=dev)
+                    q3q4.weight_to_device_layout(qt, N, K, w, sp)
+                    w = sp
+                ws.append(w.view(-1))
+            arr = (ctypes.c_void_p * len(ws))(*[w.data_ptr() for w in ws])
+            launches = L.sera_q6k_kernel_launches_qt(qt, M, N, K)
+        else:
+            ws, arr = weight_set(N, K, 7, args.copies)
+            qt = q3q4.QTYPE_Q4K_TILED if args.tiled else q3q4.QTYPE_Q4_K
+            launches = L.sera_q4k_kernel_launches(M, N, K)
+        if args.tiled and not args.q6k:
             tw = []
             for w in ws:
                 t = torch.empty(w.numel(), dtype=torch.uint8, device=dev)
@@ -169,9 +189,9 @@ def main():
         x = activations(M, K, 3)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
         ms = bench_linear(geo, arr, args.copies, x, y, 2, args.steps)
-        log(f"[bench] linear case M={M} N={N} K={K}{' tiled' if args.tiled else ''} "
+        log(f"[bench] linear case M={M} N={N} K={K} qtype {qt} "
             f"({L.q3_cuda_q4k_linear_path_for_batch(M).decode()}, "
-            f"{L.sera_q4k_kernel_launches(M, N, K)} launches, {args.copies} weight copies): "
+            f"{launches} launches, {args.copies} weight copies): "
             f"{ms * 1e3:.2f} us per call over {args.steps} calls")
         return
 
