@@ -43,6 +43,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "sera.c_amd"))
 
 HBM_PEAK_GBS = 8000.0
+WARM_MS = 40.0   # GPU time of the timed launch repeated before each measurement
 INT8_PEAK_TOPS = 5000.0
 
 
@@ -136,24 +137,41 @@ def main():
         x[:, ch] *= 20.0
         return torch.from_numpy(x).to(dev)
 
+    def warm_clocks(run):
+        """run(iters) -> ms of `iters` back-to-back launches. Repeats the timed
+        launch for WARM_MS of GPU time first: from idle the clocks take
+        10-20 ms of load to rise (the Q6_K tile kernel at 512 tokens ran 380
+        us in its first launches, 310 us after a second of load)."""
+        spent, n = 0.0, 2
+        while spent < WARM_MS:
+            spent += run(n)
+            n = min(2 * n, 1024)
+
     def bench_linear(geo, arr, n, x, y, warmup, iters):
         ms = ctypes.c_double()
-        rc = L.sera_q4k_bench_linear(ctypes.byref(geo), arr, n, ctypes.c_void_p(x.data_ptr()),
-                                     x.shape[0], ctypes.c_void_p(y.data_ptr()), sptr, warmup, iters,
-                                     ctypes.byref(ms))
-        if rc != 0:
-            raise RuntimeError(f"bench_linear rc={rc}")
-        return ms.value / iters
+
+        def run(k, w=0):
+            rc = L.sera_q4k_bench_linear(ctypes.byref(geo), arr, n, ctypes.c_void_p(x.data_ptr()),
+                                         x.shape[0], ctypes.c_void_p(y.data_ptr()), sptr, w, k, ctypes.byref(ms))
+            if rc != 0:
+                raise RuntimeError(f"bench_linear rc={rc}")
+            return ms.value
+        warm_clocks(run)
+        return run(iters, warmup) / iters
 
     def bench_kernel(path, arr, n, stage, y, partial, M, N, K, param, warmup, iters):
         avg, tot = ctypes.c_double(), ctypes.c_double()
-        rc = L.sera_q4k_bench_kernel(path, arr, n, ctypes.c_void_p(stage.data_ptr()),
-                                     ctypes.c_void_p(y.data_ptr()),
-                                     ctypes.c_void_p(partial.data_ptr() if partial is not None else 0),
-                                     M, N, K, param, sptr, warmup, iters, ctypes.byref(avg),
-                                     ctypes.byref(tot))
-        if rc != 0:
-            raise RuntimeError(f"bench_kernel rc={rc}: {L.sera_q4k_last_error().decode()}")
+
+        def run(k, w=0):
+            rc = L.sera_q4k_bench_kernel(path, arr, n, ctypes.c_void_p(stage.data_ptr()),
+                                         ctypes.c_void_p(y.data_ptr()),
+                                         ctypes.c_void_p(partial.data_ptr() if partial is not None else 0),
+                                         M, N, K, param, sptr, w, k, ctypes.byref(avg), ctypes.byref(tot))
+            if rc != 0:
+                raise RuntimeError(f"bench_kernel rc={rc}: {L.sera_q4k_last_error().decode()}")
+            return tot.value
+        warm_clocks(run)
+        run(iters, warmup)
         return avg.value, tot.value / iters
 
     if args.linear_case:
@@ -577,13 +595,25 @@ def q6k_cases(torch, q3q4, L, dev, sptr, activations, bench_linear, bench_kernel
             if M >= 5:
                 stage = torch.empty(q3q4.q6k_mmq_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
                 (q3q4.quantize_row_q6k if M <= 8 else q3q4.quantize_mmq_d4)(x, stage)
-                sp = q3q4.q6k_mmq_splits(M, N, K)
-                part = torch.empty(sp * M * N, dtype=torch.float32, device=dev) if sp > 1 else None
-                kavg, _ = bench_kernel(10 if split else 6, arr, copies, stage, y, part, M, N, K, sp, 5,
-                                       iters if M < 512 else 10)
                 tt = L.sera_q6k_mmq_tile_tokens(M, N, K) // 32
-                rows.append(row_of(layout, M, N, K, f"sera_q6k_mmq_kernel<{tt}, 2, {str(split).lower()}>",
-                                   step_ms, kavg))
+                plan = q3q4.q6k_mmq_tail_plan(M, N, K)
+                if plan:
+                    # the tail schedule the dense paths run: slots, then the zeroed counters
+                    dp, pc = plan
+                    nslot = q3q4.q6k_mmq_tail_slot_floats(M, N, K, dp, pc)
+                    part = torch.zeros(nslot + L.sera_q6k_mmq_tiles(M, N, K), dtype=torch.float32, device=dev)
+                    kavg, _ = bench_kernel(17 if split else 16, arr, copies, stage, y, part, M, N, K, dp * 64 + pc,
+                                           5, iters if M < 512 else 10)
+                    sched = f"tail: {dp} whole tiles, the rest in {pc} K pieces"
+                else:
+                    sp = q3q4.q6k_mmq_splits(M, N, K)
+                    part = torch.empty(sp * M * N, dtype=torch.float32, device=dev) if sp > 1 else None
+                    kavg, _ = bench_kernel(10 if split else 6, arr, copies, stage, y, part, M, N, K, sp, 5,
+                                           iters if M < 512 else 10)
+                    sched = f"split-K x{sp}"
+                row = row_of(layout, M, N, K, f"sera_q6k_mmq_kernel<{tt}, 2, {str(split).lower()}>", step_ms, kavg)
+                row["schedule"] = sched
+                rows.append(row)
                 continue
             stage = torch.empty(q3q4.row_stage_layout(M, K)["total"], dtype=torch.uint8, device=dev)
             q3q4.quantize_row(x, stage)
@@ -747,7 +777,7 @@ def decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr, bench_
     side = torch.cuda.Stream()   # graph capture needs a stream other than the null stream
     for label, use_graph, strm in (("", 0, sptr), ("graph_", 1, ctypes.c_void_p(side.cuda_stream))):
         ms = ctypes.c_double()
-        rc = L.sera_q4k_bench_stream(g_arr, w_arr, x_arr, m_arr, y_arr, n, strm, 2, 10, use_graph,
+        rc = L.sera_q4k_bench_stream(g_arr, w_arr, x_arr, m_arr, y_arr, n, strm, 10, 10, use_graph,
                                      ctypes.byref(ms))
         if rc != 0:
             raise RuntimeError(f"bench_stream rc={rc}: {L.sera_q4k_last_error().decode()}")
@@ -783,7 +813,7 @@ def decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr, bench_
     carr = (G.GroupCall * len(fcalls))(*fcalls)
     for label, use_graph, strm in (("fused_", 0, sptr), ("fused_graph_", 1, ctypes.c_void_p(side.cuda_stream))):
         ms = ctypes.c_double()
-        rc = L.sera_q4k_bench_group_stream(carr, len(fcalls), strm, 2, 10, use_graph, ctypes.byref(ms))
+        rc = L.sera_q4k_bench_group_stream(carr, len(fcalls), strm, 10, 10, use_graph, ctypes.byref(ms))
         if rc != 0:
             raise RuntimeError(f"bench_group_stream rc={rc}: {L.sera_q4k_last_error().decode()}")
         torch.cuda.synchronize()
@@ -810,7 +840,8 @@ def decode_stream(torch, q3q4, L, lin, quantized, activations, dev, sptr, bench_
     out["note"] = ("449 q3_cuda_q4k_linear calls (Q8_1 quantize + MMVQ each) per token, issued from C; "
                    "graph_*: the same pass captured once into a HIP graph and replayed; fused_*: the layer as "
                    "4 sera_linear_group calls (input/MLP RMSNorm, SiLU*up and both residual adds fused; q/k/v "
-                   "and gate/up grouped) plus the final-norm LM head, 514 launches per token; 10 timed tokens")
+                   "and gate/up grouped) plus the final-norm LM head, 514 launches per token; 10 timed tokens "
+                   "after 10 untimed")
     return out
 
 

@@ -351,6 +351,24 @@ int sera_q8_1_quantize_row_q6k(const float *X, int M, int K, void *stage, void *
 int sera_q6k_mmq(uint32_t qtype, const void *W, const void *q6k_mmq_stage, float *Y, float *partial, int M, int N,
                  int K, int splits, void *stream);
 int sera_q6k_mmq_splits_for(int M, int N, int K);
+/* The Q6_K tile kernel under the tail schedule (the role of mul_mat_q's
+ * stream-K decomposition, cuda/mmq/mmq.cuh:3641-4352, as for Q4_K): the
+ * first dp_tiles workgroups run one whole output tile each; each of the
+ * other sera_q6k_mmq_tiles() - dp_tiles tiles is cut into `pieces` K
+ * ranges, one workgroup per (tile, range), whose sums the range that ends
+ * last adds in range order (per-tile counters): results repeat bit for bit
+ * and no workgroup waits on another. slots: sera_q6k_mmq_tail_slot_floats()
+ * floats; counters: tiles - dp_tiles ints, zero on entry and after (both
+ * may be NULL when pieces == 1 or dp_tiles == tiles). accum != 0 adds the
+ * product to Y. sera_q6k_mmq_tail_plan returns 1 and the (dp_tiles,
+ * pieces) the dense paths run when they take this schedule (after init;
+ * slots limited to max_slot_floats, 0 = no limit), else 0 (split-K). */
+int sera_q6k_mmq_tail(uint32_t qtype, const void *W, const void *q6k_mmq_stage, float *Y, float *slots, int *counters,
+                      int M, int N, int K, int dp_tiles, int pieces, int accum, void *stream);
+int sera_q6k_mmq_tail_plan(int M, int N, int K, size_t max_slot_floats, int *dp_tiles, int *pieces);
+size_t sera_q6k_mmq_tail_slot_floats(int M, int N, int K, int dp_tiles, int pieces);
+/* Output tiles of the Q6_K tile kernel (token tile x 128 rows). */
+int sera_q6k_mmq_tiles(int M, int N, int K);
 /* Token tile of the Q6_K MMQ kernel for this shape: 32, or 64 when the
  * padded rows divide by 64 and the 64-token grid has at least 1024
  * (tile, super-block) pairs. The two give bit-identical results. */

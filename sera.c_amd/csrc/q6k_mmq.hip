@@ -118,12 +118,26 @@ __device__ __forceinline__ void q6m_barrier_vm() {
 
 }  // namespace
 
-/* Grid (tiles, K splits); splits > 1 write fp32 partials per split. */
-template <int TT, int WPE, bool SPLIT>
+/* Buffer-resource word 3 for raw 32-bit accesses and the sc1 cache-policy
+ * bit of the buffer builtins' aux operand (the tail hand-off's slots). */
+#define Q6M_SLOT_RSRC_FLAGS 0x00020000
+#define Q6M_SC1 16
+
+/* Split-K (TAIL false): grid (tiles, K splits); splits > 1 write fp32
+ * partials per split for a reduce launch.
+ * Tail (TAIL true): the first dp_tiles workgroups each run a whole tile
+ * (XCD-contiguous order); the remaining tiles are cut along K into `pieces`
+ * near-equal ranges, one workgroup per (tile, range), ranges major and
+ * token tiles fastest within one. Each piece stores its sums to its own
+ * slot (`partial`) with sc1 stores, waits for them and bumps the tile's
+ * counter; the piece that completes the count adds the slots in piece
+ * order, stores the tile and resets the counter. No workgroup waits on
+ * another, and the result does not depend on which piece ends last. */
+template <int TT, int WPE, bool SPLIT, bool TAIL = false>
 __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
         const uint8_t *__restrict__ W, const uint16_t *__restrict__ Wd, uint64_t wbytes, const _Float16 *__restrict__ xh,
-        const float *__restrict__ d8t, float *__restrict__ y, float *__restrict__ partial, int M, int Mpad,
-        int N, int K, int kb_per_split, int accum) {
+        const float *__restrict__ d8t, float *__restrict__ y, float *__restrict__ partial, int *__restrict__ counters,
+        int M, int Mpad, int N, int K, int kb_per_split, int dp_tiles, int pieces, int accum) {
     constexpr int BM = 32 * TT;
     /* activation buffers: two for 32 tokens; one for 64 (the 64 KB of a
      * second would leave one workgroup per CU) */
@@ -133,10 +147,29 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
     const int ntt = Mpad / BM, nrt = (N + Q6M_BN - 1) / Q6M_BN;
-    const int tile = q6m_tile_of(blockIdx.x, ntt * nrt);
-    const int n0 = (tile / ntt) * Q6M_BN, m0 = (tile % ntt) * BM;
     const int nb = K / Q4K_QK;
-    const int kb0 = blockIdx.y * kb_per_split, kb1 = min(nb, kb0 + kb_per_split);
+    int tile, kb0, kb1, piece = 0;
+    if constexpr (TAIL) {
+        const int wg = blockIdx.x;
+        if (wg < dp_tiles) {
+            tile = q6m_tile_of(wg, dp_tiles);
+            kb0 = 0;
+            kb1 = nb;
+        } else {
+            /* each range's tiles in the XCD-contiguous order of a whole
+             * grid, as the splits of the split-K grid */
+            const int R = ntt * nrt - dp_tiles;
+            piece = (wg - dp_tiles) / R;
+            tile = dp_tiles + q6m_tile_of(wg - dp_tiles - piece * R, R);
+            kb0 = piece * nb / pieces;
+            kb1 = (piece + 1) * nb / pieces;
+        }
+    } else {
+        tile = q6m_tile_of(blockIdx.x, ntt * nrt);
+        kb0 = blockIdx.y * kb_per_split;
+        kb1 = min(nb, kb0 + kb_per_split);
+    }
+    const int n0 = (tile / ntt) * Q6M_BN, m0 = (tile % ntt) * BM;
     /* GGUF: 210-byte blocks at any 2-byte phase; split: 208-byte aligned
      * blocks (ql, qh, sc) and d from the separate array Wd */
     constexpr uint32_t BB = SPLIT ? Q6K_SPLIT_QBYTES : Q6K_BLOCK_BYTES;
@@ -484,26 +517,73 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
 
     /* lane holds token m0 + 32t + l32 for weight rows
      * n0 + 32*wave + 8(r/4) + 4h + r%4: four consecutive outputs per g */
-    float *out = partial ? partial + (size_t)blockIdx.y * M * N : y;
-    const bool add = !partial && accum;
+    auto store = [&](float *out, bool add) {
 #pragma unroll
-    for (int t = 0; t < TT; t++) {
-        const int m = m0 + 32 * t + l32;
-        if (m >= M) continue;
-        float *row = out + (size_t)m * N;
+        for (int t = 0; t < TT; t++) {
+            const int m = m0 + 32 * t + l32;
+            if (m >= M) continue;
+            float *row = out + (size_t)m * N;
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int col = n0 + 32 * wave + 8 * g + 4 * h;
-            if ((N & 3) == 0 && col < N) {   /* 16-byte aligned, all four in range */
-                q6v4f v = {acc[t][4 * g], acc[t][4 * g + 1], acc[t][4 * g + 2], acc[t][4 * g + 3]};
-                if (add) v += *(const q6v4f *)(row + col);
-                *(q6v4f *)(row + col) = v;
-            } else {
+            for (int g = 0; g < 4; g++) {
+                const int col = n0 + 32 * wave + 8 * g + 4 * h;
+                if ((N & 3) == 0 && col < N) {   /* 16-byte aligned, all four in range */
+                    q6v4f v = {acc[t][4 * g], acc[t][4 * g + 1], acc[t][4 * g + 2], acc[t][4 * g + 3]};
+                    if (add) v += *(const q6v4f *)(row + col);
+                    *(q6v4f *)(row + col) = v;
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (col + e < N) row[col + e] = add ? row[col + e] + acc[t][4 * g + e] : acc[t][4 * g + e];
+                    for (int e = 0; e < 4; e++)
+                        if (col + e < N) row[col + e] = add ? row[col + e] + acc[t][4 * g + e] : acc[t][4 * g + e];
+                }
             }
         }
+    };
+    if constexpr (!TAIL) {
+        if (partial) store(partial + (size_t)blockIdx.y * M * N, false);
+        else store(y, accum != 0);
+        return;
+    } else {
+        if ((int)blockIdx.x < dp_tiles || pieces == 1) {
+            store(y, accum != 0);
+            return;
+        }
+        /* slot (r, p): TT * 16 floats per thread as 16-byte chunks, chunk j
+         * of thread tid at byte (j * 256 + tid) * 16 of the slot; sc1 stores
+         * and loads, as the counter's agent-scope atomics, so no stale line
+         * of another XCD's L2 is read */
+        __shared__ int s_last;
+        const int r = tile - dp_tiles;
+        constexpr int kChunks = TT * 4;
+        constexpr int kSlotBytes = TT * 16 * 256 * 4;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            partial + (size_t)r * pieces * (TT * 16 * 256), (short)0, pieces * kSlotBytes, Q6M_SLOT_RSRC_FLAGS);
+#pragma unroll
+        for (int j = 0; j < kChunks; j++) {
+            const q6v4f v = {acc[j / 4][4 * (j & 3)], acc[j / 4][4 * (j & 3) + 1], acc[j / 4][4 * (j & 3) + 2],
+                             acc[j / 4][4 * (j & 3) + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(q6v4u, v), rs, (j * 256 + tid) * 16,
+                                                   piece * kSlotBytes, Q6M_SC1);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(&counters[r], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == pieces - 1;
+        __syncthreads();
+        if (!s_last) return;
+        if (tid == 0) __hip_atomic_store(&counters[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        /* every piece's sums, this one's included, from the slots in piece
+         * order (this one's stores were acknowledged before the counter moved) */
+        for (int p = 0; p < pieces; p++) {
+#pragma unroll
+            for (int j = 0; j < kChunks; j++) {
+                const q6v4f v = __builtin_bit_cast(
+                    q6v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, (j * 256 + tid) * 16, p * kSlotBytes, Q6M_SC1));
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    acc[j / 4][4 * (j & 3) + e] = p == 0 ? v[e] : acc[j / 4][4 * (j & 3) + e] + v[e];
+            }
+        }
+        store(y, accum != 0);
     }
 }
 
@@ -539,8 +619,8 @@ static hipError_t launch_q6k_mmq(const uint8_t *W, const uint16_t *Wd, uint64_t 
     const int nkb = K / Q4K_QK;
     const int per = (nkb + splits - 1) / splits;
     splits = (nkb + per - 1) / per;
-    hipLaunchKernelGGL((sera_q6k_mmq_kernel<TT, WPE, SPLIT>), dim3(tiles, splits), dim3(256), 0, s, W, Wd, wbytes,
-                       xh, d8t, y, splits > 1 ? partial : nullptr, M, Mpad, N, K, per, accum);
+    hipLaunchKernelGGL((sera_q6k_mmq_kernel<TT, WPE, SPLIT, false>), dim3(tiles, splits), dim3(256), 0, s, W, Wd,
+                       wbytes, xh, d8t, y, splits > 1 ? partial : nullptr, nullptr, M, Mpad, N, K, per, 0, 1, accum);
     if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
     if (splits == 1) return hipSuccess;
     return sera_launch_splitk_reduce_acc(partial, y, (size_t)M * N, splits, accum, s);
@@ -578,4 +658,61 @@ extern "C" hipError_t sera_launch_q6k_mmq_acc(uint32_t qtype, const void *W, con
 extern "C" hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial,
                                           int M, int N, int K, int splits, hipStream_t s) {
     return sera_launch_q6k_mmq_acc(qtype, W, stage, y, partial, M, N, K, splits, 0, s);
+}
+
+/* Output tiles of the Q6_K tile kernel for this shape (tokens x 128 rows). */
+extern "C" int sera_q6k_mmq_tiles(int M, int N, int K) {
+    const int bm = sera_q6k_mmq_tile_tokens(M, N, K);
+    return (sera_q6k_mmq_padded_rows(M) / bm) * ((N + Q6M_BN - 1) / Q6M_BN);
+}
+
+/* Slot floats the tail schedule needs: one tile of sums per (split tile,
+ * piece). */
+extern "C" size_t sera_q6k_mmq_tail_slot_floats(int M, int N, int K, int dp_tiles, int pieces) {
+    const int T = sera_q6k_mmq_tiles(M, N, K);
+    if (pieces <= 1 || dp_tiles >= T) return 0;
+    return (size_t)(T - dp_tiles) * (size_t)pieces * (size_t)sera_q6k_mmq_tile_tokens(M, N, K) * Q6M_BN;
+}
+
+template <int TT, bool SPLIT>
+static hipError_t launch_q6k_tail(const uint8_t *W, const uint16_t *Wd, uint64_t wbytes, const _Float16 *xh,
+                                  const float *d8t, float *y, float *slots, int *counters, int M, int Mpad, int N,
+                                  int K, int dp, int pieces, int accum, hipStream_t s) {
+    const int T = (Mpad / (32 * TT)) * ((N + Q6M_BN - 1) / Q6M_BN);
+    if (pieces <= 1) {
+        dp = T;
+        pieces = 1;
+    }
+    const int grid = dp + (T - dp) * pieces;
+    hipLaunchKernelGGL((sera_q6k_mmq_kernel<TT, 2, SPLIT, true>), dim3(grid), dim3(256), 0, s, W, Wd, wbytes, xh,
+                       d8t, y, slots, counters, M, Mpad, N, K, 0, dp, pieces, accum);
+    return hipGetLastError() == hipSuccess ? hipSuccess : hipErrorLaunchFailure;
+}
+
+/* The tail schedule: dp_tiles whole tiles, the other tiles in `pieces` K
+ * ranges (0 <= dp_tiles <= tiles, 1 <= pieces <= K/256); slots:
+ * sera_q6k_mmq_tail_slot_floats floats; counters: one int per split tile,
+ * zero, left zero. */
+extern "C" hipError_t sera_launch_q6k_mmq_tail_acc(uint32_t qtype, const void *W, const void *stage, float *y,
+                                                   float *slots, int *counters, int M, int N, int K, int dp_tiles,
+                                                   int pieces, int accum, hipStream_t s) {
+    const int Mpad = sera_q6k_mmq_padded_rows(M);
+    const sera_stage_layout L = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K);
+    const char *base = (const char *)stage;
+    const _Float16 *xh = (const _Float16 *)(base + L.qs);
+    const float *d8t = (const float *)(base + L.ds);
+    const uint8_t *w = (const uint8_t *)W;
+    const uint64_t nblk = (uint64_t)N * (uint64_t)(K / Q4K_QK);
+    const bool wide = sera_q6k_mmq_tile_tokens(M, N, K) == 64;
+    if (qtype == SERA_QTYPE_Q6K_SPLIT) {
+        const uint16_t *wd = (const uint16_t *)(w + nblk * Q6K_SPLIT_QBYTES);
+        return wide ? launch_q6k_tail<2, true>(w, wd, nblk * Q6K_SPLIT_QBYTES, xh, d8t, y, slots, counters, M, Mpad,
+                                               N, K, dp_tiles, pieces, accum, s)
+                    : launch_q6k_tail<1, true>(w, wd, nblk * Q6K_SPLIT_QBYTES, xh, d8t, y, slots, counters, M, Mpad,
+                                               N, K, dp_tiles, pieces, accum, s);
+    }
+    return wide ? launch_q6k_tail<2, false>(w, nullptr, nblk * Q6K_BLOCK_BYTES, xh, d8t, y, slots, counters, M, Mpad,
+                                            N, K, dp_tiles, pieces, accum, s)
+                : launch_q6k_tail<1, false>(w, nullptr, nblk * Q6K_BLOCK_BYTES, xh, d8t, y, slots, counters, M, Mpad,
+                                            N, K, dp_tiles, pieces, accum, s);
 }

@@ -81,6 +81,11 @@ hipError_t sera_launch_q6k_mmvq_acc(uint32_t qtype, const void *W, const void *s
                                     int rows, int accum, hipStream_t s);
 int sera_q6k_mmq_splits(int M, int N, int K);
 int sera_q6k_mmq_tile_tokens(int M, int N, int K);
+int sera_q6k_mmq_tiles(int M, int N, int K);
+size_t sera_q6k_mmq_tail_slot_floats(int M, int N, int K, int dp_tiles, int pieces);
+hipError_t sera_launch_q6k_mmq_tail_acc(uint32_t qtype, const void *W, const void *stage, float *y, float *slots,
+                                        int *counters, int M, int N, int K, int dp_tiles, int pieces, int accum,
+                                        hipStream_t s);
 hipError_t sera_launch_q6k_mmq(uint32_t qtype, const void *W, const void *stage, float *y, float *partial, int M,
                                int N, int K, int splits, hipStream_t s);
 hipError_t sera_launch_q6k_mmq_acc(uint32_t qtype, const void *W, const void *stage, float *y, float *partial, int M,

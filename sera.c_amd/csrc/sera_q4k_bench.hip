@@ -89,7 +89,9 @@ hipError_t launch_stream_read(const void *p, size_t bytes, int lpt, uint32_t *si
  * by the zeroed row-group counters). path | 256: the Q4_K paths (0, 1, 4,
  * 8, 12, 13) on weights in the tiled layout (SERA_QTYPE_Q4K_TILED).
  * Path 15: MMQ under the tail schedule (param = dp_tiles * 64 + pieces;
- * partial = slots followed by the zeroed counters).
+ * partial = slots followed by the zeroed counters). Paths 16 / 17: the
+ * Q6_K tile kernel under its tail schedule on GGUF / split-layout weights
+ * (param and partial as path 15).
  * Path 14: the plain streaming read of each weight copy's N*K/256*144 bytes
  * (param = 16-byte loads per thread: 1, 2, 4, 8 or 16; y receives nothing but
  * must be 1 KB of device memory).
@@ -132,6 +134,13 @@ extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int n
                 return sera_launch_q4k_mmq_tail_acc(
                     q4, w, stage, y, partial, (int *)(partial + sera_mmq_tail_slot_floats(M, N, dp, pc)), M, N, K,
                     dp, pc, 0, s);
+            }
+            case 16:
+            case 17: {
+                const int dp = param / 64, pc = param % 64;
+                return sera_launch_q6k_mmq_tail_acc(
+                    path == 16 ? 14u : SERA_QTYPE_Q6K_SPLIT, w, stage, y, partial,
+                    (int *)(partial + sera_q6k_mmq_tail_slot_floats(M, N, K, dp, pc)), M, N, K, dp, pc, 0, s);
             }
             case 14: return launch_stream_read(w, (size_t)N * (K / Q4K_QK) * Q4K_BLOCK_BYTES, param, (uint32_t *)y, s);
             case 4: return sera_launch_q4k_mmq_streamk(

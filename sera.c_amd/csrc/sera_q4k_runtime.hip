@@ -729,6 +729,49 @@ extern "C" int sera_q6k_mmvq(uint32_t qtype, const void *W, const void *row_stag
                ? 0 : fail(-3, "sera_q6k_mmvq: launch failed");
 }
 
+namespace {
+/* Q6_K tile kernel schedule: the tail (every tile cut into K pieces handed
+ * off through counters, no reduce launch) when one round of resident
+ * workgroups (P = 2 per CU) gives each tile at least 4 pieces of at least 5
+ * super-blocks; split-K with its reduce launch otherwise. Measured on
+ * MI355X, split layout, kernel us tail / split-K: down 5120 x 25600 at 8
+ * tokens 41.8 (12 pieces) / 48.5 (16 splits), at 64 61.6 / 67.1, at 128
+ * 97.3 (6) / 102.5 (16); at 512, the same 4 K ranges both ways, 335 / 314
+ * (the hand-off's write-through slot traffic costs more than the reduce);
+ * q 8192 x 5120 at 8 (8 pieces of 2.5 super-blocks) 18.5 / 17.4. */
+bool q6k_tail_plan(int M, int N, int K, size_t cap, int *dp, int *pieces) {
+    if (!g_counters || g_cus <= 0) return false;
+    const int T = sera_q6k_mmq_tiles(M, N, K);
+    const int p = 2 * g_cus / T, nkb = K / Q4K_QK;
+    if (T > kFewtokCounterBase || p < 4 || nkb < 5 * p) return false;
+    const int pc = p < 63 ? p : 63;
+    if (sera_q6k_mmq_tail_slot_floats(M, N, K, 0, pc) > cap) return false;
+    *dp = 0;
+    *pieces = pc;
+    return true;
+}
+
+/* The Q6_K tile kernel on stage (Mpad rows) with cap floats of scratch at
+ * partial: the tail schedule or split-K (splits as sera_q6k_mmq_splits, 1
+ * when M*N % 4 or cap does not allow). */
+hipError_t q6k_tile_launch(uint32_t qt, const void *W, const void *stage, float *Y, float *partial, size_t cap, int M,
+                           int N, int K, int accum, hipStream_t s) {
+    int dp, pieces;
+    if (q6k_tail_plan(M, N, K, cap, &dp, &pieces))
+        return sera_launch_q6k_mmq_tail_acc(qt, W, stage, Y, partial, g_counters, M, N, K, dp, pieces, accum, s);
+    int sp = ((size_t)M * N) % 4 == 0 ? sera_q6k_mmq_splits(M, N, K) : 1;
+    if ((size_t)sp * M * N > cap) sp = 1;
+    return sera_launch_q6k_mmq_acc(qt, W, stage, Y, partial, M, N, K, sp, accum, s);
+}
+
+/* launches of q6k_tile_launch: 1, or 2 with a reduce */
+int q6k_tile_launches(int M, int N, int K) {
+    int dp, pieces;
+    if (q6k_tail_plan(M, N, K, (size_t)-1, &dp, &pieces)) return 1;
+    return (((size_t)M * N) % 4 == 0 && sera_q6k_mmq_splits(M, N, K) > 1) ? 2 : 1;
+}
+}  // namespace
+
 /* Q6_K batches on the MMVQ path (M <= 8) run the MFMA tile kernel on a
  * row-formula stage (the MMVQ arithmetic) instead of the MMVQ kernel where
  * that is faster. Measured on MI355X per shape (kernel us, MMVQ / tile):
@@ -763,11 +806,8 @@ extern "C" int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X,
     const int Mpad = sera_q6k_mmq_padded_rows(M);
     const size_t stage_bytes = mfma ? sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K).total
                                     : sera_row_stage_layout((size_t)M, (size_t)K).total;
-    const int splits = mfma && ((size_t)M * N) % 4 == 0 ? sera_q6k_mmq_splits(M, N, K) : 1;
-    const size_t partial_bytes = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
-    if (stage_bytes + partial_bytes > g_arena_bytes)
-        return fail(-1, "sera_q6k_dense_vec: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
-                    g_arena_bytes);
+    if (stage_bytes > g_arena_bytes)
+        return fail(-1, "sera_q6k_dense_vec: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
     if (timed) record(g_ev.quant_begin, s);
     const hipError_t qe = mfma ? sera_launch_q8_1_q6k_stage(X, M, Mpad, K, 1, g_arena, s)
                                : sera_launch_q8_1_row(X, M, K, g_arena, s);
@@ -775,8 +815,8 @@ extern "C" int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X,
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
     if (mfma) {
-        float *partial = partial_bytes ? (float *)(g_arena + stage_bytes) : nullptr;
-        if (sera_launch_q6k_mmq(qtype, W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
+        if (q6k_tile_launch(qtype, W, g_arena, Y, (float *)(g_arena + stage_bytes),
+                            (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s) != hipSuccess)
             return fail(-3, "sera_q6k_dense_vec: tile kernel launch failed");
     } else if (sera_launch_q6k_mmvq(qtype, W, g_arena, Y, M, N, K, 0, s) != hipSuccess) {
         return fail(-3, "sera_q6k_dense_vec: mmvq launch failed");
@@ -794,7 +834,7 @@ int q6k_splits(int M, int N, int K) {
 extern "C" int sera_q6k_kernel_launches_qt(uint32_t qtype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return 0;
     if (M <= SERA_Q4K_MMVQ_MAX_BATCH && !sera_q6k_vec_uses_tile_qt(qtype, M, N, K)) return 2;
-    return q6k_splits(M, N, K) > 1 ? 3 : 2;
+    return 1 + q6k_tile_launches(M, N, K);
 }
 
 extern "C" int sera_q6k_kernel_launches(int M, int N, int K) { return sera_q6k_kernel_launches_qt(14u, M, N, K); }
@@ -854,6 +894,34 @@ extern "C" int sera_q6k_mmq(uint32_t qtype, const void *W, const void *q6k_mmq_s
                ? 0 : fail(-3, "sera_q6k_mmq: launch failed");
 }
 
+extern "C" int sera_q6k_mmq_tail(uint32_t qtype, const void *W, const void *q6k_mmq_stage, float *Y, float *slots,
+                                 int *counters, int M, int N, int K, int dp_tiles, int pieces, int accum, void *stream) {
+    const char *tag = "sera_q6k_mmq_tail";
+    if (!W || !q6k_mmq_stage || !Y) return fail(-1, "%s: null pointer", tag);
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "%s: bad shape M=%d N=%d K=%d", tag, M, N, K);
+    if (!stage_ok(tag, M, K)) return -1;
+    if (((uintptr_t)W & 15u) != 0) return fail(-1, "%s: W must be 16-byte aligned", tag);
+    if (!q6k_shape_ok(tag, qtype, K)) return -1;
+    const int T = sera_q6k_mmq_tiles(M, N, K);
+    if (dp_tiles < 0 || dp_tiles > T) return fail(-1, "%s: dp_tiles=%d outside 0..%d", tag, dp_tiles, T);
+    if (pieces < 1 || pieces > K / Q4K_QK) return fail(-1, "%s: pieces=%d outside 1..K/256", tag, pieces);
+    if (pieces > 1 && dp_tiles < T && (!slots || !counters))
+        return fail(-1, "%s: a split tail needs slots and counters", tag);
+    return sera_launch_q6k_mmq_tail_acc(qtype, W, q6k_mmq_stage, Y, slots, counters, M, N, K, dp_tiles, pieces,
+                                        accum ? 1 : 0, (hipStream_t)stream) == hipSuccess
+               ? 0 : fail(-3, "%s: launch failed", tag);
+}
+
+extern "C" int sera_q6k_mmq_tail_plan(int M, int N, int K, size_t max_slot_floats, int *dp_tiles, int *pieces) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % Q4K_QK) return fail(-1, "sera_q6k_mmq_tail_plan: bad shape");
+    int dp = 0, pc = 1;
+    const size_t cap = max_slot_floats ? max_slot_floats : (size_t)-1;
+    const int tail = q6k_tail_plan(M, N, K, cap, &dp, &pc) ? 1 : 0;
+    if (dp_tiles) *dp_tiles = tail ? dp : 0;
+    if (pieces) *pieces = tail ? pc : 0;
+    return tail;
+}
+
 extern "C" int sera_q6k_dense(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,
                               void *stream, int timed) {
     if (!check_shape("sera_q6k_dense", W, X, Y, M, N, K)) return -1;
@@ -862,18 +930,15 @@ extern "C" int sera_q6k_dense(uint32_t qtype, const void *W, const float *X, flo
     hipStream_t s = (hipStream_t)stream;
     const int Mpad = sera_q6k_mmq_padded_rows(M);
     const size_t stage_bytes = sera_q6k_mmq_stage_layout((size_t)Mpad, (size_t)K).total;
-    const int splits = q6k_splits(M, N, K);
-    const size_t partial_bytes = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
-    if (stage_bytes + partial_bytes > g_arena_bytes)
-        return fail(-1, "sera_q6k_dense: arena too small (%zu + %zu > %zu)", stage_bytes, partial_bytes,
-                    g_arena_bytes);
-    float *partial = partial_bytes ? (float *)(g_arena + stage_bytes) : nullptr;
+    if (stage_bytes > g_arena_bytes)
+        return fail(-1, "sera_q6k_dense: arena too small (%zu > %zu)", stage_bytes, g_arena_bytes);
     if (timed) record(g_ev.quant_begin, s);
     if (sera_launch_q8_1_q6k_stage(X, M, Mpad, K, 0, g_arena, s) != hipSuccess)
         return fail(-2, "sera_q6k_dense: quantize launch failed");
     if (timed) record(g_ev.quant_end, s);
     if (timed) record(g_ev.kernel_begin, s);
-    if (sera_launch_q6k_mmq(qtype, W, g_arena, Y, partial, M, N, K, splits, s) != hipSuccess)
+    if (q6k_tile_launch(qtype, W, g_arena, Y, (float *)(g_arena + stage_bytes),
+                        (g_arena_bytes - stage_bytes) / sizeof(float), M, N, K, 0, s) != hipSuccess)
         return fail(-3, "sera_q6k_dense: mmq launch failed");
     if (timed) record(g_ev.kernel_end, s);
     return 0;
@@ -1137,7 +1202,6 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
     for (int i = 0; i < count; i++) {
         hipError_t e;
         const int n = N[i];
-        const bool mn4 = ((size_t)M * n) % 4 == 0;
         if (q4 && sera_q4k_mmq_uses_fewtok(M, n, K)) {
             const int rc = fewtok_launch(tag, qt, 1, weights[i], outputs[i], partial, partial_cap, M, n, K, accum, s);
             if (rc) return rc;
@@ -1148,9 +1212,7 @@ extern "C" int sera_linear_group(int count, const void *const *geometries, const
         } else if (!q6_tile) {
             e = sera_launch_q6k_mmvq_acc(qt, weights[i], g_arena, outputs[i], M, n, K, 0, accum, s);
         } else {
-            int sp = mn4 ? sera_q6k_mmq_splits(M, n, K) : 1;
-            if ((size_t)sp * M * n > partial_cap) sp = 1;
-            e = sera_launch_q6k_mmq_acc(qt, weights[i], g_arena, outputs[i], partial, M, n, K, sp, accum, s);
+            e = q6k_tile_launch(qt, weights[i], g_arena, outputs[i], partial, partial_cap, M, n, K, accum, s);
         }
         if (e != hipSuccess) return fail(-3, "%s: product %d launch failed", tag, i);
     }

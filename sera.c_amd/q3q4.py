@@ -148,6 +148,10 @@ def load():
         "sera_weight_upload": ([U32, I, I, P, P, P, SZ, P], I),
         "sera_q6k_mmq_splits_for": ([I, I, I], I),
         "sera_q6k_mmq_tile_tokens": ([I, I, I], I),
+        "sera_q6k_mmq_tiles": ([I, I, I], I),
+        "sera_q6k_mmq_tail": ([U32, P, P, P, P, P, I, I, I, I, I, I, P], I),
+        "sera_q6k_mmq_tail_plan": ([I, I, I, SZ, ctypes.POINTER(I), ctypes.POINTER(I)], I),
+        "sera_q6k_mmq_tail_slot_floats": ([I, I, I, I, I], SZ),
         "sera_candidate_logits": ([I, P, I, I, P, I, P, I, P, P], I),
         "sera_linear_group": ([I, P, P, P, P, P, P, ctypes.c_float, SZ, ctypes.c_uint, P], I),
         "sera_q4k_bench_group_stream": ([P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),
@@ -436,6 +440,30 @@ def weight_upload(qtype, N, K, host_gguf, dst, staging=None, stream=None):
 
 def q6k_mmq_splits(M, N, K):
     return load().sera_q6k_mmq_splits_for(M, N, K)
+
+
+def q6k_mmq_tail(W, stage, out, M, N, K, dp_tiles, pieces, slots=None, counters=None, accum=False, stream=None,
+                 qtype=14):
+    """The Q6_K tile kernel under the tail schedule: dp_tiles whole tiles,
+    the rest cut into `pieces` K ranges; slots (q6k_mmq_tail_slot_floats
+    float32) and counters (tiles - dp_tiles int32, zero before and after)
+    when a tail is split."""
+    _check(load().sera_q6k_mmq_tail(qtype, _ptr(W), _ptr(stage), _ptr(out), _ptr(slots), _ptr(counters), M, N, K,
+                                    dp_tiles, pieces, 1 if accum else 0, _stream(stream)), "sera_q6k_mmq_tail")
+
+
+def q6k_mmq_tail_plan(M, N, K, max_slot_floats=0):
+    """(dp_tiles, pieces) when the dense paths run the tail schedule for this
+    shape (after init), else None (split-K)."""
+    dp, pc = ctypes.c_int(), ctypes.c_int()
+    r = load().sera_q6k_mmq_tail_plan(M, N, K, max_slot_floats, ctypes.byref(dp), ctypes.byref(pc))
+    if r < 0:
+        raise RuntimeError(f"sera_q6k_mmq_tail_plan: {load().sera_q4k_last_error().decode()}")
+    return (dp.value, pc.value) if r else None
+
+
+def q6k_mmq_tail_slot_floats(M, N, K, dp_tiles, pieces):
+    return load().sera_q6k_mmq_tail_slot_floats(M, N, K, dp_tiles, pieces)
 
 
 # ---------------------------------------------------------------------------
