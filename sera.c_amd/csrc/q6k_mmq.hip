@@ -144,7 +144,8 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
     constexpr int XB = TT == 1 ? 2 : 1;
     constexpr int WINST = Q6M_BN * Q6M_WCH * 16 / 1024;   /* load-to-LDS instructions per weight tile */
     __shared__ __attribute__((aligned(16))) Q6MmqSmem<BM, XB> sm;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   /* uniform: scalar LDS addresses and branches */
     const int l32 = lane & 31, h = lane >> 5;
     const int ntt = Mpad / BM, nrt = (N + Q6M_BN - 1) / Q6M_BN;
     const int nb = K / Q4K_QK;
@@ -185,16 +186,36 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
 
     /* weight tile of K step kb -> LDS: row r's block from its 16-byte-aligned
      * start, chunks 0..13 at w[r*240 + 16c]; 1 KB per wave-instruction */
+    /* split layout: 16-byte aligned blocks, so a lane's offset is its row's
+     * chunk plus kb * 208 (the scalar offset); the two chunks past the block
+     * load the row's first chunk again (same line, never read) */
+    constexpr int WI = (WINST + 3) / 4;
+    uint32_t wvo[WI];   /* split layout only (a SPLIT-dependent bound here dropped the host stubs) */
+    if constexpr (SPLIT) {
+#pragma unroll
+        for (int i = 0; i < WI; i++) {
+            const int f = (wave + 4 * i) * 64 + lane;
+            const int r = f / Q6M_WCH, c = f - r * Q6M_WCH;
+            const uint32_t g = (uint32_t)((uint64_t)min(n0 + r, N - 1) * rb - gbase);
+            wvo[i] = g + (c < 13 ? 16u * (uint32_t)c : 0u);
+        }
+    }
     auto issue_w = [&](int kb) {
 #pragma unroll
-        for (int i = 0; i < (WINST + 3) / 4; i++) {
+        for (int i = 0; i < WI; i++) {
             const int inst = wave + 4 * i;
             if (inst < WINST) {
-                const int f = inst * 64 + lane;
-                const int r = f / Q6M_WCH, c = f - r * Q6M_WCH;
-                const uint32_t g = (uint32_t)((uint64_t)min(n0 + r, N - 1) * rb - gbase) + (uint32_t)kb * BB;
-                const uint32_t vo = c < (SPLIT ? 13 : 14) ? (g & ~15u) + 16u * (uint32_t)c : 0x80000000u;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, vo, 0, 0, 0);
+                if constexpr (SPLIT) {
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, wvo[i],
+                                                             kb * (int)BB, 0, 0);
+                } else {
+                    const int f = inst * 64 + lane;
+                    const int r = f / Q6M_WCH, c = f - r * Q6M_WCH;
+                    const uint32_t g = (uint32_t)((uint64_t)min(n0 + r, N - 1) * rb - gbase) + (uint32_t)kb * BB;
+                    const uint32_t vo = c < 14 ? (g & ~15u) + 16u * (uint32_t)c : 0x80000000u;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, vo, 0, 0,
+                                                             0);
+                }
             }
         }
         if constexpr (SPLIT) {
