@@ -147,7 +147,7 @@ def main():
             spent += run(n)
             n = min(2 * n, 1024)
 
-    def bench_linear(geo, arr, n, x, y, warmup, iters):
+    def bench_linear(geo, arr, n, x, y, warmup, iters, warm=True):
         ms = ctypes.c_double()
 
         def run(k, w=0):
@@ -156,7 +156,8 @@ def main():
             if rc != 0:
                 raise RuntimeError(f"bench_linear rc={rc}")
             return ms.value
-        warm_clocks(run)
+        if warm:
+            warm_clocks(run)
         return run(iters, warmup) / iters
 
     def bench_kernel(path, arr, n, stage, y, partial, M, N, K, param, warmup, iters):
@@ -206,7 +207,8 @@ def main():
         geo = q3q4.bind_geometry(qt, K, N)
         x = activations(M, K, 3)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
-        ms = bench_linear(geo, arr, args.copies, x, y, 2, args.steps)
+        # no clock warm-up: counter runs record every dispatch
+        ms = bench_linear(geo, arr, args.copies, x, y, 2, args.steps, warm=False)
         log(f"[bench] linear case M={M} N={N} K={K} qtype {qt} "
             f"({L.q3_cuda_q4k_linear_path_for_batch(M).decode()}, "
             f"{launches} launches, {args.copies} weight copies): "
