@@ -41,8 +41,10 @@
  *     the rows (one 32 x 32 MFMA tile per token tile), two workgroups per
  *     CU. 32 tokens double-buffer the activations per K step; 64 tokens
  *     (the operand build shared by twice the tokens) keep one buffer, in
- *     two K halves, each reloaded while the other is read. Split-K with a
- *     fixed-order reduce when tiles are few.
+ *     two K halves, each reloaded while the other is read.
+ *   - schedules: split-K with a fixed-order reduce launch when tiles are
+ *     few; or the tail schedule (whole tiles, then K pieces handed off
+ *     through per-tile counters, summed in piece order by the last piece).
  */
 #include "sera_launch.h"
 
