@@ -78,7 +78,8 @@ def kernel_of(qtype, M, N, K):
 # with split-K + reduce; stream-K (32-token tiles over a 131328-row matrix);
 # the 64-token tile with split-K + reduce and under the tail schedule (whole
 # tiles, then split tiles handed off through counters);
-# Q6_K MMVQ and the Q6_K tile kernel on the row-formula stage; the few-token
+# Q6_K MMVQ and the Q6_K tile kernel on the row-formula stage, with split-K
+# and under its tail schedule (also on the MMQ stage at 64 tokens); the few-token
 # kernel's persistent grid (more 16-row tiles than resident workgroups); the
 # same kernels on Q4_K weights in the tiled layout (268), where the few-token
 # kernel takes tall matrices from 2 tokens
@@ -97,6 +98,8 @@ CASES = [
     (14, 1, 2048, 5120, "q6k-mmvq"),
     (14, 8, 2048, 5120, "q6k-mmvq"),
     (14, 8, 4096, 5120, "q6k-tile"),
+    (14, 8, 5120, 25600, "q6k-tile+tail"),
+    (14, 64, 5120, 25600, "q6k-tile+tail"),
     (12, 16, 70001, 512, "fewtok-mmq-persistent"),
     (268, 1, 4096, 5120, "dot4"),
     (268, 2, 16384, 5120, "fewtok"),
@@ -111,8 +114,11 @@ CASES = [
 def test_graph_replay_matches_eager(torch, linear, qtype, M, N, K, kernel):
     say(f"case graph qtype={qtype} M={M} N={N} K={K} kernel={kernel}")
     persistent = kernel.endswith("-persistent")
-    kernel = kernel.replace("-persistent", "")
+    tail = kernel.endswith("+tail")
+    kernel = kernel.replace("-persistent", "").replace("+tail", "")
     assert kernel_of(qtype, M, N, K) == kernel, "dispatch moved: choose a case that reaches this kernel"
+    if tail:
+        assert q3q4.q6k_mmq_tail_plan(M, N, K) is not None, "case meant for the Q6_K tail schedule"
     if persistent:
         form = 1 if kernel == "fewtok-mmq" else 0
         assert q3q4.fewtok_splits(M, N, K) == 1 and q3q4.fewtok_grid(form, M, N, K) < q3q4.fewtok_groups(M, N, K), \
