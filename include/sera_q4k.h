@@ -124,13 +124,13 @@ int sera_q4k_vec_uses_fewtok_qt(uint32_t qtype, int M, int N, int K);
 
 /* 1 if a Q6_K call on the MMVQ path (1 <= M <= 8) runs the tile kernel on a
  * row-formula stage for an N x K matrix of GGUF bytes (from 4 tokens at
- * 16384 or more rows, from 6 at 4096-16383 rows, never below 4096), 0 if it
- * runs the Q6_K MMVQ kernel. No counterpart in the reference; a dispatch
- * query. */
+ * 16384 or more rows; at 4096-16383 rows from 6, or 5 when K >= 16384;
+ * never below 4096), 0 if it runs the Q6_K MMVQ kernel. No counterpart in
+ * the reference; a dispatch query. */
 int sera_q6k_vec_uses_tile(int M, int N, int K);
 /* The same per weight layout: qtype 14 as above; SERA_QTYPE_Q6K_SPLIT from
- * 4 tokens at 16384+ rows and from 7 at 4096-16383 (its MMVQ kernel is
- * faster than the GGUF one); 0 for any other qtype. */
+ * 4 tokens at 16384+ rows and at 4096-16383 from 7, or 6 when K >= 16384
+ * (its MMVQ kernel is faster than the GGUF one); 0 for any other qtype. */
 int sera_q6k_vec_uses_tile_qt(uint32_t qtype, int M, int N, int K);
 
 /* Event timings of the last timed dense call, valid after the caller
@@ -300,7 +300,7 @@ const char *sera_q4k_last_error(void);
  * reference quantizes Q6_K decode activations with the same
  * quantize_row_q8_1_cuda call as Q4_K. The dot4 MMVQ kernel on the row
  * stage, or, where sera_q6k_vec_uses_tile_qt says so (tall matrices from 4
- * tokens, 4096-16383 rows from 6 on GGUF bytes and from 7 on the split
+ * tokens, 4096-16383 rows from 5-6 on GGUF bytes and from 6-7 on the split
  * layout), the fp16-MFMA tile kernel on a row-formula Q6_K stage. Replaces q3_mmq_q6_K_dense_vec (cuda/q3_mmq.cu:515-519 over
  * q3_mmq_dense_vec_impl, :408-506). */
 int sera_q6k_dense_vec(uint32_t qtype, const void *W, const float *X, float *Y, int M, int N, int K,

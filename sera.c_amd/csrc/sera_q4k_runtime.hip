@@ -776,19 +776,20 @@ int q6k_tile_launches(int M, int N, int K) {
  * row-formula stage (the MMVQ arithmetic) instead of the MMVQ kernel where
  * that is faster. Measured on MI355X per shape (kernel us, MMVQ / tile):
  * the tile kernel's time is flat in M, MMVQ's grows.
- *   GGUF bytes: LM head 151936 rows: 3 tokens 219 / 222, 4: 247-253 / 220;
- *     q 8192 and down 5120 rows: 5: 20.5 / 20.6, 52.7 / 55.8; 6: 22.1 /
- *     20.2, 58.4 / 54.4; 8: 39.3 / 20.0, 91.3 / 55.0;
- *   split layout (its own MMVQ kernel is faster): LM head 4 tokens 182 /
- *     180, 5: 223 / 177; q and down 6: 16.7 / 18.6, 45.3 / 48.3; 7: 20.1 /
- *     17.8, 52.0 / 48.8;
- *   v 1024 rows: 8 tokens 8.2 / 13.8 (MMVQ at every batch, both layouts). */
+ *   GGUF bytes: LM head 151936 rows: 3 tokens 219 / 222, 4: 200-253 / 202-220;
+ *     q 8192 x 5120: 5: 20.0 / 20.0, 6: 21.6 / 19.5; down 5120 x 25600
+ *     (tail schedule): 4: 46.9 / 47.7, 5: 51.8 / 46.3;
+ *   split layout (its own MMVQ kernel is faster): LM head 4 tokens 178 /
+ *     174; q 6: 16.4 / 18.4, 7: 20.0 / 17.8; down 5: 42.5 / 44.0, 6: 45.4 /
+ *     43.7;
+ *   v 1024 rows: 8 tokens 8.2 / 13.7 (MMVQ at every batch, both layouts).
+ * On 4096-16383 rows a K of 16384 or more (down) lets the tile kernel run
+ * its tail schedule, one token earlier. */
 extern "C" int sera_q6k_vec_uses_tile_qt(uint32_t qtype, int M, int N, int K) {
-    (void)K;
     if (qtype != 14u && qtype != SERA_QTYPE_Q6K_SPLIT) return 0;
     if (M < 1 || M > SERA_Q4K_MMVQ_MAX_BATCH || N <= 0) return 0;
     if (N >= 16384) return M >= 4;
-    if (N >= 4096) return M >= (qtype == 14u ? 6 : 7);
+    if (N >= 4096) return M >= (qtype == 14u ? 6 : 7) - (K >= 16384 ? 1 : 0);
     return 0;
 }
 

@@ -110,21 +110,37 @@ def test_path_for_batch(L):
     assert L.q3_cuda_q4k_linear_path_for_batch(2048) == b"MMQ"
 
 
-def test_host_error_paths_without_device(L):
-    err = ctypes.create_string_buffer(256)
-    assert not L.q3_cuda_q4k_linear_init(-1, 16, 1024, 5120, err, 256)
-    assert b"invalid device" in err.value
-    g = q3q4.bind_geometry(12, 256, 4)
-    st = q3q4.Stats()
-    # null arguments are rejected before anything else
-    assert not L.q3_cuda_q4k_linear(ctypes.byref(g), None, None, 1, None, None, ctypes.byref(st), err, 256)
-    assert b"null argument" in err.value
-    # nothing initialised in this process
-    dummy = ctypes.c_void_p(16)
-    assert not L.q3_cuda_q4k_linear(ctypes.byref(g), dummy, dummy, 1, dummy, None, ctypes.byref(st), err, 256)
-    assert b"not initialized" in err.value
-    assert not L.q3_cuda_q4k_linear_set_workspace(None, 0, err, 256)
-    assert b"workspace too small" in err.value
+# Runs in a child process that has initialised nothing: with the library
+# initialised (as in a process that ran GPU tests first) the call with
+# placeholder pointers would pass the init check and launch on them.
+_UNINIT_CHILD = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import q3q4
+L = q3q4.load()
+err = ctypes.create_string_buffer(256)
+assert not L.q3_cuda_q4k_linear_init(-1, 16, 1024, 5120, err, 256)
+assert b"invalid device" in err.value, err.value
+g = q3q4.bind_geometry(12, 256, 4)
+st = q3q4.Stats()
+# null arguments are rejected before anything else
+assert not L.q3_cuda_q4k_linear(ctypes.byref(g), None, None, 1, None, None, ctypes.byref(st), err, 256)
+assert b"null argument" in err.value, err.value
+# nothing initialised in this process
+dummy = ctypes.c_void_p(16)
+assert not L.q3_cuda_q4k_linear(ctypes.byref(g), dummy, dummy, 1, dummy, None, ctypes.byref(st), err, 256)
+assert b"not initialized" in err.value, err.value
+assert not L.q3_cuda_q4k_linear_set_workspace(None, 0, err, 256)
+assert b"workspace too small" in err.value, err.value
+print("ok")
+"""
+
+
+def test_host_error_paths_without_device():
+    import sys as _sys
+    pkg = os.path.dirname(q3q4.__file__)
+    r = subprocess.run([_sys.executable, "-c", _UNINIT_CHILD, pkg], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
 
 
 def test_kernel_entry_points_validate_on_host(L):
@@ -362,23 +378,24 @@ def test_q6k_mmq_token_tile_rule(L):
 
 def test_q6k_vec_dispatch_rule(L):
     """Q6_K on the MMVQ path: the tile kernel on tall matrices from 4 tokens,
-    on 4096-16383 rows from 6 (GGUF bytes) or 7 (split layout), never below
-    4096 rows; launch counts follow."""
+    on 4096-16383 rows from 6 (GGUF bytes) or 7 (split layout), one token
+    earlier when K >= 16384 (down), never below 4096 rows; launch counts
+    follow."""
     f = L.sera_q6k_vec_uses_tile
     assert [f(M, 151936, 5120) for M in range(1, 9)] == [0, 0, 0, 1, 1, 1, 1, 1]
-    for N, K in ((5120, 25600), (8192, 5120)):
-        assert [f(M, N, K) for M in range(1, 9)] == [0, 0, 0, 0, 0, 1, 1, 1]
+    assert [f(M, 8192, 5120) for M in range(1, 9)] == [0, 0, 0, 0, 0, 1, 1, 1]
+    assert [f(M, 5120, 25600) for M in range(1, 9)] == [0, 0, 0, 0, 1, 1, 1, 1]   # down: tail schedule
     assert [f(M, 1024, 5120) for M in range(1, 9)] == [0] * 8
     g = L.sera_q6k_vec_uses_tile_qt
     S = q3q4.QTYPE_Q6K_SPLIT
     for N, K in ((151936, 5120), (5120, 25600), (8192, 5120), (1024, 5120)):
         assert [g(14, M, N, K) for M in range(0, 10)] == [f(M, N, K) for M in range(0, 10)]
     assert [g(S, M, 151936, 5120) for M in range(1, 9)] == [0, 0, 0, 1, 1, 1, 1, 1]
-    for N, K in ((5120, 25600), (8192, 5120)):
-        assert [g(S, M, N, K) for M in range(1, 9)] == [0, 0, 0, 0, 0, 0, 1, 1]
+    assert [g(S, M, 8192, 5120) for M in range(1, 9)] == [0, 0, 0, 0, 0, 0, 1, 1]
+    assert [g(S, M, 5120, 25600) for M in range(1, 9)] == [0, 0, 0, 0, 0, 1, 1, 1]
     assert [g(S, M, 1024, 5120) for M in range(1, 9)] == [0] * 8
     assert g(12, 8, 151936, 5120) == 0 and g(S, 9, 151936, 5120) == 0
-    assert L.sera_q6k_kernel_launches_qt(S, 6, 5120, 25600) == 2    # MMVQ on the split layout
-    assert L.sera_q6k_kernel_launches_qt(14, 6, 5120, 25600) == L.sera_q6k_kernel_launches(6, 5120, 25600)
+    assert L.sera_q6k_kernel_launches_qt(S, 6, 8192, 5120) == 2      # MMVQ on the split layout
+    assert L.sera_q6k_kernel_launches_qt(14, 6, 8192, 5120) == L.sera_q6k_kernel_launches(6, 8192, 5120)
     assert L.sera_q6k_kernel_launches(8, 1024, 5120) == 2          # MMVQ
-    assert L.sera_q6k_kernel_launches(5, 5120, 25600) == 2         # MMVQ
+    assert L.sera_q6k_kernel_launches(4, 5120, 25600) == 2         # MMVQ
