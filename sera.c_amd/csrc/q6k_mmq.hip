@@ -60,6 +60,12 @@ typedef float q6v4f __attribute__((ext_vector_type(4)));
 #define Q6M_BN 128
 #define Q6M_WCH 15    /* 16-byte LDS chunks per weight row and K step: a 210-byte block at any
                          2-byte phase needs 14; the 15th spreads row starts over more banks */
+/* GGUF bytes: row r of the tile sits at slot 15 r + (r + 16) / 32, one pad
+ * slot after row 15 of each 32. A wave's rows r and r + 16 then start 4
+ * banks apart instead of on the same bank, and consecutive rows, whose
+ * 2-byte phases differ by 8 bytes when K / 256 = 4 mod 8 (K = 5120,
+ * 25600), interleave, so a half-wave's dword reads of its 32 rows' runs
+ * hit 32 distinct banks. */
 
 template <int BM, int XB>
 struct alignas(16) Q6MmqSmem {
@@ -67,7 +73,7 @@ struct alignas(16) Q6MmqSmem {
     alignas(16) float d8[2][8][BM];
     alignas(16) float dw[4][32];   /* each wave's 32 row scales d of the K step */
     alignas(16) uint32_t wd[Q6M_BN];   /* split layout: the dword holding each row's d */
-    alignas(16) uint8_t w[Q6M_BN * Q6M_WCH * 16];
+    alignas(16) uint8_t w[31 * 1024];   /* Q6M_BN rows of Q6M_WCH chunks, one pad chunk per 32 rows on GGUF bytes */
 };
 
 namespace {
@@ -144,8 +150,12 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
     /* activation buffers: two for 32 tokens; one for 64 (the 64 KB of a
      * second would leave one workgroup per CU) */
     constexpr int XB = TT == 1 ? 2 : 1;
-    constexpr int WINST = Q6M_BN * Q6M_WCH * 16 / 1024;   /* load-to-LDS instructions per weight tile */
+    /* weight-tile slots (16-byte chunks): GGUF bytes add one pad slot after
+     * row 15 of every 32 (the row placement above) */
+    constexpr int WSLOTS = Q6M_BN * Q6M_WCH + (SPLIT ? 0 : Q6M_BN / 32);
+    constexpr int WINST = (WSLOTS + 63) / 64;   /* load-to-LDS instructions per weight tile */
     __shared__ __attribute__((aligned(16))) Q6MmqSmem<BM, XB> sm;
+    static_assert(WINST * 1024 <= (int)sizeof(sm.w), "weight tile");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   /* uniform: scalar LDS addresses and branches */
     const int l32 = lane & 31, h = lane >> 5;
@@ -191,8 +201,11 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
     /* split layout: 16-byte aligned blocks, so a lane's offset is its row's
      * chunk plus kb * 208 (the scalar offset); the two chunks past the block
      * load the row's first chunk again (same line, never read) */
-    constexpr int WI = (WINST + 3) / 4;
-    uint32_t wvo[WI];   /* split layout only (a SPLIT-dependent bound here dropped the host stubs) */
+    /* tile loads per wave: a literal, since an array bound that depends on
+     * SPLIT here made the host pass drop the kernel stubs */
+    constexpr int WI = 8;
+    static_assert((WINST + 3) / 4 == WI, "tile loads per wave");
+    uint32_t wvo[WI];   /* split layout only */
     if constexpr (SPLIT) {
 #pragma unroll
         for (int i = 0; i < WI; i++) {
@@ -211,10 +224,16 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, wvo[i],
                                                              kb * (int)BB, 0, 0);
                 } else {
+                    /* slot f: 32-row group f / 481, pad slot 240 of each */
                     const int f = inst * 64 + lane;
-                    const int r = f / Q6M_WCH, c = f - r * Q6M_WCH;
-                    const uint32_t g = (uint32_t)((uint64_t)min(n0 + r, N - 1) * rb - gbase) + (uint32_t)kb * BB;
-                    const uint32_t vo = c < 14 ? (g & ~15u) + 16u * (uint32_t)c : 0x80000000u;
+                    const int grp = f / (32 * Q6M_WCH + 1), q = f - grp * (32 * Q6M_WCH + 1);
+                    const int qq = q < 16 * Q6M_WCH ? q : q - 1;
+                    const int rr = qq / Q6M_WCH, c = qq - rr * Q6M_WCH;
+                    const int r = 32 * grp + rr;
+                    const bool live = f < WSLOTS && q != 16 * Q6M_WCH && c < 14;
+                    const uint32_t g = (uint32_t)((uint64_t)min(n0 + min(r, Q6M_BN - 1), N - 1) * rb - gbase) +
+                                       (uint32_t)kb * BB;
+                    const uint32_t vo = live ? (g & ~15u) + 16u * (uint32_t)c : 0x80000000u;
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, vo, 0, 0,
                                                              0);
                 }
@@ -302,7 +321,8 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
         const int kn = min(kb + 1, kb1 - 1);
         /* the lane's runs of this block from LDS: ql[64j + 32p + 16h + 0..15],
          * qh[32j + 16h + 0..15], bytes 192..207 (scales) and d */
-        const uint32_t base = (uint32_t)wr * (Q6M_WCH * 16) + (SPLIT ? 0u : ((rowg + (uint32_t)kb * BB) & 15u));
+        const uint32_t base = SPLIT ? (uint32_t)wr * (Q6M_WCH * 16)
+                                    : (uint32_t)(wr * Q6M_WCH + ((wr + 16) >> 5)) * 16u + ((rowg + (uint32_t)kb * BB) & 15u);
         const uint32_t sh = (base & 2u) * 8u;
         q6v4u QL[4], QH[2], SC;
         uint32_t dword = 0;
