@@ -221,25 +221,42 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     uint8_t *wbuf = ft_smem + fewtok_lds_bytes(chunk, TOK) + (size_t)wave * 2 * Ws::BUF;
     /* per copy instruction i: the lane's source in the chunk's first
      * sub-chunk and its super-block there */
-    const uint8_t *wsp[WS ? Ws::NI : 1];
+    /* The tile's first row and block as a wave-uniform base, each lane's
+     * slot as a 32-bit offset from it (rows of a 16-row tile lie in one tile
+     * of the tiled layout). The slot's (row, piece) advance by (3, 10) or
+     * (4, -8) per instruction (64 = 3 * 18 + 10): a few full-rate adds per
+     * instruction ahead of the first copy, where a division and 64-bit
+     * offsets per instruction measured slower. */
+    /* Waves whose tile lies past the last row (N < 16 NW, or the last
+     * workgroup of a grid) read the last tile's rows instead; they are
+     * never stored. */
+    const int wrow0 = min(16 * tile, 16 * ((N - 1) / 16));
+    const uint8_t *wtile = W + q4k_block_offset(tiled, (size_t)wrow0, kb0, nkb);
+    uint32_t wso[WS ? Ws::NI : 1];
     int wsu[WS ? Ws::NI : 1];
     if constexpr (WS > 0) {
+        static_assert(Ws::RS == 18, "per-instruction slot step laid out for 18 slots per row");
+        const int rmax = min(N - 1 - wrow0, 15);   /* 0..15 */
+        const uint32_t rstride = (uint32_t)q4k_row_stride(tiled, nkb);
+        int r = lane / 18, o = lane - 18 * r;
 #pragma unroll
         for (int i = 0; i < Ws::NI; i++) {
-            const int q = 64 * i + lane;
-            const int r = min(q / Ws::RS, 15), o = min(q - (q / Ws::RS) * Ws::RS, 9 * WS - 1);
-            wsu[i] = o / 9;
-            wsp[i] = W + q4k_block_offset(tiled, min(16 * tile + r, N - 1), kb0 + min(wsu[i], C - 1), nkb) +
-                     16 * (o - 9 * wsu[i]);
+            const int u = o >= 9 ? 1 : 0;
+            wsu[i] = u;
+            wso[i] = (uint32_t)min(r, rmax) * rstride + (uint32_t)(min(u, C - 1) * bstride + 16 * (o - 9 * u));
+            o += 10;
+            r += o >= 18 ? 4 : 3;
+            o -= o >= 18 ? 18 : 0;
         }
     }
     auto ws_issue = [&](int sc, int bf) {
         const bool whole = WS * sc + WS <= C;
+        const uint8_t *wsb = wtile + (size_t)(whole ? WS * sc : 0) * bstride;
 #pragma unroll
         for (int i = 0; i < Ws::NI; i++) {
             /* a whole sub-chunk moves every lane alike; the last one clamps */
-            const int du = whole ? WS * sc : min(WS * sc + wsu[i], C - 1) - min(wsu[i], C - 1);
-            __builtin_amdgcn_global_load_lds((ft_global_cvoid *)(wsp[i] + (size_t)du * bstride),
+            const uint32_t du = whole ? 0u : (uint32_t)((min(WS * sc + wsu[i], C - 1) - min(wsu[i], C - 1)) * bstride);
+            __builtin_amdgcn_global_load_lds((ft_global_cvoid *)(wsb + (wso[i] + du)),
                                              (ft_lds_void *)(wbuf + bf * Ws::BUF + 1024 * i), 16, 0, 0);
         }
     };
@@ -271,13 +288,26 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
          * constant offset from one base. */
         constexpr int XS = SERA_FEWTOK_XSLOTS;
         const int slots = C * TOK * XS;
-        for (int base = wave * 64; base < slots; base += NW * 64) {
-            const int q = base + lane;
-            const int u = q / (TOK * XS), r = q - u * (TOK * XS), t = r / XS, col = min(r - t * XS, 15);
-            const int8_t *src = xq + (size_t)min(t, M - 1) * K + (size_t)(kb0 + u) * Q4K_QK + 16 * col;
+        /* slot q = (u, t, col) with q = (u TOK + t) XS + col, decoded once
+         * and advanced by NW * 64 slots per pass with carries; the source
+         * is a 32-bit offset from the chunk's first column */
+        constexpr int STEP = NW * 64, SU = STEP / (TOK * XS), ST = STEP % (TOK * XS) / XS, SC = STEP % XS;
+        const int8_t *xbase = xq + (size_t)kb0 * Q4K_QK;
+        int q = wave * 64 + lane;
+        int u = q / (TOK * XS), t = q % (TOK * XS) / XS, col = q % XS;
+        for (int base = wave * 64; base < slots; base += STEP) {
+            const uint32_t off = (uint32_t)(min(t, M - 1) * K + u * Q4K_QK + 16 * min(col, 15));
             if (q < slots)
-                __builtin_amdgcn_global_load_lds((ft_global_cvoid *)src, (ft_lds_void *)(xs + (size_t)base * 16), 16, 0,
-                                                 0);
+                __builtin_amdgcn_global_load_lds((ft_global_cvoid *)(xbase + off), (ft_lds_void *)(xs + (size_t)base * 16),
+                                                 16, 0, 0);
+            q += STEP;
+            col += SC;
+            const int cc = col >= XS ? 1 : 0;
+            col -= cc * XS;
+            t += ST + cc;
+            const int tc = t >= TOK ? 1 : 0;
+            t -= tc * TOK;
+            u += SU + tc;
         }
         /* scales, transposed to [u][sub-block][token]: all loads first, then
          * the LDS writes. FORM 0: float4 (d_2p, d_2p+1, dS_2p, dS_2p+1) per
@@ -291,12 +321,13 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
 #pragma unroll
         for (int r = 0; r < SCR; r++) {
             const int i = min(tid + r * NW * 64, items - 1);
+            /* 32-bit element offsets from the chunk's first scales */
             if (FORM == 0) {
                 const int u = i / (TOK * 4), t = (i >> 2) % TOK, p = i & 3;
-                f[r] = ((const ft_v4u *)xsc)[(size_t)min(t, M - 1) * (K / 64) + (size_t)(kb0 + u) * 4 + p];
+                f[r] = ((const ft_v4u *)xsc + (size_t)kb0 * 4)[(uint32_t)(min(t, M - 1) * (K / 64) + u * 4 + p)];
             } else {
                 const int u = i / (TOK * 2), t = (i >> 1) % TOK, p = i & 1;
-                f[r] = ((const ft_v4u *)xsc)[(size_t)min(t, M - 1) * (K / 128) + (size_t)(kb0 + u) * 2 + p];
+                f[r] = ((const ft_v4u *)xsc + (size_t)kb0 * 2)[(uint32_t)(min(t, M - 1) * (K / 128) + u * 2 + p)];
             }
         }
 #pragma unroll
