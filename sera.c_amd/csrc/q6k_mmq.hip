@@ -254,36 +254,55 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
      * Two buffers: token rows of 512 bytes, chunk c of token t in column
      * c ^ (t & 31). One buffer: two K halves of BM rows of 256 bytes (chunk c
      * in half c >> 4, column (c & 15) ^ (t & 15)), loaded half by half. */
+    /* Buffer loads to LDS from resources over the tile's token rows: the
+     * lane's part of each address is a loop-invariant vector offset, the
+     * token row and K step a scalar offset, so the K loop spends no vector
+     * instructions on addresses (global loads from 64-bit lane pointers
+     * took one 64-bit add each). */
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16 *>(xh + (size_t)m0 * K), (short)0, (int)(2u * (uint32_t)BM * (uint32_t)K), Q6M_RSRC_FLAGS);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(d8t + m0), (short)0, (int)(4u * (uint32_t)(8 * nb) * (uint32_t)Mpad), Q6M_RSRC_FLAGS);
+    /* activation loads per wave and K step (or K half); a literal array
+     * bound, as with the tile loads below */
+    constexpr int XI = 4;
+    static_assert((XB == 1 ? BM / 16 : BM / 8) == XI, "activation loads per wave");
+    uint32_t xoff[XI];
+#pragma unroll
+    for (int i = 0; i < XI; i++) {
+        const int inst = wave + 4 * i;
+        if constexpr (XB == 1) {
+            const int tl = lane >> 4, tok = 4 * inst + tl;
+            xoff[i] = (uint32_t)(2 * (tl * K + 8 * ((lane & 15) ^ (tok & 15))));
+        } else {
+            const int tl = lane >> 5, tok = 2 * inst + tl;
+            xoff[i] = (uint32_t)(2 * (tl * K + 8 * ((lane & 31) ^ (tok & 31))));
+        }
+    }
     auto issue_xh = [&](int kb, int half) {
 #pragma unroll
         for (int i = 0; i < BM / 16; i++) {
             const int inst = wave + 4 * i;          /* 1 KB = four tokens' half rows */
-            const int tok = 4 * inst + (lane >> 4), col = lane & 15;
-            const _Float16 *src = xh + (size_t)(m0 + tok) * K + (size_t)kb * Q4K_QK + 128 * half +
-                                  8 * (col ^ (tok & 15));
-            __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src,
-                                             (q6m_lds_void *)&sm.xs[0][0][(half * BM + 4 * inst) * 128], 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (q6m_lds_void *)&sm.xs[0][0][(half * BM + 4 * inst) * 128], 16,
+                                                     xoff[i], 2 * (4 * inst * K + kb * Q4K_QK + 128 * half), 0, 0);
         }
     };
     auto issue_xs = [&](int kb, int buf) {
 #pragma unroll
         for (int i = 0; i < BM / 8; i++) {
             const int inst = wave + 4 * i;          /* 1 KB = two tokens */
-            const int tok = 2 * inst + (lane >> 5), col = lane & 31;
-            const _Float16 *src = xh + (size_t)(m0 + tok) * K + (size_t)kb * Q4K_QK + 8 * (col ^ (tok & 31));
-            __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src, (q6m_lds_void *)&sm.xs[buf][2 * inst][0], 16,
-                                             0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (q6m_lds_void *)&sm.xs[buf][2 * inst][0], 16, xoff[i],
+                                                     2 * (2 * inst * K + kb * Q4K_QK), 0, 0);
         }
     };
     /* by the last waves, which issue one weight-tile load fewer */
+    constexpr int W0 = 4 - BM / 32;
+    const uint32_t d8off = (uint32_t)(4 * ((((wave - W0) * 256 + lane * 4) / BM) * Mpad + ((wave - W0) * 256 + lane * 4) % BM));
     auto issue_d8 = [&](int kb, int buf) {
-        constexpr int W0 = 4 - BM / 32;
         if (wave >= W0) {
-            const int f = (wave - W0) * 256 + lane * 4;    /* float index in [8][BM] */
-            const int b = f / BM, t = f % BM;
-            const float *src = d8t + ((size_t)kb * 8 + b) * Mpad + m0 + t;
-            __builtin_amdgcn_global_load_lds((q6m_global_cvoid *)src,
-                                             (q6m_lds_void *)&sm.d8[buf][0][(wave - W0) * 256], 16, 0, 0);
+            /* float (b, t) of [8][BM], f = (wave - W0) * 256 + 4 lane = b BM + t */
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (q6m_lds_void *)&sm.d8[buf][0][(wave - W0) * 256], 16, d8off,
+                                                     4 * kb * 8 * Mpad, 0, 0);
         }
     };
 
