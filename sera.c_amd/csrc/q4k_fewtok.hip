@@ -298,8 +298,8 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
         for (int base = wave * 64; base < slots; base += STEP) {
             const uint32_t off = (uint32_t)(min(t, M - 1) * K + u * Q4K_QK + 16 * min(col, 15));
             if (q < slots)
-                __builtin_amdgcn_global_load_lds((ft_global_cvoid *)(xbase + off), (ft_lds_void *)(xs + (size_t)base * 16),
-                                                 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((ft_global_cvoid *)(xbase + off),
+                                                 (ft_lds_void *)(xs + (size_t)base * 16), 16, 0, 0);
             q += STEP;
             col += SC;
             const int cc = col >= XS ? 1 : 0;

@@ -295,12 +295,14 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                                                      2 * (2 * inst * K + kb * Q4K_QK), 0, 0);
         }
     };
-    /* by the last waves, which issue one weight-tile load fewer */
+    /* by the last waves, which issue one weight-tile load fewer; the lane's
+     * four floats (b, t..t+3) of [8][BM] sit at f = (wave - W0) * 256 +
+     * 4 lane = b BM + t, and at b Mpad + t in the stage's K step */
     constexpr int W0 = 4 - BM / 32;
-    const uint32_t d8off = (uint32_t)(4 * ((((wave - W0) * 256 + lane * 4) / BM) * Mpad + ((wave - W0) * 256 + lane * 4) % BM));
+    const int d8f = (wave - W0) * 256 + lane * 4;
+    const uint32_t d8off = (uint32_t)(4 * ((d8f / BM) * Mpad + d8f % BM));
     auto issue_d8 = [&](int kb, int buf) {
         if (wave >= W0) {
-            /* float (b, t) of [8][BM], f = (wave - W0) * 256 + 4 lane = b BM + t */
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (q6m_lds_void *)&sm.d8[buf][0][(wave - W0) * 256], 16, d8off,
                                                      4 * kb * 8 * Mpad, 0, 0);
         }
@@ -341,7 +343,8 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
         /* the lane's runs of this block from LDS: ql[64j + 32p + 16h + 0..15],
          * qh[32j + 16h + 0..15], bytes 192..207 (scales) and d */
         const uint32_t base = SPLIT ? (uint32_t)wr * (Q6M_WCH * 16)
-                                    : (uint32_t)(wr * Q6M_WCH + ((wr + 16) >> 5)) * 16u + ((rowg + (uint32_t)kb * BB) & 15u);
+                                    : (uint32_t)(wr * Q6M_WCH + ((wr + 16) >> 5)) * 16u +
+                                          ((rowg + (uint32_t)kb * BB) & 15u);
         const uint32_t sh = (base & 2u) * 8u;
         q6v4u QL[4], QH[2], SC;
         uint32_t dword = 0;
