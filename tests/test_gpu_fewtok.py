@@ -83,7 +83,10 @@ def run_fewtok(torch, Wd, stage, M, N, K, chunk, y=None, accum=False, form=0):
 
 # (N, K): ragged N (not a multiple of 64 or 128 rows), one super-block, K
 # below and above the 20-super-block chunk limit, the wide-N plan (8 waves)
-FEWTOK_SHAPES = [(16, 256), (1000, 512), (300, 5120), (64, 25600), (203, 2304), (16500, 1024)]
+# (64, 25600) and (100, 25600): 8-wave workgroups with staged weights whose
+# last waves own no rows (and, at 100, a ragged last tile); they read the last
+# tile's rows and store nothing
+FEWTOK_SHAPES = [(16, 256), (1000, 512), (300, 5120), (64, 25600), (100, 25600), (203, 2304), (16500, 1024)]
 
 
 @pytest.mark.parametrize("N,K", FEWTOK_SHAPES)
