@@ -113,7 +113,7 @@ __device__ __forceinline__ uint32_t q6m_raw(uint32_t ql, uint32_t qh) {
 __device__ __forceinline__ int q6m_sext8(uint32_t w, int sh) { return (int)(w << (24 - sh)) >> 24; }
 
 /* Workgroup barriers that wait only for what they name: this wave's LDS reads
- * (and, for the second, all but its VM most recent global loads), never the
+ * (and, for the second, all but its VM most recent vector memory loads), never the
  * vmcnt(0) a __syncthreads adds. The memory clobber keeps the compiler from
  * moving loads or LDS accesses across. */
 __device__ __forceinline__ void q6m_barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
