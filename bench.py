@@ -167,6 +167,7 @@ def main():
             rc = L.sera_q4k_bench_kernel(path, arr, n, ctypes.c_void_p(stage.data_ptr()),
                                          ctypes.c_void_p(y.data_ptr()),
                                          ctypes.c_void_p(partial.data_ptr() if partial is not None else 0),
+                                         partial.numel() * partial.element_size() // 4 if partial is not None else 0,
                                          M, N, K, param, sptr, w, k, ctypes.byref(avg), ctypes.byref(tot))
             if rc != 0:
                 raise RuntimeError(f"bench_kernel rc={rc}: {L.sera_q4k_last_error().decode()}")

@@ -493,10 +493,12 @@ int sera_q4k_bench_linear(const void *geometry, const void *const *weights, int 
  * a Q6_K MMQ stage, 7 / 8 = selected-row LM head on Q6_K / Q4_K rows with
  * stage = fp32 hidden [M][K], partial = the M*param candidate ids, param =
  * candidates per branch): `iters` launches back to back between one event pair
- * on `stream`; *avg_kernel_ms = pair time / iters, *elapsed_ms = pair time. */
+ * on `stream`; *avg_kernel_ms = pair time / iters, *elapsed_ms = pair time.
+ * partial_floats is the size of `partial`; a path whose scratch does not fit
+ * returns -2 without launching. */
 int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights, const void *stage,
-                          float *Y, float *partial, int M, int N, int K, int param, void *stream,
-                          int warmup, int iters, double *avg_kernel_ms, double *elapsed_ms);
+                          float *Y, float *partial, size_t partial_floats, int M, int N, int K, int param,
+                          void *stream, int warmup, int iters, double *avg_kernel_ms, double *elapsed_ms);
 
 /* `reps` timed passes (after `warmup`) over a sequence of
  * q3_cuda_q4k_linear calls: geometries[i] (q3_q4_linear_geometry*),

@@ -43,6 +43,8 @@ int sera_mmq_bm(int M);
 int sera_mmq_wgs_per_cu(int M);
 int sera_mmq_splits(int M, int N, int K);
 int sera_mmq_padded_rows(int M);
+/* Sets the message sera_q4k_last_error returns; returns code. */
+int sera_report_error(int code, const char *msg);
 int sera_mmq_tiles(int M, int N);
 int sera_mmq_slot_floats(int M);
 hipError_t sera_launch_splitk_reduce(const float *partial, float *y, size_t n, int splits, hipStream_t s);

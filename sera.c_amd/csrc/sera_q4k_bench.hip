@@ -8,6 +8,9 @@
  * weight read an HBM read.
  */
 #include "sera_launch.h"
+
+#include <stdio.h>
+
 #include "../../include/q3_q4_linear.h"
 #include "../../include/sera_q4k.h"
 
@@ -95,18 +98,53 @@ hipError_t launch_stream_read(const void *p, size_t bytes, int lpt, uint32_t *si
  * Path 14: the plain streaming read of each weight copy's N*K/256*144 bytes
  * (param = 16-byte loads per thread: 1, 2, 4, 8 or 16; y receives nothing but
  * must be 1 KB of device memory).
+ * partial_floats: the size of `partial`; a path whose scratch (split-K
+ * sums, slots and counters, candidate ids) does not fit returns -2.
  * `iters` launches back to back on `stream` between one pair of events, so
  * no timing packet sits between two launches; avg_kernel_ms is the pair's
  * elapsed time over iters (each launch's duration plus the dispatch gap to
  * the next one), elapsed_ms the pair's elapsed time. */
+/* Floats of `partial` a path writes or reads: split-K partial sums, stream-K
+ * or tail slots followed by the tile counters, or the candidate ids. */
+static size_t bench_partial_floats(int path, int M, int N, int K, int param) {
+    switch (path) {
+        case 1:
+        case 6:
+        case 10: return param > 1 ? (size_t)M * N * param : 0;
+        case 4: return (size_t)2 * param * sera_mmq_slot_floats(M) + (size_t)sera_mmq_tiles(M, N);
+        case 7:
+        case 8:
+        case 11: return (size_t)M * param;
+        case 12:
+        case 13: {
+            const int sp = sera_fewtok_splits(M, N, K, param);
+            return sp > 1 ? (size_t)sp * M * N + (size_t)sera_fewtok_groups(M, N, K) : 0;
+        }
+        case 15: return sera_mmq_tail_slot_floats(M, N, param / 64, param % 64) + (size_t)sera_mmq_tiles(M, N);
+        case 16:
+        case 17:
+            return sera_q6k_mmq_tail_slot_floats(M, N, K, param / 64, param % 64) +
+                   (size_t)sera_q6k_mmq_tiles(M, N, K);
+        default: return 0;
+    }
+}
+
 extern "C" int sera_q4k_bench_kernel(int path, const void *const *weights, int nweights,
-                                     const void *stage, float *y, float *partial, int M, int N, int K,
-                                     int param, void *stream, int warmup, int iters,
+                                     const void *stage, float *y, float *partial, size_t partial_floats, int M,
+                                     int N, int K, int param, void *stream, int warmup, int iters,
                                      double *avg_kernel_ms, double *elapsed_ms) {
     if (!weights || nweights <= 0 || iters <= 0) return -1;
     hipStream_t s = (hipStream_t)stream;
     const uint32_t q4 = (path & 256) ? SERA_QTYPE_Q4K_TILED : 12u;
     path &= 255;
+    /* the kernels trust the scratch they are given: refuse a short one */
+    const size_t need = bench_partial_floats(path, M, N, K, param);
+    if (need > 0 && (!partial || partial_floats < need)) {
+        char msg[160];
+        snprintf(msg, sizeof(msg), "sera_q4k_bench_kernel: path %d needs %zu floats of partial, got %zu", path, need,
+                 partial ? partial_floats : (size_t)0);
+        return sera_report_error(-2, msg);
+    }
     auto launch = [&](int i) -> hipError_t {
         const void *w = weights[i % nweights];
         switch (path) {

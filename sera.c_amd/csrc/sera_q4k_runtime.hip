@@ -155,6 +155,10 @@ void record(hipEvent_t e, hipStream_t s) {
 
 }  // namespace
 
+/* Records msg as the library's last error (for the other translation units
+ * of the library) and returns code. */
+int sera_report_error(int code, const char *msg) { return fail(code, "%s", msg); }
+
 extern "C" const char *sera_q4k_last_error(void) { return g_err; }
 
 /* ---- the decode path on a library-owned static scratch ------------------

@@ -158,7 +158,7 @@ def load():
         "sera_embedding": ([I, P, I, I, P, I, P, P], I),
         "sera_q4k_bench_linear": ([P, P, I, P, SZ, P, P, I, I, ctypes.POINTER(ctypes.c_double)], I),
         "sera_q4k_bench_stream": ([P, P, P, P, P, I, P, I, I, I, ctypes.POINTER(ctypes.c_double)], I),
-        "sera_q4k_bench_kernel": ([I, P, I, P, P, P, I, I, I, I, P, I, I,
+        "sera_q4k_bench_kernel": ([I, P, I, P, P, P, SZ, I, I, I, I, P, I, I,
                                    ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], I),
     }
     for name, (args, res) in sigs.items():

@@ -170,6 +170,16 @@ def test_kernel_entry_points_validate_on_host(L):
     assert b"chunk" in L.sera_q4k_last_error()
     assert L.sera_q4k_fewtok(0, d, d, d, None, None, 4, 128, 5120, 3, 0, None) == -1
     assert b"slots" in L.sera_q4k_last_error()
+    # the bench kernel loop refuses scratch shorter than its path writes,
+    # before any launch: the tail schedule's slots and counters, split-K sums
+    ws = (ctypes.c_void_p * 1)(256)
+    avg, tot = ctypes.c_double(), ctypes.c_double()
+    need = q3q4.mmq_tail_slot_floats(512, 1024, 0, 4) + L.sera_q4k_mmq_tiles(512, 1024)
+    assert L.sera_q4k_bench_kernel(15, ws, 1, d, d, d, need - 1, 512, 1024, 5120, 4, None, 0, 1,
+                                   ctypes.byref(avg), ctypes.byref(tot)) == -2
+    assert f"needs {need} floats".encode() in L.sera_q4k_last_error()
+    assert L.sera_q4k_bench_kernel(1, ws, 1, d, d, None, 0, 64, 128, 1024, 2, None, 0, 1,
+                                   ctypes.byref(avg), ctypes.byref(tot)) == -2
 
 
 def test_offset_and_grid_limits_rejected_on_host(L):
