@@ -54,6 +54,7 @@ typedef __attribute__((address_space(3))) void ft_lds_void;
 typedef __attribute__((address_space(1))) const void ft_global_cvoid;
 
 #define SERA_FEWTOK_MAX_TOKENS 16
+#define SERA_FEWTOK_RSRC_FLAGS 0x00020000   /* gfx9 buffer descriptor word 3: 32-bit dword format */
 #define SERA_FEWTOK_LDS_CHUNK_TOKENS 320   /* chunk x staged tokens: 40 super-blocks of 8, 20 of 16 */
 #define SERA_FEWTOK_XROW (Q4K_QK + 32)     /* LDS bytes per staged token and super-block: 16 columns + 2 pads */
 #define SERA_FEWTOK_XSLOTS (SERA_FEWTOK_XROW / 16)
@@ -193,7 +194,6 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     int tile = tb + wave;
     int row;
     bool row_ok;
-    const uint8_t *wr, *wnext;
     auto rows_of = [&](int t, int &r, bool &ok) {
         r = 16 * t + n;
         ok = r < N;
@@ -201,15 +201,33 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
     };
     rows_of(tile, row, row_ok);
     const int bstride = q4k_block_stride(tiled);   /* super-block to super-block of one row */
-    wr = W + q4k_block_offset(tiled, row, kb0, nkb);
-    /* super-block u of the chunk (u < C; the loop never asks for more) */
-    auto load_from = [&](const uint8_t *base, int u, FewtokW &w) {
-        const uint8_t *b = base + (size_t)u * bstride;
-        w.hd = *(const ft_v4u *)b;
-        w.q[0] = *(const ft_v4u *)(b + 16 + 16 * g);
-        w.q[1] = *(const ft_v4u *)(b + 80 + 16 * g);
+    const uint32_t rstride = (uint32_t)q4k_row_stride(tiled, nkb);
+    /* Direct loads are buffer loads from a resource over tile t (its first
+     * row and the chunk's first block, through the chunk's last block of its
+     * last row): the lane's row offset is the vector offset and the
+     * super-block step the scalar offset, so a load takes no vector address
+     * arithmetic. Rows past N read row N - 1; a tile past the last row (a
+     * wave with no tile, or the end of a workgroup's range) reads the last
+     * tile's rows and is never stored. */
+    auto tile_row0 = [&](int t) { return min(16 * t, 16 * ((N - 1) / 16)); };
+    auto tile_rsrc = [&](int t) {
+        const int r0 = tile_row0(t);
+        const uint32_t bytes = (uint32_t)(min(N - r0, 16) - 1) * rstride + (uint32_t)C * (uint32_t)bstride;
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W + q4k_block_offset(tiled, (size_t)r0, kb0, nkb)),
+                                                 (short)0, (int)bytes, SERA_FEWTOK_RSRC_FLAGS);
     };
-    auto load = [&](int u, FewtokW &w) { load_from(wr, u, w); };
+    auto tile_lane = [&](int t) { return (uint32_t)min(n, N - 1 - tile_row0(t)) * rstride; };
+    __amdgpu_buffer_rsrc_t wr = tile_rsrc(tile), wnext;
+    uint32_t wl = tile_lane(tile), wlnext;
+    /* super-block u of the chunk (u < C; the loop never asks for more) */
+    auto load_from = [&](__amdgpu_buffer_rsrc_t rs, uint32_t lo, int u, FewtokW &w) {
+        const int so = u * bstride;
+        const uint32_t lq = lo + 16 * g;
+        w.hd = __builtin_amdgcn_raw_buffer_load_b128(rs, lo, so, 0);
+        w.q[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, lq + 16, so, 0);
+        w.q[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, lq + 80, so, 0);
+    };
+    auto load = [&](int u, FewtokW &w) { load_from(wr, wl, u, w); };
     FewtokW wa, wb;
     /* WS: the wave's two weight buffers after the staged activations, and
      * the copy of sub-chunk sc (super-blocks WS sc .. WS sc + WS - 1 of the
@@ -618,8 +636,10 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             next = __builtin_amdgcn_readfirstlane(next);
             int nrow;
             bool nrow_ok;
-            rows_of(next < te ? next : tile, nrow, nrow_ok);
-            wnext = W + q4k_block_offset(tiled, nrow, kb0, nkb);
+            const int nt = next < te ? next : tile;
+            rows_of(nt, nrow, nrow_ok);
+            wnext = tile_rsrc(nt);
+            wlnext = tile_lane(nt);
             for (int u0 = 0; u0 < C; u0 += 4) {
                 load(u0 + 2, wc);
                 load(u0 + 3, wd);
@@ -627,10 +647,12 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
                 compute(u0, wa);
                 compute(u0 + 1, wb);
                 __builtin_amdgcn_sched_barrier(0);
-                int last = u0 + 4 == C;
-                __asm__ volatile("" : "+v"(last));
-                load_from(last ? wnext : wr + (size_t)(u0 + 4) * bstride, 0, wa);
-                load_from(last ? wnext + bstride : wr + (size_t)(u0 + 5) * bstride, 0, wb);
+                int last = __builtin_amdgcn_readfirstlane(u0 + 4 == C ? 1 : 0);
+                __asm__ volatile("" : "+s"(last));
+                const uint32_t lo = last ? wlnext : wl;
+                const __amdgpu_buffer_rsrc_t rs = last ? wnext : wr;
+                load_from(rs, lo, last ? 0 : u0 + 4, wa);
+                load_from(rs, lo, last ? 1 : u0 + 5, wb);
                 __builtin_amdgcn_sched_barrier(0);
                 compute(u0 + 2, wc);
                 compute(u0 + 3, wd);
@@ -641,6 +663,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             row = nrow;
             row_ok = nrow_ok;
             wr = wnext;
+            wl = wlnext;
         }
         __syncthreads();
         const int r0 = 16 * tb, nr = min(16 * te, N) - r0;
@@ -662,8 +685,10 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             next = __builtin_amdgcn_readfirstlane(next);
             int nrow;
             bool nrow_ok;
-            rows_of(next < te ? next : tile, nrow, nrow_ok);
-            wnext = W + q4k_block_offset(tiled, nrow, kb0, nkb);
+            const int nt = next < te ? next : tile;
+            rows_of(nt, nrow, nrow_ok);
+            wnext = tile_rsrc(nt);
+            wlnext = tile_lane(nt);
             /* even chunk: the select on an opaque flag keeps one loop body and
              * its exact load counting (the compiler would peel the last pair) */
             for (int u0 = 0; u0 < C; u0 += 2) {
@@ -671,9 +696,9 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
                 __builtin_amdgcn_sched_barrier(0);
                 compute(u0, wa);
                 __builtin_amdgcn_sched_barrier(0);
-                int last = u0 + 2 == C;
-                __asm__ volatile("" : "+v"(last));
-                load_from(last ? wnext : wr + (size_t)(u0 + 2) * bstride, 0, wa);
+                int last = __builtin_amdgcn_readfirstlane(u0 + 2 == C ? 1 : 0);
+                __asm__ volatile("" : "+s"(last));
+                load_from(last ? wnext : wr, last ? wlnext : wl, last ? 0 : u0 + 2, wa);
                 __builtin_amdgcn_sched_barrier(0);
                 compute(u0 + 1, wb);
                 __builtin_amdgcn_sched_barrier(0);
@@ -683,6 +708,7 @@ __global__ __launch_bounds__(NW * 64) void sera_q4k_fewtok_kernel(
             row = nrow;
             row_ok = nrow_ok;
             wr = wnext;
+            wl = wlnext;
         }
         /* the workgroup's rows [16 tb, 16 te) of every token, coalesced */
         __syncthreads();
