@@ -205,14 +205,29 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
      * SPLIT here made the host pass drop the kernel stubs */
     constexpr int WI = 8;
     static_assert((WINST + 3) / 4 == WI, "tile loads per wave");
-    uint32_t wvo[WI];   /* split layout only */
-    if constexpr (SPLIT) {
+    /* loop-invariant lane offsets of the tile loads. GGUF: the slot's row
+     * start plus 16 c, or 2^31 for a slot that holds nothing (beyond any
+     * resource range, so it loads zeros); a K step adds kb * 210 and rounds
+     * down to 16 bytes, (g & ~15) + 16 c = (g + 16 c) & ~15 */
+    uint32_t wvo[WI];
 #pragma unroll
-        for (int i = 0; i < WI; i++) {
-            const int f = (wave + 4 * i) * 64 + lane;
+    for (int i = 0; i < WI; i++) {
+        const int inst = wave + 4 * i;
+        if constexpr (SPLIT) {
+            const int f = inst * 64 + lane;
             const int r = f / Q6M_WCH, c = f - r * Q6M_WCH;
             const uint32_t g = (uint32_t)((uint64_t)min(n0 + r, N - 1) * rb - gbase);
             wvo[i] = g + (c < 13 ? 16u * (uint32_t)c : 0u);
+        } else {
+            /* slot f: 32-row group f / 481, pad slot 240 of each */
+            const int f = inst * 64 + lane;
+            const int grp = f / (32 * Q6M_WCH + 1), q = f - grp * (32 * Q6M_WCH + 1);
+            const int qq = q < 16 * Q6M_WCH ? q : q - 1;
+            const int rr = qq / Q6M_WCH, c = qq - rr * Q6M_WCH;
+            const int r = 32 * grp + rr;
+            const bool live = inst < WINST && f < WSLOTS && q != 16 * Q6M_WCH && c < 14;
+            wvo[i] = live ? (uint32_t)((uint64_t)min(n0 + min(r, Q6M_BN - 1), N - 1) * rb - gbase) + 16u * (uint32_t)c
+                          : 0x80000000u;
         }
     }
     auto issue_w = [&](int kb) {
@@ -224,18 +239,8 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, wvo[i],
                                                              kb * (int)BB, 0, 0);
                 } else {
-                    /* slot f: 32-row group f / 481, pad slot 240 of each */
-                    const int f = inst * 64 + lane;
-                    const int grp = f / (32 * Q6M_WCH + 1), q = f - grp * (32 * Q6M_WCH + 1);
-                    const int qq = q < 16 * Q6M_WCH ? q : q - 1;
-                    const int rr = qq / Q6M_WCH, c = qq - rr * Q6M_WCH;
-                    const int r = 32 * grp + rr;
-                    const bool live = f < WSLOTS && q != 16 * Q6M_WCH && c < 14;
-                    const uint32_t g = (uint32_t)((uint64_t)min(n0 + min(r, Q6M_BN - 1), N - 1) * rb - gbase) +
-                                       (uint32_t)kb * BB;
-                    const uint32_t vo = live ? (g & ~15u) + 16u * (uint32_t)c : 0x80000000u;
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16, vo, 0, 0,
-                                                             0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (q6m_lds_void *)&sm.w[inst * 1024], 16,
+                                                             (wvo[i] + (uint32_t)kb * BB) & ~15u, 0, 0, 0);
                 }
             }
         }
@@ -355,16 +360,19 @@ __global__ __launch_bounds__(256, WPE) void sera_q6k_mmq_kernel(
             for (int i = 0; i < 2; i++) QH[i] = *(const q6v4u *)&sm.w[base + 128u + 32u * i + 16u * h];
             SC = *(const q6v4u *)&sm.w[base + 192u];
         } else {
-            const uint32_t X[6] = {16u * h, 32u + 16u * h, 64u + 16u * h, 96u + 16u * h, 128u + 16u * h,
-                                   160u + 16u * h};
+            /* every run starts a multiple of 16 bytes after the block, so
+             * (base + X) & ~3 = (base & ~3) + X: one address register, the
+             * runs at immediate offsets */
+            const uint32_t *w4 = (const uint32_t *)&sm.w[(base & ~3u) + 16u * h];
+            constexpr uint32_t X[6] = {0u, 32u, 64u, 96u, 128u, 160u};
 #pragma unroll
             for (int i = 0; i < 6; i++) {
-                const uint32_t *p = (const uint32_t *)&sm.w[(base + X[i]) & ~3u];
+                const uint32_t *p = w4 + X[i] / 4;
                 const uint32_t v[5] = {p[0], p[1], p[2], p[3], p[4]};
                 if (i < 4) QL[i] = q6m_align16(v, sh);
                 else QH[i - 4] = q6m_align16(v, sh);
             }
-            const uint32_t *p = (const uint32_t *)&sm.w[(base + 192u) & ~3u];
+            const uint32_t *p = (const uint32_t *)&sm.w[(base & ~3u) + 192u];
             const uint32_t v[5] = {p[0], p[1], p[2], p[3], p[4]};
             SC = q6m_align16(v, sh);
             dword = v[4];
