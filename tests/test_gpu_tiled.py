@@ -172,8 +172,10 @@ def test_tiled_mmvq_bit_identical(torch, N, K):
             same_bits(yg, yt, f"mmvq M={M} N={N} K={K} rows={rows}")
 
 
+# (0, 4, 64, 25600): 8-wave workgroups whose last four waves own no tile (the
+# tiled bytes load directly, the GGUF bytes through the staged copy)
 FEWTOK_CASES = [(0, 2, 25600, 5120), (0, 4, 25600, 5120), (0, 8, 5120, 25600), (0, 8, 1008, 2304),
-                (1, 9, 25600, 5120), (1, 16, 151936, 5120), (1, 12, 4096, 25600), (1, 4, 16, 256)]
+                (1, 9, 25600, 5120), (1, 16, 151936, 5120), (1, 12, 4096, 25600), (1, 4, 16, 256), (0, 4, 64, 25600)]
 
 
 @pytest.mark.parametrize("form,M,N,K", FEWTOK_CASES)
